@@ -1,0 +1,167 @@
+#!/usr/bin/env python3
+"""Benchmark of libsimp_hip.so on one MI355X.
+
+Headline (the JSON line's ``value``): exact int8 GEMM throughput, u8 x s8 -> i32
+(vpdpbusd semantics), at the largest square shape of BASELINE configs[1]
+(8192^3), inputs resident in HBM.  One step = one C = A x B over the
+synthetic batch (A u8 uniform [0,255], B s8 uniform [-128,127], seed 42).
+
+Also reported on the same line: the configs[1] sweep (TOPS per shape), the
+roofline of the GEMM kernel (HIP events on the stream the kernel is launched
+on), and the CPU baseline -- the oracle's restatement of the reference's VNNI
+kernel timed on this host's cores on a bounded row-block sample of the same
+8192^3 problem.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-sweep] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "int8 GEMM TOPS (% MFMA peak); W4 decode tokens/s + HBM GB/s (1 GPU)"
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+HBM_PEAK_GBS = 8000.0
+
+
+def gemm_events(fn, a, b, c, steps, warmup, stream):
+    """Average ms per call over `steps` back-to-back launches (HIP events)."""
+    import torch
+    for _ in range(warmup):
+        fn(a, b, c)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn(a, b, c)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def make_inputs(M, N, K, dev, seed=42):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (K, N), dtype=torch.int8, device=dev, generator=g)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    return a, b, c
+
+
+def cpu_baseline(n, budget_s=12.0):
+    """Oracle VNNI restatement on host cores, row blocks of the n^3 problem."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    cores = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(42)
+    rows = 64
+    a = rng.integers(0, 256, (rows, n)).astype(np.uint8)
+    b = rng.integers(-128, 128, (n, n)).astype(np.int8)
+    bt = np.ascontiguousarray(b.T)
+    oracle.matmul_i8_vnni(a[:8], bt, a_unsigned=True, b_nk=True, nthreads=cores)  # warm
+    done, t0, hw = 0, time.perf_counter(), False
+    while True:
+        _, hw = oracle.matmul_i8_vnni(a, bt, a_unsigned=True, b_nk=True, nthreads=cores)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or done * rows >= n:
+            break
+    tops = 2.0 * done * rows * n * n / el / 1e12
+    return {"value": round(tops, 4), "unit": "TOPS", "cores": cores, "kind": "port",
+            "sample": (f"{done} blocks of {rows} rows x {n} x {n} (u8xs8->i32, B pre-transposed "
+                       f"as the reference's B_T) in {el:.1f}s; "
+                       f"{'AVX-512 VNNI' if hw else 'scalar (host lacks AVX-512 VNNI)'}")}
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        return json.load(open(p)).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--size", type=int, default=8192)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: every configuration of this path fits one "
+              "MI355X and no multi-GPU run is part of this build (use --gpus 1).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import simplang_amd as sa
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    sa.set_stream(stream)
+
+    n = args.size
+    a, b, c = make_inputs(n, n, n, dev)
+    torch.cuda.synchronize()
+    ms = gemm_events(sa.matmul_u8s8_i32, a, b, c, args.steps, args.warmup, stream)
+    ops = 2.0 * n * n * n
+    tops = ops / (ms * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.empty_cache()
+
+    sweep = []
+    if not args.no_sweep:
+        shapes = [(s, s, s) for s in (256, 512, 768, 1024, 2048, 4096)]
+        shapes += [(m, nn, k) for m in (1, 8, 64) for (k, nn) in ((768, 2048), (2048, 768),
+                                                                   (3200, 8640))]
+        for (M, N, K) in shapes:
+            a, b, c = make_inputs(M, N, K, dev)
+            reps = 50 if M * N * K < 2**33 else 10
+            t = gemm_events(sa.matmul_u8s8_i32, a, b, c, reps, 3, stream)
+            byts = M * K + K * N + 4 * M * N
+            sweep.append({"M": M, "N": N, "K": K, "us": round(t * 1e3, 2),
+                          "TOPS": round(2.0 * M * N * K / (t * 1e-3) / 1e12, 2),
+                          "GBs": round(byts / (t * 1e-3) / 1e9, 1)})
+            del a, b, c
+        torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline(n)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (u8 x s8 -> i32)",
+        "data": "synthetic: A u8 uniform [0,255], B s8 uniform [-128,127], seed 42",
+        "config": {"workload": f"int8 GEMM u8xs8->i32 {n}^3 (BASELINE configs[1], largest square)",
+                   "M": n, "N": n, "K": n, "layout": "A[M,K], B[K,N] row-major, C[M,N] i32"},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": load_traffic(f"gemm_i8_{n}")},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

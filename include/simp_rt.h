@@ -1,0 +1,103 @@
+/*
+ * simp_rt.h -- C ABI of libsimp_hip.so, the MI355X (gfx950) runtime for the
+ * tensor ops SimpLang's MLIR backend lowers into.
+ *
+ * Argument convention (the reference's host ABI, F10 of the reference
+ * programs: examples/llama2/bench_llama_quant.cpp:10-28,
+ * simptensor/benchmarks/bench_int8_parallel_runner.cpp:13-16): every array
+ * operand is an MLIR memref descriptor expanded into scalars,
+ *   rank 1 (T[] arrays):       T* alloc, T* aligned, i64 offset, i64 size, i64 stride
+ *   rank 2 (tensors):          T* alloc, T* aligned, i64 offset,
+ *                              i64 size0, i64 size1, i64 stride0, i64 stride1
+ * Elements live at aligned + offset + i*stride0 + j*stride1 (row-major,
+ * stride1 must be 1).  `alloc` is carried for ABI fidelity and is not read.
+ * Scalars follow in the operand order fixed by SimpLang's builtin parser
+ * (src/mlir/mlir_codegen.cpp:1388-1531,2068-2292).
+ *
+ * Pointers may be device memory (used in place), host ranges registered with
+ * simp_rt_register (their device mirror is used), or plain host memory
+ * (staged through device memory; the call then blocks until the outputs are
+ * back on the host).  With device / registered operands a call is
+ * asynchronous on the calling thread's stream (simp_rt_set_stream).
+ *
+ * Every entry point returns 0 on success or a negative SIMP_RT_E* status and
+ * leaves a message for simp_rt_last_error().  The reference ops have no
+ * status (they are inlined loops, src/mlir/lowering/ConvertSimpToMemRef.cpp).
+ */
+#ifndef SIMP_RT_H
+#define SIMP_RT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIMP_RT_ABI_VERSION 1
+
+#define SIMP_RT_OK 0
+#define SIMP_RT_EINVAL (-1)      /* bad shape, stride, offset or null pointer */
+#define SIMP_RT_EHIP (-2)        /* HIP runtime error */
+#define SIMP_RT_ENOMEM (-3)      /* device allocation failed */
+#define SIMP_RT_EUNSUPPORTED (-4)/* valid request this build does not handle */
+#define SIMP_RT_ENODEV (-5)      /* no HIP device */
+
+/* simp_rt_register flags */
+#define SIMP_RT_REG_IMMUTABLE 1  /* weights: uploaded once, never an output */
+
+/* ------------------------------------------------------------ runtime -- */
+/* No reference counterpart: the reference runs in-process on the CPU.  The
+ * loader it replaces is KernelRunner (runtime/include/kernel_runner.hpp:27-103). */
+const char *simp_rt_last_error(void);
+int32_t simp_rt_version(void);
+int32_t simp_rt_init(void);
+int32_t simp_rt_set_stream(void *hip_stream); /* per calling thread; NULL = null stream */
+void *simp_rt_get_stream(void);
+int32_t simp_rt_sync(void);
+int32_t simp_rt_register(const void *host_ptr, int64_t bytes, int32_t flags);
+int32_t simp_rt_unregister(const void *host_ptr);
+int32_t simp_rt_device_ptr(const void *host_ptr, void **dev_ptr);
+int32_t simp_rt_sync_to_host(const void *host_ptr, int64_t bytes);
+int32_t simp_rt_malloc(void **dev_ptr, int64_t bytes);
+int32_t simp_rt_free(void *dev_ptr);
+int32_t simp_rt_memcpy(void *dst, const void *src, int64_t bytes); /* any direction, blocking */
+
+/* --------------------------------------------------------------- int8 -- */
+
+/* tensor_matmul on i8 tensors: C[M,N] = A[M,K] x B[K,N], s8 x s8 -> i32,
+ * C overwritten.  Replaces TensorMatMulOpLowering's i8 branch
+ * (src/mlir/lowering/ConvertSimpToMemRef.cpp:3136-3279, F1) together with the
+ * VNNI rewrite of its K loop (src/mlir/passes/VNNIPass.cpp:597-999); the
+ * caller-owned C follows TensorMatMulIntoOpLowering (:3490-3627). */
+int32_t simp_rt_tensor_matmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* tensor_matmul_nt on i8: C[M,N] = A[M,K] x B_T[N,K]^T, s8 x s8 -> i32.
+ * Replaces TensorMatMulNTOpLowering (ConvertSimpToMemRef.cpp:3373-3486). */
+int32_t simp_rt_tensor_matmul_nt_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* Raw vpdpbusd semantics, u8 x s8 -> i32: C[M,N] = A[M,K](u8) x B[K,N](s8).
+ * Replaces the hand-written VNNI GEMMs the reference benchmarks against
+ * (simptensor/benchmarks/bench_int8_matmul_runner.cpp:91-185, scalar
+ * semantics simptensor/tests/test_vnni_correctness.cpp:28-42). */
+int32_t simp_rt_matmul_u8s8_i32(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* u8 x s8 -> i32 with B given transposed, B_T[N,K] (the layout the reference's
+ * VNNI kernels read, bench_int8_matmul_multicore.cpp:39-89). */
+int32_t simp_rt_matmul_nt_u8s8_i32(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SIMP_RT_H */

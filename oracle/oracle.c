@@ -1,0 +1,451 @@
+/*
+ * oracle.c -- CPU restatement of SimpLang's tensor-op hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for libsimp_hip.so, loaded by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg.  Never on the
+ * product path.  Citations are relative to the SimpLang source tree.
+ *
+ * Parity pins (see tests/test_oracle.py):
+ *   orc_vpdpbusd16            -- nine KATs of test_vnni_correctness.cpp + the
+ *                                reference scalar function compiled in place
+ *   orc_matmul_i8             -- closed forms (identity/one-hot/constant) +
+ *                                reference VNNI kernel compiled in place
+ *   orc_matmul_i8_vnni        -- equals orc_matmul_i8 bit for bit (both paths)
+ *   orc_int8_recipe_inputs    -- recipe restated; checksum vs reference kernel
+ *   orc_matmul_f32_acc        -- f64 brute force, KAT 110 (tests/test_tensor_matmul_runner.cpp:39)
+ *   orc_rmsnorm/softmax/silu  -- KATs of examples/llama2/kernels/test_*_host.cpp
+ *   orc_matmul_quant_f5       -- closed-form KAT of test_quant_roofline.cpp:71-92
+ *                                (0x55 bytes, scale .01) + f64 dequant brute force
+ *   orc_matmul_w4s            -- F6 == F5 with u = q+8, zero = -8*scale; brute force
+ *   orc_rope                  -- pos 0 identity, rotation preserves pair norms,
+ *                                closed-form angle for pair 0
+ *   orc_llama_forward         -- parity unpinned beyond its parts: the reference
+ *                                holds no golden logits (docs/benchmark/llama_results.md:81-95)
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#define ORC_HAVE_X86 1
+#else
+#define ORC_HAVE_X86 0
+#endif
+
+/* ---------------------------------------------------------------- int8 -- */
+
+void orc_vpdpbusd16(const uint8_t *a, const int8_t *b, const int32_t *acc,
+                    int32_t *out) {
+  for (int i = 0; i < 16; i++) {
+    uint32_t s = (uint32_t)acc[i];
+    for (int j = 0; j < 4; j++)
+      s += (uint32_t)((int32_t)a[4 * i + j] * (int32_t)b[4 * i + j]);
+    out[i] = (int32_t)s;
+  }
+}
+
+static inline int32_t a_elem(const void *A, int64_t idx, int a_unsigned) {
+  return a_unsigned ? (int32_t)((const uint8_t *)A)[idx]
+                    : (int32_t)((const int8_t *)A)[idx];
+}
+
+void orc_matmul_i8(const void *A, int64_t lda, const int8_t *B, int64_t ldb,
+                   int32_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                   int a_unsigned, int b_nk) {
+  for (int64_t i = 0; i < M; i++) {
+    for (int64_t j = 0; j < N; j++) {
+      uint32_t s = 0;
+      for (int64_t k = 0; k < K; k++) {
+        int32_t b = b_nk ? (int32_t)B[j * ldb + k] : (int32_t)B[k * ldb + j];
+        s += (uint32_t)(a_elem(A, i * lda + k, a_unsigned) * b);
+      }
+      C[i * ldc + j] = (int32_t)s;
+    }
+  }
+}
+
+/* B_T[N,K] from B[K,N] (ConvertSimpToMemRef.cpp:3168-3216 materialises it). */
+static int8_t *make_bt(const int8_t *B, int64_t N, int64_t K) {
+  int8_t *bt = (int8_t *)malloc((size_t)(N * K > 0 ? N * K : 1));
+  for (int64_t k = 0; k < K; k++)
+    for (int64_t j = 0; j < N; j++) bt[j * K + k] = B[k * N + j];
+  return bt;
+}
+
+/* One (row block of up to 4 rows, column j) cell group, scalar emulation of
+ * the VNNI pass's loop body (VNNIPass.cpp:752-906). */
+static void vnni_cell_scalar(const uint8_t *A, const int8_t *bt, int32_t *C,
+                             int64_t i0, int64_t rows, int64_t j, int64_t N,
+                             int64_t K, int a_unsigned) {
+  uint8_t flip = a_unsigned ? 0x00 : 0x80;
+  uint32_t acc[4] = {0, 0, 0, 0}, bias = 0, tail[4] = {0, 0, 0, 0};
+  int64_t k = 0;
+  for (; k + 64 <= K; k += 64) {
+    for (int64_t kk = k; kk < k + 64; kk++) {
+      int32_t b = bt[j * K + kk];
+      for (int r = 0; r < rows; r++)
+        acc[r] += (uint32_t)((int32_t)(uint8_t)(A[(i0 + r) * K + kk] ^ flip) * b);
+      bias += (uint32_t)b;
+    }
+  }
+  for (; k < K; k++) { /* scalar tail, on the original operand type */
+    int32_t b = bt[j * K + k];
+    for (int r = 0; r < rows; r++) {
+      int32_t a = a_unsigned ? (int32_t)A[(i0 + r) * K + k]
+                             : (int32_t)(int8_t)A[(i0 + r) * K + k];
+      tail[r] += (uint32_t)(a * b);
+    }
+  }
+  uint32_t corr = a_unsigned ? 0u : bias * 128u;
+  for (int r = 0; r < rows; r++) C[(i0 + r) * N + j] = (int32_t)(acc[r] + tail[r] - corr);
+}
+
+#if ORC_HAVE_X86
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static void vnni_block_avx512(const uint8_t *A, const int8_t *bt, int32_t *C,
+                              int64_t i0, int64_t rows, int64_t N, int64_t K,
+                              int a_unsigned) {
+  const __m512i flip = _mm512_set1_epi8(a_unsigned ? 0 : (char)0x80);
+  const __m512i ones = _mm512_set1_epi8(1);
+  for (int64_t j = 0; j < N; j++) {
+    __m512i acc[4], bias = _mm512_setzero_si512();
+    for (int r = 0; r < 4; r++) acc[r] = _mm512_setzero_si512();
+    int64_t k = 0;
+    for (; k + 64 <= K; k += 64) {
+      __m512i vb = _mm512_loadu_si512((const void *)&bt[j * K + k]);
+      for (int r = 0; r < rows; r++) {
+        __m512i va = _mm512_xor_si512(
+            _mm512_loadu_si512((const void *)&A[(i0 + r) * K + k]), flip);
+        acc[r] = _mm512_dpbusd_epi32(acc[r], va, vb);
+      }
+      bias = _mm512_dpbusd_epi32(bias, ones, vb);
+    }
+    uint32_t tail[4] = {0, 0, 0, 0};
+    for (; k < K; k++) {
+      int32_t b = bt[j * K + k];
+      for (int r = 0; r < rows; r++) {
+        int32_t a = a_unsigned ? (int32_t)A[(i0 + r) * K + k]
+                               : (int32_t)(int8_t)A[(i0 + r) * K + k];
+        tail[r] += (uint32_t)(a * b);
+      }
+    }
+    uint32_t corr = a_unsigned ? 0u : (uint32_t)_mm512_reduce_add_epi32(bias) * 128u;
+    for (int r = 0; r < rows; r++)
+      C[(i0 + r) * N + j] =
+          (int32_t)((uint32_t)_mm512_reduce_add_epi32(acc[r]) + tail[r] - corr);
+  }
+}
+#endif
+
+static int host_has_vnni(void) {
+#if ORC_HAVE_X86
+  __builtin_cpu_init();
+  return __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512bw");
+#else
+  return 0;
+#endif
+}
+
+int orc_matmul_i8_vnni(const void *A, const int8_t *B, int32_t *C, int64_t M,
+                       int64_t N, int64_t K, int a_unsigned, int b_nk,
+                       int nthreads) {
+  const uint8_t *a = (const uint8_t *)A;
+  int8_t *bt_owned = b_nk ? NULL : make_bt(B, N, K);
+  const int8_t *bt = b_nk ? B : bt_owned;
+  int use_vnni = host_has_vnni();
+  int64_t nblk = (M + 3) / 4;
+  if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+  for (int64_t blk = 0; blk < nblk; blk++) {
+    int64_t i0 = blk * 4;
+    int64_t rows = M - i0 < 4 ? M - i0 : 4;
+#if ORC_HAVE_X86
+    if (use_vnni) {
+      vnni_block_avx512(a, bt, C, i0, rows, N, K, a_unsigned);
+      continue;
+    }
+#endif
+    for (int64_t j = 0; j < N; j++) vnni_cell_scalar(a, bt, C, i0, rows, j, N, K, a_unsigned);
+  }
+  free(bt_owned);
+  return use_vnni;
+}
+
+void orc_int8_recipe_inputs(int64_t N, int8_t *A, int8_t *B) {
+  for (int64_t i = 0; i < N; i++)
+    for (int64_t j = 0; j < N; j++) {
+      int v = (int)((i * N + j) % 127) - 64;
+      A[i * N + j] = (int8_t)v;
+      B[j * N + i] = (int8_t)v;
+    }
+}
+
+int32_t orc_checksum_i32(const int32_t *C, int64_t n) {
+  uint32_t s = 0;
+  for (int64_t i = 0; i < n; i++) s += (uint32_t)C[i];
+  return (int32_t)s;
+}
+
+/* ------------------------------------------------------------ fp32 ops -- */
+
+void orc_matmul_f32_acc(const float *lhs, const float *rhs, float *out,
+                        int64_t m, int64_t k, int64_t n, int64_t lhs_off,
+                        int64_t rhs_off, int64_t out_off) {
+  const float *A = lhs + lhs_off, *B = rhs + rhs_off;
+  float *C = out + out_off;
+  for (int64_t i = 0; i < m; i++)
+    for (int64_t j = 0; j < n; j++) {
+      float acc = C[i * n + j];
+      for (int64_t kk = 0; kk < k; kk++) acc += A[i * k + kk] * B[kk * n + j];
+      C[i * n + j] = acc;
+    }
+}
+
+void orc_rmsnorm(const float *in, const float *w, float *out, int64_t size,
+                 float eps, int64_t w_off) {
+  float ss = 0.0f;
+  for (int64_t i = 0; i < size; i++) ss += in[i] * in[i];
+  float rms = sqrtf(ss / (float)size + eps);
+  for (int64_t i = 0; i < size; i++) out[i] = (in[i] / rms) * w[w_off + i];
+}
+
+void orc_softmax(const float *in, float *out, int64_t size, int64_t in_off,
+                 int64_t out_off) {
+  float mx = in[in_off];
+  for (int64_t i = 1; i < size; i++)
+    if (in[in_off + i] > mx) mx = in[in_off + i];
+  float sum = 0.0f;
+  for (int64_t i = 0; i < size; i++) {
+    float e = expf(in[in_off + i] - mx);
+    out[out_off + i] = e;
+    sum += e;
+  }
+  for (int64_t i = 0; i < size; i++) out[out_off + i] = out[out_off + i] / sum;
+}
+
+void orc_silu(const float *in, float *out, int64_t size) {
+  for (int64_t i = 0; i < size; i++) out[i] = in[i] / (1.0f + expf(-in[i]));
+}
+
+/* ------------------------------------------------------------------ W4 -- */
+
+void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
+                         const float *zeros, const float *in, float *out,
+                         int64_t rows, int64_t cols, int64_t gs, int64_t off) {
+  int64_t ngroups = cols / gs, ntiles = gs / 16;
+  for (int64_t i = 0; i < rows; i++) {
+    int64_t row_off = i * cols;
+    out[i] = 0.0f;
+    for (int64_t g = 0; g < ngroups; g++) {
+      int64_t gidx = (off + row_off) / gs + g;
+      float s = scales[gidx], z = zeros[gidx];
+      float acc = 0.0f;
+      for (int64_t t = 0; t < ntiles; t++) {
+        float tile[16];
+        int64_t k0 = g * gs + t * 16;
+        for (int j = 0; j < 16; j++) {
+          int64_t widx = off + row_off + k0 + j;
+          uint8_t byte = qw[widx >> 1];
+          uint32_t q = (widx & 1) ? (uint32_t)(byte >> 4) & 15u : (uint32_t)byte & 15u;
+          float scaled = (float)q * s;
+          tile[j] = scaled + z;
+        }
+        for (int j = 0; j < 16; j++) {
+          int64_t kg = k0 + j;
+          if (kg < cols) {
+            float prod = tile[j] * in[kg];
+            acc = acc + prod;
+          }
+        }
+      }
+      out[i] = out[i] + acc;
+    }
+  }
+}
+
+void orc_quantize_f5(const float *w, int64_t total, int64_t gs, uint8_t *qw,
+                     float *scales, float *zeros) {
+  int64_t ng = (total + gs - 1) / gs;
+  memset(qw, 0, (size_t)((total + 1) / 2));
+  for (int64_t g = 0; g < ng; g++) {
+    int64_t st = g * gs, en = st + gs < total ? st + gs : total;
+    float mn = w[st], mx = w[st];
+    for (int64_t i = st; i < en; i++) {
+      mn = w[i] < mn ? w[i] : mn;
+      mx = w[i] > mx ? w[i] : mx;
+    }
+    float sc = (mx - mn) / 15.0f;
+    if (sc < 1e-8f) sc = 1e-8f;
+    scales[g] = sc;
+    zeros[g] = mn;
+    for (int64_t i = st; i < en; i++) {
+      int q = (int)roundf((w[i] - mn) / sc);
+      q = q < 0 ? 0 : (q > 15 ? 15 : q);
+      if (i % 2 == 0) qw[i / 2] = (uint8_t)q;
+      else qw[i / 2] |= (uint8_t)(q << 4);
+    }
+  }
+}
+
+static inline int32_t s4_at(const uint8_t *row, int64_t k) {
+  uint8_t byte = row[k >> 1];
+  int32_t n = (k & 1) ? (byte >> 4) & 15 : byte & 15;
+  return n >= 8 ? n - 16 : n; /* n | 0xF0 as i8, ConvertSimpToMemRef.cpp:3030-3035 */
+}
+
+void orc_matmul_w4s(const uint8_t *qw, const float *scales, const float *x,
+                    float *out, int64_t M, int64_t N, int64_t K, int64_t gs) {
+  int64_t ng = K / gs;
+  for (int64_t m = 0; m < M; m++)
+    for (int64_t n = 0; n < N; n++) {
+      const uint8_t *row = qw + n * (K / 2);
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; k++) {
+        float w = (float)s4_at(row, k) * scales[n * ng + k / gs];
+        acc += (double)w * (double)x[m * K + k];
+      }
+      out[m * N + n] = (float)acc;
+    }
+}
+
+void orc_matmul_w4s_f32(const uint8_t *qw, const float *scales, const float *x,
+                        float *out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        int nthreads) {
+  int64_t ng = K / gs;
+  if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+  for (int64_t n = 0; n < N; n++) {
+    const uint8_t *row = qw + n * (K / 2);
+    for (int64_t m = 0; m < M; m++) {
+      float acc = 0.0f;
+      for (int64_t g = 0; g < ng; g++) {
+        float s = scales[n * ng + g], part = 0.0f;
+        for (int64_t k = g * gs; k < (g + 1) * gs; k++)
+          part += (float)s4_at(row, k) * x[m * K + k];
+        acc += part * s;
+      }
+      out[m * N + n] = acc;
+    }
+  }
+}
+
+/* -------------------------------------------------------------- decode -- */
+
+void orc_rope(float *q, float *k, int64_t dim, int64_t kv_dim, int64_t hs,
+              int64_t pos, float theta) {
+  for (int64_t i = 0; i < dim; i += 2) {
+    float hd = (float)(i % hs), hsf = (float)hs;
+    float freq = 1.0f / powf(theta, hd / hsf);
+    float val = (float)pos * freq;
+    float fcr = cosf(val), fci = sinf(val);
+    float q0 = q[i], q1 = q[i + 1];
+    q[i] = q0 * fcr - q1 * fci;
+    q[i + 1] = q0 * fci + q1 * fcr;
+    if (i < kv_dim) {
+      float k0 = k[i], k1 = k[i + 1];
+      k[i] = k0 * fcr - k1 * fci;
+      k[i + 1] = k0 * fci + k1 * fcr;
+    }
+  }
+}
+
+/* y[rows] = W[rows, cols] x, W either fp32 or F6 W4 (double accumulation). */
+static void gemv(const orc_llama_cfg *c, const float *wf, const uint8_t *wq,
+                 const float *ws, const float *x, float *y, int64_t rows,
+                 int64_t cols) {
+  if (c->w4) {
+    orc_matmul_w4s(wq, ws, x, y, 1, rows, cols, c->gs);
+    return;
+  }
+  for (int64_t r = 0; r < rows; r++) {
+    double acc = 0.0;
+    for (int64_t j = 0; j < cols; j++) acc += (double)wf[r * cols + j] * (double)x[j];
+    y[r] = (float)acc;
+  }
+}
+
+void orc_llama_forward(const orc_llama_cfg *c, const orc_llama_weights *w,
+                       float *key_cache, float *value_cache, int64_t token,
+                       int64_t pos, float *logits) {
+  int64_t dim = c->dim, hid = c->hidden, hs = dim / c->n_heads;
+  int64_t kv_dim = dim * c->n_kv_heads / c->n_heads;
+  float *x = (float *)malloc(sizeof(float) * dim);
+  float *xb = (float *)malloc(sizeof(float) * dim);
+  float *xb2 = (float *)malloc(sizeof(float) * dim);
+  float *q = (float *)malloc(sizeof(float) * dim);
+  float *kk = (float *)malloc(sizeof(float) * kv_dim);
+  float *vv = (float *)malloc(sizeof(float) * kv_dim);
+  float *hb = (float *)malloc(sizeof(float) * hid);
+  float *hb2 = (float *)malloc(sizeof(float) * hid);
+  float *att = (float *)malloc(sizeof(float) * (pos + 1));
+  float *att_soft = (float *)malloc(sizeof(float) * (pos + 1));
+  memcpy(x, w->emb + token * dim, sizeof(float) * dim);
+  float scale = sqrtf((float)hs);
+  int64_t sq_w4 = c->gs > 0 ? dim / c->gs : 0;
+  for (int64_t l = 0; l < c->n_layers; l++) {
+    orc_rmsnorm(x, w->rms_att, xb, dim, c->eps, l * dim);
+    /* per-layer W4 slices: bytes rows*cols/2, scales rows*cols/gs */
+#define WF(p, r, cl) ((p) ? (p) + l * (r) * (cl) : NULL)
+#define WQ(p, r, cl) ((p) ? (p) + l * (r) * (cl) / 2 : NULL)
+#define WS(p, r, cl) ((p) ? (p) + l * (r) * (cl) / c->gs : NULL)
+    gemv(c, WF(w->wq, dim, dim), WQ(w->q_wq, dim, dim), c->w4 ? WS(w->s_wq, dim, dim) : NULL, xb, q, dim, dim);
+    gemv(c, WF(w->wk, kv_dim, dim), WQ(w->q_wk, kv_dim, dim), c->w4 ? WS(w->s_wk, kv_dim, dim) : NULL, xb, kk, kv_dim, dim);
+    gemv(c, WF(w->wv, kv_dim, dim), WQ(w->q_wv, kv_dim, dim), c->w4 ? WS(w->s_wv, kv_dim, dim) : NULL, xb, vv, kv_dim, dim);
+    orc_rope(q, kk, dim, kv_dim, hs, pos, c->theta);
+    float *kc = key_cache + l * c->seq_len * kv_dim, *vc = value_cache + l * c->seq_len * kv_dim;
+    memcpy(kc + pos * kv_dim, kk, sizeof(float) * kv_dim);
+    memcpy(vc + pos * kv_dim, vv, sizeof(float) * kv_dim);
+    for (int64_t h = 0; h < c->n_heads; h++) {
+      int64_t kvh = h * c->n_kv_heads / c->n_heads;
+      const float *qh = q + h * hs;
+      for (int64_t t = 0; t <= pos; t++) {
+        const float *kt = kc + t * kv_dim + kvh * hs;
+        double s = 0.0;
+        for (int64_t i = 0; i < hs; i++) s += (double)qh[i] * (double)kt[i];
+        att[t] = (float)s / scale;
+      }
+      orc_softmax(att, att_soft, pos + 1, 0, 0);
+      for (int64_t i = 0; i < hs; i++) {
+        double v = 0.0;
+        for (int64_t t = 0; t <= pos; t++)
+          v += (double)att_soft[t] * (double)vc[t * kv_dim + kvh * hs + i];
+        xb[h * hs + i] = (float)v;
+      }
+    }
+    gemv(c, WF(w->wo, dim, dim), WQ(w->q_wo, dim, dim), c->w4 ? WS(w->s_wo, dim, dim) : NULL, xb, xb2, dim, dim);
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + xb2[i];
+    orc_rmsnorm(x, w->rms_ffn, xb, dim, c->eps, l * dim);
+    gemv(c, WF(w->w1, hid, dim), WQ(w->q_w1, hid, dim), c->w4 ? WS(w->s_w1, hid, dim) : NULL, xb, hb, hid, dim);
+    gemv(c, WF(w->w3, hid, dim), WQ(w->q_w3, hid, dim), c->w4 ? WS(w->s_w3, hid, dim) : NULL, xb, hb2, hid, dim);
+    orc_silu(hb, hb, hid);
+    for (int64_t i = 0; i < hid; i++) hb[i] = hb[i] * hb2[i];
+    gemv(c, WF(w->w2, dim, hid), WQ(w->q_w2, dim, hid), c->w4 ? WS(w->s_w2, dim, hid) : NULL, hb, xb, dim, hid);
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + xb[i];
+#undef WF
+#undef WQ
+#undef WS
+  }
+  (void)sq_w4;
+  orc_rmsnorm(x, w->rms_final, xb, dim, c->eps, 0);
+  gemv(c, w->wcls, w->q_wcls, w->s_wcls, xb, logits, c->vocab, dim);
+  free(x); free(xb); free(xb2); free(q); free(kk); free(vv);
+  free(hb); free(hb2); free(att); free(att_soft);
+}
+
+int64_t orc_argmax(const float *logits, int64_t n) {
+  int64_t best = 0;
+  float mv = logits[0];
+  for (int64_t i = 1; i < n; i++)
+    if (logits[i] > mv) {
+      mv = logits[i];
+      best = i;
+    }
+  return best;
+}

@@ -1,0 +1,164 @@
+/*
+ * oracle.h -- CPU restatement of SimpLang's tensor-op hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP runtime
+ * (libsimp_hip.so): it is loaded by tests/, by __graft_entry__.smoke() and by
+ * bench.py's cpu_baseline leg, and by nothing on the product path.
+ *
+ * Every function cites the reference code it restates (paths relative to the
+ * SimpLang source tree).  Parity status of each function, and what pins it,
+ * is listed next to the declaration ("pinned by ...").
+ */
+#ifndef SIMP_ORACLE_H
+#define SIMP_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- int8 -- */
+
+/* vpdpbusd on one 512-bit register: 16 lanes, each lane
+ *   out[i] = acc[i] + sum_{j<4} (u8)a[4i+j] * (s8)b[4i+j]     (i32 wraparound)
+ * Restates scalar_vpdpbusd_reference, simptensor/tests/test_vnni_correctness.cpp:28-42.
+ * Pinned by the nine known answers of that file (:76-361) and by the reference
+ * function itself, compiled in place into oracle/_ref. */
+void orc_vpdpbusd16(const uint8_t *a, const int8_t *b, const int32_t *acc,
+                    int32_t *out);
+
+/* Textbook int8 GEMM, C[M,N] = A[M,K] * B, i32 accumulation with wraparound.
+ *   a_unsigned = 0 : A is s8 (SimpLang tensor_matmul, F1:
+ *                    src/mlir/lowering/ConvertSimpToMemRef.cpp:3233-3239)
+ *   a_unsigned = 1 : A is u8 (raw vpdpbusd semantics, test_vnni_correctness.cpp:28-42)
+ *   b_nk = 0 : B is [K,N] row-major, ldb >= N (tensor_matmul)
+ *   b_nk = 1 : B is B_T[N,K] row-major, ldb >= K (tensor_matmul_nt,
+ *              ConvertSimpToMemRef.cpp:3373-3486)
+ * Strides are in elements.  Pinned by closed forms (identity, one-hot) and the
+ * reference's own VNNI kernel compiled in place. */
+void orc_matmul_i8(const void *A, int64_t lda, const int8_t *B, int64_t ldb,
+                   int32_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                   int a_unsigned, int b_nk);
+
+/* The algorithm the reference's VNNI pass emits (src/mlir/passes/VNNIPass.cpp:597-999,
+ * hand-written twin simptensor/benchmarks/bench_int8_matmul_multicore.cpp:88-132):
+ * B is first transposed to B_T[N,K]; rows are taken 4 at a time (I=4); K runs
+ * in 64-byte vpdpbusd steps; for s8 A the bytes are flipped (A^0x80 = A+128 as
+ * u8) and 128*colsum(B) is subtracted; a scalar loop covers the K tail.  Unlike
+ * the reference (defects D1/D2) it also handles M%4 != 0 and K%64 != 0.
+ * Uses AVX-512 VNNI when the host has it, a scalar emulation of the same steps
+ * otherwise.  nthreads > 1 splits the row blocks with OpenMP.  This is the
+ * "port" CPU baseline timed by bench.py.  b_nk as in orc_matmul_i8.
+ * Returns 1 if the AVX-512 VNNI path ran, 0 for the scalar path. */
+int orc_matmul_i8_vnni(const void *A, const int8_t *B, int32_t *C, int64_t M,
+                       int64_t N, int64_t K, int a_unsigned, int b_nk,
+                       int nthreads);
+
+/* Deterministic inputs of the reference's int8 benchmark:
+ *   val = ((i*N + j) % 127) - 64;  A[i,j] = val;  B[j,i] = val
+ * simptensor/benchmarks/bench_int8_matmul_runner.cpp:37-43. */
+void orc_int8_recipe_inputs(int64_t N, int8_t *A, int8_t *B);
+
+/* i32 wraparound sum of n values (bench_int8_matmul_runner.cpp:57-61). */
+int32_t orc_checksum_i32(const int32_t *C, int64_t n);
+
+/* ------------------------------------------------------------ fp32 ops -- */
+
+/* Array builtin matmul: C += A*B on 1-D arrays viewed as row-major matrices
+ * at element offsets (src/mlir/lowering/ConvertSimpToMemRef.cpp:1794-1920,
+ * F4).  K is summed in increasing order in fp32 starting from C. */
+void orc_matmul_f32_acc(const float *lhs, const float *rhs, float *out,
+                        int64_t m, int64_t k, int64_t n, int64_t lhs_off,
+                        int64_t rhs_off, int64_t out_off);
+
+/* rmsnorm: sequential fp32 sum of squares, rms = sqrtf(ss/size + eps),
+ * out[i] = (in[i] / rms) * w[w_off + i]  (ConvertSimpToMemRef.cpp:2192-2233). */
+void orc_rmsnorm(const float *in, const float *w, float *out, int64_t size,
+                 float eps, int64_t w_off);
+
+/* softmax with offsets: max seeded with in[in_off] and updated with strict '>',
+ * out = expf(x - max), sequential sum, out /= sum (ConvertSimpToMemRef.cpp:2264-2316). */
+void orc_softmax(const float *in, float *out, int64_t size, int64_t in_off,
+                 int64_t out_off);
+
+/* silu: out = x / (1 + expf(-x))  (ConvertSimpToMemRef.cpp:2345-2354). */
+void orc_silu(const float *in, float *out, int64_t size);
+
+/* ------------------------------------------------------------------ W4 -- */
+
+/* Reference W4 format (F5): unsigned nibbles, low nibble = even flat index,
+ * w = q*scale + zero, groups are flat runs of gs weights.
+ * Restates MatMulQuantOpLowering (ConvertSimpToMemRef.cpp:3906-4005): per row,
+ * out = 0; per group an fp32 partial summed over gs/16 tiles of 16 in order,
+ * then out += partial.  Two reference defects are fixed (D3): the group index
+ * includes the weight offset, (off + i*cols)/gs + g, and the tile count is
+ * gs/16 instead of a fixed 8.  Requires gs % 16 == 0 and cols % gs == 0. */
+void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
+                         const float *zeros, const float *in, float *out,
+                         int64_t rows, int64_t cols, int64_t gs, int64_t off);
+
+/* Reference quantizer for F5 (examples/llama2/bench_llama_quant.cpp:51-93):
+ * per flat group, scale = max((max-min)/15, 1e-8), zero = min,
+ * q = clamp(round((w-min)/scale), 0, 15). */
+void orc_quantize_f5(const float *w, int64_t total, int64_t gs, uint8_t *qw,
+                     float *scales, float *zeros);
+
+/* BASELINE W4 format (F6): signed nibbles in [-8,7] (sign-extended as in
+ * ConvertSimpToMemRef.cpp:3016-3037, low nibble = even k), W[N,K] packed along
+ * K (row = K/2 bytes), one fp32 scale per group of gs along K (scales[N, K/gs]),
+ * no zero point.  out[m,n] = sum_k (q[n,k]*s[n,k/gs]) * x[m,k], accumulated in
+ * double (the exact value the GPU is compared against). */
+void orc_matmul_w4s(const uint8_t *qw, const float *scales, const float *x,
+                    float *out, int64_t M, int64_t N, int64_t K, int64_t gs);
+
+/* Same math as orc_matmul_w4s with fp32 accumulation and OpenMP over rows:
+ * the CPU baseline for the W4 GEMV (bench.py). */
+void orc_matmul_w4s_f32(const uint8_t *qw, const float *scales, const float *x,
+                        float *out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                        int nthreads);
+
+/* -------------------------------------------------------------- decode -- */
+
+/* RoPE of the LLaMA programs (examples/llama2/stories110M.sl:86-112):
+ * for even i < dim: f = 1/powf(theta, (i % hs)/hs), v = pos*f,
+ * rotate (q[i], q[i+1]) by v; k likewise when i < kv_dim. */
+void orc_rope(float *q, float *k, int64_t dim, int64_t kv_dim, int64_t hs,
+              int64_t pos, float theta);
+
+/* Model shape of one decode step (examples/llama2/stories110M.sl:5-44,
+ * examples/llama2/llama2_quant.sl:7-56, made shape-parametric: D4). */
+typedef struct {
+  int64_t dim, hidden, n_layers, n_heads, n_kv_heads, vocab, seq_len;
+  float eps, theta;
+  int64_t w4; /* 0: fp32 weights, 1: F6 W4 weights with group gs */
+  int64_t gs;
+} orc_llama_cfg;
+
+/* Weights.  fp32 layout: wq[L,dim,dim], wk/wv[L,kv_dim,dim], wo[L,dim,dim],
+ * w1/w3[L,hidden,dim], w2[L,dim,hidden], wcls[vocab,dim], emb[vocab,dim],
+ * rms_att/rms_ffn[L,dim], rms_final[dim].  W4 layout: the same matrices as F6
+ * packed bytes (q_*) plus scales (s_*), one matrix after another per layer. */
+typedef struct {
+  const float *emb, *rms_att, *rms_ffn, *rms_final;
+  const float *wq, *wk, *wv, *wo, *w1, *w2, *w3, *wcls;
+  const uint8_t *q_wq, *q_wk, *q_wv, *q_wo, *q_w1, *q_w2, *q_w3, *q_wcls;
+  const float *s_wq, *s_wk, *s_wv, *s_wo, *s_w1, *s_w2, *s_w3, *s_wcls;
+} orc_llama_weights;
+
+/* One token of the decode step of stories110M.sl:44-247 with the GQA head map
+ * of llama2_quant.sl:98 and score scale 1/sqrt(hs) (F11).  key_cache and
+ * value_cache are [L, seq_len, kv_dim]; logits[vocab] is written.  Matrix-vector
+ * products accumulate in double (exact reference for the tolerance check);
+ * everything else is fp32 as in the program. */
+void orc_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
+                       float *key_cache, float *value_cache, int64_t token,
+                       int64_t pos, float *logits);
+
+/* Strict-'>' argmax, first maximum wins (examples/llama2/generate_stories110M.cpp:73-83). */
+int64_t orc_argmax(const float *logits, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,184 @@
+"""ctypes wrapper of the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  Nothing on the product path
+imports it.  The optional in-place reference build (oracle/_ref/libsimpref.so,
+only where the SimpLang sources are mounted) is exposed as ``ref`` (or None).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "_build", "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libsimpref.so")
+REF_VNNI_TEST = os.path.join(HERE, "_ref", "test_vnni_correctness")
+
+if not os.path.exists(LIB):
+    raise ImportError(f"{LIB} not built (make -C oracle)")
+_o = C.CDLL(LIB)
+ref = C.CDLL(REF_LIB) if os.path.exists(REF_LIB) else None
+
+_P, _I, _F = C.c_void_p, C.c_int64, C.c_float
+
+
+def _s(name, args, res=None):
+    f = getattr(_o, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+_s("orc_vpdpbusd16", [_P, _P, _P, _P])
+_s("orc_matmul_i8", [_P, _I, _P, _I, _P, _I, _I, _I, _I, C.c_int, C.c_int])
+_s("orc_matmul_i8_vnni", [_P, _P, _P, _I, _I, _I, C.c_int, C.c_int, C.c_int], C.c_int)
+_s("orc_int8_recipe_inputs", [_I, _P, _P])
+_s("orc_checksum_i32", [_P, _I], C.c_int32)
+_s("orc_matmul_f32_acc", [_P, _P, _P, _I, _I, _I, _I, _I, _I])
+_s("orc_rmsnorm", [_P, _P, _P, _I, _F, _I])
+_s("orc_softmax", [_P, _P, _I, _I, _I])
+_s("orc_silu", [_P, _P, _I])
+_s("orc_matmul_quant_f5", [_P, _P, _P, _P, _P, _I, _I, _I, _I])
+_s("orc_quantize_f5", [_P, _I, _I, _P, _P, _P])
+_s("orc_matmul_w4s", [_P, _P, _P, _P, _I, _I, _I, _I])
+_s("orc_matmul_w4s_f32", [_P, _P, _P, _P, _I, _I, _I, _I, C.c_int])
+_s("orc_rope", [_P, _P, _I, _I, _I, _I, _F])
+_s("orc_argmax", [_P, _I], C.c_int64)
+
+if ref is not None:
+    for n in ("ref_scalar_vpdpbusd", "ref_hw_vpdpbusd"):
+        getattr(ref, n).argtypes = [_P, _P, _P, _P]
+    for n in (64, 128, 256, 512, 1024, 2048):
+        getattr(ref, f"ref_vnni_matmul_{n}").argtypes = [_P, _P, _P]
+    for n in (32, 64, 128):
+        getattr(ref, f"ref_scalar_int4_{n}").restype = C.c_int32
+        getattr(ref, f"ref_packed_int4_{n}").restype = C.c_int32
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def vpdpbusd16(a, b, acc):
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.int8)
+    acc = np.ascontiguousarray(acc, np.int32)
+    out = np.empty(16, np.int32)
+    _o.orc_vpdpbusd16(_p(a), _p(b), _p(acc), _p(out))
+    return out
+
+
+def matmul_i8(a, b, *, a_unsigned=False, b_nk=False):
+    """Textbook int8 GEMM (i32 wraparound).  b is [K,N], or [N,K] if b_nk."""
+    a = np.ascontiguousarray(a, np.uint8 if a_unsigned else np.int8)
+    b = np.ascontiguousarray(b, np.int8)
+    M, K = a.shape
+    N = b.shape[0] if b_nk else b.shape[1]
+    c = np.empty((M, N), np.int32)
+    _o.orc_matmul_i8(_p(a), K, _p(b), b.shape[1], _p(c), N, M, N, K,
+                     int(a_unsigned), int(b_nk))
+    return c
+
+
+def matmul_i8_vnni(a, b, *, a_unsigned=False, b_nk=False, nthreads=1):
+    """The VNNI-pass algorithm (CPU baseline).  Returns (C, used_avx512_vnni)."""
+    a = np.ascontiguousarray(a, np.uint8 if a_unsigned else np.int8)
+    b = np.ascontiguousarray(b, np.int8)
+    M, K = a.shape
+    N = b.shape[0] if b_nk else b.shape[1]
+    c = np.empty((M, N), np.int32)
+    hw = _o.orc_matmul_i8_vnni(_p(a), _p(b), _p(c), M, N, K, int(a_unsigned),
+                               int(b_nk), int(nthreads))
+    return c, bool(hw)
+
+
+def recipe_inputs(n: int):
+    a = np.empty((n, n), np.int8)
+    b = np.empty((n, n), np.int8)
+    _o.orc_int8_recipe_inputs(n, _p(a), _p(b))
+    return a, b
+
+
+def checksum_i32(c) -> int:
+    c = np.ascontiguousarray(c, np.int32)
+    return int(_o.orc_checksum_i32(_p(c), c.size))
+
+
+def matmul_f32_acc(lhs, rhs, out, m, k, n, lhs_off=0, rhs_off=0, out_off=0):
+    _o.orc_matmul_f32_acc(_p(lhs), _p(rhs), _p(out), m, k, n, lhs_off, rhs_off, out_off)
+    return out
+
+
+def rmsnorm(x, w, eps=1e-5, w_off=0, size=None):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    size = x.size if size is None else size
+    out = np.empty(size, np.float32)
+    _o.orc_rmsnorm(_p(x), _p(w), _p(out), size, eps, w_off)
+    return out
+
+
+def softmax(x, out=None, size=None, in_off=0, out_off=0):
+    x = np.ascontiguousarray(x, np.float32)
+    size = x.size - in_off if size is None else size
+    if out is None:
+        out = np.zeros(out_off + size, np.float32)
+    _o.orc_softmax(_p(x), _p(out), size, in_off, out_off)
+    return out
+
+
+def silu(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    _o.orc_silu(_p(x), _p(out), x.size)
+    return out
+
+
+def matmul_quant_f5(qw, scales, zeros, x, rows, cols, gs, off=0):
+    out = np.empty(rows, np.float32)
+    _o.orc_matmul_quant_f5(_p(qw), _p(scales), _p(zeros), _p(x), _p(out), rows, cols, gs, off)
+    return out
+
+
+def quantize_f5(w, gs):
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    ng = (w.size + gs - 1) // gs
+    qw = np.empty((w.size + 1) // 2, np.uint8)
+    sc = np.empty(ng, np.float32)
+    ze = np.empty(ng, np.float32)
+    _o.orc_quantize_f5(_p(w), w.size, gs, _p(qw), _p(sc), _p(ze))
+    return qw, sc, ze
+
+
+def matmul_w4s(qw, scales, x, gs=32):
+    """F6 W4: qw [N, K/2] u8, scales [N, K/gs] f32, x [M, K] f32 -> [M, N] (f64 accumulate)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    N = qw.shape[0]
+    out = np.empty((M, N), np.float32)
+    _o.orc_matmul_w4s(_p(np.ascontiguousarray(qw)), _p(np.ascontiguousarray(scales)), _p(x),
+                      _p(out), M, N, K, gs)
+    return out
+
+
+def matmul_w4s_f32(qw, scales, x, gs=32, nthreads=1):
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    N = qw.shape[0]
+    out = np.empty((M, N), np.float32)
+    _o.orc_matmul_w4s_f32(_p(qw), _p(scales), _p(x), _p(out), M, N, K, gs, nthreads)
+    return out
+
+
+def rope(q, k, dim, kv_dim, hs, pos, theta=10000.0):
+    _o.orc_rope(_p(q), _p(k), dim, kv_dim, hs, pos, theta)
+    return q, k
+
+
+def argmax(logits) -> int:
+    logits = np.ascontiguousarray(logits, np.float32)
+    return int(_o.orc_argmax(_p(logits), logits.size))

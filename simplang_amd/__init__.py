@@ -1,0 +1,20 @@
+"""simplang_amd -- MI355X (gfx950) runtime for the tensor ops SimpLang lowers into.
+
+The product is ``libsimp_hip.so`` (C ABI declared in ``include/simp_rt.h``).
+This package is the host-side mirror of the reference's operator interface:
+each function takes the same operands, in the same order, as the SimpLang
+builtin it replaces (``src/mlir/mlir_codegen.cpp:1388-1531,2068-2292``) and
+calls the C ABI with expanded memref descriptors.  There is no CPU fallback:
+if the library is missing or fails, these functions raise.
+"""
+from .host import (  # noqa: F401
+    SimpRTError,
+    lib,
+    lib_path,
+    set_stream,
+    sync,
+    tensor_matmul_i8,
+    tensor_matmul_nt_i8,
+    matmul_u8s8_i32,
+    matmul_nt_u8s8_i32,
+)

@@ -1,0 +1,160 @@
+"""ctypes binding of libsimp_hip.so and the host-side operator mirror.
+
+Operands are torch tensors on the GPU (used in place, asynchronous on the
+stream given to :func:`set_stream`) or numpy arrays (staged by the library,
+synchronous).  Descriptor expansion follows the reference host ABI
+(``examples/llama2/bench_llama_quant.cpp:10-28``): rank-1 arrays as
+``(alloc, aligned, offset, size, stride)``, rank-2 tensors as
+``(alloc, aligned, offset, size0, size1, stride0, stride1)``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+lib_path = os.path.join(_HERE, "libsimp_hip.so")
+HEADER = os.path.join(os.path.dirname(_HERE), "include", "simp_rt.h")
+
+
+class SimpRTError(RuntimeError):
+    """A libsimp_hip.so entry point returned a negative status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} -> {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(lib_path):
+        raise ImportError(
+            f"{lib_path} is not built; run __graft_entry__.build() "
+            "(the HIP runtime has no CPU fallback)")
+    return C.CDLL(lib_path, mode=C.RTLD_GLOBAL)
+
+
+lib = _load()
+lib.simp_rt_last_error.restype = C.c_char_p
+lib.simp_rt_get_stream.restype = C.c_void_p
+
+_P, _I = C.c_void_p, C.c_int64
+_D1 = [_P, _P, _I, _I, _I]
+_D2 = [_P, _P, _I, _I, _I, _I, _I]
+
+
+def _sig(name, argtypes):
+    f = getattr(lib, name)
+    f.argtypes = argtypes
+    f.restype = C.c_int32
+    return f
+
+
+for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
+           "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32"):
+    _sig(_n, _D2 * 3)
+_sig("simp_rt_set_stream", [_P])
+_sig("simp_rt_register", [_P, _I, C.c_int32])
+_sig("simp_rt_unregister", [_P])
+
+
+def declared_symbols(header: str = HEADER) -> list[str]:
+    """Names of the entry points include/simp_rt.h declares."""
+    text = open(header).read()
+    return sorted(set(re.findall(r"\b(simp_rt_\w+)\s*\(", text)))
+
+
+def _check(fn: str, rc: int):
+    if rc != 0:
+        raise SimpRTError(fn, rc, lib.simp_rt_last_error().decode())
+
+
+# ------------------------------------------------------------------ operands
+
+def _is_torch(x) -> bool:
+    return type(x).__module__.startswith("torch")
+
+
+def _ptr_stride(x):
+    """(data pointer, row stride in elements, shape) of a 1-D/2-D operand."""
+    if _is_torch(x):
+        if x.dim() == 2:
+            if x.stride(1) != 1:
+                raise ValueError("rank-2 operand must be row-major (stride1 == 1)")
+            return x.data_ptr(), x.stride(0), tuple(x.shape)
+        if x.dim() == 1:
+            if x.stride(0) != 1:
+                raise ValueError("rank-1 operand must be contiguous")
+            return x.data_ptr(), 1, tuple(x.shape)
+        raise ValueError("operand must be rank 1 or 2")
+    import numpy as np
+    if not isinstance(x, np.ndarray):
+        raise TypeError(f"unsupported operand type {type(x)}")
+    isz = x.itemsize
+    if x.ndim == 2:
+        if x.strides[1] != isz:
+            raise ValueError("rank-2 operand must be row-major (stride1 == 1)")
+        return x.ctypes.data, x.strides[0] // isz, x.shape
+    if x.ndim == 1:
+        if x.strides[0] != isz:
+            raise ValueError("rank-1 operand must be contiguous")
+        return x.ctypes.data, 1, x.shape
+    raise ValueError("operand must be rank 1 or 2")
+
+
+def desc2(x):
+    p, st0, shape = _ptr_stride(x)
+    if len(shape) != 2:
+        raise ValueError("expected a rank-2 tensor")
+    return [p, p, 0, shape[0], shape[1], st0, 1]
+
+
+def desc1(x):
+    p, _, shape = _ptr_stride(x)
+    n = 1
+    for s in shape:
+        n *= s
+    return [p, p, 0, n, 1]
+
+
+# --------------------------------------------------------------------- ops
+
+def set_stream(stream) -> None:
+    """Make the calling thread's launches go to ``stream`` (torch stream, int or None)."""
+    if stream is None:
+        h = None
+    elif hasattr(stream, "cuda_stream"):
+        h = stream.cuda_stream
+    else:
+        h = int(stream)
+    _check("simp_rt_set_stream", lib.simp_rt_set_stream(h))
+
+
+def sync() -> None:
+    _check("simp_rt_sync", lib.simp_rt_sync())
+
+
+def _gemm(fn_name, a, b, c):
+    f = getattr(lib, fn_name)
+    _check(fn_name, f(*desc2(a), *desc2(b), *desc2(c)))
+    return c
+
+
+def tensor_matmul_i8(a, b, c):
+    """C[M,N] = A[M,K] x B[K,N], s8 x s8 -> i32 (SimpLang ``tensor_matmul`` on i8)."""
+    return _gemm("simp_rt_tensor_matmul_i8", a, b, c)
+
+
+def tensor_matmul_nt_i8(a, bt, c):
+    """C[M,N] = A[M,K] x B_T[N,K]^T, s8 x s8 -> i32 (``tensor_matmul_nt``)."""
+    return _gemm("simp_rt_tensor_matmul_nt_i8", a, bt, c)
+
+
+def matmul_u8s8_i32(a, b, c):
+    """C = A(u8) x B(s8) -> i32, vpdpbusd semantics, B as [K,N]."""
+    return _gemm("simp_rt_matmul_u8s8_i32", a, b, c)
+
+
+def matmul_nt_u8s8_i32(a, bt, c):
+    """C = A(u8) x B_T(s8)^T -> i32, vpdpbusd semantics, B as B_T[N,K]."""
+    return _gemm("simp_rt_matmul_nt_u8s8_i32", a, bt, c)

@@ -1,0 +1,450 @@
+// gemm_i8.hip -- exact int8 GEMM on CDNA4 int8 MFMA (v_mfma_i32_32x32x32_i8).
+//
+// Semantics replaced (citations into the SimpLang tree):
+//   s8 x s8 -> i32  tensor_matmul i8 branch, ConvertSimpToMemRef.cpp:3136-3279
+//                   (both operands sign-extended, :3233-3239), rewritten onto
+//                   vpdpbusd by VNNIPass.cpp:597-999 (A^0x80 and a 128*colsum(B)
+//                   bias correction, :817-830,899-906).  MFMA multiplies s8 x s8
+//                   natively, so this path needs no correction at all.
+//   u8 x s8 -> i32  raw vpdpbusd (simptensor/tests/test_vnni_correctness.cpp:28-42).
+//                   MFMA has no u8 x s8 form: A is flipped to A^0x80 = A-128 as s8
+//                   and C = MFMA(A^0x80, B) + 128*colsum(B)[j].  The column sums come
+//                   from the B fragments already in registers (v_dot4 against
+//                   0x01010101), so no extra pass over B is made.
+// Integer sums are order independent, so every tiling / split-K choice is
+// bit-exact with the reference's sequential K loop.
+//
+// Kernel structure (one workgroup = BM x BN tile of C):
+//   * K is walked in BK-byte tiles, double-buffered in LDS: the global loads of
+//     tile t+1 are in flight while the MFMAs of tile t run, one barrier per tile.
+//   * LDS holds 16-byte K-chunks, chunk-major ([BK/16][rows][16 B]), the exact
+//     operand shape of one lane of v_mfma_i32_32x32x32_i8 (16 consecutive K of
+//     one row/column).  Row indices are XOR-swizzled so that both the 128-bit
+//     stores and the 128-bit MFMA-operand reads hit distinct banks.
+//   * B given as [K,N] (tensor_matmul's layout) is transposed on the way into LDS:
+//     each thread loads 16 K-rows x 4 columns as dwords (a wave reads 256
+//     contiguous bytes per row) and transposes 4x4 byte blocks with v_perm_b32.
+//     The reference materialises B_T with a separate 8x8-tiled pass
+//     (ConvertSimpToMemRef.cpp:3168-3216); here that pass is fused away.
+//   * Workgroup ids are remapped so that each of the 8 XCDs owns a contiguous
+//     range of tiles (blocks are dispatched round-robin over XCDs), and tiles are
+//     ordered in groups of 8 tile-rows so co-resident tiles share A and B in L2.
+//   * Skinny / small problems split K over gridDim.y and combine partial tiles
+//     with integer atomics into a zero-filled C (exact).
+#include <algorithm>
+
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Row swizzle for chunk-major tiles loaded row-wise (A, and B_T): within a
+// wave's store, lanes cover 8 chunks of 2 rows; h(kc) = kc ^ (kc << 1) keeps
+// both 8-lane and 16-lane groups on distinct 16-byte bank slots.
+__device__ __forceinline__ int swz_rows(int r, int kc) { return r ^ ((kc ^ (kc << 1)) & 15); }
+// Swizzle for B transposed in registers: a store instruction covers columns
+// n = 4*lane + j; n ^ ((n >> 2) & 15) spreads them over distinct slots.
+__device__ __forceinline__ int swz_tr(int n) { return n ^ ((n >> 2) & 15); }
+
+// 4x4 byte transpose: d_r holds bytes (r, 0..3); o_j gets bytes (0..3, j).
+__device__ __forceinline__ void transpose4x4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                                             uint32_t &o0, uint32_t &o1, uint32_t &o2,
+                                             uint32_t &o3) {
+  uint32_t x0 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // a0 b0 a1 b1
+  uint32_t x1 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);  // a2 b2 a3 b3
+  uint32_t y0 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);  // c0 e0 c1 e1
+  uint32_t y1 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);  // c2 e2 c3 e3
+  o0 = __builtin_amdgcn_perm(y0, x0, 0x05040100u);           // a0 b0 c0 e0
+  o1 = __builtin_amdgcn_perm(y0, x0, 0x07060302u);           // a1 b1 c1 e1
+  o2 = __builtin_amdgcn_perm(y1, x1, 0x05040100u);
+  o3 = __builtin_amdgcn_perm(y1, x1, 0x07060302u);
+}
+
+// Maps the hardware workgroup id to a C tile: XCD-contiguous, then grouped.
+__device__ __forceinline__ void tile_of_block(int bid, int nb, int tiles_m, int tiles_n,
+                                              int &tm, int &tn) {
+  const int q = nb >> 3, r = nb & 7, xcd = bid & 7, local = bid >> 3;
+  const int t = xcd * q + min(xcd, r) + local;
+  constexpr int G = 8;
+  const int gsz = G * tiles_n;
+  const int g = t / gsz, first = g * G;
+  const int gm = min(tiles_m - first, G);
+  const int w = t - g * gsz;
+  tm = first + w % gm;
+  tn = w / gm;
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8, bool ATOMIC>
+__global__ void __launch_bounds__(WGM *WGN * 64)
+    gemm_i8_mfma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+                 int tiles_m, int tiles_n, int k_span) {
+  constexpr int NT = WGM * WGN * 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int KC = BK / 16;
+  static_assert(FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile");
+  static_assert(BK % 32 == 0, "K tile");
+  constexpr int A_TOT = BM * KC;                           // 16 B chunks of A per tile
+  constexpr int A_PER = (A_TOT + NT - 1) / NT;
+  constexpr int B_TOT = BNK ? BN * KC : (BK / 16) * (BN / 4);  // chunks or 16x4 units
+  constexpr int B_PER = (B_TOT + NT - 1) / NT;
+
+  __shared__ uint4 sA[2][KC * BM];
+  __shared__ uint4 sB[2][KC * BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  int tm, tn;
+  tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = blockIdx.y * k_span;
+  const int kend = min(K, kbeg + k_span);
+  if (kbeg >= kend) return;  // uniform per workgroup
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  uint4 ra[A_PER];
+  uint4 rbq[BNK ? B_PER : 1];
+  uint32_t rbd[BNK ? 1 : B_PER][16];
+
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (A_TOT % NT == 0 || c < A_TOT) {
+        const int kc = c % KC, m = c / KC;
+        const int gm = m0 + m, gk = k0 + kc * 16;
+        if (gm < M && gk < kend) v = *(const uint4 *)(A + (int64_t)gm * lda + gk);
+      }
+      ra[i] = v;
+    }
+    if constexpr (BNK) {
+#pragma unroll
+      for (int i = 0; i < B_PER; i++) {
+        const int c = tid + i * NT;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (B_TOT % NT == 0 || c < B_TOT) {
+          const int kc = c % KC, n = c / KC;
+          const int gn = n0 + n, gk = k0 + kc * 16;
+          if (gn < N && gk < kend) v = *(const uint4 *)(B + (int64_t)gn * ldb + gk);
+        }
+        rbq[i] = v;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_PER; i++) {
+        const int u = tid + i * NT;
+        const bool on = (B_TOT % NT == 0 || u < B_TOT);
+        const int nq = u % (BN / 4), kq = u / (BN / 4);
+        const int gn = n0 + nq * 4;
+        const int8_t *p = B + (int64_t)(k0 + kq * 16) * ldb + gn;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int gk = k0 + kq * 16 + r;
+          rbd[i][r] = (on && gn < N && gk < kend) ? *(const uint32_t *)(p + (int64_t)r * ldb) : 0u;
+        }
+      }
+    }
+  };
+
+  auto store_tile = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT;
+      if (A_TOT % NT == 0 || c < A_TOT) {
+        const int kc = c % KC, m = c / KC;
+        uint4 v = ra[i];
+        if constexpr (AU8) {
+          v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+        }
+        sA[s][kc * BM + swz_rows(m, kc)] = v;
+      }
+    }
+    if constexpr (BNK) {
+#pragma unroll
+      for (int i = 0; i < B_PER; i++) {
+        const int c = tid + i * NT;
+        if (B_TOT % NT == 0 || c < B_TOT) {
+          const int kc = c % KC, n = c / KC;
+          sB[s][kc * BN + swz_rows(n, kc)] = rbq[i];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_PER; i++) {
+        const int u = tid + i * NT;
+        if (B_TOT % NT == 0 || u < B_TOT) {
+          const int nq = u % (BN / 4), kq = u / (BN / 4);
+          uint32_t o[4][4];  // o[j][q]: column j, K bytes 4q..4q+3
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            transpose4x4(rbd[i][4 * q], rbd[i][4 * q + 1], rbd[i][4 * q + 2], rbd[i][4 * q + 3],
+                         o[0][q], o[1][q], o[2][q], o[3][q]);
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            sB[s][kq * BN + swz_tr(nq * 4 + j)] = make_uint4(o[j][0], o[j][1], o[j][2], o[j][3]);
+        }
+      }
+    }
+  };
+
+  v16i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+  int cs[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) cs[j] = 0;
+
+  load_tile(kbeg);
+  store_tile(0);
+  __syncthreads();
+
+  const int lrow = lane & 31, lk = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tile(kbeg + (kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ks++) {
+      const int kc = ks * 2 + lk;
+      v4i af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int m = wm0 + i * 32 + lrow;
+        uint4 v = sA[cur][kc * BM + swz_rows(m, kc)];
+        af[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+      }
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int n = wn0 + j * 32 + lrow;
+        uint4 v = sB[cur][kc * BN + (BNK ? swz_rows(n, kc) : swz_tr(n))];
+        bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        if constexpr (AU8) {
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].x, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].y, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].z, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].w, 0x01010101, cs[j], false);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+
+  if constexpr (AU8) {
+    // Lanes l and l^32 hold the two K halves of the same column.
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int tot = cs[j] + __shfl_xor(cs[j], 32);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][j][r] += 128 * tot;
+    }
+  }
+
+  // Output of a 32x32 i32 MFMA: lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4.
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn0 + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (row < M && col < N) {
+          int32_t *dst = C + (int64_t)row * ldc + col;
+          if constexpr (ATOMIC) atomicAdd(dst, acc[i][j][r]);
+          else *dst = acc[i][j][r];
+        }
+      }
+    }
+}
+
+// Correctness fallback for shapes the MFMA path cannot load with aligned
+// vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).
+template <bool BNK, bool AU8>
+__global__ void __launch_bounds__(256)
+    gemm_i8_generic(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+                    int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K) {
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (row >= M || col >= N) return;
+  uint32_t s = 0;
+  for (int k = 0; k < K; k++) {
+    const int32_t a = AU8 ? (int32_t)(uint8_t)A[(int64_t)row * lda + k]
+                          : (int32_t)A[(int64_t)row * lda + k];
+    const int32_t b = BNK ? (int32_t)B[(int64_t)col * ldb + k] : (int32_t)B[(int64_t)k * ldb + col];
+    s += (uint32_t)(a * b);
+  }
+  C[(int64_t)row * ldc + col] = (int32_t)s;
+}
+
+__global__ void __launch_bounds__(256)
+    fill_i32_2d(int32_t *__restrict__ C, int64_t ldc, int M, int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t r = i / N, c = i - r * N;
+  C[r * ldc + c] = 0;
+}
+
+struct GemmArgs {
+  const int8_t *A;
+  int64_t lda;
+  const int8_t *B;
+  int64_t ldb;
+  int32_t *C;
+  int64_t ldc;
+  int M, N, K;
+};
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8>
+int launch_mfma(const GemmArgs &g, int splits, hipStream_t st) {
+  const int tiles_m = (int)cdiv(g.M, BM), tiles_n = (int)cdiv(g.N, BN);
+  const int nkt = (int)cdiv(g.K, BK);
+  splits = std::max(1, std::min(splits, nkt));
+  const int k_span = (int)cdiv(nkt, splits) * BK;
+  splits = (int)cdiv(g.K, k_span);
+  dim3 grid(tiles_m * tiles_n, splits), block(WGM * WGN * 64);
+  if (splits > 1) {
+    const int64_t tot = (int64_t)g.M * g.N;
+    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C, g.ldc,
+                       g.M, g.N);
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, BK, WGM, WGN, BNK, AU8, true>), grid, block, 0, st,
+                       g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tiles_m, tiles_n,
+                       k_span);
+  } else {
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, BK, WGM, WGN, BNK, AU8, false>), grid, block, 0,
+                       st, g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tiles_m, tiles_n,
+                       k_span);
+  }
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+template <bool BNK, bool AU8>
+int dispatch(const GemmArgs &g, hipStream_t st) {
+  if (g.M == 0 || g.N == 0) return SIMP_RT_OK;
+  if (g.K == 0) {
+    const int64_t tot = (int64_t)g.M * g.N;
+    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C, g.ldc,
+                       g.M, g.N);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
+  const bool a_ok = g.K % 16 == 0 && g.lda % 16 == 0 && ((uintptr_t)g.A & 15) == 0;
+  const bool b_ok = BNK ? (g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0)
+                        : (g.N % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.B & 3) == 0);
+  if (!a_ok || !b_ok) {
+    dim3 grid((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.M, 4));
+    hipLaunchKernelGGL((gemm_i8_generic<BNK, AU8>), grid, dim3(256), 0, st, g.A, g.lda, g.B,
+                       g.ldb, g.C, g.ldc, g.M, g.N, g.K);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
+  const int64_t cus = num_cus();
+  auto tiles = [&](int bm, int bn) { return cdiv(g.M, bm) * cdiv(g.N, bn); };
+  if (tiles(256, 256) >= cus) return launch_mfma<256, 256, 128, 2, 2, BNK, AU8>(g, 1, st);
+  if (tiles(128, 128) >= cus) return launch_mfma<128, 128, 128, 2, 2, BNK, AU8>(g, 1, st);
+  if (g.M > 32) {
+    const int64_t t = tiles(64, 64);
+    const int s = (int)std::min<int64_t>(cdiv(2 * cus, t), 16);
+    return launch_mfma<64, 64, 128, 2, 2, BNK, AU8>(g, t >= cus ? 1 : s, st);
+  }
+  const int64_t t = tiles(32, 64);
+  const int s = (int)std::min<int64_t>(cdiv(2 * cus, t), 16);
+  return launch_mfma<32, 64, 128, 1, 2, BNK, AU8>(g, t >= cus ? 1 : s, st);
+}
+
+// Shared body of the four entry points.
+template <bool BNK, bool AU8>
+int gemm_entry(const char *name, const void *a, int64_t a_off, int64_t a_s0, int64_t a_s1,
+               int64_t a_st0, int64_t a_st1, const int8_t *b, int64_t b_off, int64_t b_s0,
+               int64_t b_s1, int64_t b_st0, int64_t b_st1, int32_t *c, int64_t c_off,
+               int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  int rc;
+  if ((rc = check_desc2("A", a, a_off, a_s0, a_s1, a_st0, a_st1))) return rc;
+  if ((rc = check_desc2("B", b, b_off, b_s0, b_s1, b_st0, b_st1))) return rc;
+  if ((rc = check_desc2("C", c, c_off, c_s0, c_s1, c_st0, c_st1))) return rc;
+  const int64_t M = a_s0, K = a_s1;
+  const int64_t N = BNK ? b_s0 : b_s1;
+  const int64_t Kb = BNK ? b_s1 : b_s0;
+  if (Kb != K || c_s0 != M || c_s1 != N)
+    return set_error(SIMP_RT_EINVAL,
+                     "%s: shape mismatch A[%lld,%lld] B%s[%lld,%lld] C[%lld,%lld]", name,
+                     (long long)a_s0, (long long)a_s1, BNK ? "_T" : "", (long long)b_s0,
+                     (long long)b_s1, (long long)c_s0, (long long)c_s1);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  Operand oa, ob, oc;
+  const size_t a_bytes = (M && K) ? (size_t)((M - 1) * a_st0 + K) : 0;
+  const size_t b_bytes = (b_s0 && b_s1) ? (size_t)((b_s0 - 1) * b_st0 + b_s1) : 0;
+  const size_t c_bytes = (M && N) ? (size_t)((M - 1) * c_st0 + N) * 4 : 0;
+  if ((rc = oa.bind((const int8_t *)a + a_off, a_bytes, Operand::kIn, "A"))) return rc;
+  if ((rc = ob.bind(b + b_off, b_bytes, Operand::kIn, "B"))) return rc;
+  if ((rc = oc.bind(c + c_off, c_bytes, Operand::kOut, "C"))) return rc;
+  GemmArgs g{(const int8_t *)oa.dev(), a_st0, (const int8_t *)ob.dev(), b_st0,
+             (int32_t *)oc.dev(),      c_st0, (int)M, (int)N, (int)K};
+  if ((rc = dispatch<BNK, AU8>(g, cur_stream()))) return rc;
+  Operand *ops[] = {&oa, &ob, &oc};
+  return finish(ops, 3);
+}
+
+}  // namespace
+}  // namespace simp
+
+using namespace simp;
+
+extern "C" {
+
+int32_t simp_rt_tensor_matmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  return gemm_entry<false, false>("tensor_matmul_i8", a, a_off, a_s0, a_s1, a_st0, a_st1, b, b_off,
+                                  b_s0, b_s1, b_st0, b_st1, c, c_off, c_s0, c_s1, c_st0, c_st1);
+}
+
+int32_t simp_rt_tensor_matmul_nt_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)bt_alloc; (void)c_alloc;
+  return gemm_entry<true, false>("tensor_matmul_nt_i8", a, a_off, a_s0, a_s1, a_st0, a_st1, bt,
+                                 bt_off, bt_s0, bt_s1, bt_st0, bt_st1, c, c_off, c_s0, c_s1, c_st0,
+                                 c_st1);
+}
+
+int32_t simp_rt_matmul_u8s8_i32(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  return gemm_entry<false, true>("matmul_u8s8_i32", a, a_off, a_s0, a_s1, a_st0, a_st1, b, b_off,
+                                 b_s0, b_s1, b_st0, b_st1, c, c_off, c_s0, c_s1, c_st0, c_st1);
+}
+
+int32_t simp_rt_matmul_nt_u8s8_i32(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)bt_alloc; (void)c_alloc;
+  return gemm_entry<true, true>("matmul_nt_u8s8_i32", a, a_off, a_s0, a_s1, a_st0, a_st1, bt,
+                                bt_off, bt_s0, bt_s1, bt_st0, bt_st1, c, c_off, c_s0, c_s1, c_st0,
+                                c_st1);
+}
+
+}  // extern "C"

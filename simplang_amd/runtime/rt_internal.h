@@ -1,0 +1,72 @@
+// rt_internal.h -- shared host-side plumbing of libsimp_hip.so (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "simp_rt.h"
+
+namespace simp {
+
+// Thread-local error text behind simp_rt_last_error().
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char *what);
+
+#define SIMP_HIP(call)                                         \
+  do {                                                         \
+    hipError_t _e = (call);                                    \
+    if (_e != hipSuccess) return ::simp::hip_fail(_e, #call);  \
+  } while (0)
+
+// Stream the calling thread launches on (simp_rt_set_stream, default null stream).
+hipStream_t cur_stream();
+
+// Device of the calling thread, initialised once per device on first use.
+int ensure_device();
+
+// A caller pointer made usable by a kernel.  Device memory (hipMalloc'd,
+// managed) is used as-is; a host range inside a simp_rt_register'd buffer maps
+// to its device mirror; any other host pointer is staged through a temporary
+// device buffer (copied in when it is an input, copied back when it is an
+// output, and the call then synchronises its stream).
+class Operand {
+ public:
+  enum Dir { kIn = 1, kOut = 2, kInOut = 3 };
+  Operand() = default;
+  Operand(const Operand &) = delete;
+  Operand &operator=(const Operand &) = delete;
+  ~Operand();
+  // Returns SIMP_RT_OK or a negative status.
+  int bind(const void *p, size_t bytes, Dir dir, const char *name);
+  void *dev() const { return dev_; }
+  bool staged() const { return staged_; }
+  // Copies a staged output back to its host range (on the current stream).
+  int commit();
+
+ private:
+  const void *host_ = nullptr;
+  void *dev_ = nullptr;
+  size_t bytes_ = 0;
+  Dir dir_ = kIn;
+  bool staged_ = false;
+};
+
+// Finishes an entry point: commits staged outputs and, when anything was
+// staged, waits for the stream so host buffers are valid on return.
+int finish(Operand *const *ops, int n);
+
+// Geometry checks shared by entry points.
+int check_desc2(const char *name, const void *aligned, int64_t off, int64_t s0,
+                int64_t s1, int64_t st0, int64_t st1);
+int check_desc1(const char *name, const void *aligned, int64_t off, int64_t size,
+                int64_t stride);
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Number of CUs of the current device (cached per device).
+int num_cus();
+
+}  // namespace simp

@@ -1,0 +1,137 @@
+"""GPU parity of the int8 GEMM entry points against the pinned oracle.
+
+Bit-exact for every shape (integer arithmetic).  Full BASELINE sizes that the
+CPU oracle cannot finish in seconds (4096^3, 8192^3) are checked through
+size-independent identities: row sums C*1 = A*(B*1), column sums 1^T*C =
+(1^T*A)*B (exact in int64), a sample of full rows recomputed exactly, and the
+reference's checksum recipe.
+"""
+import numpy as np
+import pytest
+
+import simplang_amd as sa
+
+pytestmark = pytest.mark.gpu
+
+SEED = 42
+
+
+def _inputs(M, N, K, seed=SEED):
+    rng = np.random.default_rng(seed + M * 7 + N * 13 + K)
+    a = rng.integers(0, 256, (M, K)).astype(np.uint8)    # config #1: A u8 uniform [0,255]
+    b = rng.integers(-128, 128, (K, N)).astype(np.int8)  #            B s8 uniform [-128,127]
+    return a, b
+
+
+def _run(dev, fn, a, b, M, N):
+    import torch
+    ta = torch.from_numpy(a).to(dev)
+    tb = torch.from_numpy(b).to(dev)
+    tc = torch.full((M, N), -7, dtype=torch.int32, device=dev)  # poison: C is overwritten
+    fn(ta, tb, tc)
+    torch.cuda.synchronize()
+    return tc.cpu().numpy()
+
+
+SHAPES = [(256, 256, 256), (512, 512, 512), (768, 768, 768), (1024, 1024, 1024),
+          (1, 2048, 768), (8, 2048, 768), (64, 2048, 768),
+          (1, 768, 2048), (8, 768, 2048), (64, 768, 2048),
+          (1, 8640, 3200), (8, 8640, 3200), (64, 8640, 3200),
+          (2048, 2048, 2048),
+          # ragged / tails: M, N not multiples of any tile, K not a multiple of 128
+          (100, 200, 48), (33, 260, 144), (300, 516, 400), (1, 4, 16)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_int8_s8s8_and_u8s8_bit_exact(dev, orc, M, N, K):
+    print(f"[int8] M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K)
+    want_u8, _ = orc.matmul_i8_vnni(a, b, a_unsigned=True, nthreads=8)
+    got = _run(dev, sa.matmul_u8s8_i32, a, b, M, N)
+    assert np.array_equal(got, want_u8)
+    a_s8 = a.view(np.int8)                               # same bytes as s8 (SimpLang i8)
+    want_s8, _ = orc.matmul_i8_vnni(a_s8, b, nthreads=8)
+    got = _run(dev, sa.tensor_matmul_i8, a_s8, b, M, N)
+    assert np.array_equal(got, want_s8)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (64, 8640, 3200), (1, 2048, 768),
+                                   (1024, 1024, 1024), (77, 130, 272)])
+def test_int8_nt_variants_bit_exact(dev, orc, M, N, K):
+    print(f"[int8-nt] M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K, seed=7)
+    bt = np.ascontiguousarray(b.T)
+    want_u8, _ = orc.matmul_i8_vnni(a, b, a_unsigned=True, nthreads=8)
+    assert np.array_equal(_run(dev, sa.matmul_nt_u8s8_i32, a, bt, M, N), want_u8)
+    want_s8, _ = orc.matmul_i8_vnni(a.view(np.int8), b, nthreads=8)
+    assert np.array_equal(_run(dev, sa.tensor_matmul_nt_i8, a.view(np.int8), bt, M, N), want_s8)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 9, 13), (3, 130, 100), (17, 6, 24)])
+def test_int8_unaligned_shapes_fallback(dev, orc, M, N, K):
+    """K % 16 != 0 or N % 4 != 0 take the generic kernel; still bit-exact."""
+    a, b = _inputs(M, N, K, seed=3)
+    assert np.array_equal(_run(dev, sa.matmul_u8s8_i32, a, b, M, N),
+                          orc.matmul_i8(a, b, a_unsigned=True))
+    assert np.array_equal(_run(dev, sa.tensor_matmul_i8, a.view(np.int8), b, M, N),
+                          orc.matmul_i8(a.view(np.int8), b))
+
+
+def test_int8_recipe_checksums(dev, orc):
+    """The reference benchmark's inputs and checksum (golden fixture)."""
+    import json
+    import os
+    gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "int8_recipe_checksums.json")))
+    for n_str, want in gold["checksums"].items():
+        n = int(n_str)
+        print(f"[recipe] N={n}", flush=True)
+        a, b = orc.recipe_inputs(n)
+        got = _run(dev, sa.tensor_matmul_i8, a, b, n, n)
+        assert orc.checksum_i32(got) == want, n
+
+
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_int8_full_size_identities(dev, orc, n):
+    import torch
+    print(f"[int8-full] N={n}", flush=True)
+    a, b = _inputs(n, n, n)
+    got = _run(dev, sa.matmul_u8s8_i32, a, b, n, n).astype(np.int64)
+    a64, b64 = a.astype(np.int64), b.astype(np.int64)
+    assert np.array_equal(got.sum(1), a64 @ b64.sum(1))          # C 1 = A (B 1)
+    assert np.array_equal(got.sum(0), a64.sum(0) @ b64)          # 1^T C = (1^T A) B
+    rows = np.random.default_rng(n).choice(n, 4, replace=False)
+    for r in rows:
+        assert np.array_equal(got[r], a64[r] @ b64)
+    del got
+    torch.cuda.empty_cache()
+
+
+def test_int8_host_pointers_are_staged(orc):
+    """numpy operands: the library stages through device memory and blocks."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    a, b = _inputs(96, 160, 224, seed=11)
+    c = np.full((96, 160), -1, np.int32)
+    sa.set_stream(None)
+    sa.matmul_u8s8_i32(a, b, c)
+    assert np.array_equal(c, orc.matmul_i8(a, b, a_unsigned=True))
+    sa.set_stream(torch.cuda.current_stream())
+
+
+def test_int8_strided_views(dev, orc):
+    """Row strides and offsets of sub-tensor views (descriptor offset/stride0)."""
+    import torch
+    a, b = _inputs(128, 256, 512, seed=5)
+    ta = torch.from_numpy(a).to(dev)[:, 64:320]        # [128, 256], stride0 512
+    tb = torch.from_numpy(b).to(dev)[128:384, :]       # [256, 256]
+    tc_full = torch.zeros((128, 300), dtype=torch.int32, device=dev)
+    tc = tc_full[:, 20:276]
+    sa.matmul_u8s8_i32(ta, tb, tc)
+    torch.cuda.synchronize()
+    want = orc.matmul_i8(np.ascontiguousarray(a[:, 64:320]), np.ascontiguousarray(b[128:384]),
+                         a_unsigned=True)
+    out = tc_full.cpu().numpy()
+    assert np.array_equal(out[:, 20:276], want)
+    assert (out[:, :20] == 0).all() and (out[:, 276:] == 0).all()

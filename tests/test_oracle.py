@@ -1,0 +1,306 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each test checks the oracle against something other than its own formula:
+the reference's known answers, the reference's own code compiled in place
+(oracle/_ref, only where the SimpLang sources are mounted), exact library
+arithmetic (numpy int64 / float64), closed forms and invariants.
+"""
+import numpy as np
+import pytest
+
+RNG = np.random.default_rng(1234)
+
+
+def _i64_matmul_wrap(a, b):
+    """Exact int64 product wrapped to i32, the reference's accumulator width."""
+    return (a.astype(np.int64) @ b.astype(np.int64)).astype(np.int32)
+
+
+# --------------------------------------------------------------- vpdpbusd --
+# Known answers of simptensor/tests/test_vnni_correctness.cpp:76-361.
+
+def test_vpdpbusd_kats(orc):
+    z16 = np.zeros(16, np.int32)
+    assert (orc.vpdpbusd16(np.zeros(64), np.zeros(64), z16) == 0).all()
+    assert (orc.vpdpbusd16(np.ones(64), np.ones(64), z16) == 4).all()
+    assert (orc.vpdpbusd16(np.full(64, 255), np.full(64, 127), z16) == 129540).all()
+    assert (orc.vpdpbusd16(np.full(64, 255), np.full(64, -128), z16) == -130560).all()
+    acc = np.arange(16, dtype=np.int32) * 1000
+    out = orc.vpdpbusd16(np.full(64, 10), np.full(64, 5), acc)
+    assert (out == np.arange(16) * 1000 + 200).all()
+    out = orc.vpdpbusd16(np.full(64, 200), np.full(64, 100), np.full(16, 2000000000, np.int32))
+    assert (out == 2000080000).all()
+
+
+def test_vpdpbusd_mixed_and_accumulate(orc):
+    i = np.arange(64)
+    a = (i + 1).astype(np.uint8)
+    b = np.where(i % 2 == 0, i + 1, -(i + 1)).astype(np.int8)
+    exp = (a.astype(np.int64) * b.astype(np.int64)).reshape(16, 4).sum(1)
+    assert (orc.vpdpbusd16(a, b, np.zeros(16, np.int32)) == exp).all()
+    # four accumulation steps (test_vnni_matmul_pattern)
+    a = ((i % 16) + 1).astype(np.uint8)
+    b = ((i // 16) + 1).astype(np.int8)
+    acc = np.zeros(16, np.int32)
+    for _ in range(4):
+        acc = orc.vpdpbusd16(a, b, acc)
+    assert (acc == 4 * (a.astype(np.int64) * b).reshape(16, 4).sum(1)).all()
+
+
+def test_vpdpbusd_random_vs_reference(orc):
+    for _ in range(200):
+        a = RNG.integers(0, 256, 64).astype(np.uint8)
+        b = RNG.integers(-128, 128, 64).astype(np.int8)
+        acc = RNG.integers(-2**30, 2**30, 16).astype(np.int32)
+        got = orc.vpdpbusd16(a, b, acc)
+        exp = (acc.astype(np.int64) + (a.astype(np.int64) * b).reshape(16, 4).sum(1))
+        assert (got == exp.astype(np.int32)).all()
+        if orc.ref is not None:
+            ref = np.empty(16, np.int32)
+            orc.ref.ref_scalar_vpdpbusd(a.ctypes.data, b.ctypes.data, acc.ctypes.data,
+                                        ref.ctypes.data)
+            assert (got == ref).all()
+
+
+def test_reference_vnni_binary_passes(orc):
+    """The reference's own KAT program, built in place, passes on this host."""
+    import os
+    import subprocess
+    if not os.path.exists(orc.REF_VNNI_TEST):
+        pytest.skip("reference not built here")
+    flags = open("/proc/cpuinfo").read()
+    if "avx512_vnni" not in flags:
+        pytest.skip("host lacks AVX-512 VNNI")
+    out = subprocess.run([orc.REF_VNNI_TEST], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and "Passed: 9/9" in out.stdout
+
+
+# -------------------------------------------------------------- int8 GEMM --
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (17, 33, 130), (64, 48, 256)])
+@pytest.mark.parametrize("a_unsigned", [False, True])
+@pytest.mark.parametrize("b_nk", [False, True])
+def test_matmul_i8_vs_int64(orc, M, N, K, a_unsigned, b_nk):
+    a = RNG.integers(0, 256, (M, K)) if a_unsigned else RNG.integers(-128, 128, (M, K))
+    a = a.astype(np.uint8 if a_unsigned else np.int8)
+    b = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    bb = np.ascontiguousarray(b.T) if b_nk else b
+    c = orc.matmul_i8(a, bb, a_unsigned=a_unsigned, b_nk=b_nk)
+    assert (c == _i64_matmul_wrap(a, b)).all()
+
+
+def test_matmul_i8_closed_forms(orc):
+    n = 37
+    eye = np.eye(n, dtype=np.int8)
+    b = RNG.integers(-128, 128, (n, 29)).astype(np.int8)
+    assert (orc.matmul_i8(eye, b) == b.astype(np.int32)).all()          # I x B = B
+    a = np.full((5, 300), -128, np.int8)
+    bb = np.full((300, 6), -128, np.int8)
+    assert (orc.matmul_i8(a, bb) == 300 * 16384).all()                  # constant
+    au = np.full((5, 300), 255, np.uint8)
+    assert (orc.matmul_i8(au, bb, a_unsigned=True) == 300 * 255 * -128).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 8, 64), (7, 9, 200), (13, 64, 128), (1, 33, 70)])
+@pytest.mark.parametrize("a_unsigned", [False, True])
+@pytest.mark.parametrize("b_nk", [False, True])
+def test_vnni_algorithm_equals_textbook(orc, M, N, K, a_unsigned, b_nk):
+    """The VNNI-pass restatement (sign flip + bias, M/K tails) is bit-exact."""
+    a = RNG.integers(0, 256, (M, K)).astype(np.uint8)
+    if not a_unsigned:
+        a = a.view(np.int8)
+    b = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    bb = np.ascontiguousarray(b.T) if b_nk else b
+    c, _ = orc.matmul_i8_vnni(a, bb, a_unsigned=a_unsigned, b_nk=b_nk, nthreads=2)
+    assert (c == orc.matmul_i8(a, bb, a_unsigned=a_unsigned, b_nk=b_nk)).all()
+
+
+@pytest.mark.parametrize("n", [64, 128, 256, 512])
+def test_vnni_vs_reference_kernel(orc, n):
+    """Oracle == the reference's vnni_matmul_single_thread<N>, compiled in place."""
+    if orc.ref is None:
+        pytest.skip("reference not built here")
+    if "avx512_vnni" not in open("/proc/cpuinfo").read():
+        pytest.skip("host lacks AVX-512 VNNI")
+    for a, b in (orc.recipe_inputs(n),
+                 (RNG.integers(-128, 128, (n, n)).astype(np.int8),
+                  RNG.integers(-128, 128, (n, n)).astype(np.int8))):
+        bt = np.ascontiguousarray(b.T)
+        ref = np.zeros((n, n), np.int32)
+        getattr(orc.ref, f"ref_vnni_matmul_{n}")(a.ctypes.data, bt.ctypes.data, ref.ctypes.data)
+        assert (orc.matmul_i8(a, b) == ref).all()
+        c, _ = orc.matmul_i8_vnni(a, b, nthreads=4)
+        assert (c == ref).all()
+
+
+def test_checksum_recipe_fixture(orc):
+    """Golden checksums of the reference's int8 benchmark recipe (tests/golden)."""
+    import json
+    import os
+    gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "int8_recipe_checksums.json")))
+    for n_str, want in gold["checksums"].items():
+        n = int(n_str)
+        if n > 512:
+            continue  # covered on the GPU; the scalar oracle is slow there
+        a, b = orc.recipe_inputs(n)
+        c, _ = orc.matmul_i8_vnni(a, b, nthreads=4)
+        assert orc.checksum_i32(c) == want, n
+
+
+def test_int4_nibble_convention_vs_reference(orc):
+    """F6 nibble unpack (low = even k, sign-extend >= 8) reproduces the
+    reference's packed int4 GEMM checksum (bench_int4_matmul_runner.cpp:74-150)."""
+    if orc.ref is None:
+        pytest.skip("reference not built here")
+    for n in (32, 64, 128):
+        idx = np.arange(n * n).reshape(n, n)
+        a = ((idx % 15) - 7).astype(np.float32)                  # A[i,k]
+        bt_vals = ((idx % 15) - 7)                                # B_T[j,k] = B[k,j]
+        nib = (bt_vals & 15).astype(np.uint8)
+        packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+        c = orc.matmul_w4s(packed, np.ones((n, n // 32 if n >= 32 else 1), np.float32),
+                           a, gs=32)
+        c16 = np.rint(c).astype(np.int64).astype(np.int16)      # i16 result type
+        chk = np.int64(c16.astype(np.int64).sum()).astype(np.int32)
+        assert int(chk) == int(getattr(orc.ref, f"ref_packed_int4_{n}")())
+        assert int(chk) == int(getattr(orc.ref, f"ref_scalar_int4_{n}")())
+
+
+# ---------------------------------------------------------------- fp32 ops --
+
+def test_matmul_f32_kat_and_accumulate(orc):
+    a = np.arange(1, 11, dtype=np.float32)
+    b = np.full(10, 2.0, np.float32)
+    out = np.zeros(1, np.float32)
+    orc.matmul_f32_acc(a, b, out, 1, 10, 1)
+    assert out[0] == 110.0               # tests/test_tensor_matmul_runner.cpp:39
+    orc.matmul_f32_acc(a, b, out, 1, 10, 1)
+    assert out[0] == 220.0               # C += A*B accumulates (F4)
+    m, k, n = 9, 33, 5
+    A = RNG.standard_normal(3 + m * k).astype(np.float32)
+    B = RNG.standard_normal(2 + k * n).astype(np.float32)
+    C = np.zeros(4 + m * n, np.float32)
+    orc.matmul_f32_acc(A, B, C, m, k, n, 3, 2, 4)
+    exp = A[3:].reshape(m, k).astype(np.float64) @ B[2:].reshape(k, n).astype(np.float64)
+    np.testing.assert_allclose(C[4:].reshape(m, n), exp, rtol=1e-5, atol=1e-5)
+    assert (C[:4] == 0).all()
+
+
+def test_rmsnorm_kat(orc):
+    out = orc.rmsnorm(np.array([1, 2, 3, 4], np.float32), np.ones(4, np.float32), 1e-5)
+    want = np.float32(1.0) / np.sqrt(np.float32(7.5) + np.float32(1e-5))
+    assert abs(out[0] - want) < 1e-4     # examples/llama2/kernels/test_rmsnorm_host.cpp:34-48
+    x = RNG.standard_normal(768).astype(np.float32)
+    w = RNG.standard_normal(2 * 768).astype(np.float32)
+    o1 = orc.rmsnorm(x, w, 1e-5, 768)
+    exp = x / np.sqrt((x.astype(np.float64) ** 2).mean() + 1e-5) * w[768:]
+    np.testing.assert_allclose(o1, exp, rtol=1e-5, atol=1e-6)
+    o2 = orc.rmsnorm(x * 7.0, w, 0.0, 768)  # scale invariance at eps = 0
+    np.testing.assert_allclose(o2, orc.rmsnorm(x, w, 0.0, 768), rtol=1e-5, atol=1e-6)
+
+
+def test_softmax_kat_and_offsets(orc):
+    out = orc.softmax(np.array([1, 2, 3, 4], np.float32))
+    e = np.exp(np.array([-3, -2, -1, 0], np.float32))
+    assert abs(out[0] - e[0] / e.sum()) < 1e-4   # test_softmax_host.cpp:34-45
+    assert np.allclose(orc.softmax(np.full(17, 3.5, np.float32)), 1 / 17)
+    x = RNG.standard_normal(50).astype(np.float32)
+    out = orc.softmax(x, np.zeros(64, np.float32), size=20, in_off=7, out_off=11)
+    ref = np.exp(x[7:27].astype(np.float64) - x[7:27].max())
+    np.testing.assert_allclose(out[11:31], ref / ref.sum(), rtol=1e-5)
+    assert (out[:11] == 0).all() and (out[31:] == 0).all()
+
+
+def test_silu_kat(orc):
+    out = orc.silu(np.array([1, 2, -1, 0], np.float32))
+    assert abs(out[0] - 1 / (1 + np.exp(-1.0))) < 1e-4  # test_silu_host.cpp:32-43
+    assert out[3] == 0.0
+    x = RNG.standard_normal(1000).astype(np.float32) * 5
+    np.testing.assert_allclose(orc.silu(x), x / (1 + np.exp(-x.astype(np.float64))),
+                               rtol=1e-5, atol=1e-6)
+
+
+# --------------------------------------------------------------------- W4 --
+
+def test_quant_f5_roofline_kat(orc):
+    """bench constants of examples/llama2/test_quant_roofline.cpp:71-92:
+    bytes 0x55 (q = 5 in both nibbles), scale 0.01, zero 0 -> every w = 0.05."""
+    rows, cols, gs = 12, 256, 128
+    qw = np.full(rows * cols // 2, 0x55, np.uint8)
+    sc = np.full(rows * cols // gs, 0.01, np.float32)
+    ze = np.zeros(rows * cols // gs, np.float32)
+    x = RNG.standard_normal(cols).astype(np.float32)
+    out = orc.matmul_quant_f5(qw, sc, ze, x, rows, cols, gs)
+    np.testing.assert_allclose(out, 0.05 * x.astype(np.float64).sum(), rtol=1e-4, atol=1e-5)
+
+
+def _dequant_f5(qw, sc, ze, total, gs):
+    q = np.empty(total, np.float64)
+    q[0::2] = qw[: (total + 1) // 2] & 15
+    q[1::2] = (qw[: total // 2] >> 4) & 15
+    g = np.arange(total) // gs
+    return q * sc[g] + ze[g]
+
+
+def test_quant_f5_vs_dequant_and_quantizer(orc):
+    rows, cols, gs = 16, 512, 128
+    w = RNG.uniform(-0.01, 0.01, rows * cols).astype(np.float32)  # bench_llama_quant.cpp:43-49
+    qw, sc, ze = orc.quantize_f5(w, gs)
+    deq = _dequant_f5(qw, sc, ze, w.size, gs)
+    assert np.abs(deq - w).max() <= sc.max() / 2 + 1e-7          # round-to-nearest bound
+    x = RNG.standard_normal(cols).astype(np.float32)
+    out = orc.matmul_quant_f5(qw, sc, ze, x, rows, cols, gs)
+    exp = deq.reshape(rows, cols) @ x.astype(np.float64)
+    np.testing.assert_allclose(out, exp, rtol=1e-4, atol=1e-5)
+    # weight offset: the second matrix in a concatenated buffer (D3 fixed)
+    w2 = RNG.uniform(-0.01, 0.01, 2 * rows * cols).astype(np.float32)
+    qw2, sc2, ze2 = orc.quantize_f5(w2, gs)
+    out2 = orc.matmul_quant_f5(qw2, sc2, ze2, x, rows, cols, gs, rows * cols)
+    deq2 = _dequant_f5(qw2, sc2, ze2, w2.size, gs)[rows * cols:]
+    np.testing.assert_allclose(out2, deq2.reshape(rows, cols) @ x, rtol=1e-4, atol=1e-5)
+
+
+def _rand_w4s(N, K, gs):
+    q = RNG.integers(-8, 8, (N, K))
+    nib = (q & 15).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    sc = (np.abs(RNG.standard_normal((N, K // gs))) * 0.02 / 7).astype(np.float32)
+    return q, packed, sc
+
+
+def test_w4s_vs_dequant_and_f5_equivalence(orc):
+    N, K, gs, M = 24, 320, 32, 3
+    q, packed, sc = _rand_w4s(N, K, gs)
+    x = RNG.standard_normal((M, K)).astype(np.float32)
+    out = orc.matmul_w4s(packed, sc, x, gs)
+    deq = (q.astype(np.float32) * np.repeat(sc, gs, axis=1)).astype(np.float64)
+    np.testing.assert_allclose(out, x.astype(np.float64) @ deq.T, rtol=1e-6, atol=1e-7)
+    # F6 == F5 with u = q + 8 and zero = -8 * scale (flat groups == row groups)
+    u = (q + 8).astype(np.uint8)
+    f5 = (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8).ravel()
+    f5_out = orc.matmul_quant_f5(f5, sc.ravel().copy(), (-8 * sc).ravel().copy(), x[0],
+                                 N, K, gs)
+    np.testing.assert_allclose(f5_out, out[0], rtol=1e-4, atol=1e-5)
+    f32 = orc.matmul_w4s_f32(packed, sc, x, gs, nthreads=2)
+    np.testing.assert_allclose(f32, out, rtol=1e-4, atol=1e-5)
+
+
+# ------------------------------------------------------------------- RoPE --
+
+def test_rope_properties(orc):
+    dim, hs = 64, 16
+    q = RNG.standard_normal(dim).astype(np.float32)
+    k = RNG.standard_normal(dim).astype(np.float32)
+    q0, k0 = q.copy(), k.copy()
+    orc.rope(q, k, dim, dim, hs, 0)
+    assert np.allclose(q, q0) and np.allclose(k, k0)      # pos 0: identity
+    pos = 5
+    orc.rope(q, k, dim, dim // 2, hs, pos)
+    pair = lambda v: v[0::2] ** 2 + v[1::2] ** 2
+    np.testing.assert_allclose(pair(q), pair(q0), rtol=1e-5)   # rotation keeps norms
+    # pair 0 of each head has freq 1: angle = pos
+    c, s = np.cos(pos), np.sin(pos)
+    np.testing.assert_allclose(q[0], q0[0] * c - q0[1] * s, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(q[hs], q0[hs] * c - q0[hs + 1] * s, rtol=1e-5, atol=1e-6)
+    assert np.allclose(k[dim // 2:], k0[dim // 2:])             # only i < kv_dim rotated
