@@ -273,6 +273,167 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
     }
 }
 
+// Large-problem kernel: B given as B_T[N,K] (callers with B[K,N] transpose it
+// first into a workspace), v_mfma_i32_16x16x64_i8, 8 waves (2 per SIMD) on a
+// 256x256 tile, BK = 128, LDS double-buffered.  All global loads are issued
+// unconditionally from clamped (in-bounds) addresses and zeroed when out of
+// range, so each K iteration is one basic block the scheduler can interleave.
+// Two waves per SIMD hide the LDS and barrier latency of one behind the MFMAs
+// of the other; the 16x16x64 shape sustains a higher int8 rate on random data
+// than 32x32x32 on MI355X.
+template <int BM, int BN, int BK, int WGM, int WGN, bool AU8>
+__global__ void __launch_bounds__(WGM *WGN * 64)
+    gemm_i8_nt16(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+                 int tiles_m, int tiles_n) {
+  constexpr int NT = WGM * WGN * 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int KC = BK / 16;
+  constexpr int A_PER = BM * KC / NT, B_PER = BN * KC / NT;
+  static_assert(BM * KC % NT == 0 && BN * KC % NT == 0, "tile/threads");
+  static_assert(BK % 64 == 0 && WM % 16 == 0 && WN % 16 == 0, "tile");
+  __shared__ uint4 sA[2][KC * BM];
+  __shared__ uint4 sB[2][KC * BN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  int tm, tn;
+  tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = (K + BK - 1) / BK;
+  uint4 ra[A_PER], rb[B_PER];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT, kc = c % KC, m = c / KC;
+      const int gm = m0 + m, gk = k0 + kc * 16;
+      uint4 v = *(const uint4 *)(A + (int64_t)min(gm, M - 1) * lda + min(gk, K - 16));
+      if (gm >= M || gk >= K) v = make_uint4(0, 0, 0, 0);
+      if constexpr (AU8) {
+        v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+      }
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const int c = tid + i * NT, kc = c % KC, n = c / KC;
+      const int gn = n0 + n, gk = k0 + kc * 16;
+      uint4 v = *(const uint4 *)(B + (int64_t)min(gn, N - 1) * ldb + min(gk, K - 16));
+      if (gn >= N || gk >= K) v = make_uint4(0, 0, 0, 0);
+      rb[i] = v;
+    }
+  };
+  auto store_tile = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT, kc = c % KC, m = c / KC;
+      sA[s][kc * BM + swz_rows(m, kc)] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const int c = tid + i * NT, kc = c % KC, n = c / KC;
+      sB[s][kc * BN + swz_rows(n, kc)] = rb[i];
+    }
+  };
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+  int cs[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) cs[j] = 0;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  const int lr = lane & 15, lk = lane >> 4;
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    load_tile(min(kt + 1, nk - 1) * BK);  // the last prefetch repeats a tile; never read
+#pragma unroll
+    for (int ks = 0; ks < BK / 64; ks++) {
+      const int kc = ks * 4 + lk;  // 16x16x64 operand: lane holds row l%16, K bytes 16*(l/16)..+16
+      v4i af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const uint4 v = sA[cur][kc * BM + swz_rows(wm0 + i * 16 + lr, kc)];
+        af[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+      }
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const uint4 v = sB[cur][kc * BN + swz_rows(wn0 + j * 16 + lr, kc)];
+        bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        if constexpr (AU8) {
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].x, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].y, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].z, 0x01010101, cs[j], false);
+          cs[j] = __builtin_amdgcn_sdot4(bf[j].w, 0x01010101, cs[j], false);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    store_tile(cur ^ 1);
+    __syncthreads();
+  }
+  if constexpr (AU8) {
+    // lanes l, l^16, l^32, l^48 hold the four K quarters of column l%16
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      int t = cs[j] + __shfl_xor(cs[j], 16);
+      t += __shfl_xor(t, 32);
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[i][j][r] += 128 * t;
+    }
+  }
+  // Output of a 16x16 i32 MFMA: lane l holds column l%16, rows 4*(l/16) + r.
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn0 + j * 16 + lr;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int row = m0 + wm0 + i * 16 + 4 * lk + r;
+        if (row < M && col < N) C[(int64_t)row * ldc + col] = acc[i][j][r];
+      }
+    }
+}
+
+// B[K,N] -> B_T[N,K] through a 64x64 LDS tile (K % 16 == 0, N % 16 == 0).
+// Feeds gemm_i8_nt16 when the caller passes tensor_matmul's [K,N] layout; the
+// reference materialises the same B_T (ConvertSimpToMemRef.cpp:3168-3216).
+__global__ void __launch_bounds__(256)
+    transpose_i8(const int8_t *__restrict__ B, int64_t ldb, int8_t *__restrict__ BT, int K, int N) {
+  __shared__ uint8_t s[64][64 + 4];
+  const int t = threadIdx.x;
+  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  {
+    const int k = t >> 2, c = t & 3;
+    const int gk = k0 + k, gn = n0 + 16 * c;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gk < K && gn < N) v = *(const uint4 *)(B + (int64_t)gk * ldb + gn);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 16; j++) s[k][16 * c + j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+  }
+  __syncthreads();
+  {
+    const int n = t >> 2, c = t & 3;
+    const int gn = n0 + n, gk = k0 + 16 * c;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; j++) w[j >> 2] |= (uint32_t)s[16 * c + j][n] << (8 * (j & 3));
+    if (gn < N && gk < K) *(uint4 *)(BT + (int64_t)gn * K + gk) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // Correctness fallback for shapes the MFMA path cannot load with aligned
 // vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).
 template <bool BNK, bool AU8>
@@ -356,7 +517,23 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
   }
   const int64_t cus = num_cus();
   auto tiles = [&](int bm, int bn) { return cdiv(g.M, bm) * cdiv(g.N, bn); };
-  if (tiles(256, 256) >= cus) return launch_mfma<256, 256, 128, 2, 2, BNK, AU8>(g, 1, st);
+  if (tiles(256, 256) >= cus && g.N % 16 == 0) {
+    GemmArgs h = g;
+    if (!BNK) {  // B[K,N] -> B_T[N,K] in the per-stream workspace
+      void *ws = nullptr;
+      int rc = workspace(st, (size_t)g.K * g.N, &ws);
+      if (rc) return rc;
+      hipLaunchKernelGGL(transpose_i8, dim3((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.K, 64)),
+                         dim3(256), 0, st, g.B, g.ldb, (int8_t *)ws, g.K, g.N);
+      h.B = (const int8_t *)ws;
+      h.ldb = g.K;
+    }
+    const int tm = (int)cdiv(g.M, 256), tn = (int)cdiv(g.N, 256);
+    hipLaunchKernelGGL((gemm_i8_nt16<256, 256, 128, 2, 4, AU8>), dim3(tm * tn), dim3(512), 0, st,
+                       h.A, h.lda, h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
   if (tiles(128, 128) >= cus) return launch_mfma<128, 128, 128, 2, 2, BNK, AU8>(g, 1, st);
   if (g.M > 32) {
     const int64_t t = tiles(64, 64);

@@ -6,6 +6,7 @@
 // status codes; SimpLang's loader reports failures with std::runtime_error
 // (runtime/include/kernel_runner.hpp:40-56).  Here every entry point returns an
 // int32 status and leaves the message in a thread-local string.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -67,6 +68,45 @@ int num_cus() {
     g_cus[dev] = n > 0 ? n : 256;
   }
   return g_cus[dev];
+}
+
+namespace {
+struct WsKey {
+  int dev;
+  hipStream_t stream;
+  bool operator<(const WsKey &o) const {
+    return dev != o.dev ? dev < o.dev : (uintptr_t)stream < (uintptr_t)o.stream;
+  }
+};
+struct WsBuf {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::map<WsKey, WsBuf> g_ws;
+}  // namespace
+
+int workspace(hipStream_t stream, size_t bytes, void **ptr) {
+  int dev = ensure_device();
+  if (dev < 0) return dev;
+  std::lock_guard<std::mutex> lk(g_mu);
+  WsBuf &b = g_ws[WsKey{dev, stream}];
+  if (b.bytes < bytes) {
+    if (b.ptr) {
+      SIMP_HIP(hipStreamSynchronize(stream));  // earlier calls may still read it
+      SIMP_HIP(hipFree(b.ptr));
+      b.ptr = nullptr;
+      b.bytes = 0;
+    }
+    size_t want = std::max(bytes, (size_t)1 << 20);
+    hipError_t e = hipMalloc(&b.ptr, want);
+    if (e != hipSuccess) {
+      b.ptr = nullptr;
+      return set_error(SIMP_RT_ENOMEM, "workspace of %zu bytes: %s", want, hipGetErrorString(e));
+    }
+    b.bytes = want;
+  }
+  *ptr = b.ptr;
+  return SIMP_RT_OK;
 }
 
 // Looks p up in the registry; returns the device address or nullptr.

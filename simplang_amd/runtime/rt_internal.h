@@ -69,4 +69,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Number of CUs of the current device (cached per device).
 int num_cus();
 
+// Library-owned device scratch for (current device, stream), grown on demand
+// and kept until the process ends.  Calls on one stream are ordered, so they
+// may share it; calls on different streams get different buffers.
+int workspace(hipStream_t stream, size_t bytes, void **ptr);
+
 }  // namespace simp

@@ -91,18 +91,29 @@ def test_int8_recipe_checksums(dev, orc):
         assert orc.checksum_i32(got) == want, n
 
 
-@pytest.mark.parametrize("n", [4096, 8192])
-def test_int8_full_size_identities(dev, orc, n):
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (8192, 8192, 8192),
+                                   (4100, 4112, 4000)])   # ragged edges on the large-tile path
+@pytest.mark.parametrize("variant", ["u8s8", "s8s8", "nt_u8s8", "nt_s8s8"])
+def test_int8_full_size_identities(dev, orc, M, N, K, variant):
     import torch
-    print(f"[int8-full] N={n}", flush=True)
-    a, b = _inputs(n, n, n)
-    got = _run(dev, sa.matmul_u8s8_i32, a, b, n, n).astype(np.int64)
+    if M == 8192 and variant.startswith("nt"):
+        pytest.skip("NT at 8192 covered by the KN path's identical kernel")
+    print(f"[int8-full] {variant} M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K)
+    if "s8s8" in variant:
+        a = a.view(np.int8)
+    fn = {"u8s8": sa.matmul_u8s8_i32, "s8s8": sa.tensor_matmul_i8,
+          "nt_u8s8": sa.matmul_nt_u8s8_i32, "nt_s8s8": sa.tensor_matmul_nt_i8}[variant]
+    bb = np.ascontiguousarray(b.T) if variant.startswith("nt") else b
+    got = _run(dev, fn, a, bb, M, N).astype(np.int64)
     a64, b64 = a.astype(np.int64), b.astype(np.int64)
     assert np.array_equal(got.sum(1), a64 @ b64.sum(1))          # C 1 = A (B 1)
     assert np.array_equal(got.sum(0), a64.sum(0) @ b64)          # 1^T C = (1^T A) B
-    rows = np.random.default_rng(n).choice(n, 4, replace=False)
-    for r in rows:
-        assert np.array_equal(got[r], a64[r] @ b64)
+    rng = np.random.default_rng(M + N)
+    for r in list(rng.choice(M, 3, replace=False)) + [M - 1]:
+        assert np.array_equal(got[r], a64[r] @ b64)              # full rows, exact
+    for c in list(rng.choice(N, 2, replace=False)) + [N - 1]:
+        assert np.array_equal(got[:, c], a64 @ b64[:, c])        # full columns, exact
     del got
     torch.cuda.empty_cache()
 
