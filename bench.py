@@ -80,6 +80,68 @@ def cpu_baseline(n, budget_s=12.0):
                        f"{'AVX-512 VNNI' if hw else 'scalar (host lacks AVX-512 VNNI)'}")}
 
 
+def graph_time_ms(calls, stream, replays=5):
+    """GPU time per call of a sequence of library calls, captured once in a HIP
+    graph and replayed (removes the Python/ctypes enqueue cost, which exceeds the
+    runtime of the small kernels)."""
+    import torch
+    import simplang_amd as sa
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        sa.set_stream(side)
+        for f in calls:
+            f()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sa.set_stream(torch.cuda.current_stream())
+        for f in calls:
+            f()
+    sa.set_stream(stream)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (replays * len(calls))
+
+
+def w4_bench(dev, stream):
+    """W4 GEMV/skinny GEMM, BASELINE configs[2].  Weight copies are rotated so
+    that more than 512 MB is touched per pass: every launch streams its weights
+    from HBM (the 256 MB Infinity Cache cannot hold them), as in a decode step.
+    Timed by HIP-graph replay of one launch per copy."""
+    import torch
+    import simplang_amd as sa
+    out = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    for (K, N) in ((3200, 8640), (8640, 3200), (3200, 32000)):
+        wbytes = N * K // 2 + 4 * N * K // 32
+        copies = max(2, -(-512 * 2**20 // wbytes))
+        ws = [torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g)
+              for _ in range(copies)]
+        ss = [(torch.rand((N, K // 32), device=dev, generator=g) * 0.02 / 7) for _ in range(copies)]
+        for M in (1, 4, 16):
+            x = torch.randn((M, K), device=dev, generator=g)
+            o = torch.empty((M, N), device=dev)
+            calls = [(lambda i=i: sa.matmul_w4s(ws[i], ss[i], x, o, 32)) for i in range(copies)]
+            ms = graph_time_ms(calls, stream)
+            byts = N * K / 2 + 4 * N * K / 32 + 4 * M * K + 4 * M * N
+            out.append({"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                        "GBs": round(byts / (ms * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+        del ws, ss
+        torch.cuda.empty_cache()
+    return out
+
+
 def load_traffic(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
@@ -137,6 +199,8 @@ def main():
             del a, b, c
         torch.cuda.empty_cache()
 
+    w4 = [] if args.no_sweep else w4_bench(dev, stream)
+
     cpu = None if args.no_cpu else cpu_baseline(n)
 
     line = {
@@ -159,6 +223,7 @@ def main():
                      "traffic": load_traffic(f"gemm_i8_{n}")},
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "w4_gemv": w4,
     }
     print(json.dumps(line), flush=True)
 

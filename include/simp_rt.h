@@ -97,6 +97,37 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
     const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
     int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
 
+/* ----------------------------------------------------------------- W4 -- */
+
+/* matmul_quant(qweights, scales, zeros, input, output, rows, cols, group_size,
+ * offset): output[i] = sum_k (q*scale + zero) * input[k] for the rows x cols
+ * matrix whose weights start at element `offset` of the packed array
+ * (unsigned nibbles, low nibble = even element; flat groups of group_size).
+ * Replaces MatMulQuantOpLowering (src/mlir/lowering/ConvertSimpToMemRef.cpp:3853-4013),
+ * operand order of src/mlir/mlir_codegen.cpp:1502-1531.  The scale/zero index
+ * includes `offset` (the reference drops it, so every layer but the first
+ * reads the wrong scales) and any group_size works (the reference requires 128). */
+int32_t simp_rt_matmul_quant(
+    const int8_t *qw_alloc, const int8_t *qw, int64_t qw_off, int64_t qw_size, int64_t qw_stride,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_size, int64_t s_stride,
+    const float *z_alloc, const float *z, int64_t z_off, int64_t z_size, int64_t z_stride,
+    const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
+    float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
+    int64_t rows, int64_t cols, int64_t group_size, int64_t offset);
+
+/* Symmetric W4 GEMV / skinny GEMM: out[M,N] = x[M,K] * W^T with W[N,K] packed
+ * as signed nibbles in [-8,7] (low nibble = even k, rows of K/2 bytes) and one
+ * fp32 scale per group of group_size along K (scales[N, K/group_size]).  The
+ * signed-nibble convention is the reference's i4 tensor packing
+ * (ConvertSimpToMemRef.cpp:48-66,3016-3037); it is the matmul_quant computation
+ * with zero = -8*scale and u = q+8. */
+int32_t simp_rt_matmul_w4s(
+    const uint8_t *w_alloc, const uint8_t *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0, int64_t w_st1,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_s0, int64_t s_s1, int64_t s_st0, int64_t s_st1,
+    const float *x_alloc, const float *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_st0, int64_t x_st1,
+    float *o_alloc, float *o, int64_t o_off, int64_t o_s0, int64_t o_s1, int64_t o_st0, int64_t o_st1,
+    int64_t group_size);
+
 #ifdef __cplusplus
 }
 #endif

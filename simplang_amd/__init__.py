@@ -17,4 +17,6 @@ from .host import (  # noqa: F401
     tensor_matmul_nt_i8,
     matmul_u8s8_i32,
     matmul_nt_u8s8_i32,
+    matmul_quant,
+    matmul_w4s,
 )

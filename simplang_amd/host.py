@@ -53,6 +53,8 @@ def _sig(name, argtypes):
 for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
            "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32"):
     _sig(_n, _D2 * 3)
+_sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
+_sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
 _sig("simp_rt_set_stream", [_P])
 _sig("simp_rt_register", [_P, _I, C.c_int32])
 _sig("simp_rt_unregister", [_P])
@@ -158,3 +160,18 @@ def matmul_u8s8_i32(a, b, c):
 def matmul_nt_u8s8_i32(a, bt, c):
     """C = A(u8) x B_T(s8)^T -> i32, vpdpbusd semantics, B as B_T[N,K]."""
     return _gemm("simp_rt_matmul_nt_u8s8_i32", a, bt, c)
+
+
+def matmul_quant(qweights, scales, zeros, inp, out, rows, cols, group_size, offset=0):
+    """``matmul_quant`` builtin (reference W4: unsigned nibbles, scale + zero per flat group)."""
+    _check("simp_rt_matmul_quant",
+           lib.simp_rt_matmul_quant(*desc1(qweights), *desc1(scales), *desc1(zeros),
+                                    *desc1(inp), *desc1(out), rows, cols, group_size, offset))
+    return out
+
+
+def matmul_w4s(w, scales, x, out, group_size=32):
+    """out[M,N] = x[M,K] W^T, W[N,K/2] signed-nibble W4 with scales[N,K/gs]."""
+    _check("simp_rt_matmul_w4s",
+           lib.simp_rt_matmul_w4s(*desc2(w), *desc2(scales), *desc2(x), *desc2(out), group_size))
+    return out

@@ -74,4 +74,11 @@ int num_cus();
 // may share it; calls on different streams get different buffers.
 int workspace(hipStream_t stream, size_t bytes, void **ptr);
 
+// Kernel launchers on device pointers, shared by the op entry points and the
+// decode step.
+int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const float *X,
+               int64_t ldx, float *O, int64_t ldo, int M, int N, int K, int gs, hipStream_t st);
+int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X, float *O, int rows,
+               int cols, int gs, int64_t off, hipStream_t st);
+
 }  // namespace simp

@@ -1,0 +1,428 @@
+// w4.hip -- W4 (4-bit weight) GEMV / skinny GEMM, HBM-bound.
+//
+// Two packed formats, both "low nibble = even index, two weights per byte":
+//   reference  (matmul_quant, MatMulQuantOpLowering, ConvertSimpToMemRef.cpp:3853-4013):
+//              unsigned q in [0,15], w = q*scale + zero, groups are flat runs of
+//              `gs` weights of the concatenated weight array starting at `offset`.
+//              The reference reads scales at (i*cols)/gs + g, ignoring `offset`,
+//              and always walks 8 tiles of 16 (gs must be 128); both are fixed
+//              here: the group index is (offset + i*cols)/gs + g and any gs that
+//              is a multiple of 32 works.
+//   symmetric  (the int4 convention of ConvertSimpToMemRef.cpp:3016-3037): signed
+//              q in [-8,7], one fp32 scale per group of `gs` along K, W[N,K] with
+//              rows of K/2 bytes, scales[N,K/gs], x[M,K] -> out[M,N].
+//
+// Kernel shape: 16 lanes cooperate on one weight row, each lane taking 16-byte
+// chunks (32 weights) of the row in turn, so a wave streams 4 rows x 256
+// contiguous bytes per load.  Per chunk the 8 dwords are split into even/odd
+// nibble bytes (and/shift) and converted with v_cvt_f32_ubyte{0..3}: 1.4 VALU
+// ops per weight for decode, then one FMA per weight and row of x.  Signed
+// nibbles are first flipped to q+8 (xor 0x88888888) and the -8*sum(x) term is
+// folded in once per chunk from per-chunk sums of x computed in the block
+// prologue (LDS), so no per-weight sign handling is needed.  Per-chunk partial
+// dot products are scaled by the group's scale (and zero) and summed in fp32;
+// the 16 lane partials are combined with a butterfly over the lane group.
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+constexpr int kRowsPerBlock = 16;  // 16 lanes per row, 256 threads
+constexpr int kLanesPerRow = 16;
+
+// Byte I of x as float in one v_cvt_f32_ubyte{I} (the compiler would emit a
+// bitfield extract plus ubyte0 for the equivalent shift-and-mask).
+template <int I>
+__device__ __forceinline__ float ubyte(uint32_t x) {
+  float r;
+  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// Unpacks the 32 nibbles of a 16-byte chunk into u[0..31] (u[k] = nibble k).
+__device__ __forceinline__ void unpack32(uint4 w, float (&u)[32]) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;
+    u[8 * i + 0] = ubyte<0>(lo);
+    u[8 * i + 1] = ubyte<0>(hi);
+    u[8 * i + 2] = ubyte<1>(lo);
+    u[8 * i + 3] = ubyte<1>(hi);
+    u[8 * i + 4] = ubyte<2>(lo);
+    u[8 * i + 5] = ubyte<2>(hi);
+    u[8 * i + 6] = ubyte<3>(lo);
+    u[8 * i + 7] = ubyte<3>(hi);
+  }
+}
+
+// Sum over the 16 lanes of a row group.
+__device__ __forceinline__ float group16_sum(float v) {
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 1);
+  return v;
+}
+
+// Per-chunk sums of x (xs[m*nchunk + c] = sum_{j<32} x[m, 32c + j]) into LDS.
+template <int MT>
+__device__ __forceinline__ void chunk_sums(const float *__restrict__ X, int64_t ldx, int M, int nchunk,
+                                           float *xs) {
+  for (int i = threadIdx.x; i < M * nchunk; i += blockDim.x) {
+    const int m = i / nchunk, c = i - m * nchunk;
+    const float4 *p = (const float4 *)(X + (int64_t)m * ldx + 32 * c);
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const float4 v = p[q];
+      s += (v.x + v.y) + (v.z + v.w);
+    }
+    xs[i] = s;
+  }
+  __syncthreads();
+}
+
+// Symmetric signed W4, one scale per `gs` weights along K.  MT = max rows of x.
+// Lane -> row mapping: a block owns RB weight rows; thread t takes row t % RB
+// and the chunks c = g, g+G, g+2G, ... of it, g = t / RB, G = 256 / RB, so a
+// wave's load covers RB rows x 64/RB consecutive chunks.  The RB lanes of a
+// group need the same x chunk.  XL: x is staged once per block in LDS, each
+// chunk's eight float4 slots rotated by the chunk index so the 64/RB chunks
+// read by one instruction fall in distinct banks, and the per-chunk sums of x
+// (the -8 offset of the flipped nibbles) are taken from LDS.  !XL (x too large
+// for LDS): x is read from global memory as broadcasts and the chunk sums are
+// split over the RB lanes sharing a chunk.  UB weight chunks are loaded before
+// any is used.  The G partial sums of a row are reduced with shuffles inside a
+// wave, then through LDS across the 4 waves.
+template <int MT, int RB, int UB, bool XL>
+__global__ void __launch_bounds__(256)
+    w4s_gemv(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
+             const float *__restrict__ X, int64_t ldx, float *__restrict__ O, int64_t ldo, int M,
+             int N, int K, int gs) {
+  constexpr int G = 256 / RB, XPER = 32 / RB;
+  static_assert(32 % RB == 0 && RB <= 32, "RB");
+  __shared__ float red[4][MT][RB];
+  extern __shared__ float smem[];  // XL: xl[M][K] then xs[M][K/32]
+  const int nchunk = K >> 5;
+  float *xl = smem, *xs = smem + (XL ? M * K : 0);
+  if constexpr (XL) {
+    for (int i = threadIdx.x; i < M * (K >> 2); i += 256) {
+      const int m = i / (K >> 2), f = i - m * (K >> 2);
+      const int c = f >> 3, q = f & 7;
+      *(float4 *)(xl + m * K + 32 * c + 4 * ((q + c) & 7)) =
+          *(const float4 *)(X + (int64_t)m * ldx + 4 * f);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < M * nchunk; i += 256) {
+      const int m = i / nchunk, c = i - m * nchunk;
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 v = *(const float4 *)(xl + m * K + 32 * c + 4 * q);
+        t += (v.x + v.y) + (v.z + v.w);
+      }
+      xs[i] = t;
+    }
+    __syncthreads();
+  }
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
+  const int n = min(blockIdx.x * RB + r, N - 1);  // clamped: rows past N compute, never store
+  const uint8_t *wrow = W + (int64_t)n * ldw;
+  const float *srow = S + (int64_t)n * lds;
+  const int cpg = gs >> 5;
+  float acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; m++) acc[m] = 0.f;
+  for (int c0 = g; c0 < nchunk; c0 += G * UB) {
+    uint4 w[UB];
+    float sc[UB];
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = min(c0 + u * G, nchunk - 1);
+      w[u] = *(const uint4 *)(wrow + 16 * c);
+      sc[u] = srow[c / cpg];
+    }
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = c0 + u * G;
+      if (c < nchunk) {  // uniform across the RB lanes of the group
+        uint4 wv = w[u];
+        wv.x ^= 0x88888888u; wv.y ^= 0x88888888u; wv.z ^= 0x88888888u; wv.w ^= 0x88888888u;
+        float uu[32];
+        unpack32(wv, uu);
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (m < M) {
+            float p = 0.f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+              const float4 v = XL ? *(const float4 *)(xl + m * K + 32 * c + 4 * ((q + c) & 7))
+                                  : *(const float4 *)(X + (int64_t)m * ldx + 32 * c + 4 * q);
+              p = fmaf(uu[4 * q + 0], v.x, p);
+              p = fmaf(uu[4 * q + 1], v.y, p);
+              p = fmaf(uu[4 * q + 2], v.z, p);
+              p = fmaf(uu[4 * q + 3], v.w, p);
+            }
+            float xsum;
+            if constexpr (XL) {
+              xsum = xs[m * nchunk + c];
+            } else {
+              const float *xc = X + (int64_t)m * ldx + 32 * c;
+              xsum = 0.f;
+#pragma unroll
+              for (int e = 0; e < XPER; e++) xsum += xc[r * XPER + e];
+#pragma unroll
+              for (int d = 1; d < RB; d <<= 1) xsum += __shfl_xor(xsum, d);
+            }
+            acc[m] = fmaf(sc[u], fmaf(-8.f, xsum, p), acc[m]);  // sum (u-8) x
+          }
+        }
+      }
+    }
+  }
+  // reduce the 64/RB groups of this wave, then the 4 waves
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int m = 0; m < MT; m++) {
+    float v = acc[m];
+#pragma unroll
+    for (int d = RB; d < 64; d <<= 1) v += __shfl_xor(v, d);
+    if ((threadIdx.x & 63) < RB) red[wave][m][r] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < RB && blockIdx.x * RB + (int)threadIdx.x < N) {
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+      if (m < M)
+        O[(int64_t)m * ldo + blockIdx.x * RB + r] = (red[0][m][r] + red[1][m][r]) + (red[2][m][r] + red[3][m][r]);
+  }
+}
+
+// Reference W4 (unsigned + zero, flat groups), one x vector.  Row i's nibbles
+// start at element offset off + i*cols (a multiple of 32 here).
+__global__ void __launch_bounds__(256)
+    w4u_gemv(const uint8_t *__restrict__ Q, const float *__restrict__ S, const float *__restrict__ Z,
+             const float *__restrict__ X, float *__restrict__ O, int rows, int cols, int gs,
+             int64_t off) {
+  extern __shared__ float xs[];
+  const int nchunk = cols >> 5;
+  chunk_sums<1>(X, 0, 1, nchunk, xs);
+  const int seg = threadIdx.x & (kLanesPerRow - 1);
+  const int i = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+  if (i >= rows) return;
+  const int64_t base = off + (int64_t)i * cols;  // element index of the row start
+  const uint8_t *qrow = Q + (base >> 1);
+  const int64_t g0 = base / gs;
+  const int cpg = gs >> 5;
+  float acc = 0.f;
+  for (int c = seg; c < nchunk; c += kLanesPerRow) {
+    const uint4 w = *(const uint4 *)(qrow + 16 * c);
+    const int64_t g = g0 + c / cpg;
+    const float s = S[g], z = Z[g];
+    float u[32];
+    unpack32(w, u);
+    const float4 *xp = (const float4 *)(X + 32 * c);
+    float p = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const float4 v = xp[q];
+      p = fmaf(u[4 * q + 0], v.x, p);
+      p = fmaf(u[4 * q + 1], v.y, p);
+      p = fmaf(u[4 * q + 2], v.z, p);
+      p = fmaf(u[4 * q + 3], v.w, p);
+    }
+    acc = fmaf(s, p, fmaf(z, xs[c], acc));  // sum (u*s + z) x
+  }
+  const float v = group16_sum(acc);
+  if (seg == 0) O[i] = v;
+}
+
+// Any-shape fallbacks (one thread per output; correctness path).
+__global__ void __launch_bounds__(256)
+    w4s_generic(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
+                const float *__restrict__ X, int64_t ldx, float *__restrict__ O, int64_t ldo, int M,
+                int N, int K, int gs) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx - (int64_t)m * N);
+  float acc = 0.f;
+  for (int k = 0; k < K; k++) {
+    const uint8_t b = W[(int64_t)n * ldw + (k >> 1)];
+    int q = (k & 1) ? (b >> 4) : (b & 15);
+    q = q >= 8 ? q - 16 : q;
+    acc = fmaf((float)q * S[(int64_t)n * lds + k / gs], X[(int64_t)m * ldx + k], acc);
+  }
+  O[(int64_t)m * ldo + n] = acc;
+}
+
+__global__ void __launch_bounds__(256)
+    w4u_generic(const uint8_t *__restrict__ Q, const float *__restrict__ S, const float *__restrict__ Z,
+                const float *__restrict__ X, float *__restrict__ O, int rows, int cols, int gs,
+                int64_t off) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows) return;
+  float acc = 0.f;
+  const int64_t base = off + (int64_t)i * cols;
+  for (int k = 0; k < cols; k++) {
+    const int64_t e = base + k;
+    const uint8_t b = Q[e >> 1];
+    const int q = (e & 1) ? (b >> 4) : (b & 15);
+    const int64_t g = e / gs;
+    acc = fmaf((float)q * S[g] + Z[g], X[k], acc);
+  }
+  O[i] = acc;
+}
+
+}  // namespace
+
+// Launches the symmetric W4 GEMV on device pointers (shared with the decode step).
+int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const float *X,
+               int64_t ldx, float *O, int64_t ldo, int M, int N, int K, int gs, hipStream_t st) {
+  if (M == 0 || N == 0) return SIMP_RT_OK;
+  const bool fast = K % 32 == 0 && gs % 32 == 0 && K % gs == 0 && ldw % 16 == 0 &&
+                    ((uintptr_t)W & 15) == 0 && ldx % 4 == 0 && ((uintptr_t)X & 15) == 0 &&
+                    M <= 16;
+  if (!fast) {
+    const int64_t tot = (int64_t)M * N;
+    hipLaunchKernelGGL(w4s_generic, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, W, ldw, S,
+                       lds, X, ldx, O, ldo, M, N, K, gs);
+  } else {
+    // 8 rows per block keeps >= 400 blocks at N = 3200; x in LDS when it fits.
+    constexpr int RB = 8;
+    const dim3 grid((unsigned)cdiv(N, RB));
+    const size_t xl_bytes = sizeof(float) * ((size_t)M * K + (size_t)M * (K / 32));
+    const bool xl = xl_bytes <= 64 * 1024;
+    const bool ub4 = K / 32 <= 4 * (256 / RB);
+    const size_t shm = xl ? xl_bytes : 0;
+#define W4S_LAUNCH(MTV)                                                                         \
+  do {                                                                                          \
+    if (xl && ub4)                                                                              \
+      hipLaunchKernelGGL((w4s_gemv<MTV, RB, 4, true>), grid, dim3(256), shm, st, W, ldw, S, lds, X, \
+                         ldx, O, ldo, M, N, K, gs);                                             \
+    else if (xl)                                                                                \
+      hipLaunchKernelGGL((w4s_gemv<MTV, RB, 8, true>), grid, dim3(256), shm, st, W, ldw, S, lds, X, \
+                         ldx, O, ldo, M, N, K, gs);                                             \
+    else                                                                                        \
+      hipLaunchKernelGGL((w4s_gemv<MTV, RB, 8, false>), grid, dim3(256), 0, st, W, ldw, S, lds, X, \
+                         ldx, O, ldo, M, N, K, gs);                                             \
+  } while (0)
+    if (M == 1) W4S_LAUNCH(1);
+    else if (M <= 4) W4S_LAUNCH(4);
+    else if (M <= 8) W4S_LAUNCH(8);
+    else W4S_LAUNCH(16);
+#undef W4S_LAUNCH
+  }
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X, float *O, int rows,
+               int cols, int gs, int64_t off, hipStream_t st) {
+  if (rows == 0) return SIMP_RT_OK;
+  const bool fast = cols % 32 == 0 && gs % 32 == 0 && off % 32 == 0 && off % gs == 0 &&
+                    cols % gs == 0 &&
+                    ((uintptr_t)Q & 15) == 0 && ((uintptr_t)X & 15) == 0;
+  if (!fast) {
+    hipLaunchKernelGGL(w4u_generic, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, Q, S, Z, X, O,
+                       rows, cols, gs, off);
+  } else {
+    hipLaunchKernelGGL(w4u_gemv, dim3((unsigned)cdiv(rows, kRowsPerBlock)), dim3(256),
+                       sizeof(float) * (size_t)(cols / 32), st, Q, S, Z, X, O, rows, cols, gs, off);
+  }
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+}  // namespace simp
+
+using namespace simp;
+
+extern "C" {
+
+int32_t simp_rt_matmul_quant(
+    const int8_t *qw_alloc, const int8_t *qw, int64_t qw_off, int64_t qw_size, int64_t qw_stride,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_size, int64_t s_stride,
+    const float *z_alloc, const float *z, int64_t z_off, int64_t z_size, int64_t z_stride,
+    const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
+    float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
+    int64_t rows, int64_t cols, int64_t group_size, int64_t offset) {
+  (void)qw_alloc; (void)s_alloc; (void)z_alloc; (void)in_alloc; (void)out_alloc;
+  int rc;
+  if ((rc = check_desc1("qweights", qw, qw_off, qw_size, qw_stride))) return rc;
+  if ((rc = check_desc1("scales", s, s_off, s_size, s_stride))) return rc;
+  if ((rc = check_desc1("zeros", z, z_off, z_size, z_stride))) return rc;
+  if ((rc = check_desc1("input", in, in_off, in_size, in_stride))) return rc;
+  if ((rc = check_desc1("output", out, out_off, out_size, out_stride))) return rc;
+  if (rows < 0 || cols < 0 || offset < 0 || group_size <= 0)
+    return set_error(SIMP_RT_EINVAL, "matmul_quant: bad rows/cols/group_size/offset");
+  if (rows == 0) return SIMP_RT_OK;
+  const int64_t last = offset + rows * cols;  // one past the last weight
+  const int64_t ngroups = (last + group_size - 1) / group_size;
+  if ((last + 1) / 2 > qw_size || ngroups > s_size || ngroups > z_size || cols > in_size ||
+      rows > out_size)
+    return set_error(SIMP_RT_EINVAL,
+                     "matmul_quant: arrays too small for rows=%lld cols=%lld gs=%lld offset=%lld",
+                     (long long)rows, (long long)cols, (long long)group_size, (long long)offset);
+  if (rows > INT32_MAX || cols > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "matmul_quant: dimension above 2^31-1");
+  Operand oq, os, oz, oi, oo;
+  if ((rc = oq.bind(qw + qw_off, (size_t)qw_size, Operand::kIn, "qweights"))) return rc;
+  if ((rc = os.bind(s + s_off, sizeof(float) * (size_t)s_size, Operand::kIn, "scales"))) return rc;
+  if ((rc = oz.bind(z + z_off, sizeof(float) * (size_t)z_size, Operand::kIn, "zeros"))) return rc;
+  if ((rc = oi.bind(in + in_off, sizeof(float) * (size_t)cols, Operand::kIn, "input"))) return rc;
+  if ((rc = oo.bind(out + out_off, sizeof(float) * (size_t)rows, Operand::kOut, "output"))) return rc;
+  if ((rc = launch_w4u((const uint8_t *)oq.dev(), (const float *)os.dev(), (const float *)oz.dev(),
+                       (const float *)oi.dev(), (float *)oo.dev(), (int)rows, (int)cols,
+                       (int)group_size, offset, cur_stream())))
+    return rc;
+  Operand *ops[] = {&oq, &os, &oz, &oi, &oo};
+  return finish(ops, 5);
+}
+
+int32_t simp_rt_matmul_w4s(
+    const uint8_t *w_alloc, const uint8_t *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0, int64_t w_st1,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_s0, int64_t s_s1, int64_t s_st0, int64_t s_st1,
+    const float *x_alloc, const float *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_st0, int64_t x_st1,
+    float *o_alloc, float *o, int64_t o_off, int64_t o_s0, int64_t o_s1, int64_t o_st0, int64_t o_st1,
+    int64_t group_size) {
+  (void)w_alloc; (void)s_alloc; (void)x_alloc; (void)o_alloc;
+  int rc;
+  if ((rc = check_desc2("W", w, w_off, w_s0, w_s1, w_st0, w_st1))) return rc;
+  if ((rc = check_desc2("scales", s, s_off, s_s0, s_s1, s_st0, s_st1))) return rc;
+  if ((rc = check_desc2("x", x, x_off, x_s0, x_s1, x_st0, x_st1))) return rc;
+  if ((rc = check_desc2("out", o, o_off, o_s0, o_s1, o_st0, o_st1))) return rc;
+  const int64_t N = w_s0, M = x_s0, K = x_s1;
+  if (group_size <= 0 || K % 2 != 0 || K % group_size != 0)
+    return set_error(SIMP_RT_EINVAL, "matmul_w4s: K=%lld must be even and a multiple of gs=%lld",
+                     (long long)K, (long long)group_size);
+  if (w_s1 != K / 2 || s_s0 != N || s_s1 != K / group_size || o_s0 != M || o_s1 != N)
+    return set_error(SIMP_RT_EINVAL,
+                     "matmul_w4s: shape mismatch W[%lld,%lld] scales[%lld,%lld] x[%lld,%lld] "
+                     "out[%lld,%lld] gs=%lld",
+                     (long long)w_s0, (long long)w_s1, (long long)s_s0, (long long)s_s1,
+                     (long long)x_s0, (long long)x_s1, (long long)o_s0, (long long)o_s1,
+                     (long long)group_size);
+  if (N > INT32_MAX || K > INT32_MAX || M > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "matmul_w4s: dimension above 2^31-1");
+  Operand ow, os, ox, oo;
+  const size_t wb = (N && K) ? (size_t)((N - 1) * w_st0 + K / 2) : 0;
+  const size_t sb = (N && K) ? sizeof(float) * (size_t)((N - 1) * s_st0 + K / group_size) : 0;
+  const size_t xb = (M && K) ? sizeof(float) * (size_t)((M - 1) * x_st0 + K) : 0;
+  const size_t ob = (M && N) ? sizeof(float) * (size_t)((M - 1) * o_st0 + N) : 0;
+  if ((rc = ow.bind(w + w_off, wb, Operand::kIn, "W"))) return rc;
+  if ((rc = os.bind(s + s_off, sb, Operand::kIn, "scales"))) return rc;
+  if ((rc = ox.bind(x + x_off, xb, Operand::kIn, "x"))) return rc;
+  if ((rc = oo.bind(o + o_off, ob, Operand::kOut, "out"))) return rc;
+  if ((rc = launch_w4s((const uint8_t *)ow.dev(), w_st0, (const float *)os.dev(), s_st0,
+                       (const float *)ox.dev(), x_st0, (float *)oo.dev(), o_st0, (int)M, (int)N,
+                       (int)K, (int)group_size, cur_stream())))
+    return rc;
+  Operand *ops[] = {&ow, &os, &ox, &oo};
+  return finish(ops, 4);
+}
+
+}  // extern "C"
