@@ -128,6 +128,70 @@ int32_t simp_rt_matmul_w4s(
     float *o_alloc, float *o, int64_t o_off, int64_t o_s0, int64_t o_s1, int64_t o_st0, int64_t o_st1,
     int64_t group_size);
 
+/* --------------------------------------------------------------- fp32 -- */
+
+/* matmul(lhs, rhs, output, m, k, n, lhs_offset, rhs_offset, output_offset):
+ * output[m,n] += lhs[m,k] * rhs[k,n] on 1-D arrays viewed as row-major
+ * matrices at the given element offsets; the caller zeroes output first when
+ * it wants a plain product.  Replaces MatMulOpLowering
+ * (src/mlir/lowering/ConvertSimpToMemRef.cpp:1794-1920), operand order of
+ * src/mlir/mlir_codegen.cpp:1388-1412. */
+int32_t simp_rt_matmul_f32(
+    const float *lhs_alloc, const float *lhs, int64_t lhs_doff, int64_t lhs_size, int64_t lhs_stride,
+    const float *rhs_alloc, const float *rhs, int64_t rhs_doff, int64_t rhs_size, int64_t rhs_stride,
+    float *out_alloc, float *out, int64_t out_doff, int64_t out_size, int64_t out_stride,
+    int64_t m, int64_t k, int64_t n, int64_t lhs_offset, int64_t rhs_offset, int64_t output_offset);
+
+/* tensor_matmul on f32 tensors: C[M,N] = A[M,K] * B[K,N] into a caller buffer.
+ * Replaces the f32 branch of TensorMatMulOpLowering (ConvertSimpToMemRef.cpp:3280-3284). */
+int32_t simp_rt_tensor_matmul_f32(
+    const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* ------------------------------------------------------ normalisations -- */
+
+/* rmsnorm(input, weight, output, size, epsilon, weight_offset):
+ * out[i] = (in[i] / sqrt(sum(in^2)/size + eps)) * weight[weight_offset + i].
+ * Replaces RMSNormOpLowering (ConvertSimpToMemRef.cpp:2157-2236); epsilon is
+ * the op's AnyFloat operand, narrowed to f32 as the lowering does. */
+int32_t simp_rt_rmsnorm(
+    const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
+    const float *w_alloc, const float *w, int64_t w_off, int64_t w_size, int64_t w_stride,
+    float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
+    int64_t size, double epsilon, int64_t weight_offset);
+
+/* softmax(input, output, size, input_offset, output_offset) over
+ * in[input_offset .. +size) into out[output_offset .. +size).
+ * Replaces SoftmaxOpLowering (ConvertSimpToMemRef.cpp:2239-2322). */
+int32_t simp_rt_softmax(
+    const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
+    float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
+    int64_t size, int64_t input_offset, int64_t output_offset);
+
+/* silu(input, output, size): out = x / (1 + exp(-x)).
+ * Replaces SiLUOpLowering (ConvertSimpToMemRef.cpp:2325-2360). */
+int32_t simp_rt_silu(
+    const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
+    float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
+    int64_t size);
+
+/* SwiGLU gate: out = silu(gate) * up, the silu call plus the elementwise
+ * product loop of examples/llama2/stories110M.sl:200-212 in one pass. */
+int32_t simp_rt_swiglu(
+    const float *g_alloc, const float *gate, int64_t g_off, int64_t g_size, int64_t g_stride,
+    const float *u_alloc, const float *up, int64_t u_off, int64_t u_size, int64_t u_stride,
+    float *o_alloc, float *out, int64_t o_off, int64_t o_size, int64_t o_stride,
+    int64_t size);
+
+/* RoPE in place on q[dim] and k[kv_dim] at position pos: for even i,
+ * f = theta^-((i % head_size)/head_size), rotate (x[i], x[i+1]) by pos*f; k
+ * only for i < kv_dim.  The scalar loop of examples/llama2/stories110M.sl:86-112. */
+int32_t simp_rt_rope(
+    float *q_alloc, float *q, int64_t q_off, int64_t q_size, int64_t q_stride,
+    float *k_alloc, float *k, int64_t k_off, int64_t k_size, int64_t k_stride,
+    int64_t dim, int64_t kv_dim, int64_t head_size, int64_t pos, double theta);
+
 #ifdef __cplusplus
 }
 #endif

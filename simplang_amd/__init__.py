@@ -19,4 +19,11 @@ from .host import (  # noqa: F401
     matmul_nt_u8s8_i32,
     matmul_quant,
     matmul_w4s,
+    matmul,
+    tensor_matmul_f32,
+    rmsnorm,
+    softmax,
+    silu,
+    swiglu,
+    rope,
 )

@@ -55,6 +55,13 @@ for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
     _sig(_n, _D2 * 3)
 _sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
 _sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
+_sig("simp_rt_matmul_f32", _D1 * 3 + [_I] * 6)
+_sig("simp_rt_tensor_matmul_f32", _D2 * 3)
+_sig("simp_rt_rmsnorm", _D1 * 3 + [_I, C.c_double, _I])
+_sig("simp_rt_softmax", _D1 * 2 + [_I, _I, _I])
+_sig("simp_rt_silu", _D1 * 2 + [_I])
+_sig("simp_rt_swiglu", _D1 * 3 + [_I])
+_sig("simp_rt_rope", _D1 * 2 + [_I, _I, _I, _I, C.c_double])
 _sig("simp_rt_set_stream", [_P])
 _sig("simp_rt_register", [_P, _I, C.c_int32])
 _sig("simp_rt_unregister", [_P])
@@ -175,3 +182,51 @@ def matmul_w4s(w, scales, x, out, group_size=32):
     _check("simp_rt_matmul_w4s",
            lib.simp_rt_matmul_w4s(*desc2(w), *desc2(scales), *desc2(x), *desc2(out), group_size))
     return out
+
+
+def matmul(lhs, rhs, out, m, k, n, lhs_offset=0, rhs_offset=0, output_offset=0):
+    """``matmul`` builtin: out[m,n] += lhs[m,k] rhs[k,n] on 1-D arrays at element offsets."""
+    _check("simp_rt_matmul_f32",
+           lib.simp_rt_matmul_f32(*desc1(lhs), *desc1(rhs), *desc1(out), m, k, n,
+                                  lhs_offset, rhs_offset, output_offset))
+    return out
+
+
+def tensor_matmul_f32(a, b, c):
+    """``tensor_matmul`` on f32 tensors: C = A B."""
+    _check("simp_rt_tensor_matmul_f32",
+           lib.simp_rt_tensor_matmul_f32(*desc2(a), *desc2(b), *desc2(c)))
+    return c
+
+
+def rmsnorm(inp, weight, out, size, epsilon=1e-5, weight_offset=0):
+    """``rmsnorm`` builtin."""
+    _check("simp_rt_rmsnorm", lib.simp_rt_rmsnorm(*desc1(inp), *desc1(weight), *desc1(out),
+                                                  size, epsilon, weight_offset))
+    return out
+
+
+def softmax(inp, out, size, input_offset=0, output_offset=0):
+    """``softmax`` builtin."""
+    _check("simp_rt_softmax", lib.simp_rt_softmax(*desc1(inp), *desc1(out), size,
+                                                  input_offset, output_offset))
+    return out
+
+
+def silu(inp, out, size):
+    """``silu`` builtin."""
+    _check("simp_rt_silu", lib.simp_rt_silu(*desc1(inp), *desc1(out), size))
+    return out
+
+
+def swiglu(gate, up, out, size):
+    """out = silu(gate) * up."""
+    _check("simp_rt_swiglu", lib.simp_rt_swiglu(*desc1(gate), *desc1(up), *desc1(out), size))
+    return out
+
+
+def rope(q, k, dim, kv_dim, head_size, pos, theta=10000.0):
+    """RoPE in place on q and k."""
+    _check("simp_rt_rope", lib.simp_rt_rope(*desc1(q), *desc1(k), dim, kv_dim, head_size, pos,
+                                            theta))
+    return q, k

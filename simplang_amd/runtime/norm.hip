@@ -1,0 +1,213 @@
+// norm.hip -- wavefront/block-reduction kernels: rmsnorm, softmax, silu, the
+// SwiGLU gate and RoPE.  Semantics follow the reference lowering loops (paths
+// relative to the SimpLang tree):
+//   rmsnorm  ConvertSimpToMemRef.cpp:2192-2233  rms = sqrt(sum x^2 / n + eps),
+//            out = (x / rms) * w[w_off + i]  (a division, as in the reference)
+//   softmax  ConvertSimpToMemRef.cpp:2264-2316  out = exp(x - max) / sum, offsets on
+//            both arrays
+//   silu     ConvertSimpToMemRef.cpp:2345-2354  out = x / (1 + exp(-x))
+//   swiglu   examples/llama2/stories110M.sl:200-212  out = silu(gate) * up
+//   rope     examples/llama2/stories110M.sl:86-112  adjacent pairs, f = theta^-(i%hs/hs)
+// The reference sums sequentially; here sums are wave/block trees (fp32), which
+// changes rounding only (checked to 1e-4 relative against the oracle).
+#include "rt_device.h"
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+__global__ void __launch_bounds__(1024)
+    rmsnorm_k(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ out,
+              int n, float eps) {
+  __shared__ float scratch[16];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
+  ss = block_sum(ss, scratch);
+  const float rms = sqrtf(ss / (float)n + eps);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] / rms) * w[i];
+}
+
+__global__ void __launch_bounds__(1024)
+    softmax_k(const float *__restrict__ x, float *__restrict__ out, int n) {
+  __shared__ float scratch[16];
+  float mx = -INFINITY;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) mx = fmaxf(mx, x[i]);
+  mx = block_max(mx, scratch);
+  float s = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const float e = expf(x[i] - mx);
+    out[i] = e;
+    s += e;
+  }
+  s = block_sum(s, scratch);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = out[i] / s;
+}
+
+__global__ void __launch_bounds__(256) silu_k(const float *__restrict__ x, float *__restrict__ out,
+                                              int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    out[i] = x[i] / (1.f + expf(-x[i]));
+}
+
+__global__ void __launch_bounds__(256)
+    swiglu_k(const float *__restrict__ gate, const float *__restrict__ up, float *__restrict__ out,
+             int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float g = gate[i];
+    out[i] = (g / (1.f + expf(-g))) * up[i];
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    rope_k(float *__restrict__ q, float *__restrict__ k, int dim, int kv_dim, int hs, int pos,
+           float theta) {
+  const int i = 2 * (blockIdx.x * 256 + threadIdx.x);
+  if (i >= dim) return;
+  const float freq = 1.f / powf(theta, (float)(i % hs) / (float)hs);
+  const float v = (float)pos * freq;
+  const float fcr = cosf(v), fci = sinf(v);
+  const float q0 = q[i], q1 = q[i + 1];
+  q[i] = q0 * fcr - q1 * fci;
+  q[i + 1] = q0 * fci + q1 * fcr;
+  if (i < kv_dim) {
+    const float k0 = k[i], k1 = k[i + 1];
+    k[i] = k0 * fcr - k1 * fci;
+    k[i + 1] = k0 * fci + k1 * fcr;
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  const int64_t b = cdiv(n, 256);
+  const int64_t cap = (int64_t)num_cus() * 8;
+  return (unsigned)(b < cap ? (b > 0 ? b : 1) : cap);
+}
+
+}  // namespace
+
+int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_k, dim3(1), dim3(1024), 0, st, x, w, out, n, eps);
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+}  // namespace simp
+
+using namespace simp;
+
+extern "C" {
+
+int32_t simp_rt_rmsnorm(const float *in_alloc, const float *in, int64_t in_off, int64_t in_size,
+                        int64_t in_stride, const float *w_alloc, const float *w, int64_t w_doff,
+                        int64_t w_size, int64_t w_stride, float *out_alloc, float *out,
+                        int64_t out_off, int64_t out_size, int64_t out_stride, int64_t size,
+                        double epsilon, int64_t weight_offset) {
+  (void)in_alloc; (void)w_alloc; (void)out_alloc;
+  int rc;
+  if ((rc = check_desc1("input", in, in_off, in_size, in_stride))) return rc;
+  if ((rc = check_desc1("weight", w, w_doff, w_size, w_stride))) return rc;
+  if ((rc = check_desc1("output", out, out_off, out_size, out_stride))) return rc;
+  if (size < 0 || weight_offset < 0 || size > in_size || size > out_size ||
+      weight_offset + size > w_size)
+    return set_error(SIMP_RT_EINVAL, "rmsnorm: size %lld / weight_offset %lld out of range",
+                     (long long)size, (long long)weight_offset);
+  if (size == 0) return SIMP_RT_OK;
+  if (size > INT32_MAX) return set_error(SIMP_RT_EUNSUPPORTED, "rmsnorm: size above 2^31-1");
+  Operand oi, ow, oo;
+  if ((rc = oi.bind(in + in_off, 4 * (size_t)size, Operand::kIn, "input"))) return rc;
+  if ((rc = ow.bind(w + w_doff + weight_offset, 4 * (size_t)size, Operand::kIn, "weight"))) return rc;
+  if ((rc = oo.bind(out + out_off, 4 * (size_t)size, Operand::kOut, "output"))) return rc;
+  if ((rc = launch_rmsnorm((const float *)oi.dev(), (const float *)ow.dev(), (float *)oo.dev(),
+                           (int)size, (float)epsilon, cur_stream())))
+    return rc;
+  Operand *ops[] = {&oi, &ow, &oo};
+  return finish(ops, 3);
+}
+
+int32_t simp_rt_softmax(const float *in_alloc, const float *in, int64_t in_doff, int64_t in_size,
+                        int64_t in_stride, float *out_alloc, float *out, int64_t out_doff,
+                        int64_t out_size, int64_t out_stride, int64_t size, int64_t input_offset,
+                        int64_t output_offset) {
+  (void)in_alloc; (void)out_alloc;
+  int rc;
+  if ((rc = check_desc1("input", in, in_doff, in_size, in_stride))) return rc;
+  if ((rc = check_desc1("output", out, out_doff, out_size, out_stride))) return rc;
+  if (size < 0 || input_offset < 0 || output_offset < 0 || input_offset + size > in_size ||
+      output_offset + size > out_size)
+    return set_error(SIMP_RT_EINVAL, "softmax: size/offsets out of range");
+  if (size == 0) return SIMP_RT_OK;
+  if (size > INT32_MAX) return set_error(SIMP_RT_EUNSUPPORTED, "softmax: size above 2^31-1");
+  Operand oi, oo;
+  if ((rc = oi.bind(in + in_doff + input_offset, 4 * (size_t)size, Operand::kIn, "input"))) return rc;
+  if ((rc = oo.bind(out + out_doff + output_offset, 4 * (size_t)size, Operand::kOut, "output"))) return rc;
+  hipLaunchKernelGGL(softmax_k, dim3(1), dim3(1024), 0, cur_stream(), (const float *)oi.dev(),
+                     (float *)oo.dev(), (int)size);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&oi, &oo};
+  return finish(ops, 2);
+}
+
+int32_t simp_rt_silu(const float *in_alloc, const float *in, int64_t in_off, int64_t in_size,
+                     int64_t in_stride, float *out_alloc, float *out, int64_t out_off,
+                     int64_t out_size, int64_t out_stride, int64_t size) {
+  (void)in_alloc; (void)out_alloc;
+  int rc;
+  if ((rc = check_desc1("input", in, in_off, in_size, in_stride))) return rc;
+  if ((rc = check_desc1("output", out, out_off, out_size, out_stride))) return rc;
+  if (size < 0 || size > in_size || size > out_size)
+    return set_error(SIMP_RT_EINVAL, "silu: size %lld out of range", (long long)size);
+  if (size == 0) return SIMP_RT_OK;
+  Operand oi, oo;
+  if ((rc = oi.bind(in + in_off, 4 * (size_t)size, Operand::kIn, "input"))) return rc;
+  if ((rc = oo.bind(out + out_off, 4 * (size_t)size, Operand::kOut, "output"))) return rc;
+  hipLaunchKernelGGL(silu_k, dim3(grid_for(size)), dim3(256), 0, cur_stream(),
+                     (const float *)oi.dev(), (float *)oo.dev(), size);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&oi, &oo};
+  return finish(ops, 2);
+}
+
+int32_t simp_rt_swiglu(const float *g_alloc, const float *gate, int64_t g_off, int64_t g_size,
+                       int64_t g_stride, const float *u_alloc, const float *up, int64_t u_off,
+                       int64_t u_size, int64_t u_stride, float *o_alloc, float *out,
+                       int64_t o_off, int64_t o_size, int64_t o_stride, int64_t size) {
+  (void)g_alloc; (void)u_alloc; (void)o_alloc;
+  int rc;
+  if ((rc = check_desc1("gate", gate, g_off, g_size, g_stride))) return rc;
+  if ((rc = check_desc1("up", up, u_off, u_size, u_stride))) return rc;
+  if ((rc = check_desc1("out", out, o_off, o_size, o_stride))) return rc;
+  if (size < 0 || size > g_size || size > u_size || size > o_size)
+    return set_error(SIMP_RT_EINVAL, "swiglu: size %lld out of range", (long long)size);
+  if (size == 0) return SIMP_RT_OK;
+  Operand og, ou, oo;
+  if ((rc = og.bind(gate + g_off, 4 * (size_t)size, Operand::kIn, "gate"))) return rc;
+  if ((rc = ou.bind(up + u_off, 4 * (size_t)size, Operand::kIn, "up"))) return rc;
+  if ((rc = oo.bind(out + o_off, 4 * (size_t)size, Operand::kOut, "out"))) return rc;
+  hipLaunchKernelGGL(swiglu_k, dim3(grid_for(size)), dim3(256), 0, cur_stream(),
+                     (const float *)og.dev(), (const float *)ou.dev(), (float *)oo.dev(), size);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&og, &ou, &oo};
+  return finish(ops, 3);
+}
+
+int32_t simp_rt_rope(float *q_alloc, float *q, int64_t q_off, int64_t q_size, int64_t q_stride,
+                     float *k_alloc, float *k, int64_t k_off, int64_t k_size, int64_t k_stride,
+                     int64_t dim, int64_t kv_dim, int64_t head_size, int64_t pos, double theta) {
+  (void)q_alloc; (void)k_alloc;
+  int rc;
+  if ((rc = check_desc1("q", q, q_off, q_size, q_stride))) return rc;
+  if ((rc = check_desc1("k", k, k_off, k_size, k_stride))) return rc;
+  if (dim <= 0 || dim % 2 || kv_dim < 0 || kv_dim > dim || head_size <= 0 || pos < 0 ||
+      dim > q_size || kv_dim > k_size || dim > INT32_MAX || pos > INT32_MAX)
+    return set_error(SIMP_RT_EINVAL, "rope: bad dim/kv_dim/head_size/pos");
+  Operand oq, ok;
+  if ((rc = oq.bind(q + q_off, 4 * (size_t)dim, Operand::kInOut, "q"))) return rc;
+  if ((rc = ok.bind(k + k_off, 4 * (size_t)kv_dim, Operand::kInOut, "k"))) return rc;
+  hipLaunchKernelGGL(rope_k, dim3((unsigned)cdiv(dim / 2, 256)), dim3(256), 0, cur_stream(),
+                     (float *)oq.dev(), (float *)ok.dev(), (int)dim, (int)kv_dim, (int)head_size,
+                     (int)pos, (float)theta);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&oq, &ok};
+  return finish(ops, 2);
+}
+
+}  // extern "C"

@@ -80,5 +80,9 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
                int64_t ldx, float *O, int64_t ldo, int M, int N, int K, int gs, hipStream_t st);
 int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X, float *O, int rows,
                int cols, int gs, int64_t off, hipStream_t st);
+int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, hipStream_t st);
+// C = beta*C + A*B (beta 0 or 1), row-major with leading dimensions in elements.
+int launch_matmul_f32(const float *A, int64_t lda, const float *B, int64_t ldb, float *C,
+                      int64_t ldc, int M, int N, int K, float beta, hipStream_t st);
 
 }  // namespace simp

@@ -1,0 +1,178 @@
+"""GPU parity of the fp32 ops (matmul, tensor_matmul f32, rmsnorm, softmax,
+silu, swiglu, rope) against the pinned oracle and the reference's KATs.
+
+Tolerance (BASELINE: fp32 within 1e-4 relative): max|gpu - ref| <= 1e-4 *
+max|ref| per output vector, ref being the oracle (matmuls: float64).
+"""
+import numpy as np
+import pytest
+
+import simplang_amd as sa
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _t(dev, a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _close(got, want, tol=TOL):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want).max() if want.size else 0.0
+    assert err <= tol * max(np.abs(want).max(), 1e-30), (err, np.abs(want).max())
+
+
+# ----------------------------------------------------------------- rmsnorm --
+
+def test_rmsnorm_kat(dev):
+    import torch
+    x = _t(dev, np.array([1, 2, 3, 4], np.float32))
+    w = torch.ones(4, device=dev)
+    out = torch.zeros(4, device=dev)
+    sa.rmsnorm(x, w, out, 4, 1e-5, 0)
+    want = np.float32(1.0) / np.sqrt(np.float32(7.5) + np.float32(1e-5))
+    assert abs(out[0].item() - want) < 1e-4       # test_rmsnorm_host.cpp:34-48
+
+
+@pytest.mark.parametrize("dim", [768, 3200, 8640, 5])
+def test_rmsnorm_vs_oracle(dev, orc, dim):
+    import torch
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal(dim).astype(np.float32)
+    w = rng.standard_normal(3 * dim).astype(np.float32)      # [layers, dim]
+    out = torch.empty(dim, device=dev)
+    sa.rmsnorm(_t(dev, x), _t(dev, w), out, dim, 1e-5, 2 * dim)
+    torch.cuda.synchronize()
+    _close(out.cpu().numpy(), orc.rmsnorm(x, w, 1e-5, 2 * dim))
+
+
+# ----------------------------------------------------------------- softmax --
+
+def test_softmax_kat(dev):
+    import torch
+    out = torch.zeros(4, device=dev)
+    sa.softmax(_t(dev, np.array([1, 2, 3, 4], np.float32)), out, 4)
+    e = np.exp(np.array([-3, -2, -1, 0], np.float64))
+    assert abs(out[0].item() - e[0] / e.sum()) < 1e-4     # test_softmax_host.cpp:34-45
+
+
+@pytest.mark.parametrize("n", [1, 7, 33, 288, 512, 4096])
+def test_softmax_offsets_vs_oracle(dev, orc, n):
+    import torch
+    rng = np.random.default_rng(n)
+    seq, h = 600 if n <= 512 else 4200, 3
+    att = rng.standard_normal(4 * seq).astype(np.float32) * 4   # [n_heads, seq_len]
+    out = torch.full((4 * seq,), -1.0, device=dev)
+    off = h * seq
+    sa.softmax(_t(dev, att), out, n, off, off)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = orc.softmax(att, np.full(4 * seq, -1.0, np.float32), n, off, off)
+    _close(got[off:off + n], want[off:off + n])
+    assert (got[:off] == -1).all() and (got[off + n:] == -1).all()
+    assert abs(got[off:off + n].astype(np.float64).sum() - 1.0) < 1e-5
+
+
+def test_softmax_constant(dev):
+    import torch
+    out = torch.empty(17, device=dev)
+    sa.softmax(torch.full((17,), 2.5, device=dev), out, 17)
+    assert np.allclose(out.cpu().numpy(), 1 / 17, rtol=1e-6)
+
+
+# -------------------------------------------------------------- silu & co --
+
+def test_silu_kat_and_vs_oracle(dev, orc):
+    import torch
+    out = torch.zeros(4, device=dev)
+    sa.silu(_t(dev, np.array([1, 2, -1, 0], np.float32)), out, 4)
+    o = out.cpu().numpy()
+    assert abs(o[0] - 1 / (1 + np.exp(-1.0))) < 1e-4 and o[3] == 0.0  # test_silu_host.cpp
+    x = (np.random.default_rng(0).standard_normal(8640) * 6).astype(np.float32)
+    out = torch.empty(8640, device=dev)
+    sa.silu(_t(dev, x), out, 8640)
+    got = out.cpu().numpy()
+    want = orc.silu(x)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_swiglu_vs_oracle(dev, orc):
+    import torch
+    rng = np.random.default_rng(1)
+    g = rng.standard_normal(2048).astype(np.float32) * 3
+    u = rng.standard_normal(2048).astype(np.float32)
+    out = torch.empty(2048, device=dev)
+    sa.swiglu(_t(dev, g), _t(dev, u), out, 2048)
+    assert np.allclose(out.cpu().numpy(), orc.silu(g) * u, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dim,kv_dim,hs,pos", [(768, 768, 64, 0), (768, 768, 64, 287),
+                                               (3200, 3200, 100, 511), (64, 32, 16, 5)])
+def test_rope_vs_oracle(dev, orc, dim, kv_dim, hs, pos):
+    rng = np.random.default_rng(pos)
+    q = rng.standard_normal(dim).astype(np.float32)
+    k = rng.standard_normal(kv_dim).astype(np.float32)
+    tq, tk = _t(dev, q), _t(dev, k)
+    sa.rope(tq, tk, dim, kv_dim, hs, pos)
+    qo, ko = q.copy(), np.concatenate([k, np.zeros(dim - kv_dim, np.float32)])
+    orc.rope(qo, ko, dim, kv_dim, hs, pos)
+    # fp32 angles as in the reference (float literals are f32, mlir_codegen.cpp:608-626):
+    # a 1-ulp powf difference between device and host libm grows with pos (~500 rad),
+    # so RoPE is held to the BASELINE tolerance, 1e-4.
+    _close(tq.cpu().numpy(), qo)
+    _close(tk.cpu().numpy(), ko[:kv_dim])
+
+
+# -------------------------------------------------------------- f32 matmul --
+
+def test_matmul_kat_110(dev):
+    import torch
+    a = _t(dev, np.arange(1, 11, dtype=np.float32))
+    b = torch.full((10,), 2.0, device=dev)
+    out = torch.zeros(1, device=dev)
+    sa.matmul(a, b, out, 1, 10, 1)
+    assert out.item() == 110.0                    # tests/test_tensor_matmul_runner.cpp:39
+    sa.matmul(a, b, out, 1, 10, 1)
+    assert out.item() == 220.0                    # accumulates (C += A*B)
+
+
+@pytest.mark.parametrize("rows,cols", [(768, 768), (2048, 768), (768, 2048), (32000, 768),
+                                       (100, 37), (5, 4096 + 64)])
+def test_matmul_gemv_layer_offsets(dev, orc, rows, cols):
+    """The decode projections: W[layer] at offset layer*rows*cols, x column, C += W x."""
+    import torch
+    rng = np.random.default_rng(rows + cols)
+    layers = 2 if rows * cols > 10**7 else 3
+    w = (rng.standard_normal(layers * rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    c0 = rng.standard_normal(rows).astype(np.float32)
+    out = _t(dev, c0)
+    off = (layers - 1) * rows * cols
+    sa.matmul(_t(dev, w), _t(dev, x), out, rows, cols, 1, off, 0, 0)
+    torch.cuda.synchronize()
+    want = c0.astype(np.float64) + w[off:off + rows * cols].reshape(rows, cols).astype(np.float64) @ x
+    _close(out.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("m,k,n", [(37, 53, 29), (128, 256, 96), (64, 768, 3)])
+def test_matmul_general_and_tensor_matmul(dev, m, k, n):
+    import torch
+    rng = np.random.default_rng(m * k * n)
+    a = rng.standard_normal(5 + m * k).astype(np.float32)
+    b = rng.standard_normal(2 + k * n).astype(np.float32)
+    c = rng.standard_normal(3 + m * n).astype(np.float32)
+    tc = _t(dev, c)
+    sa.matmul(_t(dev, a), _t(dev, b), tc, m, k, n, 5, 2, 3)
+    want = c[3:].reshape(m, n).astype(np.float64) + \
+        a[5:].reshape(m, k).astype(np.float64) @ b[2:].reshape(k, n)
+    got = tc.cpu().numpy()
+    _close(got[3:].reshape(m, n), want)
+    assert (got[:3] == c[:3]).all()
+    A = _t(dev, a[5:].reshape(m, k))
+    B = _t(dev, b[2:].reshape(k, n))
+    C = torch.full((m, n), float("nan"), device=dev)
+    sa.tensor_matmul_f32(A, B, C)                 # fresh C = A B
+    _close(C.cpu().numpy(), a[5:].reshape(m, k).astype(np.float64) @ b[2:].reshape(k, n))
