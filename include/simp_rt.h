@@ -192,6 +192,56 @@ int32_t simp_rt_rope(
     float *k_alloc, float *k, int64_t k_off, int64_t k_size, int64_t k_stride,
     int64_t dim, int64_t kv_dim, int64_t head_size, int64_t pos, double theta);
 
+/* ------------------------------------------------------- decode step -- */
+
+#define SIMP_RT_W_F32 0 /* fp32 weight matrices */
+#define SIMP_RT_W_W4S 1 /* symmetric W4 (simp_rt_matmul_w4s format) */
+
+/* Shape of the LLaMA programs examples/llama2/stories110M.sl:5-44 and
+ * examples/llama2/llama2_quant.sl:7-56 (their hyperparameter arguments),
+ * plus the weight format. */
+typedef struct {
+  int64_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+  float eps;        /* RMSNorm epsilon (the programs pass 1e-5) */
+  float rope_theta; /* 10000 in the programs */
+  int32_t weight_format;
+  int32_t group_size; /* W4S: weights per scale along K */
+} simp_rt_llama_config;
+
+/* Weights, laid out as the arrays of stories110M_forward: token_embedding
+ * [vocab,dim], rms_att/rms_ffn [n_layers,dim], rms_final [dim], and per
+ * layer wq/wo [dim,dim], wk/wv [kv_dim,dim], w1/w3 [hidden,dim], w2
+ * [dim,hidden], one layer after another, wcls [vocab,dim].  SIMP_RT_W_F32
+ * uses the fp32 pointers; SIMP_RT_W_W4S the packed q_* ([rows, cols/2] per
+ * layer) and scales s_* ([rows, cols/group_size] per layer).  All must be
+ * device memory or registered ranges. */
+typedef struct {
+  const float *token_embedding, *rms_att, *rms_ffn, *rms_final;
+  const float *wq, *wk, *wv, *wo, *w1, *w2, *w3, *wcls;
+  const uint8_t *q_wq, *q_wk, *q_wv, *q_wo, *q_w1, *q_w2, *q_w3, *q_wcls;
+  const float *s_wq, *s_wk, *s_wv, *s_wo, *s_w1, *s_w2, *s_w3, *s_wcls;
+} simp_rt_llama_weights;
+
+typedef struct simp_rt_llama simp_rt_llama;
+
+/* A decode-step engine over the given weights, with its own activations and
+ * fp32 KV cache [n_layers, seq_len, kv_dim] in device memory.  The step is the
+ * single-token forward of stories110M_forward (stories110M.sl:44-247; W4:
+ * llama2_quant_forward, llama2_quant.sl:57-198), fused into 5 kernels per layer. */
+int32_t simp_rt_llama_create(const simp_rt_llama_config *cfg, const simp_rt_llama_weights *w,
+                             simp_rt_llama **model);
+int32_t simp_rt_llama_destroy(simp_rt_llama *model);
+/* One step at (token, pos); logits[vocab] (device or host) receives the output.
+ * Blocks until done.  Replaces one call of stories110M_forward as driven by
+ * examples/llama2/generate_stories110M.cpp:236-257. */
+int32_t simp_rt_llama_forward(simp_rt_llama *model, int64_t token, int64_t pos, float *logits);
+/* Greedy generation (strict-'>' argmax, generate_stories110M.cpp:73-83): runs
+ * the prompt then n_new sampled tokens; out_tokens[n_prompt + n_new] (host)
+ * receives prompt and samples.  use_graph != 0 replays one captured HIP graph
+ * per step with the token/position state kept on the device. */
+int32_t simp_rt_llama_generate(simp_rt_llama *model, const int32_t *prompt, int64_t n_prompt,
+                               int64_t n_new, int32_t *out_tokens, int32_t use_graph);
+
 #ifdef __cplusplus
 }
 #endif

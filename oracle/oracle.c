@@ -361,9 +361,20 @@ static void gemv(const orc_llama_cfg *c, const float *wf, const uint8_t *wq,
                  const float *ws, const float *x, float *y, int64_t rows,
                  int64_t cols) {
   if (c->w4) {
-    orc_matmul_w4s(wq, ws, x, y, 1, rows, cols, c->gs);
+    int64_t ng = cols / c->gs;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+      const uint8_t *row = wq + r * (cols / 2);
+      double acc = 0.0;
+      for (int64_t k = 0; k < cols; k++) {
+        float w = (float)s4_at(row, k) * ws[r * ng + k / c->gs];
+        acc += (double)w * (double)x[k];
+      }
+      y[r] = (float)acc;
+    }
     return;
   }
+#pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; r++) {
     double acc = 0.0;
     for (int64_t j = 0; j < cols; j++) acc += (double)wf[r * cols + j] * (double)x[j];

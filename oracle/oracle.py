@@ -48,6 +48,50 @@ _s("orc_matmul_w4s_f32", [_P, _P, _P, _P, _I, _I, _I, _I, C.c_int])
 _s("orc_rope", [_P, _P, _I, _I, _I, _I, _F])
 _s("orc_argmax", [_P, _I], C.c_int64)
 
+
+class OrcLlamaCfg(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads",
+                                         "vocab", "seq_len")] + [
+        ("eps", C.c_float), ("theta", C.c_float), ("w4", C.c_int64), ("gs", C.c_int64)]
+
+
+_ORC_W = ("emb", "rms_att", "rms_ffn", "rms_final", "wq", "wk", "wv", "wo", "w1", "w2", "w3",
+          "wcls", "q_wq", "q_wk", "q_wv", "q_wo", "q_w1", "q_w2", "q_w3", "q_wcls",
+          "s_wq", "s_wk", "s_wv", "s_wo", "s_w1", "s_w2", "s_w3", "s_wcls")
+
+
+class OrcLlamaWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _ORC_W]
+
+
+_s("orc_llama_forward", [_P, _P, _P, _P, _I, _I, _P])
+
+
+class LlamaOracle:
+    """orc_llama_forward over numpy weights (names as simp_rt_llama_weights;
+    token_embedding -> emb).  Keeps its own KV cache."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = cfg
+        self._w = {k: np.ascontiguousarray(v) for k, v in weights.items()}
+        kv_dim = cfg["dim"] * cfg["n_kv_heads"] // cfg["n_heads"]
+        self.c = OrcLlamaCfg(dim=cfg["dim"], hidden=cfg["hidden_dim"], n_layers=cfg["n_layers"],
+                             n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv_heads"],
+                             vocab=cfg["vocab_size"], seq_len=cfg["seq_len"],
+                             eps=cfg.get("eps", 1e-5), theta=cfg.get("rope_theta", 10000.0),
+                             w4=int(cfg.get("weight_format", 0) == 1), gs=cfg.get("group_size", 32))
+        ptrs = {("emb" if k == "token_embedding" else k): v.ctypes.data for k, v in self._w.items()}
+        self.w = OrcLlamaWeights(**ptrs)
+        n = cfg["n_layers"] * cfg["seq_len"] * kv_dim
+        self.kc = np.zeros(n, np.float32)
+        self.vc = np.zeros(n, np.float32)
+
+    def forward(self, token: int, pos: int):
+        logits = np.empty(self.cfg["vocab_size"], np.float32)
+        _o.orc_llama_forward(C.byref(self.c), C.byref(self.w), self.kc.ctypes.data,
+                             self.vc.ctypes.data, token, pos, logits.ctypes.data)
+        return logits
+
 if ref is not None:
     for n in ("ref_scalar_vpdpbusd", "ref_hw_vpdpbusd"):
         getattr(ref, n).argtypes = [_P, _P, _P, _P]

@@ -26,4 +26,7 @@ from .host import (  # noqa: F401
     silu,
     swiglu,
     rope,
+    Llama,
+    W_F32,
+    W_W4S,
 )

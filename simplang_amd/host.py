@@ -62,6 +62,10 @@ _sig("simp_rt_softmax", _D1 * 2 + [_I, _I, _I])
 _sig("simp_rt_silu", _D1 * 2 + [_I])
 _sig("simp_rt_swiglu", _D1 * 3 + [_I])
 _sig("simp_rt_rope", _D1 * 2 + [_I, _I, _I, _I, C.c_double])
+_sig("simp_rt_llama_create", [_P, _P, _P])
+_sig("simp_rt_llama_destroy", [_P])
+_sig("simp_rt_llama_forward", [_P, _I, _I, _P])
+_sig("simp_rt_llama_generate", [_P, _P, _I, _I, _P, C.c_int32])
 _sig("simp_rt_set_stream", [_P])
 _sig("simp_rt_register", [_P, _I, C.c_int32])
 _sig("simp_rt_unregister", [_P])
@@ -230,3 +234,70 @@ def rope(q, k, dim, kv_dim, head_size, pos, theta=10000.0):
     _check("simp_rt_rope", lib.simp_rt_rope(*desc1(q), *desc1(k), dim, kv_dim, head_size, pos,
                                             theta))
     return q, k
+
+
+# ------------------------------------------------------------------ decode
+
+W_F32, W_W4S = 0, 1
+_CFG_INTS = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size", "seq_len")
+_W_NAMES = ("token_embedding", "rms_att", "rms_ffn", "rms_final",
+            "wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls",
+            "q_wq", "q_wk", "q_wv", "q_wo", "q_w1", "q_w2", "q_w3", "q_wcls",
+            "s_wq", "s_wk", "s_wv", "s_wo", "s_w1", "s_w2", "s_w3", "s_wcls")
+
+
+class LlamaConfig(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in _CFG_INTS] + [
+        ("eps", C.c_float), ("rope_theta", C.c_float),
+        ("weight_format", C.c_int32), ("group_size", C.c_int32)]
+
+
+class LlamaWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _W_NAMES]
+
+
+class Llama:
+    """Decode-step engine (simp_rt_llama_*) over device-resident weights.
+
+    ``cfg``: dict with the keys of simp_rt_llama_config; ``weights``: dict of
+    device tensors named as simp_rt_llama_weights (kept alive here)."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = dict(cfg)
+        self._w = dict(weights)
+        c = LlamaConfig(**{k: int(cfg[k]) for k in _CFG_INTS},
+                        eps=float(cfg.get("eps", 1e-5)),
+                        rope_theta=float(cfg.get("rope_theta", 10000.0)),
+                        weight_format=int(cfg.get("weight_format", W_F32)),
+                        group_size=int(cfg.get("group_size", 32)))
+        w = LlamaWeights(**{k: (v.data_ptr() if hasattr(v, "data_ptr") else v)
+                            for k, v in weights.items()})
+        h = C.c_void_p()
+        _check("simp_rt_llama_create", lib.simp_rt_llama_create(C.byref(c), C.byref(w), C.byref(h)))
+        self._h = h
+
+    def forward(self, token: int, pos: int, logits):
+        """One step; logits (device tensor or numpy float32[vocab]) receives the output."""
+        p = logits.data_ptr() if hasattr(logits, "data_ptr") else logits.ctypes.data
+        _check("simp_rt_llama_forward", lib.simp_rt_llama_forward(self._h, token, pos, p))
+        return logits
+
+    def generate(self, prompt, n_new: int, use_graph: bool = True):
+        import numpy as np
+        pr = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(len(pr) + n_new, np.int32)
+        _check("simp_rt_llama_generate",
+               lib.simp_rt_llama_generate(self._h, pr.ctypes.data, len(pr), n_new,
+                                          out.ctypes.data, int(use_graph)))
+        return out
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.simp_rt_llama_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,669 @@
+// decode.hip -- single-token LLaMA decode step and greedy generation.
+//
+// The step is the one of examples/llama2/stories110M.sl:44-247 (fp32 weights)
+// and examples/llama2/llama2_quant.sl:57-198 (W4 weights), shape-parametric
+// (both reference programs hard-code their dims), with the GQA head map of
+// llama2_quant.sl:98, score scale 1/sqrt(head_size) (stories110M.sl:140 writes
+// /8.0, which is the same for head_size 64), RoPE as in stories110M.sl:86-112
+// (llama2_quant.sl omits it) and greedy strict-'>' argmax
+// (examples/llama2/generate_stories110M.cpp:73-83).
+//
+// Per layer the reference issues ~12 loops/ops; here they are 5 kernels:
+//   1 QKV GEMV (Wq|Wk|Wv as one launch) with the attention RMSNorm computed in
+//     the prologue of every block (x is dim floats; recomputing it is cheaper
+//     than a launch)
+//   2 attention, one block per head: RoPE of q and of the head's k, store of
+//     k,v into the KV cache at pos, scores, softmax, weighted sum of V
+//   3 Wo GEMV accumulating into x (the residual add)
+//   4 W1|W3 GEMV with the FFN RMSNorm in the prologue
+//   5 W2 GEMV with silu(h1)*h3 formed in the prologue, accumulating into x
+// then a final RMSNorm+classifier GEMV and an argmax kernel that also advances
+// the step state (token, pos) on the device, so a captured step graph can be
+// replayed for every token with no host round trip.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "rt_device.h"
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+constexpr int kMaxSeg = 3;
+
+enum Prologue { kPlain = 0, kRmsNorm = 1, kSwiGLU = 2 };
+
+struct Seg {
+  const void *W;    // fp32 rows [rows, K] or packed W4 rows [rows, K/2]
+  const float *S;   // W4 scales [rows, K/gs] (unused for fp32)
+  float *out;       // [rows]
+  int rows;
+  int tile0;        // first row tile of this segment (W4 kernel)
+};
+struct Segs {
+  Seg s[kMaxSeg];
+  int n;
+};
+
+// Step state on the device: [0] token, [1] pos, [2] n_prompt, [3] n_total.
+struct StepState {
+  int token, pos, n_prompt, n_total;
+};
+
+// Stages the GEMV input (K floats) into LDS, applying the prologue.
+template <int PRO>
+__device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x0,
+                                        const float *__restrict__ x1,
+                                        const float *__restrict__ nw, int K, float eps,
+                                        float *scratch) {
+  if constexpr (PRO == kRmsNorm) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) ss = fmaf(x0[i], x0[i], ss);
+    ss = block_sum(ss, scratch);
+    const float rms = sqrtf(ss / (float)K + eps);
+    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = (x0[i] / rms) * nw[i];
+  } else if constexpr (PRO == kSwiGLU) {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+      const float g = x0[i];
+      xs[i] = (g / (1.f + expf(-g))) * x1[i];
+    }
+  } else {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x0[i];
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
+  int i = 0;
+  while (i + 1 < sg.n && row >= sg.s[i].rows) {
+    row -= sg.s[i].rows;
+    i++;
+  }
+  return sg.s[i];
+}
+
+// fp32 multi-matrix GEMV: one wave per row, lanes along K (float4), x in LDS.
+template <int PRO, bool ACC>
+__global__ void __launch_bounds__(256)
+    dgemv_f32(Segs sg, int total_rows, int K, const float *__restrict__ x0,
+              const float *__restrict__ x1, const float *__restrict__ nw, float eps) {
+  extern __shared__ float xs[];
+  __shared__ float scratch[16];
+  stage_x<PRO>(xs, x0, x1, nw, K, eps, scratch);
+  const int lane = threadIdx.x & 63;
+  const int nw_total = gridDim.x * 4;
+  const int K4 = K >> 2;
+  for (int r = blockIdx.x * 4 + (threadIdx.x >> 6); r < total_rows; r += nw_total) {
+    int row = r;
+    const Seg &sgm = seg_of_row(sg, row);
+    const float4 *w = (const float4 *)((const float *)sgm.W + (int64_t)row * K);
+    float s = 0.f;
+    for (int j = lane; j < K4; j += 64) {
+      const float4 a = w[j];
+      const float4 b = *(const float4 *)(xs + 4 * j);
+      s = fmaf(a.x, b.x, s);
+      s = fmaf(a.y, b.y, s);
+      s = fmaf(a.z, b.z, s);
+      s = fmaf(a.w, b.w, s);
+    }
+    s = wave_sum(s);
+    if (lane == 0) sgm.out[row] = ACC ? sgm.out[row] + s : s;
+  }
+}
+
+__device__ __forceinline__ float ubyte0(uint32_t x) { float r; asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x)); return r; }
+__device__ __forceinline__ float ubyte1(uint32_t x) { float r; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x)); return r; }
+__device__ __forceinline__ float ubyte2(uint32_t x) { float r; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x)); return r; }
+__device__ __forceinline__ float ubyte3(uint32_t x) { float r; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x)); return r; }
+
+// W4 (symmetric, group gs) multi-matrix GEMV; same lane -> row mapping as the
+// standalone W4 kernel (8 rows per block, 32 chunk groups), x staged in LDS
+// with the prologue applied and chunk-rotated, per-chunk sums of x in LDS.
+template <int PRO, bool ACC, int UB>
+__global__ void __launch_bounds__(256)
+    dgemv_w4(Segs sg, int K, int gs, const float *__restrict__ x0, const float *__restrict__ x1,
+             const float *__restrict__ nw, float eps) {
+  constexpr int RB = 8, G = 256 / RB;
+  extern __shared__ float sm[];
+  __shared__ float scratch[16];
+  __shared__ float red[4][RB];
+  const int nchunk = K >> 5;
+  float *xl = sm, *xsum = sm + K;
+  // prologue, written chunk-rotated: element 32c + j goes to float4 slot ((j/4 + c) % 8)
+  if constexpr (PRO == kRmsNorm) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(x0[i], x0[i], ss);
+    ss = block_sum(ss, scratch);
+    const float rms = sqrtf(ss / (float)K + eps);
+    for (int i = threadIdx.x; i < K; i += 256) {
+      const int c = i >> 5, j = i & 31;
+      xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = (x0[i] / rms) * nw[i];
+    }
+  } else {
+    for (int i = threadIdx.x; i < K; i += 256) {
+      const int c = i >> 5, j = i & 31;
+      float v = x0[i];
+      if constexpr (PRO == kSwiGLU) v = (v / (1.f + expf(-v))) * x1[i];
+      xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = v;
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < nchunk; c += 256) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const float4 v = *(const float4 *)(xl + 32 * c + 4 * q);
+      t += (v.x + v.y) + (v.z + v.w);
+    }
+    xsum[c] = t;
+  }
+  __syncthreads();
+  // which segment / row tile
+  int si = 0;
+  while (si + 1 < sg.n && (int)blockIdx.x >= sg.s[si + 1].tile0) si++;
+  const Seg &sgm = sg.s[si];
+  const int row0 = ((int)blockIdx.x - sgm.tile0) * RB;
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
+  const int n = min(row0 + r, sgm.rows - 1);
+  const uint8_t *wrow = (const uint8_t *)sgm.W + (int64_t)n * (K >> 1);
+  const float *srow = sgm.S + (int64_t)n * (K / gs);
+  const int cpg = gs >> 5;
+  float acc = 0.f;
+  for (int c0 = g; c0 < nchunk; c0 += G * UB) {
+    uint4 w[UB];
+    float sc[UB];
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = min(c0 + u * G, nchunk - 1);
+      w[u] = *(const uint4 *)(wrow + 16 * c);
+      sc[u] = srow[c / cpg];
+    }
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = c0 + u * G;
+      if (c < nchunk) {
+        const uint32_t d[4] = {w[u].x ^ 0x88888888u, w[u].y ^ 0x88888888u, w[u].z ^ 0x88888888u,
+                               w[u].w ^ 0x88888888u};
+        float p = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint32_t lo = d[q] & 0x0F0F0F0Fu, hi = (d[q] >> 4) & 0x0F0F0F0Fu;
+          const float4 a = *(const float4 *)(xl + 32 * c + 4 * (((2 * q) + c) & 7));
+          const float4 b = *(const float4 *)(xl + 32 * c + 4 * (((2 * q + 1) + c) & 7));
+          p = fmaf(ubyte0(lo), a.x, p);
+          p = fmaf(ubyte0(hi), a.y, p);
+          p = fmaf(ubyte1(lo), a.z, p);
+          p = fmaf(ubyte1(hi), a.w, p);
+          p = fmaf(ubyte2(lo), b.x, p);
+          p = fmaf(ubyte2(hi), b.y, p);
+          p = fmaf(ubyte3(lo), b.z, p);
+          p = fmaf(ubyte3(hi), b.w, p);
+        }
+        acc = fmaf(sc[u], fmaf(-8.f, xsum[c], p), acc);
+      }
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  float v = acc;
+#pragma unroll
+  for (int dd = RB; dd < 64; dd <<= 1) v += __shfl_xor(v, dd);
+  if ((threadIdx.x & 63) < RB) red[wave][r] = v;
+  __syncthreads();
+  if (threadIdx.x < RB && row0 + (int)threadIdx.x < sgm.rows) {
+    const float t = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+    float *o = sgm.out + row0 + r;
+    *o = ACC ? *o + t : t;
+  }
+}
+
+// One block per head.  qkv = [q(dim) | k(kv_dim) | v(kv_dim)] of this layer,
+// kc/vc the layer's caches [seq_len, kv_dim], out = xb[dim].
+__global__ void __launch_bounds__(256)
+    attn_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
+           float *__restrict__ out, const StepState *__restrict__ st, int dim, int kv_dim,
+           int n_heads, int n_kv_heads, int hs, float theta) {
+  extern __shared__ float sm[];           // q[hs], knew[hs], vnew[hs], att[pos+1], part[...]
+  __shared__ float scratch[16];
+  const int h = blockIdx.x;
+  const int pos = st->pos;
+  const int kvh = h * n_kv_heads / n_heads;
+  float *qs = sm, *kn = sm + hs, *vn = sm + 2 * hs, *att = sm + 3 * hs;
+  const float *q = qkv + h * hs;
+  const float *k = qkv + dim + kvh * hs;
+  const float *v = qkv + dim + kv_dim + kvh * hs;
+  // RoPE on adjacent pairs; the pair index within the head gives the frequency
+  for (int j = 2 * threadIdx.x; j < hs; j += 2 * blockDim.x) {
+    const float freq = 1.f / powf(theta, (float)j / (float)hs);
+    const float a = (float)pos * freq;
+    const float fcr = cosf(a), fci = sinf(a);
+    qs[j] = q[j] * fcr - q[j + 1] * fci;
+    qs[j + 1] = q[j] * fci + q[j + 1] * fcr;
+    kn[j] = k[j] * fcr - k[j + 1] * fci;
+    kn[j + 1] = k[j] * fci + k[j + 1] * fcr;
+    vn[j] = v[j];
+    vn[j + 1] = v[j + 1];
+  }
+  __syncthreads();
+  const bool writer = h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh;
+  if (writer) {  // first head of this kv head stores the new k, v at pos
+    for (int j = threadIdx.x; j < hs; j += blockDim.x) {
+      kc[(int64_t)pos * kv_dim + kvh * hs + j] = kn[j];
+      vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
+    }
+  }
+  const float scale = sqrtf((float)hs);
+  float mx = -INFINITY;
+  for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
+    float s = 0.f;
+    if (t == pos) {
+      for (int j = 0; j < hs; j++) s = fmaf(qs[j], kn[j], s);
+    } else {
+      const float *kr = kc + (int64_t)t * kv_dim + kvh * hs;
+      for (int j = 0; j < hs; j++) s = fmaf(qs[j], kr[j], s);
+    }
+    s = s / scale;
+    att[t] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = block_max(mx, scratch);
+  float sum = 0.f;
+  for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
+    const float e = expf(att[t] - mx);
+    att[t] = e;
+    sum += e;
+  }
+  sum = block_sum(sum, scratch);  // ends with barriers: att[] complete
+  // weighted sum of V: thread (j, tp) sums t = tp, tp + P, ... for dim j
+  const int P = blockDim.x / hs > 0 ? blockDim.x / hs : 1;
+  float *part = att + (pos + 1);
+  const int j = threadIdx.x % hs, tp = threadIdx.x / hs;
+  float acc = 0.f;
+  if (tp < P) {
+    for (int t = tp; t <= pos; t += P) {
+      const float vv = (t == pos) ? vn[j] : vc[(int64_t)t * kv_dim + kvh * hs + j];
+      acc = fmaf(att[t], vv, acc);
+    }
+    part[tp * hs + j] = acc;
+  }
+  __syncthreads();
+  for (int jj = threadIdx.x; jj < hs; jj += blockDim.x) {
+    float t = 0.f;
+    for (int p = 0; p < P; p++) t += part[p * hs + jj];
+    out[h * hs + jj] = t / sum;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    embed_k(const float *__restrict__ emb, float *__restrict__ x, const StepState *__restrict__ st,
+            int dim) {
+  const int64_t tok = st->token;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) x[i] = emb[tok * dim + i];
+}
+
+// Greedy argmax (first maximum wins) and step advance:
+//   out_tokens[pos+1] = next = (pos+1 < n_prompt) ? prompt[pos+1] : argmax(logits)
+__global__ void __launch_bounds__(1024)
+    argmax_advance_k(const float *__restrict__ logits, int vocab, StepState *st,
+                     const int *__restrict__ prompt, int *__restrict__ out_tokens) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+    const float v = logits[i];
+    if (v > best) { best = v; idx = i; }  // strictly greater: first max per thread
+  }
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ov = __shfl_xor(best, d);
+    const int oi = __shfl_xor(idx, d);
+    if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b0 = bv[0];
+    int i0 = bi[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+      if (bv[w] > b0 || (bv[w] == b0 && bi[w] < i0)) { b0 = bv[w]; i0 = bi[w]; }
+    const int p = st->pos + 1;
+    const int next = (p < st->n_prompt) ? prompt[p] : i0;
+    if (p < st->n_total) out_tokens[p] = next;
+    st->token = next;
+    st->pos = p;
+  }
+}
+
+}  // namespace
+
+struct LlamaModel {
+  simp_rt_llama_config cfg;
+  simp_rt_llama_weights w;
+  int kv_dim, hs;
+  int device;
+  hipStream_t stream = nullptr;
+  // device buffers
+  float *x = nullptr, *xb = nullptr, *qkv = nullptr, *h13 = nullptr, *logits = nullptr;
+  float *kcache = nullptr, *vcache = nullptr;
+  StepState *state = nullptr;
+  int *prompt = nullptr, *tokens = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+int gemv(LlamaModel &m, Segs sg, int K, int pro, bool acc, const float *x0, const float *x1,
+         const float *nw) {
+  const float eps = m.cfg.eps;
+  hipStream_t st = m.stream;
+  if (m.cfg.weight_format == SIMP_RT_W_F32) {
+    int total = 0;
+    for (int i = 0; i < sg.n; i++) total += sg.s[i].rows;
+    const unsigned grid = (unsigned)std::min<int64_t>(cdiv(total, 4), (int64_t)num_cus() * 8);
+    const size_t shm = sizeof(float) * (size_t)K;
+#define DG(P, A) hipLaunchKernelGGL((dgemv_f32<P, A>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, x1, nw, eps)
+    if (pro == kRmsNorm) { if (acc) DG(kRmsNorm, true); else DG(kRmsNorm, false); }
+    else if (pro == kSwiGLU) { if (acc) DG(kSwiGLU, true); else DG(kSwiGLU, false); }
+    else { if (acc) DG(kPlain, true); else DG(kPlain, false); }
+#undef DG
+  } else {
+    int tiles = 0;
+    for (int i = 0; i < sg.n; i++) {
+      sg.s[i].tile0 = tiles;
+      tiles += (int)cdiv(sg.s[i].rows, 8);
+    }
+    const size_t shm = sizeof(float) * ((size_t)K + (size_t)K / 32);
+    const int gs = m.cfg.group_size;
+#define DW(P, A)                                                                          \
+  do {                                                                                    \
+    if (K / 32 <= 128)                                                                    \
+      hipLaunchKernelGGL((dgemv_w4<P, A, 4>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
+    else                                                                                  \
+      hipLaunchKernelGGL((dgemv_w4<P, A, 8>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
+  } while (0)
+    if (pro == kRmsNorm) { if (acc) DW(kRmsNorm, true); else DW(kRmsNorm, false); }
+    else if (pro == kSwiGLU) { if (acc) DW(kSwiGLU, true); else DW(kSwiGLU, false); }
+    else { if (acc) DW(kPlain, true); else DW(kPlain, false); }
+#undef DW
+  }
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+Seg seg_f32(const float *W, float *out, int rows) { return Seg{W, nullptr, out, rows, 0}; }
+Seg seg_w4(const uint8_t *W, const float *S, float *out, int rows) { return Seg{W, S, out, rows, 0}; }
+
+// Enqueues one decode step (token and pos read from the device state).
+int enqueue_step(LlamaModel &m) {
+  const auto &c = m.cfg;
+  const int dim = (int)c.dim, hid = (int)c.hidden_dim, kv = m.kv_dim, hs = m.hs;
+  const int L = (int)c.n_layers, gs = c.group_size;
+  const bool w4 = c.weight_format == SIMP_RT_W_W4S;
+  hipStream_t st = m.stream;
+  int rc;
+  hipLaunchKernelGGL(embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st,
+                     m.w.token_embedding, m.x, m.state, dim);
+  SIMP_HIP(hipGetLastError());
+  float *q = m.qkv, *k = m.qkv + dim, *v = m.qkv + dim + kv;
+  float *h1 = m.h13, *h3 = m.h13 + hid;
+  for (int l = 0; l < L; l++) {
+    const int64_t lq = (int64_t)l * dim * dim, lk = (int64_t)l * kv * dim;
+    const int64_t lf = (int64_t)l * hid * dim;
+    Segs s{};
+    // 1. QKV with the attention RMSNorm
+    if (w4) {
+      s.s[0] = seg_w4(m.w.q_wq + lq / 2, m.w.s_wq + lq / gs, q, dim);
+      s.s[1] = seg_w4(m.w.q_wk + lk / 2, m.w.s_wk + lk / gs, k, kv);
+      s.s[2] = seg_w4(m.w.q_wv + lk / 2, m.w.s_wv + lk / gs, v, kv);
+    } else {
+      s.s[0] = seg_f32(m.w.wq + lq, q, dim);
+      s.s[1] = seg_f32(m.w.wk + lk, k, kv);
+      s.s[2] = seg_f32(m.w.wv + lk, v, kv);
+    }
+    s.n = 3;
+    if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_att + (int64_t)l * dim))) return rc;
+    // 2. attention (RoPE, cache store at pos, softmax, V sum)
+    float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
+    const int P = std::max(1, 256 / hs);
+    const size_t shm = sizeof(float) * (3 * (size_t)hs + (size_t)c.seq_len + (size_t)P * hs);
+    hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(256), shm, st, m.qkv, kc, vc, m.xb,
+                       m.state, dim, kv, (int)c.n_heads, (int)c.n_kv_heads, hs, c.rope_theta);
+    SIMP_HIP(hipGetLastError());
+    // 3. Wo, accumulated into x (residual)
+    s = Segs{};
+    s.s[0] = w4 ? seg_w4(m.w.q_wo + lq / 2, m.w.s_wo + lq / gs, m.x, dim) : seg_f32(m.w.wo + lq, m.x, dim);
+    s.n = 1;
+    if ((rc = gemv(m, s, dim, kPlain, true, m.xb, nullptr, nullptr))) return rc;
+    // 4. W1 | W3 with the FFN RMSNorm
+    s = Segs{};
+    if (w4) {
+      s.s[0] = seg_w4(m.w.q_w1 + lf / 2, m.w.s_w1 + lf / gs, h1, hid);
+      s.s[1] = seg_w4(m.w.q_w3 + lf / 2, m.w.s_w3 + lf / gs, h3, hid);
+    } else {
+      s.s[0] = seg_f32(m.w.w1 + lf, h1, hid);
+      s.s[1] = seg_f32(m.w.w3 + lf, h3, hid);
+    }
+    s.n = 2;
+    if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_ffn + (int64_t)l * dim))) return rc;
+    // 5. W2 on silu(h1) * h3, accumulated into x
+    s = Segs{};
+    s.s[0] = w4 ? seg_w4(m.w.q_w2 + lf / 2, m.w.s_w2 + lf / gs, m.x, dim) : seg_f32(m.w.w2 + lf, m.x, dim);
+    s.n = 1;
+    if ((rc = gemv(m, s, hid, kSwiGLU, true, h1, h3, nullptr))) return rc;
+  }
+  // final RMSNorm + classifier
+  Segs s{};
+  s.s[0] = w4 ? seg_w4(m.w.q_wcls, m.w.s_wcls, m.logits, (int)c.vocab_size)
+              : seg_f32(m.w.wcls, m.logits, (int)c.vocab_size);
+  s.n = 1;
+  if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_final))) return rc;
+  hipLaunchKernelGGL(argmax_advance_k, dim3(1), dim3(1024), 0, st, m.logits, (int)c.vocab_size,
+                     m.state, m.prompt, m.tokens);
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+int check_cfg(const simp_rt_llama_config &c) {
+  if (c.dim <= 0 || c.hidden_dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 ||
+      c.n_kv_heads <= 0 || c.vocab_size <= 0 || c.seq_len <= 0)
+    return set_error(SIMP_RT_EINVAL, "llama: non-positive dimension in config");
+  if (c.dim % c.n_heads || c.n_heads % c.n_kv_heads || (c.dim / c.n_heads) % 2)
+    return set_error(SIMP_RT_EINVAL, "llama: dim must split into even-sized heads, n_heads into kv heads");
+  if (c.dim % 4 || c.hidden_dim % 4)
+    return set_error(SIMP_RT_EINVAL, "llama: dim and hidden_dim must be multiples of 4");
+  if (c.weight_format == SIMP_RT_W_W4S) {
+    const int gs = c.group_size;
+    const int64_t kv = c.dim * c.n_kv_heads / c.n_heads;
+    if (gs <= 0 || gs % 32 || c.dim % gs || c.hidden_dim % gs)
+      return set_error(SIMP_RT_EINVAL, "llama W4: group_size must be a multiple of 32 dividing dim and hidden_dim");
+    (void)kv;
+  } else if (c.weight_format != SIMP_RT_W_F32) {
+    return set_error(SIMP_RT_EINVAL, "llama: unknown weight_format %d", c.weight_format);
+  }
+  const int64_t hs = c.dim / c.n_heads;
+  if (hs > 256) return set_error(SIMP_RT_EUNSUPPORTED, "llama: head_size above 256");
+  const size_t attn_lds = sizeof(float) * (3 * hs + c.seq_len + std::max<int64_t>(1, 256 / hs) * hs);
+  if (attn_lds > 64 * 1024)
+    return set_error(SIMP_RT_EUNSUPPORTED, "llama: seq_len %lld too long for the attention kernel",
+                     (long long)c.seq_len);
+  if (sizeof(float) * (size_t)(std::max(c.dim, c.hidden_dim) * 33 / 32) > 64 * 1024)
+    return set_error(SIMP_RT_EUNSUPPORTED, "llama: hidden_dim too large for the GEMV prologue");
+  return SIMP_RT_OK;
+}
+
+}  // namespace
+}  // namespace simp
+
+using namespace simp;
+
+extern "C" {
+
+int32_t simp_rt_llama_create(const simp_rt_llama_config *cfg, const simp_rt_llama_weights *w,
+                             simp_rt_llama **out) {
+  if (!cfg || !w || !out) return set_error(SIMP_RT_EINVAL, "llama_create: null argument");
+  *out = nullptr;
+  int rc;
+  if ((rc = check_cfg(*cfg))) return rc;
+  const bool w4 = cfg->weight_format == SIMP_RT_W_W4S;
+  const void *need[] = {w->token_embedding, w->rms_att, w->rms_ffn, w->rms_final,
+                        w4 ? (const void *)w->q_wq : (const void *)w->wq,
+                        w4 ? (const void *)w->q_wk : (const void *)w->wk,
+                        w4 ? (const void *)w->q_wv : (const void *)w->wv,
+                        w4 ? (const void *)w->q_wo : (const void *)w->wo,
+                        w4 ? (const void *)w->q_w1 : (const void *)w->w1,
+                        w4 ? (const void *)w->q_w2 : (const void *)w->w2,
+                        w4 ? (const void *)w->q_w3 : (const void *)w->w3,
+                        w4 ? (const void *)w->q_wcls : (const void *)w->wcls};
+  for (const void *p : need)
+    if (!p) return set_error(SIMP_RT_EINVAL, "llama_create: missing weight pointer");
+  if (w4 && (!w->s_wq || !w->s_wk || !w->s_wv || !w->s_wo || !w->s_w1 || !w->s_w2 || !w->s_w3 ||
+             !w->s_wcls))
+    return set_error(SIMP_RT_EINVAL, "llama_create: missing W4 scales pointer");
+  // every weight must already be device-resident (device memory or a registered range)
+  const int64_t dim = cfg->dim, hid = cfg->hidden_dim, L = cfg->n_layers, V = cfg->vocab_size;
+  const int64_t kvd = dim * cfg->n_kv_heads / cfg->n_heads;
+  simp_rt_llama_weights dw = *w;
+  struct Need { const void **p; size_t bytes; const char *name; };
+  std::vector<Need> needs = {
+      {(const void **)&dw.token_embedding, 4 * (size_t)(V * dim), "token_embedding"},
+      {(const void **)&dw.rms_att, 4 * (size_t)(L * dim), "rms_att"},
+      {(const void **)&dw.rms_ffn, 4 * (size_t)(L * dim), "rms_ffn"},
+      {(const void **)&dw.rms_final, 4 * (size_t)dim, "rms_final"}};
+  const int64_t mats[8][2] = {{dim, dim}, {kvd, dim}, {kvd, dim}, {dim, dim},
+                              {hid, dim}, {dim, hid}, {hid, dim}, {V, dim}};
+  const char *names[8] = {"wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls"};
+  const void **fp[8] = {(const void **)&dw.wq, (const void **)&dw.wk, (const void **)&dw.wv,
+                        (const void **)&dw.wo, (const void **)&dw.w1, (const void **)&dw.w2,
+                        (const void **)&dw.w3, (const void **)&dw.wcls};
+  const void **qp[8] = {(const void **)&dw.q_wq, (const void **)&dw.q_wk, (const void **)&dw.q_wv,
+                        (const void **)&dw.q_wo, (const void **)&dw.q_w1, (const void **)&dw.q_w2,
+                        (const void **)&dw.q_w3, (const void **)&dw.q_wcls};
+  const void **sp[8] = {(const void **)&dw.s_wq, (const void **)&dw.s_wk, (const void **)&dw.s_wv,
+                        (const void **)&dw.s_wo, (const void **)&dw.s_w1, (const void **)&dw.s_w2,
+                        (const void **)&dw.s_w3, (const void **)&dw.s_wcls};
+  for (int i = 0; i < 8; i++) {
+    const int64_t cnt = mats[i][0] * mats[i][1] * (i == 7 ? 1 : L);
+    if (w4) {
+      needs.push_back({qp[i], (size_t)(cnt / 2), names[i]});
+      needs.push_back({sp[i], 4 * (size_t)(cnt / cfg->group_size), names[i]});
+    } else {
+      needs.push_back({fp[i], 4 * (size_t)cnt, names[i]});
+    }
+  }
+  for (auto &nd : needs)
+    if ((rc = device_view(*nd.p, nd.bytes, nd.p, nd.name))) return rc;
+  auto *m = new LlamaModel();
+  m->cfg = *cfg;
+  m->w = dw;
+  m->kv_dim = (int)(cfg->dim * cfg->n_kv_heads / cfg->n_heads);
+  m->hs = (int)(cfg->dim / cfg->n_heads);
+  m->device = ensure_device();
+  m->stream = cur_stream();
+  auto alloc = [&](void **p, size_t bytes) -> int {
+    hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 16));
+    if (e != hipSuccess) return set_error(SIMP_RT_ENOMEM, "llama_create: %s", hipGetErrorString(e));
+    return SIMP_RT_OK;
+  };
+  const size_t kvb = sizeof(float) * (size_t)(cfg->n_layers * cfg->seq_len * m->kv_dim);
+  if ((rc = alloc((void **)&m->x, 4 * cfg->dim)) || (rc = alloc((void **)&m->xb, 4 * cfg->dim)) ||
+      (rc = alloc((void **)&m->qkv, 4 * (cfg->dim + 2 * m->kv_dim))) ||
+      (rc = alloc((void **)&m->h13, 8 * cfg->hidden_dim)) ||
+      (rc = alloc((void **)&m->logits, 4 * cfg->vocab_size)) ||
+      (rc = alloc((void **)&m->kcache, kvb)) || (rc = alloc((void **)&m->vcache, kvb)) ||
+      (rc = alloc((void **)&m->state, sizeof(StepState))) ||
+      (rc = alloc((void **)&m->prompt, 4 * cfg->seq_len)) ||
+      (rc = alloc((void **)&m->tokens, 4 * cfg->seq_len))) {
+    simp_rt_llama_destroy((simp_rt_llama *)m);
+    return rc;
+  }
+  *out = (simp_rt_llama *)m;
+  return SIMP_RT_OK;
+}
+
+int32_t simp_rt_llama_destroy(simp_rt_llama *h) {
+  auto *m = (LlamaModel *)h;
+  if (!m) return SIMP_RT_OK;
+  (void)hipStreamSynchronize(m->stream);
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (void *p : {(void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->h13, (void *)m->logits,
+                  (void *)m->kcache, (void *)m->vcache, (void *)m->state, (void *)m->prompt,
+                  (void *)m->tokens})
+    if (p) (void)hipFree(p);
+  delete m;
+  return SIMP_RT_OK;
+}
+
+int32_t simp_rt_llama_forward(simp_rt_llama *h, int64_t token, int64_t pos, float *logits) {
+  auto *m = (LlamaModel *)h;
+  if (!m) return set_error(SIMP_RT_EINVAL, "llama_forward: null model");
+  if (token < 0 || token >= m->cfg.vocab_size || pos < 0 || pos >= m->cfg.seq_len)
+    return set_error(SIMP_RT_EINVAL, "llama_forward: token %lld / pos %lld out of range",
+                     (long long)token, (long long)pos);
+  m->stream = cur_stream();
+  StepState s{(int)token, (int)pos, 0, 0};
+  SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->stream));
+  int rc = enqueue_step(*m);
+  if (rc) return rc;
+  if (logits) {
+    Operand ol;
+    if ((rc = ol.bind(logits, 4 * (size_t)m->cfg.vocab_size, Operand::kOut, "logits"))) return rc;
+    SIMP_HIP(hipMemcpyAsync(ol.dev(), m->logits, 4 * (size_t)m->cfg.vocab_size,
+                            hipMemcpyDeviceToDevice, m->stream));
+    Operand *ops[] = {&ol};
+    if ((rc = finish(ops, 1))) return rc;
+  }
+  SIMP_HIP(hipStreamSynchronize(m->stream));
+  return SIMP_RT_OK;
+}
+
+int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t n_prompt,
+                               int64_t n_new, int32_t *out_tokens, int32_t use_graph) {
+  auto *m = (LlamaModel *)h;
+  if (!m || !prompt || !out_tokens) return set_error(SIMP_RT_EINVAL, "llama_generate: null argument");
+  if (n_prompt <= 0 || n_new < 0 || n_prompt + n_new > m->cfg.seq_len)
+    return set_error(SIMP_RT_EINVAL, "llama_generate: n_prompt %lld + n_new %lld exceeds seq_len %lld",
+                     (long long)n_prompt, (long long)n_new, (long long)m->cfg.seq_len);
+  for (int64_t i = 0; i < n_prompt; i++)
+    if (prompt[i] < 0 || prompt[i] >= m->cfg.vocab_size)
+      return set_error(SIMP_RT_EINVAL, "llama_generate: prompt token %lld out of range", (long long)i);
+  m->stream = cur_stream();
+  hipStream_t st = m->stream;
+  const int64_t total = n_prompt + n_new;
+  SIMP_HIP(hipMemcpyAsync(m->prompt, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, st));
+  SIMP_HIP(hipMemcpyAsync(m->tokens, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, st));
+  StepState s{prompt[0], 0, (int)n_prompt, (int)total};
+  SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, st));
+  int rc;
+  const int64_t steps = total - 1;  // the last sampled token needs no forward pass
+  if (use_graph) {
+    if (!m->exec) {
+      SIMP_HIP(hipStreamSynchronize(st));
+      hipStream_t cap;
+      SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+      hipStream_t saved = m->stream;
+      m->stream = cap;
+      SIMP_HIP(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal));
+      rc = enqueue_step(*m);
+      hipGraph_t g = nullptr;
+      hipError_t e = hipStreamEndCapture(cap, &g);
+      m->stream = saved;
+      (void)hipStreamDestroy(cap);
+      if (rc) return rc;
+      if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+      m->graph = g;
+      SIMP_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    }
+    for (int64_t i = 0; i < steps; i++) SIMP_HIP(hipGraphLaunch(m->exec, st));
+  } else {
+    for (int64_t i = 0; i < steps; i++)
+      if ((rc = enqueue_step(*m))) return rc;
+  }
+  SIMP_HIP(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, st));
+  SIMP_HIP(hipStreamSynchronize(st));
+  return SIMP_RT_OK;
+}
+
+}  // extern "C"

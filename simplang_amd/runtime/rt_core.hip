@@ -132,6 +132,20 @@ static bool is_device_memory(const void *p) {
   return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
+int device_view(const void *p, size_t bytes, const void **dev, const char *name) {
+  if (!p) return set_error(SIMP_RT_EINVAL, "%s: null pointer", name);
+  if (is_device_memory(p)) {
+    *dev = p;
+    return SIMP_RT_OK;
+  }
+  if (void *m = find_mirror(p, bytes, nullptr)) {
+    *dev = m;
+    return SIMP_RT_OK;
+  }
+  return set_error(SIMP_RT_EINVAL,
+                   "%s: must be device memory or inside a simp_rt_register'd range", name);
+}
+
 Operand::~Operand() {
   if (staged_ && dev_) (void)hipFree(dev_);
 }

@@ -54,6 +54,10 @@ class Operand {
   bool staged_ = false;
 };
 
+// Device address of a caller range that must already be device-resident
+// (device memory, or inside a simp_rt_register'd range); no staging.
+int device_view(const void *p, size_t bytes, const void **dev, const char *name);
+
 // Finishes an entry point: commits staged outputs and, when anything was
 // staged, waits for the stream so host buffers are valid on return.
 int finish(Operand *const *ops, int n);
