@@ -142,6 +142,58 @@ def w4_bench(dev, stream):
     return out
 
 
+def decode_bench(dev, stream, with_cpu=True):
+    """Greedy decode tok/s, BASELINE configs[3] (110M fp32) and configs[4]
+    (3B W4): random-init weights, random prompt of 32 tokens, then 256 / 128
+    greedy tokens, every step one replay of the captured step graph.  tok/s =
+    steps / wall time of the generation (one token per step, prompt steps
+    included, as bench_llama_quant.cpp:255-292 times every forward call)."""
+    import numpy as np
+    import torch
+    import simplang_amd as sa
+    from simplang_amd.llama_synth import CFG_110M, CFG_3B_W4, make_model, weight_bytes, kv_bytes
+    out = []
+    for name, cfg, n_new, cpu_steps in (("llama-110M f32", CFG_110M, 256, 4),
+                                        ("llama-3B W4 g32", CFG_3B_W4, 128, 2)):
+        w = make_model(cfg, dev, seed=42)
+        prompt = np.random.default_rng(42).integers(0, cfg["vocab_size"], 32).astype(np.int32)
+        m = sa.Llama(cfg, w)
+        m.generate(prompt, 8, use_graph=True)            # capture + warm
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        toks = m.generate(prompt, n_new, use_graph=True)
+        el = time.perf_counter() - t0
+        steps = len(prompt) + n_new - 1
+        m.close()
+        byts = np.mean([weight_bytes(cfg) + kv_bytes(cfg, p) for p in range(steps)])
+        rec = {"model": name, "prompt": 32, "generated": n_new, "tok_s": round(steps / el, 1),
+               "ms_per_token": round(el / steps * 1e3, 3),
+               "GBs": round(byts * steps / el / 1e9, 1),
+               "frac_hbm": round(byts * steps / el / 1e9 / HBM_PEAK_GBS, 3),
+               "tokens_head": [int(t) for t in toks[32:40]]}
+        if with_cpu:
+            rec["cpu_baseline"] = decode_cpu(cfg, w, prompt, cpu_steps)
+        out.append(rec)
+        del w
+        torch.cuda.empty_cache()
+    return out
+
+
+def decode_cpu(cfg, w, prompt, steps):
+    """The oracle's restatement of the decode step on the host cores (OpenMP
+    GEMVs, double accumulation), timed over a few steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    wn = {k: v.detach().cpu().numpy() for k, v in w.items()}
+    o = oracle.LlamaOracle(cfg, wn)
+    t0 = time.perf_counter()
+    for p in range(steps):
+        o.forward(int(prompt[p]), p)
+    el = time.perf_counter() - t0
+    return {"tok_s": round(steps / el, 3), "cores": min(os.cpu_count() or 1, 16), "kind": "port",
+            "sample": f"{steps} decode steps of the oracle forward"}
+
+
 def load_traffic(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (committed summary)."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
@@ -159,6 +211,9 @@ def main():
     ap.add_argument("--size", type=int, default=8192)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--only", choices=["gemm", "w4", "decode"], default=None,
+                    help="run one section (for profiling); the JSON line is still printed")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: every configuration of this path fits one "
@@ -174,14 +229,18 @@ def main():
     stream = torch.cuda.current_stream()
     sa.set_stream(stream)
 
+    if args.only is not None:
+        args.no_sweep = args.only != "gemm" or args.no_sweep
+        args.no_decode = args.only != "decode"
     n = args.size
-    a, b, c = make_inputs(n, n, n, dev)
-    torch.cuda.synchronize()
-    ms = gemm_events(sa.matmul_u8s8_i32, a, b, c, args.steps, args.warmup, stream)
-    ops = 2.0 * n * n * n
-    tops = ops / (ms * 1e-3) / 1e12
-    del a, b, c
-    torch.cuda.empty_cache()
+    ms = tops = 0.0
+    if args.only in (None, "gemm"):
+        a, b, c = make_inputs(n, n, n, dev)
+        torch.cuda.synchronize()
+        ms = gemm_events(sa.matmul_u8s8_i32, a, b, c, args.steps, args.warmup, stream)
+        tops = 2.0 * n * n * n / (ms * 1e-3) / 1e12
+        del a, b, c
+        torch.cuda.empty_cache()
 
     sweep = []
     if not args.no_sweep:
@@ -190,8 +249,8 @@ def main():
                                                                    (3200, 8640))]
         for (M, N, K) in shapes:
             a, b, c = make_inputs(M, N, K, dev)
-            reps = 50 if M * N * K < 2**33 else 10
-            t = gemm_events(sa.matmul_u8s8_i32, a, b, c, reps, 3, stream)
+            reps = 20 if M * N * K < 2**33 else 5
+            t = graph_time_ms([lambda: sa.matmul_u8s8_i32(a, b, c)] * reps, stream)
             byts = M * K + K * N + 4 * M * N
             sweep.append({"M": M, "N": N, "K": K, "us": round(t * 1e3, 2),
                           "TOPS": round(2.0 * M * N * K / (t * 1e-3) / 1e12, 2),
@@ -199,9 +258,10 @@ def main():
             del a, b, c
         torch.cuda.empty_cache()
 
-    w4 = [] if args.no_sweep else w4_bench(dev, stream)
+    w4 = w4_bench(dev, stream) if args.only == "w4" or (args.only is None and not args.no_sweep) else []
+    decode = [] if args.no_decode else decode_bench(dev, stream, with_cpu=not args.no_cpu)
 
-    cpu = None if args.no_cpu else cpu_baseline(n)
+    cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baseline(n)
 
     line = {
         "metric": METRIC,
@@ -224,6 +284,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "w4_gemv": w4,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
 

@@ -1,4 +1,4 @@
-"""Random-init LLaMA weights for the decode tests and bench (no checkpoints
+"""Random-init LLaMA weights for the decode engine (tests and bench.py) (no checkpoints
 exist offline; the reference's own hosts use random weights too:
 examples/llama2/test_stories110M.cpp:20-22,122-133, N(0, 0.02) for every array).
 
@@ -51,3 +51,22 @@ def make_model(cfg, device, seed=42):
 
 def to_numpy(w):
     return {k: v.detach().cpu().numpy() for k, v in w.items()}
+
+
+def weight_bytes(cfg):
+    """Bytes of weights one decode step streams (all matrices, the norms and one
+    embedding row), the algorithmic traffic of a step without the KV cache."""
+    mats, vecs = shapes(cfg)
+    n = sum(int(np.prod(s)) for s in mats.values())
+    if cfg.get("weight_format", 0) == 0:
+        b = 4 * n
+    else:
+        b = n // 2 + 4 * n // cfg.get("group_size", 32)
+    d, L = cfg["dim"], cfg["n_layers"]
+    return b + 4 * (2 * L * d + d) + 4 * d
+
+
+def kv_bytes(cfg, pos):
+    """KV-cache bytes the attention of one step at position pos reads and writes."""
+    kv = cfg["dim"] * cfg["n_kv_heads"] // cfg["n_heads"]
+    return 2 * cfg["n_layers"] * (pos + 1) * kv * 4

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import simplang_amd as sa
-from llama_models import CFG_110M, CFG_3B_W4, make_model, to_numpy
+from simplang_amd.llama_synth import CFG_110M, CFG_3B_W4, make_model, to_numpy
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
