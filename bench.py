@@ -95,8 +95,8 @@ def graph_time_ms(calls, stream, replays=5):
     stream.wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        sa.set_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=side):    # same stream as the warm-up: workspaces exist
+        sa.set_stream(side)
         for f in calls:
             f()
     sa.set_stream(stream)

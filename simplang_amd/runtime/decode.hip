@@ -51,28 +51,45 @@ struct StepState {
   int token, pos, n_prompt, n_total;
 };
 
-// Stages the GEMV input (K floats) into LDS, applying the prologue.
-template <int PRO>
-__device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x0,
-                                        const float *__restrict__ x1,
-                                        const float *__restrict__ nw, int K, float eps,
-                                        float *scratch) {
-  if constexpr (PRO == kRmsNorm) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) ss = fmaf(x0[i], x0[i], ss);
-    ss = block_sum(ss, scratch);
-    const float rms = sqrtf(ss / (float)K + eps);
-    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = (x0[i] / rms) * nw[i];
-  } else if constexpr (PRO == kSwiGLU) {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) {
-      const float g = x0[i];
-      xs[i] = (g / (1.f + expf(-g))) * x1[i];
+// GEMV input staging in two phases, so that the input loads can be issued
+// before a kernel's first weight loads (vmcnt retires loads in issue order):
+//   load():   x0 (and x1 or the norm weight) into registers, KP slots per thread
+//   finish(): the prologue math, then the result into LDS (through `put`)
+template <int PRO, int KP>
+struct XStage {
+  float a[KP], b[KP];
+  __device__ __forceinline__ void load(const float *__restrict__ x0, const float *__restrict__ x1,
+                                       const float *__restrict__ nw, int K) {
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+      const int i = threadIdx.x + 256 * k;
+      a[k] = i < K ? x0[i] : 0.f;
+      if constexpr (PRO == kRmsNorm) b[k] = i < K ? nw[i] : 0.f;
+      if constexpr (PRO == kSwiGLU) b[k] = i < K ? x1[i] : 0.f;
     }
-  } else {
-    for (int i = threadIdx.x; i < K; i += blockDim.x) xs[i] = x0[i];
   }
-  __syncthreads();
-}
+  template <class Put>
+  __device__ __forceinline__ void finish(int K, float eps, float *scratch, Put put) {
+    float rms = 1.f;
+    if constexpr (PRO == kRmsNorm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < KP; k++) ss = fmaf(a[k], a[k], ss);
+      ss = block_sum(ss, scratch);
+      rms = sqrtf(ss / (float)K + eps);
+    }
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < K) {
+        float v = a[k];
+        if constexpr (PRO == kRmsNorm) v = (v / rms) * b[k];
+        if constexpr (PRO == kSwiGLU) v = (v / (1.f + expf(-v))) * b[k];
+        put(i, v);
+      }
+    }
+  }
+};
 
 __device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
   int i = 0;
@@ -83,29 +100,67 @@ __device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
   return sg.s[i];
 }
 
-// fp32 multi-matrix GEMV: one wave per row, lanes along K (float4), x in LDS.
-template <int PRO, bool ACC>
+// fp32 multi-matrix GEMV: one wave per row, lanes along K (float4 slots
+// j*64 + lane, J per lane), x in LDS.  The wave's first row is loaded before
+// the prologue and every next row while the current one is reduced, so the
+// prologue and the reductions overlap weight traffic.  J == 0: any K (loop).
+template <int PRO, bool ACC, int J, int KP>
 __global__ void __launch_bounds__(256)
     dgemv_f32(Segs sg, int total_rows, int K, const float *__restrict__ x0,
               const float *__restrict__ x1, const float *__restrict__ nw, float eps) {
   extern __shared__ float xs[];
   __shared__ float scratch[16];
-  stage_x<PRO>(xs, x0, x1, nw, K, eps, scratch);
   const int lane = threadIdx.x & 63;
   const int nw_total = gridDim.x * 4;
   const int K4 = K >> 2;
-  for (int r = blockIdx.x * 4 + (threadIdx.x >> 6); r < total_rows; r += nw_total) {
-    int row = r;
+  int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int JJ = J > 0 ? J : 1;
+  float4 a[JJ];
+  auto load = [&](int rr, float4 (&v)[JJ]) {
+    int row = rr;
     const Seg &sgm = seg_of_row(sg, row);
     const float4 *w = (const float4 *)((const float *)sgm.W + (int64_t)row * K);
+#pragma unroll
+    for (int j = 0; j < JJ; j++) {
+      const int q = lane + 64 * j;
+      v[j] = q < K4 ? w[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  XStage<PRO, KP> xst;
+  xst.load(x0, x1, nw, K);                     // input loads first ...
+  if (J > 0 && r < total_rows) load(r, a);     // ... then the first row's weights
+  xst.finish(K, eps, scratch, [&](int i, float v) { xs[i] = v; });
+  __syncthreads();
+  for (; r < total_rows; r += nw_total) {
+    int row = r;
+    const Seg &sgm = seg_of_row(sg, row);
     float s = 0.f;
-    for (int j = lane; j < K4; j += 64) {
-      const float4 a = w[j];
-      const float4 b = *(const float4 *)(xs + 4 * j);
-      s = fmaf(a.x, b.x, s);
-      s = fmaf(a.y, b.y, s);
-      s = fmaf(a.z, b.z, s);
-      s = fmaf(a.w, b.w, s);
+    if constexpr (J > 0) {
+      float4 b[JJ];
+      if (r + nw_total < total_rows) load(r + nw_total, b);
+#pragma unroll
+      for (int j = 0; j < JJ; j++) {
+        const int q = lane + 64 * j;
+        if (q < K4) {
+          const float4 xv = *(const float4 *)(xs + 4 * q);
+          s = fmaf(a[j].x, xv.x, s);
+          s = fmaf(a[j].y, xv.y, s);
+          s = fmaf(a[j].z, xv.z, s);
+          s = fmaf(a[j].w, xv.w, s);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < JJ; j++) a[j] = b[j];
+    } else {
+      const float4 *w = (const float4 *)((const float *)sgm.W + (int64_t)row * K);
+      for (int q = lane; q < K4; q += 64) {
+        const float4 av = w[q];
+        const float4 xv = *(const float4 *)(xs + 4 * q);
+        s = fmaf(av.x, xv.x, s);
+        s = fmaf(av.y, xv.y, s);
+        s = fmaf(av.z, xv.z, s);
+        s = fmaf(av.w, xv.w, s);
+      }
     }
     s = wave_sum(s);
     if (lane == 0) sgm.out[row] = ACC ? sgm.out[row] + s : s;
@@ -120,7 +175,7 @@ __device__ __forceinline__ float ubyte3(uint32_t x) { float r; asm("v_cvt_f32_ub
 // W4 (symmetric, group gs) multi-matrix GEMV; same lane -> row mapping as the
 // standalone W4 kernel (8 rows per block, 32 chunk groups), x staged in LDS
 // with the prologue applied and chunk-rotated, per-chunk sums of x in LDS.
-template <int PRO, bool ACC, int UB>
+template <int PRO, bool ACC, int UB, int KP>
 __global__ void __launch_bounds__(256)
     dgemv_w4(Segs sg, int K, int gs, const float *__restrict__ x0, const float *__restrict__ x1,
              const float *__restrict__ nw, float eps) {
@@ -130,24 +185,34 @@ __global__ void __launch_bounds__(256)
   __shared__ float red[4][RB];
   const int nchunk = K >> 5;
   float *xl = sm, *xsum = sm + K;
-  // prologue, written chunk-rotated: element 32c + j goes to float4 slot ((j/4 + c) % 8)
-  if constexpr (PRO == kRmsNorm) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += 256) ss = fmaf(x0[i], x0[i], ss);
-    ss = block_sum(ss, scratch);
-    const float rms = sqrtf(ss / (float)K + eps);
-    for (int i = threadIdx.x; i < K; i += 256) {
-      const int c = i >> 5, j = i & 31;
-      xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = (x0[i] / rms) * nw[i];
+  XStage<PRO, KP> xst;
+  xst.load(x0, x1, nw, K);  // input loads first (vmcnt retires in issue order)
+  // this block's segment / row tile and the first batch of its weight loads
+  int si = 0;
+  while (si + 1 < sg.n && (int)blockIdx.x >= sg.s[si + 1].tile0) si++;
+  const Seg &sgm = sg.s[si];
+  const int row0 = ((int)blockIdx.x - sgm.tile0) * RB;
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
+  const int n = min(row0 + r, sgm.rows - 1);
+  const uint8_t *wrow = (const uint8_t *)sgm.W + (int64_t)n * (K >> 1);
+  const float *srow = sgm.S + (int64_t)n * (K / gs);
+  const int cpg = gs >> 5;
+  uint4 w[UB];
+  float sc[UB];
+  auto load_batch = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = min(c0 + u * G, nchunk - 1);
+      w[u] = *(const uint4 *)(wrow + 16 * c);
+      sc[u] = srow[c / cpg];
     }
-  } else {
-    for (int i = threadIdx.x; i < K; i += 256) {
-      const int c = i >> 5, j = i & 31;
-      float v = x0[i];
-      if constexpr (PRO == kSwiGLU) v = (v / (1.f + expf(-v))) * x1[i];
-      xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = v;
-    }
-  }
+  };
+  load_batch(g);
+  // prologue into LDS, chunk-rotated: element 32c + j goes to float4 slot ((j/4 + c) % 8)
+  xst.finish(K, eps, scratch, [&](int i, float v) {
+    const int c = i >> 5, j = i & 31;
+    xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = v;
+  });
   __syncthreads();
   for (int c = threadIdx.x; c < nchunk; c += 256) {
     float t = 0.f;
@@ -159,26 +224,9 @@ __global__ void __launch_bounds__(256)
     xsum[c] = t;
   }
   __syncthreads();
-  // which segment / row tile
-  int si = 0;
-  while (si + 1 < sg.n && (int)blockIdx.x >= sg.s[si + 1].tile0) si++;
-  const Seg &sgm = sg.s[si];
-  const int row0 = ((int)blockIdx.x - sgm.tile0) * RB;
-  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
-  const int n = min(row0 + r, sgm.rows - 1);
-  const uint8_t *wrow = (const uint8_t *)sgm.W + (int64_t)n * (K >> 1);
-  const float *srow = sgm.S + (int64_t)n * (K / gs);
-  const int cpg = gs >> 5;
   float acc = 0.f;
   for (int c0 = g; c0 < nchunk; c0 += G * UB) {
-    uint4 w[UB];
-    float sc[UB];
-#pragma unroll
-    for (int u = 0; u < UB; u++) {
-      const int c = min(c0 + u * G, nchunk - 1);
-      w[u] = *(const uint4 *)(wrow + 16 * c);
-      sc[u] = srow[c / cpg];
-    }
+    if (c0 != g) load_batch(c0);
 #pragma unroll
     for (int u = 0; u < UB; u++) {
       const int c = c0 + u * G;
@@ -218,21 +266,26 @@ __global__ void __launch_bounds__(256)
 }
 
 // One block per head.  qkv = [q(dim) | k(kv_dim) | v(kv_dim)] of this layer,
-// kc/vc the layer's caches [seq_len, kv_dim], out = xb[dim].
+// kc/vc the layer's caches [seq_len, kv_dim], out = xb[dim].  Lanes run along
+// the head dimension (dims d = lane + 64*i, i < DPL), so a cache row is read
+// as one coalesced 4*hs-byte access; the 4 waves split the positions, each
+// wave keeping 4 positions in flight.  Scores use the new k for t == pos (the
+// writer head stores it to the cache for later steps).
 __global__ void __launch_bounds__(256)
     attn_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
            float *__restrict__ out, const StepState *__restrict__ st, int dim, int kv_dim,
            int n_heads, int n_kv_heads, int hs, float theta) {
-  extern __shared__ float sm[];           // q[hs], knew[hs], vnew[hs], att[pos+1], part[...]
+  constexpr int DPL = 4;                   // dims per lane, hs <= 256
+  extern __shared__ float sm[];            // q[hs], knew[hs], vnew[hs], att[seq], part[4*hs]
   __shared__ float scratch[16];
   const int h = blockIdx.x;
   const int pos = st->pos;
   const int kvh = h * n_kv_heads / n_heads;
   float *qs = sm, *kn = sm + hs, *vn = sm + 2 * hs, *att = sm + 3 * hs;
+  float *part = att + (pos + 1);
   const float *q = qkv + h * hs;
   const float *k = qkv + dim + kvh * hs;
   const float *v = qkv + dim + kv_dim + kvh * hs;
-  // RoPE on adjacent pairs; the pair index within the head gives the frequency
   for (int j = 2 * threadIdx.x; j < hs; j += 2 * blockDim.x) {
     const float freq = 1.f / powf(theta, (float)j / (float)hs);
     const float a = (float)pos * freq;
@@ -252,20 +305,32 @@ __global__ void __launch_bounds__(256)
       vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
     }
   }
-  const float scale = sqrtf((float)hs);
-  float mx = -INFINITY;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
+  const float inv_scale = 1.f / sqrtf((float)hs);
+  const float *kbase = kc + kvh * hs;
+  const float *vbase = vc + kvh * hs;
+  // scores: one thread per position, the cache row read as float4s (hs % 4 == 0)
+  // and q as LDS broadcasts
+  const int hs4 = hs >> 2;
   for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
-    float s = 0.f;
-    if (t == pos) {
-      for (int j = 0; j < hs; j++) s = fmaf(qs[j], kn[j], s);
-    } else {
-      const float *kr = kc + (int64_t)t * kv_dim + kvh * hs;
-      for (int j = 0; j < hs; j++) s = fmaf(qs[j], kr[j], s);
+    const float4 *kr = (const float4 *)(t == pos ? kn : kbase + (int64_t)t * kv_dim);
+    const float4 *q4 = (const float4 *)qs;
+    float s0 = 0.f, s1 = 0.f;
+    int j = 0;
+    for (; j + 1 < hs4; j += 2) {
+      const float4 a = kr[j], b = kr[j + 1], qa = q4[j], qb = q4[j + 1];
+      s0 = fmaf(a.x, qa.x, s0); s0 = fmaf(a.y, qa.y, s0); s0 = fmaf(a.z, qa.z, s0); s0 = fmaf(a.w, qa.w, s0);
+      s1 = fmaf(b.x, qb.x, s1); s1 = fmaf(b.y, qb.y, s1); s1 = fmaf(b.z, qb.z, s1); s1 = fmaf(b.w, qb.w, s1);
     }
-    s = s / scale;
-    att[t] = s;
-    mx = fmaxf(mx, s);
+    if (j < hs4) {
+      const float4 a = kr[j], qa = q4[j];
+      s0 = fmaf(a.x, qa.x, s0); s0 = fmaf(a.y, qa.y, s0); s0 = fmaf(a.z, qa.z, s0); s0 = fmaf(a.w, qa.w, s0);
+    }
+    att[t] = (s0 + s1) * inv_scale;
   }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int t = threadIdx.x; t <= pos; t += blockDim.x) mx = fmaxf(mx, att[t]);
   mx = block_max(mx, scratch);
   float sum = 0.f;
   for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
@@ -273,24 +338,30 @@ __global__ void __launch_bounds__(256)
     att[t] = e;
     sum += e;
   }
-  sum = block_sum(sum, scratch);  // ends with barriers: att[] complete
-  // weighted sum of V: thread (j, tp) sums t = tp, tp + P, ... for dim j
-  const int P = blockDim.x / hs > 0 ? blockDim.x / hs : 1;
-  float *part = att + (pos + 1);
-  const int j = threadIdx.x % hs, tp = threadIdx.x / hs;
-  float acc = 0.f;
-  if (tp < P) {
-    for (int t = tp; t <= pos; t += P) {
-      const float vv = (t == pos) ? vn[j] : vc[(int64_t)t * kv_dim + kvh * hs + j];
-      acc = fmaf(att[t], vv, acc);
+  sum = block_sum(sum, scratch);  // its barriers also publish att[]
+  // weighted sum of V: wave w takes t = w, w + nwv, ...; lanes along d
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; i++) acc[i] = 0.f;
+  for (int t = wave; t <= pos; t += nwv) {
+    const float a = att[t];
+    const float *vr = (t == pos) ? vn : vbase + (int64_t)t * kv_dim;
+#pragma unroll
+    for (int i = 0; i < DPL; i++) {
+      const int d = lane + 64 * i;
+      if (d < hs) acc[i] = fmaf(a, vr[d], acc[i]);
     }
-    part[tp * hs + j] = acc;
+  }
+#pragma unroll
+  for (int i = 0; i < DPL; i++) {
+    const int d = lane + 64 * i;
+    if (d < hs) part[wave * hs + d] = acc[i];
   }
   __syncthreads();
-  for (int jj = threadIdx.x; jj < hs; jj += blockDim.x) {
+  for (int d = threadIdx.x; d < hs; d += blockDim.x) {
     float t = 0.f;
-    for (int p = 0; p < P; p++) t += part[p * hs + jj];
-    out[h * hs + jj] = t / sum;
+    for (int w = 0; w < nwv; w++) t += part[w * hs + d];
+    out[h * hs + d] = t / sum;
   }
 }
 
@@ -363,11 +434,20 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, bool acc, const float *x0, cons
     for (int i = 0; i < sg.n; i++) total += sg.s[i].rows;
     const unsigned grid = (unsigned)std::min<int64_t>(cdiv(total, 4), (int64_t)num_cus() * 8);
     const size_t shm = sizeof(float) * (size_t)K;
-#define DG(P, A) hipLaunchKernelGGL((dgemv_f32<P, A>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, x1, nw, eps)
+    const int J = (int)cdiv(K / 4, 64);
+#define DGJ(P, A, JV, KPV) hipLaunchKernelGGL((dgemv_f32<P, A, JV, KPV>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, x1, nw, eps)
+#define DG(P, A)                                              \
+  do {                                                        \
+    if (J <= 4) DGJ(P, A, 4, 4);                              \
+    else if (J <= 8) DGJ(P, A, 8, 8);                         \
+    else if (J <= 16) DGJ(P, A, 16, 16);                      \
+    else DGJ(P, A, 0, 36);                                    \
+  } while (0)
     if (pro == kRmsNorm) { if (acc) DG(kRmsNorm, true); else DG(kRmsNorm, false); }
     else if (pro == kSwiGLU) { if (acc) DG(kSwiGLU, true); else DG(kSwiGLU, false); }
     else { if (acc) DG(kPlain, true); else DG(kPlain, false); }
 #undef DG
+#undef DGJ
   } else {
     int tiles = 0;
     for (int i = 0; i < sg.n; i++) {
@@ -376,12 +456,14 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, bool acc, const float *x0, cons
     }
     const size_t shm = sizeof(float) * ((size_t)K + (size_t)K / 32);
     const int gs = m.cfg.group_size;
-#define DW(P, A)                                                                          \
-  do {                                                                                    \
-    if (K / 32 <= 128)                                                                    \
-      hipLaunchKernelGGL((dgemv_w4<P, A, 4>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
-    else                                                                                  \
-      hipLaunchKernelGGL((dgemv_w4<P, A, 8>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
+#define DW(P, A)                                                                                        \
+  do {                                                                                                  \
+    if (K <= 1024)                                                                                      \
+      hipLaunchKernelGGL((dgemv_w4<P, A, 4, 4>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps);  \
+    else if (K <= 4096)                                                                                 \
+      hipLaunchKernelGGL((dgemv_w4<P, A, 4, 16>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
+    else                                                                                                \
+      hipLaunchKernelGGL((dgemv_w4<P, A, 8, 36>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
   } while (0)
     if (pro == kRmsNorm) { if (acc) DW(kRmsNorm, true); else DW(kRmsNorm, false); }
     else if (pro == kSwiGLU) { if (acc) DW(kSwiGLU, true); else DW(kSwiGLU, false); }
@@ -426,8 +508,7 @@ int enqueue_step(LlamaModel &m) {
     if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_att + (int64_t)l * dim))) return rc;
     // 2. attention (RoPE, cache store at pos, softmax, V sum)
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
-    const int P = std::max(1, 256 / hs);
-    const size_t shm = sizeof(float) * (3 * (size_t)hs + (size_t)c.seq_len + (size_t)P * hs);
+    const size_t shm = sizeof(float) * (3 * (size_t)hs + (size_t)c.seq_len + 4 * (size_t)hs);
     hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(256), shm, st, m.qkv, kc, vc, m.xb,
                        m.state, dim, kv, (int)c.n_heads, (int)c.n_kv_heads, hs, c.rope_theta);
     SIMP_HIP(hipGetLastError());
@@ -483,13 +564,14 @@ int check_cfg(const simp_rt_llama_config &c) {
     return set_error(SIMP_RT_EINVAL, "llama: unknown weight_format %d", c.weight_format);
   }
   const int64_t hs = c.dim / c.n_heads;
-  if (hs > 256) return set_error(SIMP_RT_EUNSUPPORTED, "llama: head_size above 256");
-  const size_t attn_lds = sizeof(float) * (3 * hs + c.seq_len + std::max<int64_t>(1, 256 / hs) * hs);
+  if (hs > 256 || hs % 4)
+    return set_error(SIMP_RT_EUNSUPPORTED, "llama: head_size must be a multiple of 4, at most 256");
+  const size_t attn_lds = sizeof(float) * (3 * hs + c.seq_len + 4 * hs);
   if (attn_lds > 64 * 1024)
     return set_error(SIMP_RT_EUNSUPPORTED, "llama: seq_len %lld too long for the attention kernel",
                      (long long)c.seq_len);
-  if (sizeof(float) * (size_t)(std::max(c.dim, c.hidden_dim) * 33 / 32) > 64 * 1024)
-    return set_error(SIMP_RT_EUNSUPPORTED, "llama: hidden_dim too large for the GEMV prologue");
+  if (std::max(c.dim, c.hidden_dim) > 256 * 36)
+    return set_error(SIMP_RT_EUNSUPPORTED, "llama: dim and hidden_dim must be at most 9216");
   return SIMP_RT_OK;
 }
 

@@ -91,6 +91,11 @@ int workspace(hipStream_t stream, size_t bytes, void **ptr) {
   std::lock_guard<std::mutex> lk(g_mu);
   WsBuf &b = g_ws[WsKey{dev, stream}];
   if (b.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return set_error(SIMP_RT_EUNSUPPORTED,
+                       "workspace of %zu bytes needed while the stream is being captured; "
+                       "make one uncaptured call of the same size on this stream first", bytes);
     if (b.ptr) {
       SIMP_HIP(hipStreamSynchronize(stream));  // earlier calls may still read it
       SIMP_HIP(hipFree(b.ptr));
