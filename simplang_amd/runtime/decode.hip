@@ -265,24 +265,29 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// One block per head.  qkv = [q(dim) | k(kv_dim) | v(kv_dim)] of this layer,
-// kc/vc the layer's caches [seq_len, kv_dim], out = xb[dim].  Lanes run along
-// the head dimension (dims d = lane + 64*i, i < DPL), so a cache row is read
-// as one coalesced 4*hs-byte access; the 4 waves split the positions, each
-// wave keeping 4 positions in flight.  Scores use the new k for t == pos (the
-// writer head stores it to the cache for later steps).
-__global__ void __launch_bounds__(256)
+// Attention, one 1024-thread block per head (no cross-block communication: a
+// device-scope fence to publish partials between blocks costs an L2 write-back
+// on this multi-XCD part, more than the whole head's work).  RoPE of q and of
+// the head's new k; the first head of a kv head stores k, v at pos.  Scores:
+// 4 lanes per position, each a quarter of the head dimension in float4s.  V
+// sum: thread (d, p) sums positions p, p + P, ... with 8 loads in flight, and
+// the P partitions are added through LDS.  Uses 3*256 + seq_len + 1024 floats
+// of LDS (dynamic part: att[seq_len]).
+constexpr int kAttnThreads = 1024;
+
+__global__ void __launch_bounds__(kAttnThreads)
     attn_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
            float *__restrict__ out, const StepState *__restrict__ st, int dim, int kv_dim,
            int n_heads, int n_kv_heads, int hs, float theta) {
-  constexpr int DPL = 4;                   // dims per lane, hs <= 256
-  extern __shared__ float sm[];            // q[hs], knew[hs], vnew[hs], att[seq], part[4*hs]
+  __shared__ __align__(16) float qs[256];
+  __shared__ __align__(16) float kn[256];
+  __shared__ __align__(16) float vn[256];
+  __shared__ float red[kAttnThreads];
   __shared__ float scratch[16];
+  extern __shared__ float att[];  // [pos + 1]
   const int h = blockIdx.x;
   const int pos = st->pos;
   const int kvh = h * n_kv_heads / n_heads;
-  float *qs = sm, *kn = sm + hs, *vn = sm + 2 * hs, *att = sm + 3 * hs;
-  float *part = att + (pos + 1);
   const float *q = qkv + h * hs;
   const float *k = qkv + dim + kvh * hs;
   const float *v = qkv + dim + kv_dim + kvh * hs;
@@ -299,69 +304,70 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   const bool writer = h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh;
-  if (writer) {  // first head of this kv head stores the new k, v at pos
+  if (writer) {
     for (int j = threadIdx.x; j < hs; j += blockDim.x) {
       kc[(int64_t)pos * kv_dim + kvh * hs + j] = kn[j];
       vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
     }
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwv = blockDim.x >> 6;
   const float inv_scale = 1.f / sqrtf((float)hs);
   const float *kbase = kc + kvh * hs;
   const float *vbase = vc + kvh * hs;
-  // scores: one thread per position, the cache row read as float4s (hs % 4 == 0)
-  // and q as LDS broadcasts
   const int hs4 = hs >> 2;
-  for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
-    const float4 *kr = (const float4 *)(t == pos ? kn : kbase + (int64_t)t * kv_dim);
-    const float4 *q4 = (const float4 *)qs;
-    float s0 = 0.f, s1 = 0.f;
-    int j = 0;
-    for (; j + 1 < hs4; j += 2) {
-      const float4 a = kr[j], b = kr[j + 1], qa = q4[j], qb = q4[j + 1];
-      s0 = fmaf(a.x, qa.x, s0); s0 = fmaf(a.y, qa.y, s0); s0 = fmaf(a.z, qa.z, s0); s0 = fmaf(a.w, qa.w, s0);
-      s1 = fmaf(b.x, qb.x, s1); s1 = fmaf(b.y, qb.y, s1); s1 = fmaf(b.z, qb.z, s1); s1 = fmaf(b.w, qb.w, s1);
+  const int lt = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  for (int tb = 0; tb <= pos; tb += kAttnThreads / 4) {
+    const int t = tb + lt;
+    float sacc = 0.f;
+    if (t <= pos) {
+      const float4 *kr = (const float4 *)(t == pos ? kn : kbase + (int64_t)t * kv_dim);
+      const float4 *q4 = (const float4 *)qs;
+      for (int j = sub; j < hs4; j += 4) {
+        const float4 a = kr[j], b = q4[j];
+        sacc = fmaf(a.x, b.x, sacc);
+        sacc = fmaf(a.y, b.y, sacc);
+        sacc = fmaf(a.z, b.z, sacc);
+        sacc = fmaf(a.w, b.w, sacc);
+      }
     }
-    if (j < hs4) {
-      const float4 a = kr[j], qa = q4[j];
-      s0 = fmaf(a.x, qa.x, s0); s0 = fmaf(a.y, qa.y, s0); s0 = fmaf(a.z, qa.z, s0); s0 = fmaf(a.w, qa.w, s0);
-    }
-    att[t] = (s0 + s1) * inv_scale;
+    sacc += __shfl_xor(sacc, 1);
+    sacc += __shfl_xor(sacc, 2);
+    if (sub == 0 && t <= pos) att[t] = sacc * inv_scale;
   }
   __syncthreads();
-  float mx = -INFINITY;
-  for (int t = threadIdx.x; t <= pos; t += blockDim.x) mx = fmaxf(mx, att[t]);
-  mx = block_max(mx, scratch);
-  float sum = 0.f;
+  float m = -INFINITY;
+  for (int t = threadIdx.x; t <= pos; t += blockDim.x) m = fmaxf(m, att[t]);
+  m = block_max(m, scratch);
+  float l = 0.f;
   for (int t = threadIdx.x; t <= pos; t += blockDim.x) {
-    const float e = expf(att[t] - mx);
+    const float e = expf(att[t] - m);
     att[t] = e;
-    sum += e;
+    l += e;
   }
-  sum = block_sum(sum, scratch);  // its barriers also publish att[]
-  // weighted sum of V: wave w takes t = w, w + nwv, ...; lanes along d
-  float acc[DPL];
+  l = block_sum(l, scratch);
+  // V sum: thread (d, p), P = blockDim / hs partitions of the positions
+  const int P = blockDim.x / hs;
+  const int d = threadIdx.x % hs, p = threadIdx.x / hs;
+  float o = 0.f;
+  if (p < P) {
+    int t = p;
+    for (; t + 7 * P <= pos; t += 8 * P) {
+      float vv[8];
 #pragma unroll
-  for (int i = 0; i < DPL; i++) acc[i] = 0.f;
-  for (int t = wave; t <= pos; t += nwv) {
-    const float a = att[t];
-    const float *vr = (t == pos) ? vn : vbase + (int64_t)t * kv_dim;
+      for (int e = 0; e < 8; e++) {
+        const int te = t + e * P;
+        vv[e] = te == pos ? vn[d] : vbase[(int64_t)te * kv_dim + d];
+      }
 #pragma unroll
-    for (int i = 0; i < DPL; i++) {
-      const int d = lane + 64 * i;
-      if (d < hs) acc[i] = fmaf(a, vr[d], acc[i]);
+      for (int e = 0; e < 8; e++) o = fmaf(att[t + e * P], vv[e], o);
     }
-  }
-#pragma unroll
-  for (int i = 0; i < DPL; i++) {
-    const int d = lane + 64 * i;
-    if (d < hs) part[wave * hs + d] = acc[i];
+    for (; t <= pos; t += P) o = fmaf(att[t], t == pos ? vn[d] : vbase[(int64_t)t * kv_dim + d], o);
+    red[p * hs + d] = o;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < hs; d += blockDim.x) {
-    float t = 0.f;
-    for (int w = 0; w < nwv; w++) t += part[w * hs + d];
-    out[h * hs + d] = t / sum;
+  for (int dd = threadIdx.x; dd < hs; dd += blockDim.x) {
+    float sacc = 0.f;
+    for (int pp = 0; pp < P; pp++) sacc += red[pp * hs + dd];
+    out[h * hs + dd] = sacc / l;
   }
 }
 
@@ -506,11 +512,11 @@ int enqueue_step(LlamaModel &m) {
     }
     s.n = 3;
     if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_att + (int64_t)l * dim))) return rc;
-    // 2. attention (RoPE, cache store at pos, softmax, V sum)
+    // 2. attention (RoPE, cache store at pos, softmax, V sum), one block per head
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
-    const size_t shm = sizeof(float) * (3 * (size_t)hs + (size_t)c.seq_len + 4 * (size_t)hs);
-    hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(256), shm, st, m.qkv, kc, vc, m.xb,
-                       m.state, dim, kv, (int)c.n_heads, (int)c.n_kv_heads, hs, c.rope_theta);
+    hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(kAttnThreads),
+                       sizeof(float) * (size_t)c.seq_len, st, m.qkv, kc, vc, m.xb, m.state, dim, kv,
+                       (int)c.n_heads, (int)c.n_kv_heads, hs, c.rope_theta);
     SIMP_HIP(hipGetLastError());
     // 3. Wo, accumulated into x (residual)
     s = Segs{};
@@ -566,8 +572,7 @@ int check_cfg(const simp_rt_llama_config &c) {
   const int64_t hs = c.dim / c.n_heads;
   if (hs > 256 || hs % 4)
     return set_error(SIMP_RT_EUNSUPPORTED, "llama: head_size must be a multiple of 4, at most 256");
-  const size_t attn_lds = sizeof(float) * (3 * hs + c.seq_len + 4 * hs);
-  if (attn_lds > 64 * 1024)
+  if (sizeof(float) * (size_t)(c.seq_len + 3 * 256 + 1024 + 16) > 64 * 1024)
     return set_error(SIMP_RT_EUNSUPPORTED, "llama: seq_len %lld too long for the attention kernel",
                      (long long)c.seq_len);
   if (std::max(c.dim, c.hidden_dim) > 256 * 36)
