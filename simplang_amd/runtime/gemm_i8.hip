@@ -285,7 +285,7 @@ template <int BM, int BN, int BK, int WGM, int WGN, bool AU8>
 __global__ void __launch_bounds__(WGM *WGN * 64)
     gemm_i8_nt16(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
                  int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
-                 int tiles_m, int tiles_n) {
+                 int tiles_m, int tiles_n, const int32_t *__restrict__ colsum) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int FM = WM / 16, FN = WN / 16;
@@ -302,37 +302,41 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = (K + BK - 1) / BK;
   uint4 ra[A_PER], rb[B_PER];
+  // Clamped (always valid) addresses; out-of-range data is zeroed by a mask applied
+  // when the tile is written to LDS (recomputed there rather than kept in registers).
+  // A branch around the load, or masking right after it, makes the compiler wait for
+  // each load in turn.
   auto load_tile = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
       const int c = tid + i * NT, kc = c % KC, m = c / KC;
-      const int gm = m0 + m, gk = k0 + kc * 16;
-      uint4 v = *(const uint4 *)(A + (int64_t)min(gm, M - 1) * lda + min(gk, K - 16));
-      if (gm >= M || gk >= K) v = make_uint4(0, 0, 0, 0);
-      if constexpr (AU8) {
-        v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
-      }
-      ra[i] = v;
+      ra[i] = *(const uint4 *)(A + (int64_t)min(m0 + m, M - 1) * lda + min(k0 + kc * 16, K - 16));
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
       const int c = tid + i * NT, kc = c % KC, n = c / KC;
-      const int gn = n0 + n, gk = k0 + kc * 16;
-      uint4 v = *(const uint4 *)(B + (int64_t)min(gn, N - 1) * ldb + min(gk, K - 16));
-      if (gn >= N || gk >= K) v = make_uint4(0, 0, 0, 0);
-      rb[i] = v;
+      rb[i] = *(const uint4 *)(B + (int64_t)min(n0 + n, N - 1) * ldb + min(k0 + kc * 16, K - 16));
     }
   };
-  auto store_tile = [&](int s) {
+  auto store_tile = [&](int s, int k0) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
       const int c = tid + i * NT, kc = c % KC, m = c / KC;
-      sA[s][kc * BM + swz_rows(m, kc)] = ra[i];
+      const uint32_t keep = (m0 + m < M && k0 + kc * 16 < K) ? 0xffffffffu : 0u;
+      uint4 v = ra[i];
+      v.x &= keep; v.y &= keep; v.z &= keep; v.w &= keep;
+      if constexpr (AU8) {
+        v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+      }
+      sA[s][kc * BM + swz_rows(m, kc)] = v;
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
       const int c = tid + i * NT, kc = c % KC, n = c / KC;
-      sB[s][kc * BN + swz_rows(n, kc)] = rb[i];
+      const uint32_t keep = (n0 + n < N && k0 + kc * 16 < K) ? 0xffffffffu : 0u;
+      uint4 v = rb[i];
+      v.x &= keep; v.y &= keep; v.z &= keep; v.w &= keep;
+      sB[s][kc * BN + swz_rows(n, kc)] = v;
     }
   };
   v4i acc[FM][FN];
@@ -340,17 +344,18 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-  int cs[FN];
-#pragma unroll
-  for (int j = 0; j < FN; j++) cs[j] = 0;
 
   load_tile(0);
-  store_tile(0);
+  store_tile(0, 0);
   __syncthreads();
   const int lr = lane & 15, lk = lane >> 4;
   for (int kt = 0; kt < nk; kt++) {
     const int cur = kt & 1;
-    load_tile(min(kt + 1, nk - 1) * BK);  // the last prefetch repeats a tile; never read
+    const int knext = min(kt + 1, nk - 1) * BK;  // the last prefetch repeats a tile; never read
+    load_tile(knext);
+    // keep the next tile's loads at the top of the iteration: left alone, the
+    // scheduler sinks them next to the LDS stores and their latency is exposed
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < BK / 64; ks++) {
       const int kc = ks * 4 + lk;  // 16x16x64 operand: lane holds row l%16, K bytes 16*(l/16)..+16
@@ -364,12 +369,6 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
       for (int j = 0; j < FN; j++) {
         const uint4 v = sB[cur][kc * BN + swz_rows(wn0 + j * 16 + lr, kc)];
         bf[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-        if constexpr (AU8) {
-          cs[j] = __builtin_amdgcn_sdot4(bf[j].x, 0x01010101, cs[j], false);
-          cs[j] = __builtin_amdgcn_sdot4(bf[j].y, 0x01010101, cs[j], false);
-          cs[j] = __builtin_amdgcn_sdot4(bf[j].z, 0x01010101, cs[j], false);
-          cs[j] = __builtin_amdgcn_sdot4(bf[j].w, 0x01010101, cs[j], false);
-        }
       }
 #pragma unroll
       for (int i = 0; i < FM; i++)
@@ -377,61 +376,100 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
         for (int j = 0; j < FN; j++)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    store_tile(cur ^ 1);
+    // and the masking of those loads at the bottom, so no MFMA above waits for them
+    __builtin_amdgcn_sched_barrier(0);
+    store_tile(cur ^ 1, knext);
     __syncthreads();
-  }
-  if constexpr (AU8) {
-    // lanes l, l^16, l^32, l^48 hold the four K quarters of column l%16
-#pragma unroll
-    for (int j = 0; j < FN; j++) {
-      int t = cs[j] + __shfl_xor(cs[j], 16);
-      t += __shfl_xor(t, 32);
-#pragma unroll
-      for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[i][j][r] += 128 * t;
-    }
   }
   // Output of a 16x16 i32 MFMA: lane l holds column l%16, rows 4*(l/16) + r.
 #pragma unroll
-  for (int i = 0; i < FM; i++)
+  for (int j = 0; j < FN; j++) {
+    const int col = n0 + wn0 + j * 16 + lr;
+    // u8 x s8: C = (A^0x80) B + 128 colsum(B)
+    const int bias = (AU8 && col < N) ? 128 * colsum[col] : 0;
 #pragma unroll
-    for (int j = 0; j < FN; j++) {
-      const int col = n0 + wn0 + j * 16 + lr;
+    for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int row = m0 + wm0 + i * 16 + 4 * lk + r;
-        if (row < M && col < N) C[(int64_t)row * ldc + col] = acc[i][j][r];
+        if (row < M && col < N) C[(int64_t)row * ldc + col] = acc[i][j][r] + bias;
       }
-    }
+  }
 }
 
-// B[K,N] -> B_T[N,K] through a 64x64 LDS tile (K % 16 == 0, N % 16 == 0).
-// Feeds gemm_i8_nt16 when the caller passes tensor_matmul's [K,N] layout; the
-// reference materialises the same B_T (ConvertSimpToMemRef.cpp:3168-3216).
+// B[K,N] -> B_T[N,K] (K % 16 == 0, N % 16 == 0), one 64-column strip of KT rows
+// of K per workgroup, through 64x64 LDS tiles; 4x4 byte blocks are transposed in
+// registers. Feeds gemm_i8_nt16 when the caller passes tensor_matmul's [K,N]
+// layout; the reference materialises the same B_T (ConvertSimpToMemRef.cpp:3168-3216).
+// With colsum != nullptr (u8 x s8) it also adds each column's sum over the strip
+// into colsum[n], which the caller zero-fills first.
+template <int KT>
 __global__ void __launch_bounds__(256)
-    transpose_i8(const int8_t *__restrict__ B, int64_t ldb, int8_t *__restrict__ BT, int K, int N) {
-  __shared__ uint8_t s[64][64 + 4];
+    transpose_i8(const int8_t *__restrict__ B, int64_t ldb, int8_t *__restrict__ BT, int K, int N,
+                 int32_t *__restrict__ colsum) {
+  __shared__ uint32_t s[64][17];  // [k][n/4]; the odd row pitch spreads phase-2 reads over banks
   const int t = threadIdx.x;
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  {
-    const int k = t >> 2, c = t & 3;
-    const int gk = k0 + k, gn = n0 + 16 * c;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (gk < K && gn < N) v = *(const uint4 *)(B + (int64_t)gk * ldb + gn);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  const int n0 = blockIdx.x * 64;
+  const int k_begin = blockIdx.y * KT, k_end = min(K, k_begin + KT);
+  const int lk = t >> 2, lc = t & 3;    // phase 1: row k, 16 columns 16*lc..
+  const int qn = t >> 4, qk = t & 15;   // phase 2: columns 4*qn..+3, rows 4*qk..+3
+  int sum[4] = {0, 0, 0, 0};
+  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
+    {
+      const int gk = k0 + lk, gn = n0 + 16 * lc;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (gk < K && gn < N) v = *(const uint4 *)(B + (int64_t)gk * ldb + gn);
+      s[lk][4 * lc + 0] = v.x;
+      s[lk][4 * lc + 1] = v.y;
+      s[lk][4 * lc + 2] = v.z;
+      s[lk][4 * lc + 3] = v.w;
+    }
+    __syncthreads();
+    uint32_t o[4];
+    transpose4x4(s[4 * qk][qn], s[4 * qk + 1][qn], s[4 * qk + 2][qn], s[4 * qk + 3][qn], o[0],
+                 o[1], o[2], o[3]);
+    const int gk = k0 + 4 * qk;
 #pragma unroll
-    for (int j = 0; j < 16; j++) s[k][16 * c + j] = (uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+    for (int j = 0; j < 4; j++) {
+      const int gn = n0 + 4 * qn + j;
+      if (gn < N && gk < K) *(uint32_t *)(BT + (int64_t)gn * K + gk) = o[j];
+      sum[j] = __builtin_amdgcn_sdot4((int)o[j], 0x01010101, sum[j], false);
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  {
-    const int n = t >> 2, c = t & 3;
-    const int gn = n0 + n, gk = k0 + 16 * c;
-    uint32_t w[4] = {0, 0, 0, 0};
+  if (colsum) {
 #pragma unroll
-    for (int j = 0; j < 16; j++) w[j >> 2] |= (uint32_t)s[16 * c + j][n] << (8 * (j & 3));
-    if (gn < N && gk < K) *(uint4 *)(BT + (int64_t)gn * K + gk) = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int j = 0; j < 4; j++) {
+      int v = sum[j];
+      v += __shfl_xor(v, 1);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 8);
+      const int gn = n0 + 4 * qn + j;
+      if (qk == 0 && gn < N) atomicAdd(colsum + gn, v);
+    }
   }
+}
+
+// colsum[n] = sum_k B_T[n,k] as signed bytes, one wave per row (K % 16 == 0,
+// 16-byte aligned rows).
+__global__ void __launch_bounds__(256)
+    colsum_nk_i8(const int8_t *__restrict__ BT, int64_t ldb, int32_t *__restrict__ colsum, int N,
+                 int K) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const int8_t *row = BT + (int64_t)n * ldb;
+  int acc = 0;
+  for (int k = lane * 16; k < K; k += 64 * 16) {
+    const uint4 v = *(const uint4 *)(row + k);
+    acc = __builtin_amdgcn_sdot4((int)v.x, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)v.y, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)v.w, 0x01010101, acc, false);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) colsum[n] = acc;
 }
 
 // Correctness fallback for shapes the MFMA path cannot load with aligned
@@ -518,19 +556,31 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
   const int64_t cus = num_cus();
   auto tiles = [&](int bm, int bn) { return cdiv(g.M, bm) * cdiv(g.N, bn); };
   if (tiles(256, 256) >= cus && g.N % 16 == 0) {
+    // Workspace: [colsum: N int32, 256-byte aligned][B_T: N x K bytes when B is [K,N]]
     GemmArgs h = g;
-    if (!BNK) {  // B[K,N] -> B_T[N,K] in the per-stream workspace
-      void *ws = nullptr;
-      int rc = workspace(st, (size_t)g.K * g.N, &ws);
-      if (rc) return rc;
-      hipLaunchKernelGGL(transpose_i8, dim3((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.K, 64)),
-                         dim3(256), 0, st, g.B, g.ldb, (int8_t *)ws, g.K, g.N);
-      h.B = (const int8_t *)ws;
+    const size_t cs_bytes = AU8 ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
+    void *ws = nullptr;
+    int rc = workspace(st, cs_bytes + (BNK ? 0 : (size_t)g.K * g.N), &ws);
+    if (rc) return rc;
+    int32_t *colsum = AU8 ? (int32_t *)ws : nullptr;
+    if (!BNK) {  // B[K,N] -> B_T[N,K], column sums on the way
+      constexpr int KT = 256;
+      int8_t *bt = (int8_t *)ws + cs_bytes;
+      if (AU8)
+        hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
+                           (int64_t)g.N, 1, g.N);
+      hipLaunchKernelGGL(transpose_i8<KT>, dim3((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.K, KT)),
+                         dim3(256), 0, st, g.B, g.ldb, bt, g.K, g.N, colsum);
+      h.B = bt;
       h.ldb = g.K;
+    } else if (AU8) {
+      hipLaunchKernelGGL(colsum_nk_i8, dim3((unsigned)cdiv(g.N, 4)), dim3(256), 0, st, g.B, g.ldb,
+                         colsum, g.N, g.K);
     }
     const int tm = (int)cdiv(g.M, 256), tn = (int)cdiv(g.N, 256);
     hipLaunchKernelGGL((gemm_i8_nt16<256, 256, 128, 2, 4, AU8>), dim3(tm * tn), dim3(512), 0, st,
-                       h.A, h.lda, h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn);
+                       h.A, h.lda, h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn,
+                       (const int32_t *)colsum);
     SIMP_HIP(hipGetLastError());
     return SIMP_RT_OK;
   }
