@@ -6,13 +6,21 @@ Headline (the JSON line's ``value``): exact int8 GEMM throughput, u8 x s8 -> i32
 (8192^3), inputs resident in HBM.  One step = one C = A x B over the
 synthetic batch (A u8 uniform [0,255], B s8 uniform [-128,127], seed 42).
 
-Also reported on the same line: the configs[1] sweep (TOPS per shape), the
-roofline of the GEMM kernel (HIP events on the stream the kernel is launched
-on), and the CPU baseline -- the oracle's restatement of the reference's VNNI
-kernel timed on this host's cores on a bounded row-block sample of the same
-8192^3 problem.
+``value`` and ``ms_per_step`` cover the whole call (B transpose + column sums +
+GEMM).  ``roofline`` is the dominant kernel alone: its launches are bracketed
+with HIP events on the stream they run on (simp_rt_timing), so ``achieved`` is
+2*M*N*K over that kernel's average launch time.
+
+Also reported on the same line: the configs[1] sweep (TOPS per shape), the W4
+GEMV and decode sections, and the CPU baseline -- the oracle's restatement of
+the reference's VNNI kernel timed on this host's cores on a bounded row-block
+sample of the same 8192^3 problem.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-sweep] [--no-cpu]
+                    [--only gemm|w4|decode|copy]
+
+``--only copy`` times a plain 256 MiB device copy (the calibration run for the
+rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and prints its own JSON line.
 """
 import argparse
 import json
@@ -212,7 +220,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "w4", "decode"], default=None,
+    ap.add_argument("--only", choices=["gemm", "w4", "decode", "copy"], default=None,
                     help="run one section (for profiling); the JSON line is still printed")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -234,11 +242,43 @@ def main():
         args.no_decode = args.only != "decode"
     n = args.size
     ms = tops = 0.0
+    kern, kern_ms = None, 0.0
+    if args.only == "copy":
+        # calibration for the --pmc FETCH_SIZE / WRITE_SIZE counters: one plain
+        # device copy of a known size per launch
+        nbytes = 256 << 20
+        src = torch.randint(-128, 127, (nbytes,), dtype=torch.int8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / args.steps
+        print(json.dumps({"calibration": "device copy", "bytes_read": nbytes,
+                          "bytes_written": nbytes, "us": round(t * 1e3, 2),
+                          "GBs": round(2 * nbytes / (t * 1e-3) / 1e9, 1)}), flush=True)
+        return
     if args.only in (None, "gemm"):
         a, b, c = make_inputs(n, n, n, dev)
         torch.cuda.synchronize()
         ms = gemm_events(sa.matmul_u8s8_i32, a, b, c, args.steps, args.warmup, stream)
         tops = 2.0 * n * n * n / (ms * 1e-3) / 1e12
+        # the dominant kernel alone: HIP events around its launches, on its stream
+        sa.timing(True)
+        for _ in range(args.steps):
+            sa.matmul_u8s8_i32(a, b, c)
+        torch.cuda.synchronize()
+        for k in ("gemm_i8_dma", "gemm_i8_nt16", "gemm_i8_mfma"):
+            kms, kn = sa.timing_query(k)
+            if kn:
+                kern, kern_ms = k, kms / kn
+                break
+        sa.timing(False)
         del a, b, c
         torch.cuda.empty_cache()
 
@@ -263,6 +303,7 @@ def main():
 
     cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baseline(n)
 
+    ktops = 2.0 * n * n * n / (kern_ms * 1e-3) / 1e12 if kern_ms > 0 else 0.0
     line = {
         "metric": METRIC,
         "value": round(tops, 2),
@@ -278,9 +319,10 @@ def main():
         "data": "synthetic: A u8 uniform [0,255], B s8 uniform [-128,127], seed 42",
         "config": {"workload": f"int8 GEMM u8xs8->i32 {n}^3 (BASELINE configs[1], largest square)",
                    "M": n, "N": n, "K": n, "layout": "A[M,K], B[K,N] row-major, C[M,N] i32"},
-        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
-                     "traffic": load_traffic(f"gemm_i8_{n}")},
+        "roofline": {"bound": "mfma", "achieved": round(ktops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(ktops / INT8_PEAK_TOPS, 4),
+                     "traffic": load_traffic(f"{kern}_{n}"), "kernel": kern,
+                     "launch_us": round(kern_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "sweep": sweep,
         "w4_gemv": w4,

@@ -61,6 +61,14 @@ int32_t simp_rt_sync_to_host(const void *host_ptr, int64_t bytes);
 int32_t simp_rt_malloc(void **dev_ptr, int64_t bytes);
 int32_t simp_rt_free(void *dev_ptr);
 int32_t simp_rt_memcpy(void *dst, const void *src, int64_t bytes); /* any direction, blocking */
+/* Per-kernel timing for profiling (no reference counterpart).  simp_rt_timing(1)
+ * clears earlier records and brackets every later launch of the library's main
+ * kernels with HIP events on its stream; simp_rt_timing(0) stops and clears.
+ * simp_rt_timing_query waits for the recorded launches of one kernel (e.g.
+ * "gemm_i8_nt16", "gemm_i8_mfma", "transpose_i8", "w4s_gemv") and returns their
+ * summed duration and count.  Launches under stream capture are not recorded. */
+int32_t simp_rt_timing(int32_t on);
+int32_t simp_rt_timing_query(const char *kernel, double *total_ms, int64_t *launches);
 
 /* --------------------------------------------------------------- int8 -- */
 

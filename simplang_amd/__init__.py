@@ -13,6 +13,8 @@ from .host import (  # noqa: F401
     lib_path,
     set_stream,
     sync,
+    timing,
+    timing_query,
     tensor_matmul_i8,
     tensor_matmul_nt_i8,
     matmul_u8s8_i32,

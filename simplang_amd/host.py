@@ -69,6 +69,8 @@ _sig("simp_rt_llama_generate", [_P, _P, _I, _I, _P, C.c_int32])
 _sig("simp_rt_set_stream", [_P])
 _sig("simp_rt_register", [_P, _I, C.c_int32])
 _sig("simp_rt_unregister", [_P])
+_sig("simp_rt_timing", [C.c_int32])
+_sig("simp_rt_timing_query", [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)])
 
 
 def declared_symbols(header: str = HEADER) -> list[str]:
@@ -145,6 +147,18 @@ def set_stream(stream) -> None:
 
 def sync() -> None:
     _check("simp_rt_sync", lib.simp_rt_sync())
+
+
+def timing(on: bool) -> None:
+    """Start (clearing earlier records) or stop per-kernel HIP-event timing."""
+    _check("simp_rt_timing", lib.simp_rt_timing(1 if on else 0))
+
+
+def timing_query(kernel: str):
+    """(total ms, launches) recorded for ``kernel`` since timing(True)."""
+    ms, n = C.c_double(), C.c_int64()
+    _check("simp_rt_timing_query", lib.simp_rt_timing_query(kernel.encode(), C.byref(ms), C.byref(n)))
+    return ms.value, n.value
 
 
 def _gemm(fn_name, a, b, c):

@@ -397,6 +397,186 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   }
 }
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate that waits for lgkmcnt == 0 only.
+constexpr int waitcnt_lgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// One global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at
+// lds_off + 16*lane.  Issued as asm because the compiler, seeing the builtin's
+// LDS write, waits for every outstanding load before any later LDS read; the
+// kernel below counts these loads with its own s_waitcnt instead.
+__device__ __forceinline__ void dma16(const int8_t *src, uint32_t lds_off) {
+  uint32_t saved;
+  // M0 is saved and restored around the load (the compiler owns it); one wait
+  // state separates the M0 write from the LDS-DMA load that reads it.
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(src)
+      : "memory");
+}
+
+// LDS byte offset of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Large-problem kernel for K % 64 == 0, B given as B_T[N,K]: 256x256 C tiles,
+// 8 waves (2 per SIMD) of 128x64, v_mfma_i32_16x16x64_i8, BK = 64.
+//   * Operand tiles go global -> LDS directly (global_load_lds_dwordx4), with no
+//     register staging, into a ring of STAGES 32 KB stages, STAGES-1 K-steps
+//     ahead of the MFMAs that consume them; one barrier per K-step.
+//   * Per stage, A and B are each 16 blocks of 1 KB = 16 rows x 64 B.  A DMA
+//     instruction fills one block in lane order; lane l loads row l/4, 16-byte
+//     chunk (l%4)^((row>>1)&3), so four consecutive lanes read one row's 64
+//     contiguous bytes (the coalescer merges consecutive lanes only) and the
+//     XOR keeps the MFMA operand reads (lane l: row l%16, chunk l/16) at full
+//     LDS bandwidth.
+//   * Operand fragments are double-buffered in registers: each K-step certifies
+//     the next stage (wait + barrier), starts reading its fragments, and runs
+//     the MFMAs of the current stage meanwhile.
+//   * Persistent: gridDim.x (a multiple of 8) workgroups walk the tiles, so a
+//     tile's stores drain while the next tile's loads start.  Virtual block ids
+//     keep the XCD-contiguous, row-grouped tile order of tile_of_block.
+//   * Rows beyond M (N) load from a clamped in-bounds row; their results are
+//     never stored.
+//   * The MFMA computes C^T tiles (B fragment as the first operand), so a lane
+//     ends with 4 consecutive columns of one row of C: 16-byte stores.
+template <int STAGES, bool AU8>
+__global__ void __launch_bounds__(512)
+    gemm_i8_dma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+                int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+                int tiles_m, int tiles_n, const int32_t *__restrict__ colsum, int vec_store) {
+  constexpr int BM = 256, BN = 256, BK = 64, WGN = 4;
+  constexpr int WM = 128, WN = 64, FM = WM / 16, FN = WN / 16;
+  constexpr int STAGE = (BM + BN) * BK;  // bytes
+  __shared__ uint4 lds[STAGES * STAGE / 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int nk = K / BK;
+  const int ntiles = tiles_m * tiles_n;
+  const int lrow = lane & 15, lkc = lane >> 4;
+  const int drow = lane >> 2, dkc = (lane & 3) ^ ((drow >> 1) & 3);  // DMA lane -> row, chunk
+  const int rslot = lrow * 4 + (lkc ^ ((lrow >> 1) & 3));          // operand lane -> slot
+  const uint32_t lds_wave = lds_offset(lds) + 2048 * wave;  // wave w fills blocks 2w, 2w+1
+
+  for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
+    int tm, tn;
+    tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int8_t *srcA0 = A + (int64_t)min(m0 + 32 * wave + drow, M - 1) * lda + 16 * dkc;
+    const int8_t *srcA1 = A + (int64_t)min(m0 + 32 * wave + 16 + drow, M - 1) * lda + 16 * dkc;
+    const int8_t *srcB0 = B + (int64_t)min(n0 + 32 * wave + drow, N - 1) * ldb + 16 * dkc;
+    const int8_t *srcB1 = B + (int64_t)min(n0 + 32 * wave + 16 + drow, N - 1) * ldb + 16 * dkc;
+    auto issue = [&](int kt) {
+      const uint32_t st = lds_wave + (kt % STAGES) * STAGE;
+      const int64_t k0 = (int64_t)kt * BK;
+      dma16(srcA0 + k0, st);
+      dma16(srcA1 + k0, st + 1024);
+      dma16(srcB0 + k0, st + BM * BK);
+      dma16(srcB1 + k0, st + BM * BK + 1024);
+    };
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    // Fragments: A single-buffered and refilled in place right after its last
+    // MFMA of the step; B double-buffered (read at the start of the step).
+    v4i fa[FM], fb[2][FN];
+    auto frag = [&](int kt, int blk) {
+      const uint4 v = lds[(kt % STAGES) * (STAGE / 16) + blk * 64 + rslot];
+      return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+    };
+    constexpr int BOFF = BM * BK / 1024;  // first B block of a stage
+    // The previous tile's stores (also counted by vmcnt) drain before this tile's
+    // load accounting starts; every wave finished reading LDS at that tile's last
+    // barrier, so its stages may be overwritten.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+#pragma unroll
+    for (int p = 0; p < STAGES; p++)
+      if (p < nk) issue(p);
+    // stage 0 done on this wave (later issued stages may be outstanding) ...
+    if (nk >= STAGES) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * (STAGES - 1)));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    block_barrier();  // ... and on every wave
+#pragma unroll
+    for (int j = 0; j < FN; j++) fb[0][j] = frag(0, BOFF + wn0 / 16 + j);
+#pragma unroll
+    for (int i = 0; i < FM; i++) fa[i] = frag(0, wm0 / 16 + i);
+    // K-step kt: certify stage kt+1, refill the buffer of stage kt (its fragments
+    // are in registers on every wave) with stage kt+STAGES, and run stage kt's
+    // MFMAs while stage kt+1's fragments are read.
+    auto step = [&](int kt, int cb) {
+      const bool more = kt + 1 < nk;  // stage kt+1 exists
+      if (more) {
+        // issued: stages up to min(kt+STAGES-1, nk-1); stage kt+1 must be done
+        if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * (STAGES - 2)));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
+      __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0);  // this wave's reads of stage kt landed
+      block_barrier();
+      if (kt + STAGES < nk) issue(kt + STAGES);
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) fb[cb ^ 1][j] = frag(kt + 1, BOFF + wn0 / 16 + j);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        v4i a = fa[i];
+        if constexpr (AU8) a ^= (int)0x80808080;  // u8 a -> s8 (a - 128)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][j], a, acc[i][j], 0, 0, 0);
+        if (more) fa[i] = frag(kt + 1, wm0 / 16 + i);
+      }
+    };
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      step(kt, 0);
+      step(kt + 1, 1);
+    }
+    if (kt < nk) step(kt, 0);
+    // acc[i][j][r] = C[m0 + wm0 + 16 i + l%16][n0 + wn0 + 16 j + 4 (l/16) + r]
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn0 + 16 * j + 4 * lkc;
+      // u8 x s8: C = (A^0x80) B + 128 colsum(B)
+      // (N % 16 == 0 and col % 4 == 0, so col < N covers col..col+3)
+      v4i bias = v4i{0, 0, 0, 0};
+      if constexpr (AU8) {
+        if (col < N) bias = *(const v4i *)(colsum + col) * 128;
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int row = m0 + wm0 + 16 * i + lrow;
+        if (row >= M || col >= N) continue;
+        const v4i v = acc[i][j] + bias;
+        int32_t *dst = C + (int64_t)row * ldc + col;
+        if (vec_store) {
+          *(v4i *)dst = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            if (col + r < N) dst[r] = v[r];
+        }
+      }
+    }
+  }
+}
+
 // B[K,N] -> B_T[N,K] (K % 16 == 0, N % 16 == 0), one 64-column strip of KT rows
 // of K per workgroup, through 64x64 LDS tiles; 4x4 byte blocks are transposed in
 // registers. Feeds gemm_i8_nt16 when the caller passes tensor_matmul's [K,N]
@@ -517,6 +697,7 @@ int launch_mfma(const GemmArgs &g, int splits, hipStream_t st) {
   const int k_span = (int)cdiv(nkt, splits) * BK;
   splits = (int)cdiv(g.K, k_span);
   dim3 grid(tiles_m * tiles_n, splits), block(WGM * WGN * 64);
+  KernelTimer kt(st, "gemm_i8_mfma");
   if (splits > 1) {
     const int64_t tot = (int64_t)g.M * g.N;
     hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C, g.ldc,
@@ -569,6 +750,7 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       if (AU8)
         hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
                            (int64_t)g.N, 1, g.N);
+      KernelTimer kt(st, "transpose_i8");
       hipLaunchKernelGGL(transpose_i8<KT>, dim3((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.K, KT)),
                          dim3(256), 0, st, g.B, g.ldb, bt, g.K, g.N, colsum);
       h.B = bt;
@@ -578,9 +760,19 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
                          colsum, g.N, g.K);
     }
     const int tm = (int)cdiv(g.M, 256), tn = (int)cdiv(g.N, 256);
-    hipLaunchKernelGGL((gemm_i8_nt16<256, 256, 128, 2, 4, AU8>), dim3(tm * tn), dim3(512), 0, st,
-                       h.A, h.lda, h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn,
-                       (const int32_t *)colsum);
+    if (g.K % 64 == 0) {
+      const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
+      // persistent grid: one workgroup per CU, a multiple of 8 (XCD round-robin)
+      const int grid = (int)std::max<int64_t>(8, std::min<int64_t>(cus, (int64_t)tm * tn) / 8 * 8);
+      KernelTimer kt(st, "gemm_i8_dma");
+      hipLaunchKernelGGL((gemm_i8_dma<4, AU8>), dim3(grid), dim3(512), 0, st, h.A, h.lda, h.B,
+                         h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn, (const int32_t *)colsum, vec);
+    } else {
+      KernelTimer kt(st, "gemm_i8_nt16");
+      hipLaunchKernelGGL((gemm_i8_nt16<256, 256, 128, 2, 4, AU8>), dim3(tm * tn), dim3(512), 0,
+                         st, h.A, h.lda, h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn,
+                         (const int32_t *)colsum);
+    }
     SIMP_HIP(hipGetLastError());
     return SIMP_RT_OK;
   }

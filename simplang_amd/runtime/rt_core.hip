@@ -7,6 +7,7 @@
 // (runtime/include/kernel_runner.hpp:40-56).  Here every entry point returns an
 // int32 status and leaves the message in a thread-local string.
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -14,6 +15,7 @@
 #include <mutex>
 #include <vector>
 
+#include <atomic>
 #include "rt_internal.h"
 
 namespace simp {
@@ -234,11 +236,83 @@ int check_desc1(const char *name, const void *aligned, int64_t off, int64_t size
   return SIMP_RT_OK;
 }
 
+// ------------------------------------------------------------ kernel timing
+namespace {
+struct TimedLaunch {
+  std::string name;
+  hipEvent_t start, end;
+};
+std::atomic<bool> g_timing{false};
+std::mutex g_timing_mu;
+std::vector<TimedLaunch> g_timed;
+
+void clear_timed() {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  for (auto &t : g_timed) {
+    (void)hipEventDestroy(t.start);
+    (void)hipEventDestroy(t.end);
+  }
+  g_timed.clear();
+}
+}  // namespace
+
+KernelTimer::KernelTimer(hipStream_t st, const char *name) : st_(st) {
+  if (!g_timing.load(std::memory_order_relaxed)) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+  hipEvent_t a = nullptr, b = nullptr;
+  if (hipEventCreate(&a) != hipSuccess) return;
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return;
+  }
+  if (hipEventRecord(a, st) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return;
+  }
+  end_ = b;
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  g_timed.push_back(TimedLaunch{name, a, b});
+}
+
+void KernelTimer::stop() {
+  if (!end_) return;
+  (void)hipEventRecord(end_, st_);
+  end_ = nullptr;
+}
+
 }  // namespace simp
 
 using namespace simp;
 
 extern "C" {
+
+int32_t simp_rt_timing(int32_t on) {
+  g_timing.store(false);
+  clear_timed();
+  g_timing.store(on != 0);
+  return SIMP_RT_OK;
+}
+
+int32_t simp_rt_timing_query(const char *kernel, double *total_ms, int64_t *launches) {
+  if (!kernel || !total_ms || !launches)
+    return set_error(SIMP_RT_EINVAL, "timing_query: null argument");
+  double tot = 0.0;
+  int64_t n = 0;
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  for (auto &t : g_timed) {
+    if (t.name != kernel) continue;
+    SIMP_HIP(hipEventSynchronize(t.end));
+    float ms = 0.f;
+    SIMP_HIP(hipEventElapsedTime(&ms, t.start, t.end));
+    tot += ms;
+    n++;
+  }
+  *total_ms = tot;
+  *launches = n;
+  return SIMP_RT_OK;
+}
 
 const char *simp_rt_last_error(void) { return t_err.c_str(); }
 

@@ -78,6 +78,23 @@ int num_cus();
 // may share it; calls on different streams get different buffers.
 int workspace(hipStream_t stream, size_t bytes, void **ptr);
 
+// Optional per-kernel timing (simp_rt_timing): while enabled, a KernelTimer
+// brackets the launches between its construction and stop() with HIP events on
+// their stream, recorded under the given kernel name.  Inactive (no events) when
+// timing is off or the stream is being captured.
+class KernelTimer {
+ public:
+  KernelTimer(hipStream_t st, const char *name);
+  KernelTimer(const KernelTimer &) = delete;
+  KernelTimer &operator=(const KernelTimer &) = delete;
+  void stop();
+  ~KernelTimer() { stop(); }
+
+ private:
+  hipStream_t st_;
+  hipEvent_t end_ = nullptr;
+};
+
 // Kernel launchers on device pointers, shared by the op entry points and the
 // decode step.
 int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const float *X,

@@ -298,6 +298,7 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     const bool xl = xl_bytes <= 64 * 1024;
     const bool ub4 = K / 32 <= 4 * (256 / RB);
     const size_t shm = xl ? xl_bytes : 0;
+    KernelTimer kt(st, "w4s_gemv");
 #define W4S_LAUNCH(MTV)                                                                         \
   do {                                                                                          \
     if (xl && ub4)                                                                              \
@@ -330,6 +331,7 @@ int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X,
     hipLaunchKernelGGL(w4u_generic, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, Q, S, Z, X, O,
                        rows, cols, gs, off);
   } else {
+    KernelTimer kt(st, "w4u_gemv");
     hipLaunchKernelGGL(w4u_gemv, dim3((unsigned)cdiv(rows, kRowsPerBlock)), dim3(256),
                        sizeof(float) * (size_t)(cols / 32), st, Q, S, Z, X, O, rows, cols, gs, off);
   }

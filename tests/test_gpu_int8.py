@@ -92,7 +92,8 @@ def test_int8_recipe_checksums(dev, orc):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (8192, 8192, 8192),
-                                   (4100, 4112, 4000)])   # ragged edges on the large-tile path
+                                   (4100, 4112, 4096),    # ragged M, N on the LDS-DMA kernel
+                                   (4100, 4112, 4000)])   # K % 64 != 0: register-staged kernel
 @pytest.mark.parametrize("variant", ["u8s8", "s8s8", "nt_u8s8", "nt_s8s8"])
 def test_int8_full_size_identities(dev, orc, M, N, K, variant):
     import torch
@@ -146,3 +147,25 @@ def test_int8_strided_views(dev, orc):
     out = tc_full.cpu().numpy()
     assert np.array_equal(out[:, 20:276], want)
     assert (out[:, :20] == 0).all() and (out[:, 276:] == 0).all()
+
+
+@pytest.mark.parametrize("variant", ["u8s8", "nt_s8s8"])
+def test_int8_large_tile_unaligned_c(dev, orc, variant):
+    """Large-tile kernels with a C view that is only 4-byte aligned (scalar stores)."""
+    import torch
+    M, N, K = 4096, 4096, 192
+    print(f"[int8-unaligned-c] {variant}", flush=True)
+    a, b = _inputs(M, N, K, seed=3)
+    if variant == "nt_s8s8":
+        a = a.view(np.int8)
+    want, _ = orc.matmul_i8_vnni(a, b, a_unsigned=variant == "u8s8", nthreads=8)
+    ta = torch.from_numpy(a).to(dev)
+    tb = torch.from_numpy(np.ascontiguousarray(b.T) if variant == "nt_s8s8" else b).to(dev)
+    c_full = torch.full((M, N + 4), -7, dtype=torch.int32, device=dev)
+    tc = c_full[:, 1:N + 1]
+    fn = sa.matmul_u8s8_i32 if variant == "u8s8" else sa.tensor_matmul_nt_i8
+    fn(ta, tb, tc)
+    torch.cuda.synchronize()
+    out = c_full.cpu().numpy()
+    assert np.array_equal(out[:, 1:N + 1], want)
+    assert (out[:, 0] == -7).all() and (out[:, N + 1:] == -7).all()
