@@ -105,6 +105,17 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
     const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
     int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
 
+/* tensor_matmul on packed i4 tensors: C[M,N] (i16) = A[M,K] x B[K,N], where A
+ * is passed packed as int8 [M,(K+1)/2] (two signed nibbles per byte along K, low
+ * nibble = even index) and B packed as int8 [K,(N+1)/2] along N.  Each C is the
+ * i32 sum truncated to i16.  Replaces TensorMatMulOpLowering's packed-i4 branch
+ * (src/mlir/lowering/ConvertSimpToMemRef.cpp:2953-3133) with the i4 memref
+ * packing of its type converter (:48-66); C is caller-owned. */
+int32_t simp_rt_tensor_matmul_i4(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int16_t *c_alloc, int16_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
 /* ----------------------------------------------------------------- W4 -- */
 
 /* matmul_quant(qweights, scales, zeros, input, output, rows, cols, group_size,

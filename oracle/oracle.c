@@ -12,6 +12,9 @@
  *                                reference VNNI kernel compiled in place
  *   orc_matmul_i8_vnni        -- equals orc_matmul_i8 bit for bit (both paths)
  *   orc_int8_recipe_inputs    -- recipe restated; checksum vs reference kernel
+ *   orc_matmul_i4             -- reference packed_matmul_int4<N> checksums (32, 64,
+ *                                128) on orc_int4_recipe_inputs; equals the int8
+ *                                product of the unpacked nibbles truncated to i16
  *   orc_matmul_f32_acc        -- f64 brute force, KAT 110 (tests/test_tensor_matmul_runner.cpp:39)
  *   orc_rmsnorm/softmax/silu  -- KATs of examples/llama2/kernels/test_*_host.cpp
  *   orc_matmul_quant_f5       -- closed-form KAT of test_quant_roofline.cpp:71-92
@@ -176,6 +179,55 @@ int orc_matmul_i8_vnni(const void *A, const int8_t *B, int32_t *C, int64_t M,
   }
   free(bt_owned);
   return use_vnni;
+}
+
+static inline int32_t i4_at(const uint8_t *row, int64_t e) {
+  const uint8_t byte = row[e >> 1];
+  const int nib = (e & 1) ? (byte >> 4) : (byte & 15);
+  return nib >= 8 ? nib - 16 : nib;  /* nibble | 0xF0 as s8 */
+}
+
+void orc_matmul_i4(const uint8_t *Ap, int64_t lda_p, const uint8_t *Bp, int64_t ldb_p,
+                   int16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+  /* the lowering's phases: unpack A, unpack B to B_T, i32 K-innermost sum, trunc */
+  int8_t *bt = (int8_t *)malloc((size_t)(N > 0 ? N : 1) * (size_t)(K > 0 ? K : 1));
+  for (int64_t j = 0; j < N; j++)
+    for (int64_t k = 0; k < K; k++) bt[j * K + k] = (int8_t)i4_at(Bp + k * ldb_p, j);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; i++) {
+    int8_t *a = (int8_t *)malloc((size_t)(K > 0 ? K : 1));
+    for (int64_t k = 0; k < K; k++) a[k] = (int8_t)i4_at(Ap + i * lda_p, k);
+    for (int64_t j = 0; j < N; j++) {
+      uint32_t acc = 0;  /* i32 wraparound */
+      const int8_t *b = bt + j * K;
+      for (int64_t k = 0; k < K; k++) acc += (uint32_t)(int32_t)((int16_t)a[k] * (int16_t)b[k]);
+      C[i * ldc + j] = (int16_t)(uint16_t)(acc & 0xffffu);
+    }
+    free(a);
+  }
+  free(bt);
+}
+
+void orc_int4_recipe_inputs(int64_t N, uint8_t *Ap, uint8_t *Bp) {
+  const int64_t pd = (N + 1) / 2;
+  for (int64_t i = 0; i < N; i++)
+    for (int64_t j = 0; j < N; j += 2) {
+      const int v0 = (int)((i * N + j) % 15) - 7;
+      const int v1 = j + 1 < N ? (int)((i * N + j + 1) % 15) - 7 : 0;
+      Ap[i * pd + j / 2] = (uint8_t)((v0 & 15) | ((v1 & 15) << 4));
+    }
+  for (int64_t k = 0; k < N; k++)
+    for (int64_t j = 0; j < N; j += 2) {
+      const int v0 = (int)((j * N + k) % 15) - 7;
+      const int v1 = j + 1 < N ? (int)(((j + 1) * N + k) % 15) - 7 : 0;
+      Bp[k * pd + j / 2] = (uint8_t)((v0 & 15) | ((v1 & 15) << 4));
+    }
+}
+
+int32_t orc_checksum_i16(const int16_t *C, int64_t n) {
+  uint32_t s = 0;
+  for (int64_t i = 0; i < n; i++) s += (uint32_t)(int32_t)C[i];
+  return (int32_t)s;
 }
 
 void orc_int8_recipe_inputs(int64_t N, int8_t *A, int8_t *B) {

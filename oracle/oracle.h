@@ -63,6 +63,25 @@ void orc_int8_recipe_inputs(int64_t N, int8_t *A, int8_t *B);
 /* i32 wraparound sum of n values (bench_int8_matmul_runner.cpp:57-61). */
 int32_t orc_checksum_i32(const int32_t *C, int64_t n);
 
+/* ---------------------------------------------------------------- int4 -- */
+
+/* Packed signed-nibble tensor_matmul (src/mlir/lowering/ConvertSimpToMemRef.cpp:
+ * 2953-3133): A[M,K] packed along K into bytes Ap[M, lda_p] and B[K,N] packed
+ * along N into Bp[K, ldb_p]; element e of a row sits in byte e/2, low nibble for
+ * even e, sign-extended (>= 8 -> |0xF0).  Each C[i,j] is the i32 sum over K of
+ * the products, truncated to i16 (:3119-3122). */
+void orc_matmul_i4(const uint8_t *Ap, int64_t lda_p, const uint8_t *Bp, int64_t ldb_p,
+                   int16_t *C, int64_t ldc, int64_t M, int64_t N, int64_t K);
+
+/* Deterministic packed inputs of the reference's int4 benchmark
+ * (simptensor/benchmarks/bench_int4_matmul_runner.cpp:76-113):
+ * A[i,k] = ((i*N + k) % 15) - 7 packed along k;  B[k,j] = ((j*N + k) % 15) - 7
+ * packed along j; an odd last nibble of a row is 0.  Ap and Bp are [N, (N+1)/2]. */
+void orc_int4_recipe_inputs(int64_t N, uint8_t *Ap, uint8_t *Bp);
+
+/* Sum of n i16 values as i32 (bench_int4_matmul_runner.cpp:139-143). */
+int32_t orc_checksum_i16(const int16_t *C, int64_t n);
+
 /* ------------------------------------------------------------ fp32 ops -- */
 
 /* Array builtin matmul: C += A*B on 1-D arrays viewed as row-major matrices

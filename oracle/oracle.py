@@ -37,6 +37,9 @@ _s("orc_matmul_i8", [_P, _I, _P, _I, _P, _I, _I, _I, _I, C.c_int, C.c_int])
 _s("orc_matmul_i8_vnni", [_P, _P, _P, _I, _I, _I, C.c_int, C.c_int, C.c_int], C.c_int)
 _s("orc_int8_recipe_inputs", [_I, _P, _P])
 _s("orc_checksum_i32", [_P, _I], C.c_int32)
+_s("orc_matmul_i4", [_P, _I, _P, _I, _P, _I, _I, _I, _I])
+_s("orc_int4_recipe_inputs", [_I, _P, _P])
+_s("orc_checksum_i16", [_P, _I], C.c_int32)
 _s("orc_matmul_f32_acc", [_P, _P, _P, _I, _I, _I, _I, _I, _I])
 _s("orc_rmsnorm", [_P, _P, _P, _I, _F, _I])
 _s("orc_softmax", [_P, _P, _I, _I, _I])
@@ -145,6 +148,41 @@ def recipe_inputs(n: int):
     b = np.empty((n, n), np.int8)
     _o.orc_int8_recipe_inputs(n, _p(a), _p(b))
     return a, b
+
+
+def matmul_i4(ap, bp, m: int, n: int, k: int):
+    """Packed signed-nibble product: ap [M, >=(K+1)/2] u8 packed along K, bp
+    [K, >=(N+1)/2] u8 packed along N; returns C [M, N] i16 (i32 sum truncated)."""
+    ap = np.ascontiguousarray(ap, np.uint8)
+    bp = np.ascontiguousarray(bp, np.uint8)
+    c = np.zeros((m, n), np.int16)
+    _o.orc_matmul_i4(_p(ap), ap.shape[1] if ap.ndim == 2 else 0, _p(bp),
+                     bp.shape[1] if bp.ndim == 2 else 0, _p(c), n, m, n, k)
+    return c
+
+
+def int4_recipe_inputs(n: int):
+    pd = (n + 1) // 2
+    ap = np.zeros((n, pd), np.uint8)
+    bp = np.zeros((n, pd), np.uint8)
+    _o.orc_int4_recipe_inputs(n, _p(ap), _p(bp))
+    return ap, bp
+
+
+def checksum_i16(c) -> int:
+    c = np.ascontiguousarray(c, np.int16)
+    return int(_o.orc_checksum_i16(_p(c), c.size))
+
+
+def pack_i4(v, axis=-1):
+    """Pack signed values in [-8, 7] two per byte along `axis` (low nibble = even)."""
+    v = np.asarray(v)
+    v = np.moveaxis(v, axis, -1)
+    if v.shape[-1] % 2:
+        v = np.concatenate([v, np.zeros(v.shape[:-1] + (1,), v.dtype)], -1)
+    u = (v.astype(np.int16) & 15).astype(np.uint8)
+    p = u[..., 0::2] | (u[..., 1::2] << 4)
+    return np.ascontiguousarray(np.moveaxis(p, -1, axis))
 
 
 def checksum_i32(c) -> int:

@@ -17,6 +17,7 @@ from .host import (  # noqa: F401
     timing_query,
     tensor_matmul_i8,
     tensor_matmul_nt_i8,
+    tensor_matmul_i4,
     matmul_u8s8_i32,
     matmul_nt_u8s8_i32,
     matmul_quant,

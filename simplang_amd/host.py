@@ -51,7 +51,7 @@ def _sig(name, argtypes):
 
 
 for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
-           "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32"):
+           "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32", "simp_rt_tensor_matmul_i4"):
     _sig(_n, _D2 * 3)
 _sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
 _sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
@@ -175,6 +175,13 @@ def tensor_matmul_i8(a, b, c):
 def tensor_matmul_nt_i8(a, bt, c):
     """C[M,N] = A[M,K] x B_T[N,K]^T, s8 x s8 -> i32 (``tensor_matmul_nt``)."""
     return _gemm("simp_rt_tensor_matmul_nt_i8", a, bt, c)
+
+
+def tensor_matmul_i4(a_packed, b_packed, c):
+    """C[M,N] (int16) = A[M,K] x B[K,N] on packed signed nibbles: a_packed is
+    [M,(K+1)/2] bytes packed along K, b_packed [K,(N+1)/2] packed along N (low
+    nibble = even index); each sum is truncated to i16 (``tensor_matmul`` on i4)."""
+    return _gemm("simp_rt_tensor_matmul_i4", a_packed, b_packed, c)
 
 
 def matmul_u8s8_i32(a, b, c):

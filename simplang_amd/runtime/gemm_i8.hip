@@ -787,6 +787,80 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
   return launch_mfma<32, 64, 128, 1, 2, BNK, AU8>(g, t >= cus ? 1 : s, st);
 }
 
+// ------------------------------------------------------------------ int4 --
+// Packed signed nibbles (ConvertSimpToMemRef.cpp:2953-3133): element e of a row
+// is nibble e%2 (low = even) of byte e/2, sign-extended.  The product is formed
+// exactly on the int8 MFMA path from unpacked operands; the i32 sums are then
+// truncated to i16 (:3119-3122).
+__device__ __forceinline__ uint32_t sext4(uint32_t nib) { return (nib ^ 8u) - 8u; }
+
+// A[rows, K] packed along K (rows of ldp bytes) -> out[rows, Kp] s8, zero for
+// K <= k < Kp (Kp % 16 == 0).  One thread per 16 outputs (8 packed bytes).
+__global__ void __launch_bounds__(256)
+    unpack_i4_rows(const uint8_t *__restrict__ P, int64_t ldp, int8_t *__restrict__ out,
+                   int64_t ldo, int rows, int K, int Kp) {
+  const int64_t chunks = Kp / 16;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)rows * chunks) return;
+  const int64_t r = idx / chunks;
+  const int c = (int)(idx - r * chunks);
+  const uint8_t *src = P + r * ldp;
+  uint32_t w[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const int byte = c * 8 + q * 2 + b, e = 2 * byte;
+      const uint32_t v = e < K ? src[byte] : 0u;
+      const uint32_t lo = sext4(v & 15u) & 255u;
+      const uint32_t hi = e + 1 < K ? sext4(v >> 4) & 255u : 0u;  // odd K: pad nibble
+      word |= (lo | (hi << 8)) << (16 * b);
+    }
+    w[q] = word;
+  }
+  *(uint4 *)(out + r * ldo + 16 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// B[K, N] packed along N (rows of ldp bytes) -> B_T[N, Kp] s8 (row pitch ldt),
+// zero for K <= k < Kp, through a 64x64 LDS tile.
+__global__ void __launch_bounds__(256)
+    unpack_i4_transpose(const uint8_t *__restrict__ P, int64_t ldp, int8_t *__restrict__ BT,
+                        int64_t ldt, int K, int N, int Kp) {
+  __shared__ uint8_t s[64][64 + 4];
+  const int t = threadIdx.x;
+  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  {
+    const int k = t >> 2, c = t & 3, gk = k0 + k;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const int n = n0 + 16 * c + 2 * b;  // even element of the pair
+      const uint32_t v = (gk < K && n < N) ? P[(int64_t)gk * ldp + n / 2] : 0u;
+      s[k][16 * c + 2 * b] = (uint8_t)sext4(v & 15u);
+      s[k][16 * c + 2 * b + 1] = n + 1 < N ? (uint8_t)sext4(v >> 4) : (uint8_t)0;
+    }
+  }
+  __syncthreads();
+  {
+    const int n = t >> 2, c = t & 3;
+    const int gn = n0 + n, gk = k0 + 16 * c;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 16; j++) w[j >> 2] |= (uint32_t)s[16 * c + j][n] << (8 * (j & 3));
+    if (gn < N && gk < Kp) *(uint4 *)(BT + (int64_t)gn * ldt + gk) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// C16[r, c] = (int16) C32[r, c]
+__global__ void __launch_bounds__(256)
+    store_i16(const int32_t *__restrict__ C32, int64_t ld32, int16_t *__restrict__ C, int64_t ldc,
+              int M, int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int64_t r = i / N, c = i - r * N;
+  C[r * ldc + c] = (int16_t)C32[r * ld32 + c];
+}
+
 // Shared body of the four entry points.
 template <bool BNK, bool AU8>
 int gemm_entry(const char *name, const void *a, int64_t a_off, int64_t a_s0, int64_t a_s1,
@@ -864,6 +938,58 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
   return gemm_entry<true, true>("matmul_nt_u8s8_i32", a, a_off, a_s0, a_s1, a_st0, a_st1, bt,
                                 bt_off, bt_s0, bt_s1, bt_st0, bt_st1, c, c_off, c_s0, c_s1, c_st0,
                                 c_st1);
+}
+
+int32_t simp_rt_tensor_matmul_i4(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int16_t *c_alloc, int16_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  const char *name = "tensor_matmul_i4";
+  int rc;
+  if ((rc = check_desc2("A", a, a_off, a_s0, a_s1, a_st0, a_st1))) return rc;
+  if ((rc = check_desc2("B", b, b_off, b_s0, b_s1, b_st0, b_st1))) return rc;
+  if ((rc = check_desc2("C", c, c_off, c_s0, c_s1, c_st0, c_st1))) return rc;
+  // logical sizes: M = A rows, K = B rows, N = C columns; packed widths follow
+  const int64_t M = a_s0, K = b_s0, N = c_s1;
+  if (c_s0 != M || a_s1 != (K + 1) / 2 || b_s1 != (N + 1) / 2)
+    return set_error(SIMP_RT_EINVAL,
+                     "%s: shape mismatch A[%lld,%lld] B[%lld,%lld] C[%lld,%lld] "
+                     "(packed: A[M,(K+1)/2], B[K,(N+1)/2], C[M,N])",
+                     name, (long long)a_s0, (long long)a_s1, (long long)b_s0, (long long)b_s1,
+                     (long long)c_s0, (long long)c_s1);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX - 64)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  if (M == 0 || N == 0) return SIMP_RT_OK;
+  Operand oa, ob, oc;
+  const size_t a_bytes = a_s1 ? (size_t)((M - 1) * a_st0 + a_s1) : 0;
+  const size_t b_bytes = (K && b_s1) ? (size_t)((K - 1) * b_st0 + b_s1) : 0;
+  const size_t c_bytes = (size_t)((M - 1) * c_st0 + N) * 2;
+  if ((rc = oa.bind(a + a_off, a_bytes, Operand::kIn, "A"))) return rc;
+  if ((rc = ob.bind(b + b_off, b_bytes, Operand::kIn, "B"))) return rc;
+  if ((rc = oc.bind(c + c_off, c_bytes, Operand::kOut, "C"))) return rc;
+  hipStream_t st = cur_stream();
+  // staging (workspace slot 1): A8[M,Kp] | B_T8[N,Kp] | C32[M,N], 256-byte aligned
+  const int64_t Kp = std::max<int64_t>(64, cdiv(K, 64) * 64);
+  auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+  const size_t a8 = al((size_t)M * Kp), b8 = al((size_t)N * Kp), c32 = al((size_t)M * N * 4);
+  void *ws = nullptr;
+  if ((rc = workspace(st, a8 + b8 + c32, &ws, 1))) return rc;
+  int8_t *A8 = (int8_t *)ws, *BT8 = A8 + a8;
+  int32_t *C32 = (int32_t *)(BT8 + b8);
+  hipLaunchKernelGGL(unpack_i4_rows, dim3((unsigned)cdiv(M * (Kp / 16), 256)), dim3(256), 0, st,
+                     (const uint8_t *)oa.dev(), a_st0, A8, Kp, (int)M, (int)K, (int)Kp);
+  hipLaunchKernelGGL(unpack_i4_transpose, dim3((unsigned)cdiv(N, 64), (unsigned)(Kp / 64)),
+                     dim3(256), 0, st, (const uint8_t *)ob.dev(), b_st0, BT8, Kp, (int)K, (int)N,
+                     (int)Kp);
+  SIMP_HIP(hipGetLastError());
+  GemmArgs g{A8, Kp, BT8, Kp, C32, N, (int)M, (int)N, (int)Kp};
+  if ((rc = dispatch<true, false>(g, st))) return rc;
+  hipLaunchKernelGGL(store_i16, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0, st,
+                     (const int32_t *)C32, N, (int16_t *)oc.dev(), c_st0, (int)M, (int)N);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&oa, &ob, &oc};
+  return finish(ops, 3);
 }
 
 }  // extern "C"

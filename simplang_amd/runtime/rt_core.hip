@@ -76,8 +76,11 @@ namespace {
 struct WsKey {
   int dev;
   hipStream_t stream;
+  int slot;
   bool operator<(const WsKey &o) const {
-    return dev != o.dev ? dev < o.dev : (uintptr_t)stream < (uintptr_t)o.stream;
+    if (dev != o.dev) return dev < o.dev;
+    if (stream != o.stream) return (uintptr_t)stream < (uintptr_t)o.stream;
+    return slot < o.slot;
   }
 };
 struct WsBuf {
@@ -87,11 +90,11 @@ struct WsBuf {
 std::map<WsKey, WsBuf> g_ws;
 }  // namespace
 
-int workspace(hipStream_t stream, size_t bytes, void **ptr) {
+int workspace(hipStream_t stream, size_t bytes, void **ptr, int slot) {
   int dev = ensure_device();
   if (dev < 0) return dev;
   std::lock_guard<std::mutex> lk(g_mu);
-  WsBuf &b = g_ws[WsKey{dev, stream}];
+  WsBuf &b = g_ws[WsKey{dev, stream, slot}];
   if (b.bytes < bytes) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)

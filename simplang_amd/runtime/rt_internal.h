@@ -73,10 +73,12 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Number of CUs of the current device (cached per device).
 int num_cus();
 
-// Library-owned device scratch for (current device, stream), grown on demand
-// and kept until the process ends.  Calls on one stream are ordered, so they
-// may share it; calls on different streams get different buffers.
-int workspace(hipStream_t stream, size_t bytes, void **ptr);
+// Library-owned device scratch for (current device, stream, slot), grown on
+// demand and kept until the process ends.  Calls on one stream are ordered, so
+// they may share it; calls on different streams get different buffers.  Slot 0
+// belongs to the int8 GEMM dispatch; an entry point that stages operands for it
+// (the i4 product) uses slot 1.
+int workspace(hipStream_t stream, size_t bytes, void **ptr, int slot = 0);
 
 // Optional per-kernel timing (simp_rt_timing): while enabled, a KernelTimer
 // brackets the launches between its construction and stop() with HIP events on
