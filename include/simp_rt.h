@@ -105,6 +105,15 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
     const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
     int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
 
+/* tensor_matvecmul on i8 tensors: the same s8 x s8 -> i32 product as
+ * simp_rt_tensor_matmul_i8 (A[M,K] x B[K,N], C overwritten).  Replaces
+ * TensorMatVecMulOpLowering's int8 branch (ConvertSimpToMemRef.cpp:3632-3762),
+ * whose B transpose for N < K is a layout choice made internally here too. */
+int32_t simp_rt_tensor_matvecmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
 /* tensor_matmul on packed i4 tensors: C[M,N] (i16) = A[M,K] x B[K,N], where A
  * is passed packed as int8 [M,(K+1)/2] (two signed nibbles per byte along K, low
  * nibble = even index) and B packed as int8 [K,(N+1)/2] along N.  Each C is the
@@ -164,6 +173,21 @@ int32_t simp_rt_matmul_f32(
 /* tensor_matmul on f32 tensors: C[M,N] = A[M,K] * B[K,N] into a caller buffer.
  * Replaces the f32 branch of TensorMatMulOpLowering (ConvertSimpToMemRef.cpp:3280-3284). */
 int32_t simp_rt_tensor_matmul_f32(
+    const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* tensor_matmul_nt on f32: C[M,N] = A[M,K] x B_T[N,K]^T, C overwritten.
+ * Replaces the float branch of TensorMatMulNTOpLowering (ConvertSimpToMemRef.cpp:
+ * 3445-3481).  M == 1 runs as a GEMV over the rows of B_T. */
+int32_t simp_rt_tensor_matmul_nt_f32(
+    const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const float *bt_alloc, const float *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
+    float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* tensor_matvecmul on f32: the same product as simp_rt_tensor_matmul_f32.
+ * Replaces TensorMatVecMulOpLowering's float loops (ConvertSimpToMemRef.cpp:3763-3787). */
+int32_t simp_rt_tensor_matvecmul_f32(
     const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
     const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
     float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);

@@ -18,12 +18,15 @@ from .host import (  # noqa: F401
     tensor_matmul_i8,
     tensor_matmul_nt_i8,
     tensor_matmul_i4,
+    tensor_matvecmul_i8,
     matmul_u8s8_i32,
     matmul_nt_u8s8_i32,
     matmul_quant,
     matmul_w4s,
     matmul,
     tensor_matmul_f32,
+    tensor_matmul_nt_f32,
+    tensor_matvecmul_f32,
     rmsnorm,
     softmax,
     silu,

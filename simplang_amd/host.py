@@ -51,12 +51,15 @@ def _sig(name, argtypes):
 
 
 for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
-           "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32", "simp_rt_tensor_matmul_i4"):
+           "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32", "simp_rt_tensor_matmul_i4",
+           "simp_rt_tensor_matvecmul_i8"):
     _sig(_n, _D2 * 3)
 _sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
 _sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
 _sig("simp_rt_matmul_f32", _D1 * 3 + [_I] * 6)
 _sig("simp_rt_tensor_matmul_f32", _D2 * 3)
+_sig("simp_rt_tensor_matmul_nt_f32", _D2 * 3)
+_sig("simp_rt_tensor_matvecmul_f32", _D2 * 3)
 _sig("simp_rt_rmsnorm", _D1 * 3 + [_I, C.c_double, _I])
 _sig("simp_rt_softmax", _D1 * 2 + [_I, _I, _I])
 _sig("simp_rt_silu", _D1 * 2 + [_I])
@@ -177,6 +180,11 @@ def tensor_matmul_nt_i8(a, bt, c):
     return _gemm("simp_rt_tensor_matmul_nt_i8", a, bt, c)
 
 
+def tensor_matvecmul_i8(a, b, c):
+    """``tensor_matvecmul`` on i8: the same C = A x B, s8 x s8 -> i32."""
+    return _gemm("simp_rt_tensor_matvecmul_i8", a, b, c)
+
+
 def tensor_matmul_i4(a_packed, b_packed, c):
     """C[M,N] (int16) = A[M,K] x B[K,N] on packed signed nibbles: a_packed is
     [M,(K+1)/2] bytes packed along K, b_packed [K,(N+1)/2] packed along N (low
@@ -221,6 +229,20 @@ def tensor_matmul_f32(a, b, c):
     """``tensor_matmul`` on f32 tensors: C = A B."""
     _check("simp_rt_tensor_matmul_f32",
            lib.simp_rt_tensor_matmul_f32(*desc2(a), *desc2(b), *desc2(c)))
+    return c
+
+
+def tensor_matmul_nt_f32(a, bt, c):
+    """C[M,N] = A[M,K] x B_T[N,K]^T in fp32 (``tensor_matmul_nt``), C overwritten."""
+    _check("simp_rt_tensor_matmul_nt_f32",
+           lib.simp_rt_tensor_matmul_nt_f32(*desc2(a), *desc2(bt), *desc2(c)))
+    return c
+
+
+def tensor_matvecmul_f32(a, b, c):
+    """``tensor_matvecmul`` on f32: the same C = A x B as tensor_matmul_f32."""
+    _check("simp_rt_tensor_matvecmul_f32",
+           lib.simp_rt_tensor_matvecmul_f32(*desc2(a), *desc2(b), *desc2(c)))
     return c
 
 

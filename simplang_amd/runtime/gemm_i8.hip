@@ -940,6 +940,16 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
                                 c_st1);
 }
 
+int32_t simp_rt_tensor_matvecmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  return gemm_entry<false, false>("tensor_matvecmul_i8", a, a_off, a_s0, a_s1, a_st0, a_st1, b,
+                                  b_off, b_s0, b_s1, b_st0, b_st1, c, c_off, c_s0, c_s1, c_st0,
+                                  c_st1);
+}
+
 int32_t simp_rt_tensor_matmul_i4(
     const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
     const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,

@@ -176,3 +176,42 @@ def test_matmul_general_and_tensor_matmul(dev, m, k, n):
     C = torch.full((m, n), float("nan"), device=dev)
     sa.tensor_matmul_f32(A, B, C)                 # fresh C = A B
     _close(C.cpu().numpy(), a[5:].reshape(m, k).astype(np.float64) @ b[2:].reshape(k, n))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 768, 32000), (1, 3200, 8640), (37, 53, 29), (128, 256, 96),
+                                   (1, 7, 5)])
+def test_tensor_matmul_nt_f32(dev, m, k, n):
+    """C = A B_T^T (tensor_matmul_nt float branch); M == 1 takes the GEMV path."""
+    import torch
+    rng = np.random.default_rng(m * k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bt = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    c = torch.full((m, n), float("nan"), device=dev)
+    sa.tensor_matmul_nt_f32(_t(dev, a), _t(dev, bt), c)
+    torch.cuda.synchronize()
+    want = a.astype(np.float64) @ bt.astype(np.float64).T
+    got = c.cpu().numpy()
+    for i in range(m):
+        _close(got[i], want[i])
+
+
+def test_tensor_matvecmul_f32_and_i8(dev, orc):
+    """tensor_matvecmul: the same product as tensor_matmul ([1024,1024] x [1024,64],
+    the Attn x V shape its N < K transpose targets)."""
+    import torch
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((1024, 1024)).astype(np.float32)
+    b = rng.standard_normal((1024, 64)).astype(np.float32)
+    c = torch.empty((1024, 64), device=dev)
+    sa.tensor_matvecmul_f32(_t(dev, a), _t(dev, b), c)
+    torch.cuda.synchronize()
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    got = c.cpu().numpy()
+    for i in range(0, 1024, 97):
+        _close(got[i], want[i])
+    a8 = rng.integers(-128, 128, (1024, 1024)).astype(np.int8)
+    b8 = rng.integers(-128, 128, (1024, 64)).astype(np.int8)
+    c8 = torch.full((1024, 64), -1, dtype=torch.int32, device=dev)
+    sa.tensor_matvecmul_i8(_t(dev, a8), _t(dev, b8), c8)
+    torch.cuda.synchronize()
+    assert np.array_equal(c8.cpu().numpy(), orc.matmul_i8(a8, b8))
