@@ -202,6 +202,91 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Symmetric W4 with one x vector (the decode shape).  Same lane -> row mapping
+// as w4s_gemv (RB = 8 rows per block, chunk groups g = t / 8, chunks g + 32u),
+// but no block-wide barrier before the compute: a block barrier makes every
+// wave wait for all of its outstanding weight loads (the fence drains vmcnt),
+// which serialises the unpack/FMA work behind the last byte of the transfer.
+// Instead each wave stages into its own LDS region just the x chunks its lanes
+// use, with the x loads issued before the weight loads (loads retire in issue
+// order), and each chunk's work then waits only for that chunk's bytes.
+// Requires 32 * UB >= K / 32.
+template <int UB>
+__global__ void __launch_bounds__(256)
+    w4s_gemv1(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
+              const float *__restrict__ X, float *__restrict__ O, int N, int K, int gs) {
+  constexpr int RB = 8, G = 256 / RB, GW = 64 / RB;  // chunk groups per block / per wave
+  constexpr int CW = GW * UB;                         // x chunks staged per wave
+  constexpr int XPL = CW * 8 / 64;                    // x float4 per lane
+  __shared__ float red[4][RB];
+  __shared__ __align__(16) float xw[4][CW][32];
+  __shared__ float xsw[4][CW];
+  const int nchunk = K >> 5, cpg = gs >> 5;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
+  const int n = min((int)blockIdx.x * RB + r, N - 1);  // clamped: rows past N never stored
+  const uint8_t *wrow = W + (int64_t)n * ldw;
+  const float *srow = S + (int64_t)n * lds;
+  // x of the wave's chunks: local j = u*GW + gl' holds chunk wave*GW + gl' + G*u
+  float4 xv[XPL];
+#pragma unroll
+  for (int i = 0; i < XPL; i++) {
+    const int f = lane + 64 * i, j = f >> 3, q = f & 7;
+    const int c = min(wave * GW + j % GW + G * (j / GW), nchunk - 1);
+    xv[i] = *(const float4 *)(X + 32 * c + 4 * q);
+  }
+  uint4 w[UB];
+  float sc[UB];
+#pragma unroll
+  for (int u = 0; u < UB; u++) {
+    const int c = min(g + u * G, nchunk - 1);
+    w[u] = *(const uint4 *)(wrow + 16 * c);
+    sc[u] = srow[c / cpg];
+  }
+  // stage x (float4 slots of chunk j rotated by j: the GW chunks one read touches
+  // fall in distinct banks) and the per-chunk sums of x
+#pragma unroll
+  for (int i = 0; i < XPL; i++) {
+    const int f = lane + 64 * i, j = f >> 3, q = f & 7;
+    *(float4 *)(&xw[wave][j][4 * ((q + j) & 7)]) = xv[i];
+    float t = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+    t += __shfl_xor(t, 1);
+    t += __shfl_xor(t, 2);
+    t += __shfl_xor(t, 4);
+    if (q == 0) xsw[wave][j] = t;
+  }
+  // the wave's own LDS writes are complete before its lanes read each other's
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < UB; u++) {
+    const int c = g + u * G, j = u * GW + gl;
+    if (c < nchunk) {  // uniform across the RB lanes of the group
+      uint4 wv = w[u];
+      wv.x ^= 0x88888888u; wv.y ^= 0x88888888u; wv.z ^= 0x88888888u; wv.w ^= 0x88888888u;
+      float uu[32];
+      unpack32(wv, uu);
+      float p = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 v = *(const float4 *)(&xw[wave][j][4 * ((q + j) & 7)]);
+        p = fmaf(uu[4 * q + 0], v.x, p);
+        p = fmaf(uu[4 * q + 1], v.y, p);
+        p = fmaf(uu[4 * q + 2], v.z, p);
+        p = fmaf(uu[4 * q + 3], v.w, p);
+      }
+      acc = fmaf(sc[u], fmaf(-8.f, xsw[wave][j], p), acc);  // sum (u-8) x
+    }
+  }
+#pragma unroll
+  for (int d = RB; d < 64; d <<= 1) acc += __shfl_xor(acc, d);
+  if (lane < RB) red[wave][r] = acc;
+  __syncthreads();
+  if (threadIdx.x < RB && (int)blockIdx.x * RB + (int)threadIdx.x < N)
+    O[blockIdx.x * RB + r] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+}
+
 // Reference W4 (unsigned + zero, flat groups), one x vector.  Row i's nibbles
 // start at element offset off + i*cols (a multiple of 32 here).
 __global__ void __launch_bounds__(256)
@@ -290,6 +375,18 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     const int64_t tot = (int64_t)M * N;
     hipLaunchKernelGGL(w4s_generic, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, W, ldw, S,
                        lds, X, ldx, O, ldo, M, N, K, gs);
+  } else if (M == 1 && K / 32 <= 32 * 16) {
+    // one x vector: the barrier-free kernel, UB chunks per lane with 32*UB >= K/32
+    const int nchunk = K / 32;
+    const dim3 grid((unsigned)cdiv(N, 8));
+    KernelTimer kt(st, "w4s_gemv");
+#define W4S1(U) hipLaunchKernelGGL((w4s_gemv1<U>), grid, dim3(256), 0, st, W, ldw, S, lds, X, O, N, K, gs)
+    if (nchunk <= 64) W4S1(2);
+    else if (nchunk <= 128) W4S1(4);
+    else if (nchunk <= 256) W4S1(8);
+    else if (nchunk <= 384) W4S1(12);
+    else W4S1(16);
+#undef W4S1
   } else {
     // 8 rows per block keeps >= 400 blocks at N = 3200; x in LDS when it fits.
     constexpr int RB = 8;
