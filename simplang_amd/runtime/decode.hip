@@ -75,7 +75,7 @@ struct XStage {
       float ss = 0.f;
 #pragma unroll
       for (int k = 0; k < KP; k++) ss = fmaf(a[k], a[k], ss);
-      ss = block_sum(ss, scratch);
+      ss = block_sum_lds(ss, scratch);  // weight loads issued before stay in flight
       rms = sqrtf(ss / (float)K + eps);
     }
 #pragma unroll
@@ -130,7 +130,7 @@ __global__ void __launch_bounds__(256)
   xst.load(x0, x1, nw, K);                     // input loads first ...
   if (J > 0 && r < total_rows) load(r, a);     // ... then the first row's weights
   xst.finish(K, eps, scratch, [&](int i, float v) { xs[i] = v; });
-  __syncthreads();
+  lds_barrier();
   for (; r < total_rows; r += nw_total) {
     int row = r;
     const Seg &sgm = seg_of_row(sg, row);
@@ -213,7 +213,7 @@ __global__ void __launch_bounds__(256)
     const int c = i >> 5, j = i & 31;
     xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = v;
   });
-  __syncthreads();
+  lds_barrier();  // (LDS only: the weight batch requested above stays in flight)
   for (int c = threadIdx.x; c < nchunk; c += 256) {
     float t = 0.f;
 #pragma unroll
@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(256)
     }
     xsum[c] = t;
   }
-  __syncthreads();
+  lds_barrier();
   float acc = 0.f;
   for (int c0 = g; c0 < nchunk; c0 += G * UB) {
     if (c0 != g) load_batch(c0);

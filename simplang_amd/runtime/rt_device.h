@@ -18,6 +18,31 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Workgroup barrier for LDS traffic only: this wave's LDS operations complete
+// (lgkmcnt(0)), then s_barrier.  __syncthreads() also waits for every
+// outstanding global load of the wave (its fence drains vmcnt), which would
+// stall loads a kernel issued early on purpose; this one leaves them in flight.
+// It orders LDS only: global memory written before it is not made visible to
+// the other waves.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// block_sum through LDS with lds_barrier(): global loads stay in flight.
+__device__ __forceinline__ float block_sum_lds(float v, float *scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  lds_barrier();  // scratch may still be read by a previous call
+  if (lane == 0) scratch[wave] = v;
+  lds_barrier();
+  float t = 0.f;
+  for (int i = 0; i < nw; i++) t += scratch[i];
+  return t;
+}
+
 // Block-wide sum for blockDim.x <= 1024 (multiple of 64); every thread gets the
 // result.  `scratch` holds at least 16 floats of LDS; it is reused on return.
 __device__ __forceinline__ float block_sum(float v, float *scratch) {

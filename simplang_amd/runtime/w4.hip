@@ -22,6 +22,7 @@
 // prologue (LDS), so no per-weight sign handling is needed.  Per-chunk partial
 // dot products are scaled by the group's scale (and zero) and summed in fp32;
 // the 16 lane partials are combined with a butterfly over the lane group.
+#include "rt_device.h"
 #include "rt_internal.h"
 
 namespace simp {
@@ -83,7 +84,7 @@ __device__ __forceinline__ void chunk_sums(const float *__restrict__ X, int64_t 
     }
     xs[i] = s;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Symmetric signed W4, one scale per `gs` weights along K.  MT = max rows of x.
@@ -109,6 +110,24 @@ __global__ void __launch_bounds__(256)
   extern __shared__ float smem[];  // XL: xl[M][K] then xs[M][K/32]
   const int nchunk = K >> 5;
   float *xl = smem, *xs = smem + (XL ? M * K : 0);
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
+  const int n = min(blockIdx.x * RB + r, N - 1);  // clamped: rows past N compute, never store
+  const uint8_t *wrow = W + (int64_t)n * ldw;
+  const float *srow = S + (int64_t)n * lds;
+  const int cpg = gs >> 5;
+  uint4 w[UB];
+  float sc[UB];
+  auto load_batch = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < UB; u++) {
+      const int c = min(c0 + u * G, nchunk - 1);
+      w[u] = *(const uint4 *)(wrow + 16 * c);
+      sc[u] = srow[c / cpg];
+    }
+  };
+  // the first weight batch is requested before x is staged; the staging
+  // barriers are LDS-only, so these loads stay in flight through them
+  load_batch(g);
   if constexpr (XL) {
     for (int i = threadIdx.x; i < M * (K >> 2); i += 256) {
       const int m = i / (K >> 2), f = i - m * (K >> 2);
@@ -116,7 +135,7 @@ __global__ void __launch_bounds__(256)
       *(float4 *)(xl + m * K + 32 * c + 4 * ((q + c) & 7)) =
           *(const float4 *)(X + (int64_t)m * ldx + 4 * f);
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = threadIdx.x; i < M * nchunk; i += 256) {
       const int m = i / nchunk, c = i - m * nchunk;
       float t = 0.f;
@@ -127,25 +146,13 @@ __global__ void __launch_bounds__(256)
       }
       xs[i] = t;
     }
-    __syncthreads();
+    lds_barrier();
   }
-  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
-  const int n = min(blockIdx.x * RB + r, N - 1);  // clamped: rows past N compute, never store
-  const uint8_t *wrow = W + (int64_t)n * ldw;
-  const float *srow = S + (int64_t)n * lds;
-  const int cpg = gs >> 5;
   float acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; m++) acc[m] = 0.f;
   for (int c0 = g; c0 < nchunk; c0 += G * UB) {
-    uint4 w[UB];
-    float sc[UB];
-#pragma unroll
-    for (int u = 0; u < UB; u++) {
-      const int c = min(c0 + u * G, nchunk - 1);
-      w[u] = *(const uint4 *)(wrow + 16 * c);
-      sc[u] = srow[c / cpg];
-    }
+    if (c0 != g) load_batch(c0);
 #pragma unroll
     for (int u = 0; u < UB; u++) {
       const int c = c0 + u * G;
