@@ -285,6 +285,34 @@ int32_t simp_rt_llama_forward(simp_rt_llama *model, int64_t token, int64_t pos, 
 int32_t simp_rt_llama_generate(simp_rt_llama *model, const int32_t *prompt, int64_t n_prompt,
                                int64_t n_new, int32_t *out_tokens, int32_t use_graph);
 
+/* ------------------------------------------------ model-level exports -- */
+/* The compiled program's entry point, byte-identical signature: every f32[]
+ * argument is a rank-1 memref descriptor (alloc, aligned, offset, size, stride),
+ * followed by the nine i64 hyperparameters; one token per call, logits written,
+ * logits[0] returned.  Replaces stories110M_forward
+ * (examples/llama2/stories110M.sl:5-44) as bound by
+ * examples/llama2/generate_stories110M.cpp:15-21,136,236-257, so an unmodified
+ * host can dlopen this library instead of the compiled .so.
+ * Weights may be device memory (used in place) or host memory (mirrored once
+ * on the device as immutable and assumed unchanged afterwards).  The KV cache
+ * is kept on the device; each call copies the K and V rows at pos back into
+ * key_cache / value_cache.  The scratch activation arrays (x ... att_soft) are
+ * left untouched.  On error the return is NaN and simp_rt_last_error() says why. */
+#define SIMP_RT_DESC_F32(n) float *n##_alloc, float *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+float stories110M_forward(
+    SIMP_RT_DESC_F32(token_embedding_table), SIMP_RT_DESC_F32(rms_att_w), SIMP_RT_DESC_F32(wq),
+    SIMP_RT_DESC_F32(wk), SIMP_RT_DESC_F32(wv), SIMP_RT_DESC_F32(wo), SIMP_RT_DESC_F32(rms_ffn_w),
+    SIMP_RT_DESC_F32(w1), SIMP_RT_DESC_F32(w2), SIMP_RT_DESC_F32(w3), SIMP_RT_DESC_F32(rms_final_w),
+    SIMP_RT_DESC_F32(wcls), SIMP_RT_DESC_F32(x), SIMP_RT_DESC_F32(xb), SIMP_RT_DESC_F32(xb2),
+    SIMP_RT_DESC_F32(hb), SIMP_RT_DESC_F32(hb_silu), SIMP_RT_DESC_F32(q), SIMP_RT_DESC_F32(k),
+    SIMP_RT_DESC_F32(v), SIMP_RT_DESC_F32(att), SIMP_RT_DESC_F32(att_soft), SIMP_RT_DESC_F32(logits),
+    SIMP_RT_DESC_F32(key_cache), SIMP_RT_DESC_F32(value_cache), int64_t token, int64_t pos,
+    int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
+    int64_t vocab_size, int64_t seq_len);
+/* Frees the engines and device mirrors the model-level exports created (no
+ * reference counterpart). */
+int32_t simp_rt_forward_cache_clear(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,8 @@ from .host import (  # noqa: F401
     swiglu,
     rope,
     Llama,
+    stories110M_forward,
+    forward_cache_clear,
     W_F32,
     W_W4S,
 )

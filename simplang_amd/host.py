@@ -73,13 +73,19 @@ _sig("simp_rt_set_stream", [_P])
 _sig("simp_rt_register", [_P, _I, C.c_int32])
 _sig("simp_rt_unregister", [_P])
 _sig("simp_rt_timing", [C.c_int32])
+_sig("simp_rt_forward_cache_clear", [])
+lib.stories110M_forward.argtypes = [_P, _P, _I, _I, _I] * 25 + [_I] * 9
+lib.stories110M_forward.restype = C.c_float
 _sig("simp_rt_timing_query", [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)])
 
 
 def declared_symbols(header: str = HEADER) -> list[str]:
     """Names of the entry points include/simp_rt.h declares."""
     text = open(header).read()
-    return sorted(set(re.findall(r"\b(simp_rt_\w+)\s*\(", text)))
+    names = set(re.findall(r"\b(simp_rt_\w+)\s*\(", text))
+    # model-level exports keep the reference program's names
+    names |= set(re.findall(r"^float\s+(\w+_forward)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def _check(fn: str, rc: int):
@@ -178,6 +184,33 @@ def tensor_matmul_i8(a, b, c):
 def tensor_matmul_nt_i8(a, bt, c):
     """C[M,N] = A[M,K] x B_T[N,K]^T, s8 x s8 -> i32 (``tensor_matmul_nt``)."""
     return _gemm("simp_rt_tensor_matmul_nt_i8", a, bt, c)
+
+
+STORIES_ARRAYS = ("token_embedding_table", "rms_att_w", "wq", "wk", "wv", "wo", "rms_ffn_w",
+                  "w1", "w2", "w3", "rms_final_w", "wcls", "x", "xb", "xb2", "hb", "hb_silu",
+                  "q", "k", "v", "att", "att_soft", "logits", "key_cache", "value_cache")
+
+
+def stories110M_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_heads,
+                        n_kv_heads, vocab_size, seq_len) -> float:
+    """The compiled program's entry point (examples/llama2/stories110M.sl:5-44):
+    ``arrays`` maps the 25 f32[] parameter names to 1-D numpy arrays or torch
+    tensors; returns logits[0].  Raises on a NaN return with the library's
+    error message."""
+    args = []
+    for name in STORIES_ARRAYS:
+        args += desc1(arrays[name])
+    r = lib.stories110M_forward(*args, token, pos, dim, hidden_dim, n_layers, n_heads,
+                                n_kv_heads, vocab_size, seq_len)
+    if r != r:
+        msg = lib.simp_rt_last_error().decode()
+        if msg:
+            raise SimpRTError("stories110M_forward", -1, msg)
+    return r
+
+
+def forward_cache_clear() -> None:
+    _check("simp_rt_forward_cache_clear", lib.simp_rt_forward_cache_clear())
 
 
 def tensor_matvecmul_i8(a, b, c):

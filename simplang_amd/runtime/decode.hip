@@ -22,6 +22,9 @@
 // replayed for every token with no host round trip.
 #include <algorithm>
 #include <cmath>
+#include <limits>
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "rt_device.h"
@@ -750,6 +753,173 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
   }
   SIMP_HIP(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, st));
   SIMP_HIP(hipStreamSynchronize(st));
+  return SIMP_RT_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------- model-level drop-in exports
+// stories110M_forward with the signature of the compiled program
+// (examples/llama2/stories110M.sl:5-44 as bound by
+// examples/llama2/generate_stories110M.cpp:15-21,136): every array is a rank-1
+// memref descriptor, the call computes one token and returns logits[0].
+namespace simp {
+namespace {
+
+// One engine instance per (weights, config) seen by a model-level export.
+// Weights that are device memory are used in place; host weights are mirrored
+// once as immutable registered ranges (a reference host passes the same
+// std::vector buffers on every call and never writes them).
+struct ForwardEntry {
+  simp_rt_llama *model = nullptr;
+  std::vector<const void *> registered;
+};
+std::mutex g_fwd_mu;
+std::map<std::vector<int64_t>, ForwardEntry> g_fwd;
+
+int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *name,
+                  std::vector<const void *> &registered) {
+  if (device_view(p, bytes, dev, name) == SIMP_RT_OK) return SIMP_RT_OK;
+  int rc = simp_rt_register(p, (int64_t)bytes, SIMP_RT_REG_IMMUTABLE);
+  if (rc) return rc;
+  registered.push_back(p);
+  return device_view(p, bytes, dev, name);
+}
+
+}  // namespace
+}  // namespace simp
+
+extern "C" {
+
+#define SIMP_DESC_F32(n) float *n##_alloc, float *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+
+float stories110M_forward(
+    SIMP_DESC_F32(token_embedding_table), SIMP_DESC_F32(rms_att_w), SIMP_DESC_F32(wq),
+    SIMP_DESC_F32(wk), SIMP_DESC_F32(wv), SIMP_DESC_F32(wo), SIMP_DESC_F32(rms_ffn_w),
+    SIMP_DESC_F32(w1), SIMP_DESC_F32(w2), SIMP_DESC_F32(w3), SIMP_DESC_F32(rms_final_w),
+    SIMP_DESC_F32(wcls), SIMP_DESC_F32(x), SIMP_DESC_F32(xb), SIMP_DESC_F32(xb2), SIMP_DESC_F32(hb),
+    SIMP_DESC_F32(hb_silu), SIMP_DESC_F32(q), SIMP_DESC_F32(k), SIMP_DESC_F32(v),
+    SIMP_DESC_F32(att), SIMP_DESC_F32(att_soft), SIMP_DESC_F32(logits), SIMP_DESC_F32(key_cache),
+    SIMP_DESC_F32(value_cache), int64_t token, int64_t pos, int64_t dim, int64_t hidden_dim,
+    int64_t n_layers, int64_t n_heads, int64_t n_kv_heads, int64_t vocab_size, int64_t seq_len) {
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  // the scratch activations of the program (x ... att_soft) are not used: the
+  // engine keeps its own device buffers and leaves the caller's unchanged
+  (void)x; (void)xb; (void)xb2; (void)hb; (void)hb_silu; (void)q; (void)k; (void)v; (void)att;
+  (void)att_soft;
+  simp_rt_llama_config cfg{};
+  cfg.dim = dim;
+  cfg.hidden_dim = hidden_dim;
+  cfg.n_layers = n_layers;
+  cfg.n_heads = n_heads;
+  cfg.n_kv_heads = n_kv_heads;
+  cfg.vocab_size = vocab_size;
+  cfg.seq_len = seq_len;
+  cfg.eps = 1e-5f;         // stories110M.sl:61,185,235
+  cfg.rope_theta = 10000.f;  // stories110M.sl:86-112
+  cfg.weight_format = SIMP_RT_W_F32;
+  cfg.group_size = 32;
+  if (check_cfg(cfg)) return nan;
+  const int64_t L = n_layers, D = dim, H = hidden_dim, V = vocab_size;
+  const int64_t kvd = D * n_kv_heads / n_heads;
+  struct In { const float *p; int64_t off, size, stride, need; const char *name; };
+  const In ins[] = {
+      {token_embedding_table, token_embedding_table_off, token_embedding_table_size,
+       token_embedding_table_stride, V * D, "token_embedding_table"},
+      {rms_att_w, rms_att_w_off, rms_att_w_size, rms_att_w_stride, L * D, "rms_att_w"},
+      {wq, wq_off, wq_size, wq_stride, L * D * D, "wq"},
+      {wk, wk_off, wk_size, wk_stride, L * kvd * D, "wk"},
+      {wv, wv_off, wv_size, wv_stride, L * kvd * D, "wv"},
+      {wo, wo_off, wo_size, wo_stride, L * D * D, "wo"},
+      {rms_ffn_w, rms_ffn_w_off, rms_ffn_w_size, rms_ffn_w_stride, L * D, "rms_ffn_w"},
+      {w1, w1_off, w1_size, w1_stride, L * H * D, "w1"},
+      {w2, w2_off, w2_size, w2_stride, L * D * H, "w2"},
+      {w3, w3_off, w3_size, w3_stride, L * H * D, "w3"},
+      {rms_final_w, rms_final_w_off, rms_final_w_size, rms_final_w_stride, D, "rms_final_w"},
+      {wcls, wcls_off, wcls_size, wcls_stride, V * D, "wcls"},
+      {logits, logits_off, logits_size, logits_stride, V, "logits"},
+      {key_cache, key_cache_off, key_cache_size, key_cache_stride, L * seq_len * kvd, "key_cache"},
+      {value_cache, value_cache_off, value_cache_size, value_cache_stride, L * seq_len * kvd,
+       "value_cache"}};
+  for (const In &a : ins) {
+    if (check_desc1(a.name, a.p, a.off, a.size, a.stride)) return nan;
+    if (a.size < a.need) {
+      set_error(SIMP_RT_EINVAL, "stories110M_forward: %s has %lld elements, needs %lld", a.name,
+                (long long)a.size, (long long)a.need);
+      return nan;
+    }
+  }
+  if (token < 0 || token >= V || pos < 0 || pos >= seq_len) {
+    set_error(SIMP_RT_EINVAL, "stories110M_forward: token %lld / pos %lld out of range",
+              (long long)token, (long long)pos);
+    return nan;
+  }
+  const float *wp[12];
+  for (int i = 0; i < 12; i++) wp[i] = ins[i].p + ins[i].off;
+  std::vector<int64_t> key = {dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len};
+  for (int i = 0; i < 12; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
+  simp_rt_llama *model = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_fwd_mu);
+    ForwardEntry &e = g_fwd[key];
+    if (!e.model) {
+      const void *d[12];
+      for (int i = 0; i < 12; i++)
+        if (dev_or_mirror(wp[i], 4 * (size_t)ins[i].need, &d[i], ins[i].name, e.registered))
+          return nan;
+      simp_rt_llama_weights w{};
+      w.token_embedding = (const float *)d[0];
+      w.rms_att = (const float *)d[1];
+      w.wq = (const float *)d[2];
+      w.wk = (const float *)d[3];
+      w.wv = (const float *)d[4];
+      w.wo = (const float *)d[5];
+      w.rms_ffn = (const float *)d[6];
+      w.w1 = (const float *)d[7];
+      w.w2 = (const float *)d[8];
+      w.w3 = (const float *)d[9];
+      w.rms_final = (const float *)d[10];
+      w.wcls = (const float *)d[11];
+      if (simp_rt_llama_create(&cfg, &w, &e.model)) {
+        e.model = nullptr;
+        return nan;
+      }
+    }
+    model = e.model;
+  }
+  float *lg = logits + logits_off;
+  if (simp_rt_llama_forward(model, token, pos, lg)) return nan;
+  // the step's K and V rows at pos go back into the caller's caches
+  // ([n_layers, seq_len, kv_dim], stories110M.sl:115-121)
+  auto *m = (LlamaModel *)model;
+  const size_t pitch = 4 * (size_t)(seq_len * kvd), row = 4 * (size_t)kvd;
+  const size_t at = (size_t)(pos * kvd);
+  hipError_t e1 = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kcache + at, pitch, row,
+                                   (size_t)L, hipMemcpyDefault, m->stream);
+  hipError_t e2 = e1 == hipSuccess
+                      ? hipMemcpy2DAsync(value_cache + value_cache_off + at, pitch, m->vcache + at,
+                                         pitch, row, (size_t)L, hipMemcpyDefault, m->stream)
+                      : e1;
+  if (e2 == hipSuccess) e2 = hipStreamSynchronize(m->stream);
+  if (e2 != hipSuccess) {
+    hip_fail(e2, "stories110M_forward: KV row copy");
+    return nan;
+  }
+  // logits are on the host now (simp_rt_llama_forward synchronised)
+  float l0 = nan;
+  if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
+  return l0;
+}
+
+#undef SIMP_DESC_F32
+
+int32_t simp_rt_forward_cache_clear(void) {
+  std::lock_guard<std::mutex> lk(g_fwd_mu);
+  for (auto &kv : g_fwd) {
+    if (kv.second.model) simp_rt_llama_destroy(kv.second.model);
+    for (const void *p : kv.second.registered) (void)simp_rt_unregister(p);
+  }
+  g_fwd.clear();
   return SIMP_RT_OK;
 }
 

@@ -1,0 +1,90 @@
+"""The model-level drop-in export stories110M_forward (signature of
+examples/llama2/stories110M.sl:5-44 as bound by generate_stories110M.cpp:15-21):
+called the way the reference host calls it -- 25 host arrays as rank-1
+descriptors plus nine i64 -- and checked against the oracle's restatement of
+the program: logits within 1e-4 of max|logit|, the returned logits[0], and the
+K/V rows the call writes back into the caller's caches."""
+import numpy as np
+import pytest
+
+import simplang_amd as sa
+from simplang_amd.host import STORIES_ARRAYS
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+CFG = dict(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=512,
+           seq_len=16)
+
+
+def _host_model(seed):
+    rng = np.random.default_rng(seed)
+    d, h, L, V, S = (CFG[k] for k in ("dim", "hidden_dim", "n_layers", "vocab_size", "seq_len"))
+    kv = d * CFG["n_kv_heads"] // CFG["n_heads"]
+    r = lambda *s: (rng.standard_normal(s) * 0.02).astype(np.float32)
+    w = {"token_embedding": r(V, d), "rms_att": r(L, d) + 1, "rms_ffn": r(L, d) + 1,
+         "rms_final": r(d) + 1, "wq": r(L, d, d), "wk": r(L, kv, d), "wv": r(L, kv, d),
+         "wo": r(L, d, d), "w1": r(L, h, d), "w2": r(L, d, h), "w3": r(L, h, d), "wcls": r(V, d)}
+    arrays = {"token_embedding_table": w["token_embedding"], "rms_att_w": w["rms_att"],
+              "rms_ffn_w": w["rms_ffn"], "rms_final_w": w["rms_final"]}
+    for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls"):
+        arrays[k] = w[k]
+    arrays = {k: np.ascontiguousarray(v).reshape(-1) for k, v in arrays.items()}
+    for k, n in (("x", d), ("xb", d), ("xb2", d), ("hb", h), ("hb_silu", h), ("q", d), ("k", kv),
+                 ("v", kv), ("att", CFG["n_heads"] * S), ("att_soft", CFG["n_heads"] * S),
+                 ("logits", V), ("key_cache", L * S * kv), ("value_cache", L * S * kv)):
+        arrays[k] = np.zeros(n, np.float32)
+    return w, arrays
+
+
+def _cfg_args():
+    return (CFG["dim"], CFG["hidden_dim"], CFG["n_layers"], CFG["n_heads"], CFG["n_kv_heads"],
+            CFG["vocab_size"], CFG["seq_len"])
+
+
+def test_stories110M_forward_host_arrays(dev, orc):
+    w, arrays = _host_model(11)
+    o = orc.LlamaOracle(dict(CFG, eps=1e-5, rope_theta=10000.0, weight_format=0), w)
+    tokens = [5, 300, 17, 511, 42, 0]
+    for pos, t in enumerate(tokens):
+        print(f"[forward-export] pos={pos}", flush=True)
+        r = sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+        want = o.forward(t, pos).astype(np.float64)
+        got = arrays["logits"].astype(np.float64)
+        assert np.abs(got - want).max() <= TOL * np.abs(want).max(), pos
+        assert r == arrays["logits"][0]
+    # the caches hold the rows of every position computed so far
+    n = len(tokens) * CFG["dim"] * CFG["n_kv_heads"] // CFG["n_heads"]
+    kv = CFG["dim"] * CFG["n_kv_heads"] // CFG["n_heads"]
+    for name, ref in (("key_cache", o.kc), ("value_cache", o.vc)):
+        got = arrays[name].reshape(CFG["n_layers"], CFG["seq_len"], kv)
+        want = ref.reshape(CFG["n_layers"], CFG["seq_len"], kv)
+        used = slice(0, len(tokens))
+        assert np.abs(got[:, used] - want[:, used]).max() <= TOL * np.abs(want[:, used]).max()
+        assert (got[:, len(tokens):] == 0).all()
+    assert n > 0
+    # untouched scratch arrays (the engine keeps its own)
+    assert (arrays["x"] == 0).all() and (arrays["att"] == 0).all()
+    sa.forward_cache_clear()
+
+
+def test_stories110M_forward_device_arrays_and_errors(dev, orc):
+    import torch
+    w, arrays = _host_model(12)
+    host_logits = []
+    for pos, t in enumerate([1, 2, 3]):
+        sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+        host_logits.append(arrays["logits"].copy())
+    darr = {k: torch.from_numpy(v.copy()).to(dev) for k, v in arrays.items()}
+    for k in ("logits", "key_cache", "value_cache"):
+        darr[k].zero_()
+    for pos, t in enumerate([1, 2, 3]):
+        r = sa.stories110M_forward(darr, t, pos, *_cfg_args())
+        got = darr["logits"].cpu().numpy()
+        assert np.abs(got - host_logits[pos]).max() <= 1e-6 * np.abs(host_logits[pos]).max() + 1e-7
+        assert r == got[0]
+    with pytest.raises(sa.SimpRTError):
+        sa.stories110M_forward(arrays, 0, CFG["seq_len"], *_cfg_args())   # pos out of range
+    bad = dict(arrays, wq=arrays["wq"][:10])
+    with pytest.raises(sa.SimpRTError):
+        sa.stories110M_forward(bad, 0, 0, *_cfg_args())                   # array too short
+    sa.forward_cache_clear()
