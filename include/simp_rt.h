@@ -309,6 +309,27 @@ float stories110M_forward(
     SIMP_RT_DESC_F32(key_cache), SIMP_RT_DESC_F32(value_cache), int64_t token, int64_t pos,
     int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
     int64_t vocab_size, int64_t seq_len);
+/* The reference W4 program's entry point, byte-identical signature (f32[] and
+ * i8[] rank-1 descriptors, then token, pos, seven dims incl. group_size, and the
+ * seven element offsets of wq..w3 in qweights).  Replaces llama2_quant_forward
+ * (examples/llama2/llama2_quant.sl:7-56) as bound by
+ * examples/llama2/bench_llama_quant.cpp:15-24,320.  The layer matrices are in
+ * the reference W4 format (u4 + scale/zero per flat group, matmul_quant
+ * semantics with the offset-aware group index), the classifier is fp32 and no
+ * RoPE is applied, as in the program; dims come from the arguments.  Weights,
+ * KV cache, scratch arrays and errors are handled as for stories110M_forward. */
+#define SIMP_RT_DESC_I8(n) int8_t *n##_alloc, int8_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+float llama2_quant_forward(
+    SIMP_RT_DESC_F32(token_emb), SIMP_RT_DESC_F32(rms_att_w), SIMP_RT_DESC_F32(rms_ffn_w),
+    SIMP_RT_DESC_F32(rms_final_w), SIMP_RT_DESC_F32(wcls), SIMP_RT_DESC_I8(qweights),
+    SIMP_RT_DESC_F32(scales), SIMP_RT_DESC_F32(zeros), SIMP_RT_DESC_F32(x), SIMP_RT_DESC_F32(xb),
+    SIMP_RT_DESC_F32(xb2), SIMP_RT_DESC_F32(q), SIMP_RT_DESC_F32(k), SIMP_RT_DESC_F32(v),
+    SIMP_RT_DESC_F32(att), SIMP_RT_DESC_F32(att_soft), SIMP_RT_DESC_F32(hb),
+    SIMP_RT_DESC_F32(hb_silu), SIMP_RT_DESC_F32(hb2), SIMP_RT_DESC_F32(logits),
+    SIMP_RT_DESC_F32(key_cache), SIMP_RT_DESC_F32(value_cache), int64_t token, int64_t pos,
+    int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
+    int64_t vocab_size, int64_t seq_len, int64_t group_size, int64_t wq_off, int64_t wk_off,
+    int64_t wv_off, int64_t wo_off, int64_t w1_off, int64_t w2_off, int64_t w3_off);
 /* Frees the engines and device mirrors the model-level exports created (no
  * reference counterpart). */
 int32_t simp_rt_forward_cache_clear(void);

@@ -22,7 +22,8 @@
  *   orc_matmul_w4s            -- F6 == F5 with u = q+8, zero = -8*scale; brute force
  *   orc_rope                  -- pos 0 identity, rotation preserves pair norms,
  *                                closed-form angle for pair 0
- *   orc_llama_forward         -- parity unpinned beyond its parts: the reference
+ *   orc_llama_forward,
+ *   orc_llama_quant_forward   -- parity unpinned beyond its parts: the reference
  *                                holds no golden logits (docs/benchmark/llama_results.md:81-95)
  */
 #include "oracle.h"
@@ -498,6 +499,72 @@ void orc_llama_forward(const orc_llama_cfg *c, const orc_llama_weights *w,
   (void)sq_w4;
   orc_rmsnorm(x, w->rms_final, xb, dim, c->eps, 0);
   gemv(c, w->wcls, w->q_wcls, w->s_wcls, xb, logits, c->vocab, dim);
+  free(x); free(xb); free(xb2); free(q); free(kk); free(vv);
+  free(hb); free(hb2); free(att); free(att_soft);
+}
+
+void orc_llama_quant_forward(const orc_llama_cfg *c, const float *emb, const float *rms_att,
+                             const float *rms_ffn, const float *rms_final, const float *wcls,
+                             const uint8_t *qw, const float *scales, const float *zeros,
+                             int64_t gs, const int64_t off[7], float *key_cache,
+                             float *value_cache, int64_t token, int64_t pos, float *logits) {
+  const int64_t dim = c->dim, hid = c->hidden, hs = dim / c->n_heads;
+  const int64_t kv_dim = dim * c->n_kv_heads / c->n_heads;
+  float *x = (float *)malloc(sizeof(float) * dim);
+  float *xb = (float *)malloc(sizeof(float) * dim);
+  float *xb2 = (float *)malloc(sizeof(float) * dim);
+  float *q = (float *)malloc(sizeof(float) * dim);
+  float *kk = (float *)malloc(sizeof(float) * kv_dim);
+  float *vv = (float *)malloc(sizeof(float) * kv_dim);
+  float *hb = (float *)malloc(sizeof(float) * hid);
+  float *hb2 = (float *)malloc(sizeof(float) * hid);
+  float *att = (float *)malloc(sizeof(float) * (pos + 1));
+  float *att_soft = (float *)malloc(sizeof(float) * (pos + 1));
+  memcpy(x, emb + token * dim, sizeof(float) * dim);                 /* :61-66 */
+  for (int64_t l = 0; l < c->n_layers; l++) {
+    orc_rmsnorm(x, rms_att, xb, dim, c->eps, l * dim);                /* :73 */
+    /* :77-83, the matrix element offsets advance by rows*cols per layer */
+    orc_matmul_quant_f5(qw, scales, zeros, xb, q, dim, dim, gs, off[0] + l * dim * dim);
+    orc_matmul_quant_f5(qw, scales, zeros, xb, kk, kv_dim, dim, gs, off[1] + l * dim * kv_dim);
+    orc_matmul_quant_f5(qw, scales, zeros, xb, vv, kv_dim, dim, gs, off[2] + l * dim * kv_dim);
+    float *kc = key_cache + l * c->seq_len * kv_dim, *vc = value_cache + l * c->seq_len * kv_dim;
+    memcpy(kc + pos * kv_dim, kk, sizeof(float) * kv_dim);          /* :86-92 */
+    memcpy(vc + pos * kv_dim, vv, sizeof(float) * kv_dim);
+    const float scale = sqrtf((float)hs);
+    for (int64_t h = 0; h < c->n_heads; h++) {                       /* :95-133 */
+      const int64_t kvh = h * c->n_kv_heads / c->n_heads;
+      const float *qh = q + h * hs;
+      for (int64_t t = 0; t <= pos; t++) {
+        const float *kt = kc + t * kv_dim + kvh * hs;
+        double sc = 0.0;
+        for (int64_t i = 0; i < hs; i++) sc += (double)qh[i] * (double)kt[i];
+        att[t] = (float)sc / scale;
+      }
+      orc_softmax(att, att_soft, pos + 1, 0, 0);
+      for (int64_t i = 0; i < hs; i++) {
+        double v = 0.0;
+        for (int64_t t = 0; t <= pos; t++)
+          v += (double)att_soft[t] * (double)vc[t * kv_dim + kvh * hs + i];
+        xb2[h * hs + i] = (float)v;
+      }
+    }
+    orc_matmul_quant_f5(qw, scales, zeros, xb2, xb, dim, dim, gs, off[3] + l * dim * dim); /* :136 */
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + xb[i];            /* :139-143 */
+    orc_rmsnorm(x, rms_ffn, xb, dim, c->eps, l * dim);                /* :146 */
+    orc_matmul_quant_f5(qw, scales, zeros, xb, hb, hid, dim, gs, off[4] + l * hid * dim);
+    orc_matmul_quant_f5(qw, scales, zeros, xb, hb2, hid, dim, gs, off[6] + l * hid * dim);
+    orc_silu(hb, hb, hid);                                            /* :163 */
+    for (int64_t i = 0; i < hid; i++) hb[i] = hb[i] * hb2[i];         /* :165-169 */
+    orc_matmul_quant_f5(qw, scales, zeros, hb, xb, dim, hid, gs, off[5] + l * dim * hid);
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + xb[i];            /* :174-178 */
+  }
+  orc_rmsnorm(x, rms_final, xb, dim, c->eps, 0);                      /* :184 */
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < c->vocab; i++) {                            /* :187-196 */
+    double sm = 0.0;
+    for (int64_t j = 0; j < dim; j++) sm += (double)wcls[i * dim + j] * (double)xb[j];
+    logits[i] = (float)sm;
+  }
   free(x); free(xb); free(xb2); free(q); free(kk); free(vv);
   free(hb); free(hb2); free(att); free(att_soft);
 }

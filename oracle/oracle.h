@@ -174,6 +174,19 @@ void orc_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
                        float *key_cache, float *value_cache, int64_t token,
                        int64_t pos, float *logits);
 
+/* One token of llama2_quant_forward (examples/llama2/llama2_quant.sl:57-198):
+ * the reference's W4 format F5 for the seven layer matrices (one flat nibble
+ * array qw with scales/zeros per flat group of gs, per-matrix element offsets
+ * wq_off.. advanced per layer by rows*cols as in :77-79,136,156-158), no RoPE,
+ * score scale 1/sqrt(head_size), fp32 classifier wcls[vocab, dim].  Dims are
+ * taken from cfg (the program hard-codes 1536/6144/128, deviation D4).
+ * cfg->w4 / gs / theta are ignored; group size is `gs`. */
+void orc_llama_quant_forward(const orc_llama_cfg *cfg, const float *emb, const float *rms_att,
+                             const float *rms_ffn, const float *rms_final, const float *wcls,
+                             const uint8_t *qw, const float *scales, const float *zeros,
+                             int64_t gs, const int64_t off[7], float *key_cache,
+                             float *value_cache, int64_t token, int64_t pos, float *logits);
+
 /* Strict-'>' argmax, first maximum wins (examples/llama2/generate_stories110M.cpp:73-83). */
 int64_t orc_argmax(const float *logits, int64_t n);
 

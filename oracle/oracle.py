@@ -38,6 +38,7 @@ _s("orc_matmul_i8_vnni", [_P, _P, _P, _I, _I, _I, C.c_int, C.c_int, C.c_int], C.
 _s("orc_int8_recipe_inputs", [_I, _P, _P])
 _s("orc_checksum_i32", [_P, _I], C.c_int32)
 _s("orc_matmul_i4", [_P, _I, _P, _I, _P, _I, _I, _I, _I])
+_s("orc_llama_quant_forward", [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _P])
 _s("orc_int4_recipe_inputs", [_I, _P, _P])
 _s("orc_checksum_i16", [_P, _I], C.c_int32)
 _s("orc_matmul_f32_acc", [_P, _P, _P, _I, _I, _I, _I, _I, _I])
@@ -94,6 +95,36 @@ class LlamaOracle:
         _o.orc_llama_forward(C.byref(self.c), C.byref(self.w), self.kc.ctypes.data,
                              self.vc.ctypes.data, token, pos, logits.ctypes.data)
         return logits
+
+class LlamaQuantOracle:
+    """orc_llama_quant_forward (llama2_quant.sl) over numpy arrays named as the
+    program's parameters; keeps its own KV cache."""
+
+    def __init__(self, cfg: dict, arrays: dict, group_size: int, offsets):
+        self.cfg = cfg
+        self.a = {k: np.ascontiguousarray(v) for k, v in arrays.items()}
+        self.gs = group_size
+        self.off = (C.c_int64 * 7)(*offsets)
+        kv_dim = cfg["dim"] * cfg["n_kv_heads"] // cfg["n_heads"]
+        self.c = OrcLlamaCfg(dim=cfg["dim"], hidden=cfg["hidden_dim"], n_layers=cfg["n_layers"],
+                             n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv_heads"],
+                             vocab=cfg["vocab_size"], seq_len=cfg["seq_len"], eps=1e-5, theta=0.0,
+                             w4=0, gs=group_size)
+        n = cfg["n_layers"] * cfg["seq_len"] * kv_dim
+        self.kc = np.zeros(n, np.float32)
+        self.vc = np.zeros(n, np.float32)
+
+    def forward(self, token: int, pos: int):
+        a = self.a
+        logits = np.empty(self.cfg["vocab_size"], np.float32)
+        _o.orc_llama_quant_forward(C.byref(self.c), a["token_emb"].ctypes.data,
+                                   a["rms_att_w"].ctypes.data, a["rms_ffn_w"].ctypes.data,
+                                   a["rms_final_w"].ctypes.data, a["wcls"].ctypes.data,
+                                   a["qweights"].ctypes.data, a["scales"].ctypes.data,
+                                   a["zeros"].ctypes.data, self.gs, self.off, self.kc.ctypes.data,
+                                   self.vc.ctypes.data, token, pos, logits.ctypes.data)
+        return logits
+
 
 if ref is not None:
     for n in ("ref_scalar_vpdpbusd", "ref_hw_vpdpbusd"):

@@ -34,6 +34,7 @@ from .host import (  # noqa: F401
     rope,
     Llama,
     stories110M_forward,
+    llama2_quant_forward,
     forward_cache_clear,
     W_F32,
     W_W4S,

@@ -76,6 +76,8 @@ _sig("simp_rt_timing", [C.c_int32])
 _sig("simp_rt_forward_cache_clear", [])
 lib.stories110M_forward.argtypes = [_P, _P, _I, _I, _I] * 25 + [_I] * 9
 lib.stories110M_forward.restype = C.c_float
+lib.llama2_quant_forward.argtypes = [_P, _P, _I, _I, _I] * 22 + [_I] * 17
+lib.llama2_quant_forward.restype = C.c_float
 _sig("simp_rt_timing_query", [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)])
 
 
@@ -206,6 +208,28 @@ def stories110M_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_h
         msg = lib.simp_rt_last_error().decode()
         if msg:
             raise SimpRTError("stories110M_forward", -1, msg)
+    return r
+
+
+QUANT_ARRAYS = ("token_emb", "rms_att_w", "rms_ffn_w", "rms_final_w", "wcls", "qweights",
+                "scales", "zeros", "x", "xb", "xb2", "q", "k", "v", "att", "att_soft", "hb",
+                "hb_silu", "hb2", "logits", "key_cache", "value_cache")
+
+
+def llama2_quant_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                         vocab_size, seq_len, group_size, offsets) -> float:
+    """The reference W4 program's entry point (examples/llama2/llama2_quant.sl:7-56):
+    ``arrays`` maps its 22 array parameters to 1-D arrays (``qweights`` int8),
+    ``offsets`` = (wq, wk, wv, wo, w1, w2, w3) element offsets; returns logits[0]."""
+    args = []
+    for name in QUANT_ARRAYS:
+        args += desc1(arrays[name])
+    r = lib.llama2_quant_forward(*args, token, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                                 vocab_size, seq_len, group_size, *offsets)
+    if r != r:
+        msg = lib.simp_rt_last_error().decode()
+        if msg:
+            raise SimpRTError("llama2_quant_forward", -1, msg)
     return r
 
 

@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Attention, one 1024-thread block per head (no cross-block communication: a
+// Attention, one 1024-thread block per head (theta <= 0 skips RoPE) (no cross-block communication: a
 // device-scope fence to publish partials between blocks costs an L2 write-back
 // on this multi-XCD part, more than the whole head's work).  RoPE of q and of
 // the head's new k; the first head of a kv head stores k, v at pos.  Scores:
@@ -295,9 +295,10 @@ __global__ void __launch_bounds__(kAttnThreads)
   const float *k = qkv + dim + kvh * hs;
   const float *v = qkv + dim + kv_dim + kvh * hs;
   for (int j = 2 * threadIdx.x; j < hs; j += 2 * blockDim.x) {
-    const float freq = 1.f / powf(theta, (float)j / (float)hs);
+    // theta <= 0: no rotation (llama2_quant.sl applies no RoPE)
+    const float freq = theta > 0.f ? 1.f / powf(theta, (float)j / (float)hs) : 0.f;
     const float a = (float)pos * freq;
-    const float fcr = cosf(a), fci = sinf(a);
+    const float fcr = theta > 0.f ? cosf(a) : 1.f, fci = theta > 0.f ? sinf(a) : 0.f;
     qs[j] = q[j] * fcr - q[j + 1] * fci;
     qs[j + 1] = q[j] * fci + q[j + 1] * fcr;
     kn[j] = k[j] * fcr - k[j + 1] * fci;
@@ -913,6 +914,228 @@ float stories110M_forward(
 
 #undef SIMP_DESC_F32
 
+
+}  // extern "C"
+
+// llama2_quant_forward (examples/llama2/llama2_quant.sl:7-56 as bound by
+// examples/llama2/bench_llama_quant.cpp:15-24,320): the reference W4 program.
+// Its seven layer matrices are in the reference format (one flat nibble array,
+// u4 with a scale and zero per flat group of group_size, per-matrix element
+// offsets advanced per layer), the classifier is fp32 and there is no RoPE.
+// Dims come from the arguments (the program hard-codes 1536/6144/128).  The
+// step runs as a sequence of the library's kernels.
+namespace simp {
+namespace {
+
+__global__ void __launch_bounds__(256) add_inplace_k(float *__restrict__ x, const float *__restrict__ y, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) x[i] = x[i] + y[i];
+}
+
+// hb = silu(hb) * hb2  (llama2_quant.sl:163-169)
+__global__ void __launch_bounds__(256) swiglu_inplace_k(float *__restrict__ hb, const float *__restrict__ hb2, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const float g = hb[i];
+    hb[i] = (g / (1.f + expf(-g))) * hb2[i];
+  }
+}
+
+struct QuantModel {
+  int64_t dim, hid, L, nh, nkv, V, seq, gs, off[7];
+  int kv_dim, hs;
+  const float *emb, *rms_att, *rms_ffn, *rms_final, *wcls, *scales, *zeros;
+  const uint8_t *qw;
+  float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *qkv = nullptr, *hb = nullptr, *hb2 = nullptr,
+        *logits = nullptr, *kc = nullptr, *vc = nullptr;
+  StepState *state = nullptr;
+  std::vector<const void *> registered;
+};
+
+void quant_free(QuantModel &m) {
+  for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.xb2, (void *)m.qkv, (void *)m.hb,
+                  (void *)m.hb2, (void *)m.logits, (void *)m.kc, (void *)m.vc, (void *)m.state})
+    if (p) (void)hipFree(p);
+  for (const void *p : m.registered) (void)simp_rt_unregister(p);
+}
+
+int quant_alloc(QuantModel &m) {
+  const size_t kv = (size_t)(m.L * m.seq * m.kv_dim);
+  struct B { float **p; size_t n; };
+  const B bufs[] = {{&m.x, (size_t)m.dim}, {&m.xb, (size_t)m.dim}, {&m.xb2, (size_t)m.dim},
+                    {&m.qkv, (size_t)(m.dim + 2 * m.kv_dim)}, {&m.hb, (size_t)m.hid},
+                    {&m.hb2, (size_t)m.hid}, {&m.logits, (size_t)m.V}, {&m.kc, kv}, {&m.vc, kv}};
+  for (const B &b : bufs) {
+    if (hipMalloc((void **)b.p, 4 * b.n) != hipSuccess)
+      return set_error(SIMP_RT_ENOMEM, "llama2_quant_forward: device buffers");
+    SIMP_HIP(hipMemset(*b.p, 0, 4 * b.n));
+  }
+  if (hipMalloc((void **)&m.state, sizeof(StepState)) != hipSuccess)
+    return set_error(SIMP_RT_ENOMEM, "llama2_quant_forward: device buffers");
+  return SIMP_RT_OK;
+}
+
+int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
+  const int dim = (int)m.dim, hid = (int)m.hid, kvd = m.kv_dim, gs = (int)m.gs;
+  const float eps = 1e-5f;  // llama2_quant.sl:73,146,184
+  StepState s{(int)token, (int)pos, 0, 0};
+  SIMP_HIP(hipMemcpyAsync(m.state, &s, sizeof s, hipMemcpyHostToDevice, st));
+  SIMP_HIP(hipMemcpyAsync(m.x, m.emb + token * m.dim, 4 * (size_t)dim, hipMemcpyDeviceToDevice, st));
+  const unsigned gd = (unsigned)cdiv(dim, 256), gh = (unsigned)cdiv(hid, 256);
+  int rc;
+  for (int64_t l = 0; l < m.L; l++) {
+    if ((rc = launch_rmsnorm(m.x, m.rms_att + l * dim, m.xb, dim, eps, st))) return rc;
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv, dim, dim, gs, m.off[0] + l * m.dim * m.dim, st))) return rc;
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim, kvd, dim, gs, m.off[1] + l * m.dim * kvd, st))) return rc;
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim + kvd, kvd, dim, gs, m.off[2] + l * m.dim * kvd, st))) return rc;
+    float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
+    hipLaunchKernelGGL(attn_k, dim3((unsigned)m.nh), dim3(kAttnThreads), sizeof(float) * (size_t)m.seq,
+                       st, m.qkv, kc, vc, m.xb2, m.state, dim, kvd, (int)m.nh, (int)m.nkv, m.hs, 0.f);
+    SIMP_HIP(hipGetLastError());
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb2, m.xb, dim, dim, gs, m.off[3] + l * m.dim * m.dim, st))) return rc;
+    hipLaunchKernelGGL(add_inplace_k, dim3(gd), dim3(256), 0, st, m.x, (const float *)m.xb, dim);
+    if ((rc = launch_rmsnorm(m.x, m.rms_ffn + l * dim, m.xb, dim, eps, st))) return rc;
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.hb, hid, dim, gs, m.off[4] + l * m.hid * m.dim, st))) return rc;
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.hb2, hid, dim, gs, m.off[6] + l * m.hid * m.dim, st))) return rc;
+    hipLaunchKernelGGL(swiglu_inplace_k, dim3(gh), dim3(256), 0, st, m.hb, (const float *)m.hb2, hid);
+    if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.hb, m.xb, dim, hid, gs, m.off[5] + l * m.dim * m.hid, st))) return rc;
+    hipLaunchKernelGGL(add_inplace_k, dim3(gd), dim3(256), 0, st, m.x, (const float *)m.xb, dim);
+    SIMP_HIP(hipGetLastError());
+  }
+  if ((rc = launch_rmsnorm(m.x, m.rms_final, m.xb, dim, eps, st))) return rc;
+  return launch_matmul_f32(m.wcls, dim, m.xb, 1, m.logits, 1, (int)m.V, 1, dim, 0.f, st);
+}
+
+std::map<std::vector<int64_t>, QuantModel> g_qfwd;
+
+}  // namespace
+}  // namespace simp
+
+extern "C" {
+
+#define SIMP_DESC_F32(n) float *n##_alloc, float *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+#define SIMP_DESC_I8(n) int8_t *n##_alloc, int8_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+
+float llama2_quant_forward(
+    SIMP_DESC_F32(token_emb), SIMP_DESC_F32(rms_att_w), SIMP_DESC_F32(rms_ffn_w),
+    SIMP_DESC_F32(rms_final_w), SIMP_DESC_F32(wcls), SIMP_DESC_I8(qweights), SIMP_DESC_F32(scales),
+    SIMP_DESC_F32(zeros), SIMP_DESC_F32(x), SIMP_DESC_F32(xb), SIMP_DESC_F32(xb2), SIMP_DESC_F32(q),
+    SIMP_DESC_F32(k), SIMP_DESC_F32(v), SIMP_DESC_F32(att), SIMP_DESC_F32(att_soft),
+    SIMP_DESC_F32(hb), SIMP_DESC_F32(hb_silu), SIMP_DESC_F32(hb2), SIMP_DESC_F32(logits),
+    SIMP_DESC_F32(key_cache), SIMP_DESC_F32(value_cache), int64_t token, int64_t pos,
+    int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
+    int64_t vocab_size, int64_t seq_len, int64_t group_size, int64_t wq_off, int64_t wk_off,
+    int64_t wv_off, int64_t wo_off, int64_t w1_off, int64_t w2_off, int64_t w3_off) {
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  (void)x; (void)xb; (void)xb2; (void)q; (void)k; (void)v; (void)att; (void)att_soft; (void)hb;
+  (void)hb_silu; (void)hb2;
+  auto fail = [&](const char *msg) {
+    set_error(SIMP_RT_EINVAL, "llama2_quant_forward: %s", msg);
+    return nan;
+  };
+  if (dim <= 0 || hidden_dim <= 0 || n_layers <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      vocab_size <= 0 || seq_len <= 0 || dim % n_heads || n_heads % n_kv_heads)
+    return fail("bad model dimensions");
+  const int64_t hs = dim / n_heads, kvd = dim * n_kv_heads / n_heads;
+  if (hs % 4 || hs > 256 || 4 * seq_len > 64 * 1024 || dim > INT32_MAX || hidden_dim > INT32_MAX)
+    return fail("head_size must be a multiple of 4 and <= 256, seq_len <= 16384");
+  if (group_size <= 0) return fail("group_size must be positive");
+  if (token < 0 || token >= vocab_size || pos < 0 || pos >= seq_len)
+    return fail("token or pos out of range");
+  const int64_t L = n_layers, D = dim, H = hidden_dim;
+  const int64_t offs[7] = {wq_off, wk_off, wv_off, wo_off, w1_off, w2_off, w3_off};
+  const int64_t per[7] = {D * D, D * kvd, D * kvd, D * D, H * D, D * H, H * D};  // per-layer elements
+  int64_t end = 0;
+  for (int i = 0; i < 7; i++) {
+    if (offs[i] < 0) return fail("negative weight offset");
+    end = std::max(end, offs[i] + L * per[i]);
+  }
+  struct In { const void *p; int64_t off, size, stride, need; const char *name; };
+  const In ins[] = {
+      {token_emb, token_emb_off, token_emb_size, token_emb_stride, vocab_size * D, "token_emb"},
+      {rms_att_w, rms_att_w_off, rms_att_w_size, rms_att_w_stride, L * D, "rms_att_w"},
+      {rms_ffn_w, rms_ffn_w_off, rms_ffn_w_size, rms_ffn_w_stride, L * D, "rms_ffn_w"},
+      {rms_final_w, rms_final_w_off, rms_final_w_size, rms_final_w_stride, D, "rms_final_w"},
+      {wcls, wcls_off, wcls_size, wcls_stride, vocab_size * D, "wcls"},
+      {qweights, qweights_off, qweights_size, qweights_stride, (end + 1) / 2, "qweights"},
+      {scales, scales_off, scales_size, scales_stride, cdiv(end, group_size), "scales"},
+      {zeros, zeros_off, zeros_size, zeros_stride, cdiv(end, group_size), "zeros"},
+      {logits, logits_off, logits_size, logits_stride, vocab_size, "logits"},
+      {key_cache, key_cache_off, key_cache_size, key_cache_stride, L * seq_len * kvd, "key_cache"},
+      {value_cache, value_cache_off, value_cache_size, value_cache_stride, L * seq_len * kvd,
+       "value_cache"}};
+  for (const In &a : ins) {
+    if (check_desc1(a.name, a.p, a.off, a.size, a.stride)) return nan;
+    if (a.size < a.need) {
+      set_error(SIMP_RT_EINVAL, "llama2_quant_forward: %s has %lld elements, needs %lld", a.name,
+                (long long)a.size, (long long)a.need);
+      return nan;
+    }
+  }
+  const size_t esz[8] = {4, 4, 4, 4, 4, 1, 4, 4};
+  const void *wp[8];
+  for (int i = 0; i < 8; i++) wp[i] = (const char *)ins[i].p + esz[i] * (size_t)ins[i].off;
+  std::vector<int64_t> key = {dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len,
+                              group_size};
+  for (int i = 0; i < 7; i++) key.push_back(offs[i]);
+  for (int i = 0; i < 8; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
+  hipStream_t st = cur_stream();
+  QuantModel *m = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_fwd_mu);
+    auto it = g_qfwd.find(key);
+    if (it == g_qfwd.end()) {
+      QuantModel nm;
+      nm.dim = dim; nm.hid = hidden_dim; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
+      nm.V = vocab_size; nm.seq = seq_len; nm.gs = group_size;
+      for (int i = 0; i < 7; i++) nm.off[i] = offs[i];
+      nm.kv_dim = (int)kvd;
+      nm.hs = (int)hs;
+      const void *d[8];
+      for (int i = 0; i < 8; i++)
+        if (dev_or_mirror(wp[i], esz[i] * (size_t)ins[i].need, &d[i], ins[i].name, nm.registered)) {
+          quant_free(nm);
+          return nan;
+        }
+      nm.emb = (const float *)d[0]; nm.rms_att = (const float *)d[1]; nm.rms_ffn = (const float *)d[2];
+      nm.rms_final = (const float *)d[3]; nm.wcls = (const float *)d[4];
+      nm.qw = (const uint8_t *)d[5]; nm.scales = (const float *)d[6]; nm.zeros = (const float *)d[7];
+      if (quant_alloc(nm)) {
+        quant_free(nm);
+        return nan;
+      }
+      it = g_qfwd.emplace(key, std::move(nm)).first;
+    }
+    m = &it->second;
+  }
+  if (quant_step(*m, token, pos, st)) return nan;
+  float *lg = logits + logits_off;
+  const size_t pitch = 4 * (size_t)(seq_len * kvd), row = 4 * (size_t)kvd;
+  const size_t at = (size_t)(pos * kvd);
+  hipError_t e = hipMemcpyAsync(lg, m->logits, 4 * (size_t)vocab_size, hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kc + at, pitch, row, (size_t)L,
+                         hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(value_cache + value_cache_off + at, pitch, m->vc + at, pitch, row,
+                         (size_t)L, hipMemcpyDefault, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    hip_fail(e, "llama2_quant_forward: result copies");
+    return nan;
+  }
+  float l0 = nan;
+  if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
+  return l0;
+}
+
+#undef SIMP_DESC_F32
+#undef SIMP_DESC_I8
+
+}  // extern "C"
+
+extern "C" {
+
 int32_t simp_rt_forward_cache_clear(void) {
   std::lock_guard<std::mutex> lk(g_fwd_mu);
   for (auto &kv : g_fwd) {
@@ -920,6 +1143,11 @@ int32_t simp_rt_forward_cache_clear(void) {
     for (const void *p : kv.second.registered) (void)simp_rt_unregister(p);
   }
   g_fwd.clear();
+  for (auto &kv : g_qfwd) {
+    (void)hipDeviceSynchronize();
+    quant_free(kv.second);
+  }
+  g_qfwd.clear();
   return SIMP_RT_OK;
 }
 

@@ -88,3 +88,60 @@ def test_stories110M_forward_device_arrays_and_errors(dev, orc):
     with pytest.raises(sa.SimpRTError):
         sa.stories110M_forward(bad, 0, 0, *_cfg_args())                   # array too short
     sa.forward_cache_clear()
+
+
+QCFG = dict(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=4, vocab_size=512,
+            seq_len=16)
+
+
+def _quant_model(orc, seed, gs=128):
+    """Arrays of llama2_quant_forward built the way bench_llama_quant.cpp:157-209
+    builds them: random fp32 matrices quantized with the reference quantizer
+    into one flat qweights array, offsets in elements."""
+    rng = np.random.default_rng(seed)
+    d, h, L, V, S = (QCFG[k] for k in ("dim", "hidden_dim", "n_layers", "vocab_size", "seq_len"))
+    kv = d * QCFG["n_kv_heads"] // QCFG["n_heads"]
+    r = lambda *s: (rng.standard_normal(s) * 0.05).astype(np.float32)
+    mats = [r(L, d, d), r(L, kv, d), r(L, kv, d), r(L, d, d), r(L, h, d), r(L, d, h), r(L, h, d)]
+    qs, ss, zs, offs, at = [], [], [], [], 0
+    for m in mats:
+        q, sc, ze = orc.quantize_f5(m, gs)
+        qs.append(q); ss.append(sc); zs.append(ze); offs.append(at)
+        at += m.size
+    arrays = {"token_emb": r(V, d).ravel(), "rms_att_w": (r(L, d) + 1).ravel(),
+              "rms_ffn_w": (r(L, d) + 1).ravel(), "rms_final_w": r(d) + 1, "wcls": r(V, d).ravel(),
+              "qweights": np.concatenate(qs).view(np.int8), "scales": np.concatenate(ss),
+              "zeros": np.concatenate(zs)}
+    for k, n in (("x", d), ("xb", d), ("xb2", d), ("q", d), ("k", kv), ("v", kv),
+                 ("att", QCFG["n_heads"] * S), ("att_soft", QCFG["n_heads"] * S), ("hb", h),
+                 ("hb_silu", h), ("hb2", h), ("logits", V), ("key_cache", L * S * kv),
+                 ("value_cache", L * S * kv)):
+        arrays[k] = np.zeros(n, np.float32)
+    return arrays, offs
+
+
+def test_llama2_quant_forward_host_arrays(dev, orc):
+    gs = 128
+    arrays, offs = _quant_model(orc, 21, gs)
+    o = orc.LlamaQuantOracle(QCFG, {k: arrays[k] for k in ("token_emb", "rms_att_w", "rms_ffn_w",
+                                                           "rms_final_w", "wcls", "scales",
+                                                           "zeros")} |
+                             {"qweights": arrays["qweights"].view(np.uint8)}, gs, offs)
+    dims = tuple(QCFG[k] for k in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
+                                   "vocab_size", "seq_len"))
+    for pos, t in enumerate([50, 60, 70, 80, 90]):     # bench_llama_quant.cpp:258 tokens
+        print(f"[quant-export] pos={pos}", flush=True)
+        r = sa.llama2_quant_forward(arrays, t, pos, *dims, gs, offs)
+        want = o.forward(t, pos).astype(np.float64)
+        got = arrays["logits"].astype(np.float64)
+        assert np.abs(got - want).max() <= TOL * np.abs(want).max(), pos
+        assert r == arrays["logits"][0] and np.isfinite(r)
+    kv = QCFG["dim"] * QCFG["n_kv_heads"] // QCFG["n_heads"]
+    for name, ref in (("key_cache", o.kc), ("value_cache", o.vc)):
+        got = arrays[name].reshape(QCFG["n_layers"], QCFG["seq_len"], kv)[:, :5]
+        want = ref.reshape(QCFG["n_layers"], QCFG["seq_len"], kv)[:, :5]
+        assert np.abs(got - want).max() <= TOL * np.abs(want).max()
+    bad = dict(arrays, scales=arrays["scales"][:5])
+    with pytest.raises(sa.SimpRTError):
+        sa.llama2_quant_forward(bad, 0, 0, *dims, gs, offs)
+    sa.forward_cache_clear()
