@@ -577,43 +577,55 @@ __global__ void __launch_bounds__(512)
   }
 }
 
-// B[K,N] -> B_T[N,K] (K % 16 == 0, N % 16 == 0), one 64-column strip of KT rows
-// of K per workgroup, through 64x64 LDS tiles; 4x4 byte blocks are transposed in
-// registers. Feeds gemm_i8_nt16 when the caller passes tensor_matmul's [K,N]
-// layout; the reference materialises the same B_T (ConvertSimpToMemRef.cpp:3168-3216).
-// With colsum != nullptr (u8 x s8) it also adds each column's sum over the strip
-// into colsum[n], which the caller zero-fills first.
+// B[K,N] -> B_T[N,K] (K % 16 == 0, N % 16 == 0): a workgroup takes 128
+// columns and KT rows of B, through 128x128 LDS tiles.  Reads: 8 lanes per row,
+// 16 bytes each, so a wave reads whole 128-byte lines.  Writes: a thread
+// transposes four 4x4 byte blocks in registers and stores 16 bytes of each of
+// 4 B_T rows; 8 lanes cover 128 contiguous bytes of a row.  The reference
+// materialises the same B_T (ConvertSimpToMemRef.cpp:3168-3216).  With
+// colsum != nullptr (u8 x s8) each column's sum over the KT rows is added into
+// colsum[n], which the caller zero-fills first.
 template <int KT>
 __global__ void __launch_bounds__(256)
     transpose_i8(const int8_t *__restrict__ B, int64_t ldb, int8_t *__restrict__ BT, int K, int N,
                  int32_t *__restrict__ colsum) {
-  __shared__ uint32_t s[64][17];  // [k][n/4]; the odd row pitch spreads phase-2 reads over banks
+  constexpr int P = 33;            // LDS row pitch in words (32 words of data)
+  __shared__ uint32_t s[128 * P];  // [k][n/4]
   const int t = threadIdx.x;
-  const int n0 = blockIdx.x * 64;
+  const int n0 = blockIdx.x * 128;
   const int k_begin = blockIdx.y * KT, k_end = min(K, k_begin + KT);
-  const int lk = t >> 2, lc = t & 3;    // phase 1: row k, 16 columns 16*lc..
-  const int qn = t >> 4, qk = t & 15;   // phase 2: columns 4*qn..+3, rows 4*qk..+3
+  const int rk = t >> 3, rc = t & 7;    // phase 1: rows rk, rk+32, .., 16-byte chunk rc
+  const int qn = t >> 3, ko = t & 7;    // phase 2: columns 4qn..+3, rows 16ko..+15
   int sum[4] = {0, 0, 0, 0};
-  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
-    {
-      const int gk = k0 + lk, gn = n0 + 16 * lc;
+  for (int k0 = k_begin; k0 < k_end; k0 += 128) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int k = rk + 32 * i, gk = k0 + k, gn = n0 + 16 * rc;
       uint4 v = make_uint4(0, 0, 0, 0);
       if (gk < K && gn < N) v = *(const uint4 *)(B + (int64_t)gk * ldb + gn);
-      s[lk][4 * lc + 0] = v.x;
-      s[lk][4 * lc + 1] = v.y;
-      s[lk][4 * lc + 2] = v.z;
-      s[lk][4 * lc + 3] = v.w;
+      uint32_t *row = s + k * P + 4 * rc;
+      row[0] = v.x;
+      row[1] = v.y;
+      row[2] = v.z;
+      row[3] = v.w;
     }
     __syncthreads();
-    uint32_t o[4];
-    transpose4x4(s[4 * qk][qn], s[4 * qk + 1][qn], s[4 * qk + 2][qn], s[4 * qk + 3][qn], o[0],
-                 o[1], o[2], o[3]);
-    const int gk = k0 + 4 * qk;
+    uint32_t o[4][4];  // o[j][q]: column 4qn+j, rows 16ko+4q..+3
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int k = 16 * ko + 4 * q;
+      transpose4x4(s[k * P + qn], s[(k + 1) * P + qn], s[(k + 2) * P + qn], s[(k + 3) * P + qn],
+                   o[0][q], o[1][q], o[2][q], o[3][q]);
+    }
+    const int gk = k0 + 16 * ko;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int gn = n0 + 4 * qn + j;
-      if (gn < N && gk < K) *(uint32_t *)(BT + (int64_t)gn * K + gk) = o[j];
-      sum[j] = __builtin_amdgcn_sdot4((int)o[j], 0x01010101, sum[j], false);
+      if (gn < N && gk < K)
+        *(uint4 *)(BT + (int64_t)gn * K + gk) = make_uint4(o[j][0], o[j][1], o[j][2], o[j][3]);
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        sum[j] = __builtin_amdgcn_sdot4((int)o[j][q], 0x01010101, sum[j], false);
     }
     __syncthreads();
   }
@@ -624,9 +636,8 @@ __global__ void __launch_bounds__(256)
       v += __shfl_xor(v, 1);
       v += __shfl_xor(v, 2);
       v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 8);
       const int gn = n0 + 4 * qn + j;
-      if (qk == 0 && gn < N) atomicAdd(colsum + gn, v);
+      if (ko == 0 && gn < N) atomicAdd(colsum + gn, v);
     }
   }
 }
@@ -751,7 +762,7 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
         hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
                            (int64_t)g.N, 1, g.N);
       KernelTimer kt(st, "transpose_i8");
-      hipLaunchKernelGGL(transpose_i8<KT>, dim3((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.K, KT)),
+      hipLaunchKernelGGL(transpose_i8<KT>, dim3((unsigned)cdiv(g.N, 128), (unsigned)cdiv(g.K, KT)),
                          dim3(256), 0, st, g.B, g.ldb, bt, g.K, g.N, colsum);
       h.B = bt;
       h.ldb = g.K;
