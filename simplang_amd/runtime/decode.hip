@@ -15,8 +15,9 @@
 //   2 attention, one block per head: RoPE of q and of the head's k, store of
 //     k,v into the KV cache at pos, scores, softmax, weighted sum of V
 //   3 Wo GEMV accumulating into x (the residual add)
-//   4 W1|W3 GEMV with the FFN RMSNorm in the prologue
-//   5 W2 GEMV with silu(h1)*h3 formed in the prologue, accumulating into x
+//   4 W1|W3 GEMV with the FFN RMSNorm in the prologue; rows i of W1 and W3 are
+//     computed side by side and the epilogue writes g[i] = silu(h1[i]) * h3[i]
+//   5 W2 GEMV on g, accumulating into x
 // then a final RMSNorm+classifier GEMV and an argmax kernel that also advances
 // the step state (token, pos) on the device, so a captured step graph can be
 // replayed for every token with no host round trip.
@@ -35,7 +36,11 @@ namespace {
 
 constexpr int kMaxSeg = 3;
 
-enum Prologue { kPlain = 0, kRmsNorm = 1, kSwiGLU = 2 };
+enum Prologue { kPlain = 0, kRmsNorm = 1 };
+// GEMV output modes: store, accumulate into the output (residual add), or
+// paired rows: row i of segment 0 (W1) and of segment 1 (W3) are computed
+// together and segment 0's output receives silu(h1[i]) * h3[i].
+enum OutMode { kStore = 0, kAccum = 1, kPairSwiGLU = 2 };
 
 struct Seg {
   const void *W;    // fp32 rows [rows, K] or packed W4 rows [rows, K/2]
@@ -54,21 +59,24 @@ struct StepState {
   int token, pos, n_prompt, n_total;
 };
 
+__device__ __forceinline__ float silu_mul(float h1, float h3) {
+  return (h1 / (1.f + expf(-h1))) * h3;
+}
+
 // GEMV input staging in two phases, so that the input loads can be issued
 // before a kernel's first weight loads (vmcnt retires loads in issue order):
-//   load():   x0 (and x1 or the norm weight) into registers, KP slots per thread
+//   load():   x0 (and the norm weight) into registers, KP slots per thread
 //   finish(): the prologue math, then the result into LDS (through `put`)
 template <int PRO, int KP>
 struct XStage {
   float a[KP], b[KP];
-  __device__ __forceinline__ void load(const float *__restrict__ x0, const float *__restrict__ x1,
-                                       const float *__restrict__ nw, int K) {
+  __device__ __forceinline__ void load(const float *__restrict__ x0, const float *__restrict__ nw,
+                                       int K) {
 #pragma unroll
     for (int k = 0; k < KP; k++) {
       const int i = threadIdx.x + 256 * k;
       a[k] = i < K ? x0[i] : 0.f;
       if constexpr (PRO == kRmsNorm) b[k] = i < K ? nw[i] : 0.f;
-      if constexpr (PRO == kSwiGLU) b[k] = i < K ? x1[i] : 0.f;
     }
   }
   template <class Put>
@@ -87,7 +95,6 @@ struct XStage {
       if (i < K) {
         float v = a[k];
         if constexpr (PRO == kRmsNorm) v = (v / rms) * b[k];
-        if constexpr (PRO == kSwiGLU) v = (v / (1.f + expf(-v))) * b[k];
         put(i, v);
       }
     }
@@ -107,10 +114,13 @@ __device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
 // j*64 + lane, J per lane), x in LDS.  The wave's first row is loaded before
 // the prologue and every next row while the current one is reduced, so the
 // prologue and the reductions overlap weight traffic.  J == 0: any K (loop).
-template <int PRO, bool ACC, int J, int KP>
+// OUT == kPairSwiGLU: "row" i is the pair (W1 row i, W3 row i) of segments 0
+// and 1; the wave computes both dot products and stores silu(h1) * h3.
+template <int PRO, int OUT, int J, int KP>
 __global__ void __launch_bounds__(256)
     dgemv_f32(Segs sg, int total_rows, int K, const float *__restrict__ x0,
-              const float *__restrict__ x1, const float *__restrict__ nw, float eps) {
+              const float *__restrict__ nw, float eps) {
+  constexpr int NR = OUT == kPairSwiGLU ? 2 : 1;  // weight rows per output row
   extern __shared__ float xs[];
   __shared__ float scratch[16];
   const int lane = threadIdx.x & 63;
@@ -118,165 +128,220 @@ __global__ void __launch_bounds__(256)
   const int K4 = K >> 2;
   int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   constexpr int JJ = J > 0 ? J : 1;
-  float4 a[JJ];
-  auto load = [&](int rr, float4 (&v)[JJ]) {
+  float4 a[NR][JJ];
+  auto rowptr = [&](int rr, int e) {
     int row = rr;
-    const Seg &sgm = seg_of_row(sg, row);
-    const float4 *w = (const float4 *)((const float *)sgm.W + (int64_t)row * K);
+    const Seg &sgm = OUT == kPairSwiGLU ? sg.s[e] : seg_of_row(sg, row);
+    return (const float4 *)((const float *)sgm.W + (int64_t)row * K);
+  };
+  auto load = [&](int rr, float4 (&v)[NR][JJ]) {
 #pragma unroll
-    for (int j = 0; j < JJ; j++) {
-      const int q = lane + 64 * j;
-      v[j] = q < K4 ? w[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e = 0; e < NR; e++) {
+      const float4 *w = rowptr(rr, e);
+#pragma unroll
+      for (int j = 0; j < JJ; j++) {
+        const int q = lane + 64 * j;
+        v[e][j] = q < K4 ? w[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
   };
   XStage<PRO, KP> xst;
-  xst.load(x0, x1, nw, K);                     // input loads first ...
+  xst.load(x0, nw, K);                         // input loads first ...
   if (J > 0 && r < total_rows) load(r, a);     // ... then the first row's weights
   xst.finish(K, eps, scratch, [&](int i, float v) { xs[i] = v; });
   lds_barrier();
   for (; r < total_rows; r += nw_total) {
-    int row = r;
-    const Seg &sgm = seg_of_row(sg, row);
-    float s = 0.f;
+    float s[NR];
+#pragma unroll
+    for (int e = 0; e < NR; e++) s[e] = 0.f;
     if constexpr (J > 0) {
-      float4 b[JJ];
+      float4 b[NR][JJ];
       if (r + nw_total < total_rows) load(r + nw_total, b);
 #pragma unroll
       for (int j = 0; j < JJ; j++) {
         const int q = lane + 64 * j;
         if (q < K4) {
           const float4 xv = *(const float4 *)(xs + 4 * q);
-          s = fmaf(a[j].x, xv.x, s);
-          s = fmaf(a[j].y, xv.y, s);
-          s = fmaf(a[j].z, xv.z, s);
-          s = fmaf(a[j].w, xv.w, s);
+#pragma unroll
+          for (int e = 0; e < NR; e++) {
+            s[e] = fmaf(a[e][j].x, xv.x, s[e]);
+            s[e] = fmaf(a[e][j].y, xv.y, s[e]);
+            s[e] = fmaf(a[e][j].z, xv.z, s[e]);
+            s[e] = fmaf(a[e][j].w, xv.w, s[e]);
+          }
         }
       }
 #pragma unroll
-      for (int j = 0; j < JJ; j++) a[j] = b[j];
+      for (int e = 0; e < NR; e++)
+#pragma unroll
+        for (int j = 0; j < JJ; j++) a[e][j] = b[e][j];
     } else {
-      const float4 *w = (const float4 *)((const float *)sgm.W + (int64_t)row * K);
-      for (int q = lane; q < K4; q += 64) {
-        const float4 av = w[q];
-        const float4 xv = *(const float4 *)(xs + 4 * q);
-        s = fmaf(av.x, xv.x, s);
-        s = fmaf(av.y, xv.y, s);
-        s = fmaf(av.z, xv.z, s);
-        s = fmaf(av.w, xv.w, s);
+#pragma unroll
+      for (int e = 0; e < NR; e++) {
+        const float4 *w = rowptr(r, e);
+        for (int q = lane; q < K4; q += 64) {
+          const float4 av = w[q];
+          const float4 xv = *(const float4 *)(xs + 4 * q);
+          s[e] = fmaf(av.x, xv.x, s[e]);
+          s[e] = fmaf(av.y, xv.y, s[e]);
+          s[e] = fmaf(av.z, xv.z, s[e]);
+          s[e] = fmaf(av.w, xv.w, s[e]);
+        }
       }
     }
-    s = wave_sum(s);
-    if (lane == 0) sgm.out[row] = ACC ? sgm.out[row] + s : s;
+#pragma unroll
+    for (int e = 0; e < NR; e++) s[e] = wave_sum(s[e]);
+    if (lane == 0) {
+      int row = r;
+      const Seg &sgm = OUT == kPairSwiGLU ? sg.s[0] : seg_of_row(sg, row);
+      float *o = sgm.out + row;
+      if constexpr (OUT == kPairSwiGLU) *o = silu_mul(s[0], s[NR - 1]);
+      else *o = OUT == kAccum ? *o + s[0] : s[0];
+    }
   }
 }
 
-__device__ __forceinline__ float ubyte0(uint32_t x) { float r; asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x)); return r; }
-__device__ __forceinline__ float ubyte1(uint32_t x) { float r; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x)); return r; }
-__device__ __forceinline__ float ubyte2(uint32_t x) { float r; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x)); return r; }
-__device__ __forceinline__ float ubyte3(uint32_t x) { float r; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x)); return r; }
-
-// W4 (symmetric, group gs) multi-matrix GEMV; same lane -> row mapping as the
-// standalone W4 kernel (8 rows per block, 32 chunk groups), x staged in LDS
-// with the prologue applied and chunk-rotated, per-chunk sums of x in LDS.
-template <int PRO, bool ACC, int UB, int KP>
+// W4 (symmetric, group gs) multi-matrix GEMV: lane -> row (8 rows per block),
+// 32 chunk groups of 16-byte chunks per block, 8 per wave.  The four waves
+// partition a row's chunks (wave w takes the chunks c with c % 32 in
+// [8w, 8w + 8)), so each wave stages only its own x chunks in LDS and no block
+// barrier precedes the compute: a chunk's work waits only for its own bytes
+// (x loads are issued first, then the weights; loads retire in issue order).
+// x's float4 slots of chunk j are rotated by j (conflict-free reads), and the
+// per-chunk sums of x fold in the -8 of the q+8 nibble flip.
+//   PRO kRmsNorm: the wave stages x * norm_weight and its share of sum(x^2);
+//     the 1/rms factor multiplies the finished row sums.
+//   OUT kPairSwiGLU: lanes r < 4 take row i of segment 0 (W1), lanes r >= 4
+//     the same row of segment 1 (W3); segment 0's output gets silu(h1) * h3.
+template <int PRO, int OUT, int UB>
 __global__ void __launch_bounds__(256)
-    dgemv_w4(Segs sg, int K, int gs, const float *__restrict__ x0, const float *__restrict__ x1,
-             const float *__restrict__ nw, float eps) {
-  constexpr int RB = 8, G = 256 / RB;
-  extern __shared__ float sm[];
-  __shared__ float scratch[16];
+    dgemv_w4(Segs sg, int K, int gs, const float *__restrict__ x0, const float *__restrict__ nw,
+             float eps) {
+  constexpr int RB = 8, G = 256 / RB, GW = 64 / RB;
+  constexpr int CW = GW * UB;         // x chunks staged per wave
+  constexpr int XPL = CW * 8 / 64;    // x float4 per lane
   __shared__ float red[4][RB];
-  const int nchunk = K >> 5;
-  float *xl = sm, *xsum = sm + K;
-  XStage<PRO, KP> xst;
-  xst.load(x0, x1, nw, K);  // input loads first (vmcnt retires in issue order)
-  // this block's segment / row tile and the first batch of its weight loads
-  int si = 0;
-  while (si + 1 < sg.n && (int)blockIdx.x >= sg.s[si + 1].tile0) si++;
+  __shared__ float ssq[4];
+  __shared__ __align__(16) float xw[4][CW][32];
+  __shared__ float xsw[4][CW];
+  const int nchunk = K >> 5, cpg = gs >> 5;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
+  int si = 0, row0, rr;
+  if constexpr (OUT == kPairSwiGLU) {
+    si = r >> 2;
+    row0 = (int)blockIdx.x * (RB / 2);
+    rr = r & 3;
+  } else {
+    while (si + 1 < sg.n && (int)blockIdx.x >= sg.s[si + 1].tile0) si++;
+    row0 = ((int)blockIdx.x - sg.s[si].tile0) * RB;
+    rr = r;
+  }
   const Seg &sgm = sg.s[si];
-  const int row0 = ((int)blockIdx.x - sgm.tile0) * RB;
-  const int r = threadIdx.x % RB, g = threadIdx.x / RB;
-  const int n = min(row0 + r, sgm.rows - 1);
+  const int n = min(row0 + rr, sgm.rows - 1);  // clamped: rows past the end are never stored
   const uint8_t *wrow = (const uint8_t *)sgm.W + (int64_t)n * (K >> 1);
   const float *srow = sgm.S + (int64_t)n * (K / gs);
-  const int cpg = gs >> 5;
+  // the wave's x chunks: local j = u*GW + jj holds chunk wave*GW + jj + G*u
+  float4 xv[XPL], nv[XPL];
+#pragma unroll
+  for (int i = 0; i < XPL; i++) {
+    const int f = lane + 64 * i, j = f >> 3, q = f & 7;
+    const int c = min(wave * GW + j % GW + G * (j / GW), nchunk - 1);
+    xv[i] = *(const float4 *)(x0 + 32 * c + 4 * q);
+    if constexpr (PRO == kRmsNorm) nv[i] = *(const float4 *)(nw + 32 * c + 4 * q);
+  }
   uint4 w[UB];
   float sc[UB];
-  auto load_batch = [&](int c0) {
 #pragma unroll
-    for (int u = 0; u < UB; u++) {
-      const int c = min(c0 + u * G, nchunk - 1);
-      w[u] = *(const uint4 *)(wrow + 16 * c);
-      sc[u] = srow[c / cpg];
-    }
-  };
-  load_batch(g);
-  // prologue into LDS, chunk-rotated: element 32c + j goes to float4 slot ((j/4 + c) % 8)
-  xst.finish(K, eps, scratch, [&](int i, float v) {
-    const int c = i >> 5, j = i & 31;
-    xl[32 * c + (((j >> 2) + c) & 7) * 4 + (j & 3)] = v;
-  });
-  lds_barrier();  // (LDS only: the weight batch requested above stays in flight)
-  for (int c = threadIdx.x; c < nchunk; c += 256) {
-    float t = 0.f;
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      const float4 v = *(const float4 *)(xl + 32 * c + 4 * q);
-      t += (v.x + v.y) + (v.z + v.w);
-    }
-    xsum[c] = t;
+  for (int u = 0; u < UB; u++) {
+    const int c = min(g + u * G, nchunk - 1);
+    w[u] = *(const uint4 *)(wrow + 16 * c);
+    sc[u] = srow[c / cpg];
   }
-  lds_barrier();
-  float acc = 0.f;
-  for (int c0 = g; c0 < nchunk; c0 += G * UB) {
-    if (c0 != g) load_batch(c0);
+  float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < UB; u++) {
-      const int c = c0 + u * G;
-      if (c < nchunk) {
-        const uint32_t d[4] = {w[u].x ^ 0x88888888u, w[u].y ^ 0x88888888u, w[u].z ^ 0x88888888u,
-                               w[u].w ^ 0x88888888u};
-        float p = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const uint32_t lo = d[q] & 0x0F0F0F0Fu, hi = (d[q] >> 4) & 0x0F0F0F0Fu;
-          const float4 a = *(const float4 *)(xl + 32 * c + 4 * (((2 * q) + c) & 7));
-          const float4 b = *(const float4 *)(xl + 32 * c + 4 * (((2 * q + 1) + c) & 7));
-          p = fmaf(ubyte0(lo), a.x, p);
-          p = fmaf(ubyte0(hi), a.y, p);
-          p = fmaf(ubyte1(lo), a.z, p);
-          p = fmaf(ubyte1(hi), a.w, p);
-          p = fmaf(ubyte2(lo), b.x, p);
-          p = fmaf(ubyte2(hi), b.y, p);
-          p = fmaf(ubyte3(lo), b.z, p);
-          p = fmaf(ubyte3(hi), b.w, p);
-        }
-        acc = fmaf(sc[u], fmaf(-8.f, xsum[c], p), acc);
+  for (int i = 0; i < XPL; i++) {
+    const int f = lane + 64 * i, j = f >> 3, q = f & 7;
+    float4 v = xv[i];
+    if constexpr (PRO == kRmsNorm) {
+      if (wave * GW + j % GW + G * (j / GW) < nchunk) {  // each chunk once per block
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
       }
+      v = make_float4(v.x * nv[i].x, v.y * nv[i].y, v.z * nv[i].z, v.w * nv[i].w);
+    }
+    *(float4 *)(&xw[wave][j][4 * ((q + j) & 7)]) = v;
+    float t = (v.x + v.y) + (v.z + v.w);
+    t += __shfl_xor(t, 1);
+    t += __shfl_xor(t, 2);
+    t += __shfl_xor(t, 4);
+    if (q == 0) xsw[wave][j] = t;
+  }
+  if constexpr (PRO == kRmsNorm) {
+    ss = wave_sum(ss);
+    if (lane == 0) ssq[wave] = ss;
+  }
+  // the wave's own LDS writes are complete before its lanes read each other's
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < UB; u++) {
+    const int c = g + u * G, j = u * GW + gl;
+    if (c < nchunk) {  // uniform across the RB lanes of the group
+      uint4 wv = w[u];
+      wv.x ^= 0x88888888u; wv.y ^= 0x88888888u; wv.z ^= 0x88888888u; wv.w ^= 0x88888888u;
+      float uu[32];
+      unpack32(wv, uu);
+      float p = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 v = *(const float4 *)(&xw[wave][j][4 * ((q + j) & 7)]);
+        p = fmaf(uu[4 * q + 0], v.x, p);
+        p = fmaf(uu[4 * q + 1], v.y, p);
+        p = fmaf(uu[4 * q + 2], v.z, p);
+        p = fmaf(uu[4 * q + 3], v.w, p);
+      }
+      acc = fmaf(sc[u], fmaf(-8.f, xsw[wave][j], p), acc);  // sum (u-8) x
     }
   }
-  const int wave = threadIdx.x >> 6;
-  float v = acc;
 #pragma unroll
-  for (int dd = RB; dd < 64; dd <<= 1) v += __shfl_xor(v, dd);
-  if ((threadIdx.x & 63) < RB) red[wave][r] = v;
+  for (int d = RB; d < 64; d <<= 1) acc += __shfl_xor(acc, d);
+  if (lane < RB) red[wave][r] = acc;
   __syncthreads();
-  if (threadIdx.x < RB && row0 + (int)threadIdx.x < sgm.rows) {
-    const float t = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+  float scale = 1.f;
+  if constexpr (PRO == kRmsNorm)
+    scale = 1.f / sqrtf(((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) / (float)K + eps);
+  auto row_sum = [&](int rr2) {
+    return ((red[0][rr2] + red[1][rr2]) + (red[2][rr2] + red[3][rr2])) * scale;
+  };
+  if constexpr (OUT == kPairSwiGLU) {
+    if (threadIdx.x < RB / 2 && row0 + r < sgm.rows)  // r < 4: segment 0
+      sgm.out[row0 + r] = silu_mul(row_sum(r), row_sum(r + RB / 2));
+  } else if (threadIdx.x < RB && row0 + r < sgm.rows) {
     float *o = sgm.out + row0 + r;
-    *o = ACC ? *o + t : t;
+    const float t = row_sum(r);
+    *o = OUT == kAccum ? *o + t : t;
   }
 }
 
-// Attention, one 1024-thread block per head (theta <= 0 skips RoPE) (no cross-block communication: a
-// device-scope fence to publish partials between blocks costs an L2 write-back
-// on this multi-XCD part, more than the whole head's work).  RoPE of q and of
-// the head's new k; the first head of a kv head stores k, v at pos.  Scores:
-// 4 lanes per position, each a quarter of the head dimension in float4s.  V
-// sum: thread (d, p) sums positions p, p + P, ... with 8 loads in flight, and
-// the P partitions are added through LDS.  Uses 3*256 + seq_len + 1024 floats
-// of LDS (dynamic part: att[seq_len]).
+// Attention, one 1024-thread block per head (theta <= 0 skips RoPE).  No
+// cross-block communication: a device-scope fence to publish partials between
+// blocks costs an L2 write-back on this multi-XCD part, more than the whole
+// head's work.  Latency is the cost here, so every cache load that depends
+// only on pos is issued first, into registers: the K rows of the first 256
+// positions (4 lanes per position, a quarter of the head dimension each, as
+// float4) and up to kAttnVE V values per thread (thread (d, p) holds
+// positions p, p + P, ...; P = blockDim / head_size).  Then RoPE of q and of
+// the head's new k, the KV store at pos (first head of each kv head), scores,
+// softmax, and the V sum from registers; positions past the register window
+// are loaded in loops.  LDS: 3*256 + seq_len + 1024 floats (dynamic part:
+// att[seq_len]).
 constexpr int kAttnThreads = 1024;
+constexpr int kAttnKF = 7;   // K float4 per lane: head_size <= 112 on the register path
+constexpr int kAttnVE = 24;  // V values per thread in registers
 
 __global__ void __launch_bounds__(kAttnThreads)
     attn_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
@@ -294,8 +359,27 @@ __global__ void __launch_bounds__(kAttnThreads)
   const float *q = qkv + h * hs;
   const float *k = qkv + dim + kvh * hs;
   const float *v = qkv + dim + kv_dim + kvh * hs;
+  const float *kbase = kc + kvh * hs;
+  const float *vbase = vc + kvh * hs;
+  const int hs4 = hs >> 2;
+  const int lt = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  const int P = blockDim.x / hs;
+  const int d = threadIdx.x % hs, p = threadIdx.x / hs;
+  const int last = max(pos - 1, 0);  // clamped row index: out-of-range lanes load a valid row
+  // 1. cache loads (unconditional, clamped addresses; out-of-range values unused)
+  float vv[kAttnVE];
+#pragma unroll
+  for (int e = 0; e < kAttnVE; e++)
+    vv[e] = vbase[(int64_t)min(p + e * P, last) * kv_dim + d];
+  const bool kreg = hs4 <= 4 * kAttnKF;
+  float4 kr[kAttnKF];
+  {
+    const float4 *krow = (const float4 *)(kbase + (int64_t)min(lt, last) * kv_dim);
+#pragma unroll
+    for (int i = 0; i < kAttnKF; i++) kr[i] = krow[min(sub + 4 * i, hs4 - 1)];
+  }
+  // 2. this token's q, k, v (RoPE on q and k)
   for (int j = 2 * threadIdx.x; j < hs; j += 2 * blockDim.x) {
-    // theta <= 0: no rotation (llama2_quant.sl applies no RoPE)
     const float freq = theta > 0.f ? 1.f / powf(theta, (float)j / (float)hs) : 0.f;
     const float a = (float)pos * freq;
     const float fcr = theta > 0.f ? cosf(a) : 1.f, fci = theta > 0.f ? sinf(a) : 0.f;
@@ -314,23 +398,34 @@ __global__ void __launch_bounds__(kAttnThreads)
       vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
     }
   }
+  // 3. scores
   const float inv_scale = 1.f / sqrtf((float)hs);
-  const float *kbase = kc + kvh * hs;
-  const float *vbase = vc + kvh * hs;
-  const int hs4 = hs >> 2;
-  const int lt = threadIdx.x >> 2, sub = threadIdx.x & 3;
+  const float4 *q4 = (const float4 *)qs;
   for (int tb = 0; tb <= pos; tb += kAttnThreads / 4) {
     const int t = tb + lt;
     float sacc = 0.f;
     if (t <= pos) {
-      const float4 *kr = (const float4 *)(t == pos ? kn : kbase + (int64_t)t * kv_dim);
-      const float4 *q4 = (const float4 *)qs;
-      for (int j = sub; j < hs4; j += 4) {
-        const float4 a = kr[j], b = q4[j];
-        sacc = fmaf(a.x, b.x, sacc);
-        sacc = fmaf(a.y, b.y, sacc);
-        sacc = fmaf(a.z, b.z, sacc);
-        sacc = fmaf(a.w, b.w, sacc);
+      if (tb == 0 && t < pos && kreg) {
+#pragma unroll
+        for (int i = 0; i < kAttnKF; i++) {
+          const int j = sub + 4 * i;
+          if (j < hs4) {
+            const float4 a = kr[i], b = q4[j];
+            sacc = fmaf(a.x, b.x, sacc);
+            sacc = fmaf(a.y, b.y, sacc);
+            sacc = fmaf(a.z, b.z, sacc);
+            sacc = fmaf(a.w, b.w, sacc);
+          }
+        }
+      } else {
+        const float4 *krow = (const float4 *)(t == pos ? kn : kbase + (int64_t)t * kv_dim);
+        for (int j = sub; j < hs4; j += 4) {
+          const float4 a = krow[j], b = q4[j];
+          sacc = fmaf(a.x, b.x, sacc);
+          sacc = fmaf(a.y, b.y, sacc);
+          sacc = fmaf(a.z, b.z, sacc);
+          sacc = fmaf(a.w, b.w, sacc);
+        }
       }
     }
     sacc += __shfl_xor(sacc, 1);
@@ -338,6 +433,7 @@ __global__ void __launch_bounds__(kAttnThreads)
     if (sub == 0 && t <= pos) att[t] = sacc * inv_scale;
   }
   __syncthreads();
+  // 4. softmax
   float m = -INFINITY;
   for (int t = threadIdx.x; t <= pos; t += blockDim.x) m = fmaxf(m, att[t]);
   m = block_max(m, scratch);
@@ -348,23 +444,16 @@ __global__ void __launch_bounds__(kAttnThreads)
     l += e;
   }
   l = block_sum(l, scratch);
-  // V sum: thread (d, p), P = blockDim / hs partitions of the positions
-  const int P = blockDim.x / hs;
-  const int d = threadIdx.x % hs, p = threadIdx.x / hs;
-  float o = 0.f;
+  // 5. V sum: thread (d, p) over positions p, p + P, ...; partitions added through LDS
   if (p < P) {
-    int t = p;
-    for (; t + 7 * P <= pos; t += 8 * P) {
-      float vv[8];
+    float o = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int te = t + e * P;
-        vv[e] = te == pos ? vn[d] : vbase[(int64_t)te * kv_dim + d];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) o = fmaf(att[t + e * P], vv[e], o);
+    for (int e = 0; e < kAttnVE; e++) {
+      const int t = p + e * P;
+      if (t < pos) o = fmaf(att[t], vv[e], o);
     }
-    for (; t <= pos; t += P) o = fmaf(att[t], t == pos ? vn[d] : vbase[(int64_t)t * kv_dim + d], o);
+    for (int t = p + kAttnVE * P; t < pos; t += P) o = fmaf(att[t], vbase[(int64_t)t * kv_dim + d], o);
+    if (p == pos % P) o = fmaf(att[pos], vn[d], o);
     red[p * hs + d] = o;
   }
   __syncthreads();
@@ -435,50 +524,58 @@ struct LlamaModel {
 
 namespace {
 
-int gemv(LlamaModel &m, Segs sg, int K, int pro, bool acc, const float *x0, const float *x1,
-         const float *nw) {
+// out_mode kPairSwiGLU: segments 0 and 1 are W1 and W3 (same rows), the
+// output is segment 0's.
+int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
   const float eps = m.cfg.eps;
   hipStream_t st = m.stream;
+  const bool pair = out_mode == kPairSwiGLU;
   if (m.cfg.weight_format == SIMP_RT_W_F32) {
     int total = 0;
-    for (int i = 0; i < sg.n; i++) total += sg.s[i].rows;
+    if (pair) total = sg.s[0].rows;
+    else for (int i = 0; i < sg.n; i++) total += sg.s[i].rows;
     const unsigned grid = (unsigned)std::min<int64_t>(cdiv(total, 4), (int64_t)num_cus() * 8);
     const size_t shm = sizeof(float) * (size_t)K;
     const int J = (int)cdiv(K / 4, 64);
-#define DGJ(P, A, JV, KPV) hipLaunchKernelGGL((dgemv_f32<P, A, JV, KPV>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, x1, nw, eps)
-#define DG(P, A)                                              \
+#define DGJ(P, O, JV, KPV) hipLaunchKernelGGL((dgemv_f32<P, O, JV, KPV>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, nw, eps)
+// (paired rows hold two rows of weights per wave: the 16-slot variant is left
+// to the loop form there)
+#define DG(P, O)                                              \
   do {                                                        \
-    if (J <= 4) DGJ(P, A, 4, 4);                              \
-    else if (J <= 8) DGJ(P, A, 8, 8);                         \
-    else if (J <= 16) DGJ(P, A, 16, 16);                      \
-    else DGJ(P, A, 0, 36);                                    \
+    if (J <= 4) DGJ(P, O, 4, 4);                              \
+    else if (J <= 8) DGJ(P, O, 8, 8);                         \
+    else if (J <= 16 && O != kPairSwiGLU) DGJ(P, O, 16, 16);  \
+    else DGJ(P, O, 0, 36);                                    \
   } while (0)
-    if (pro == kRmsNorm) { if (acc) DG(kRmsNorm, true); else DG(kRmsNorm, false); }
-    else if (pro == kSwiGLU) { if (acc) DG(kSwiGLU, true); else DG(kSwiGLU, false); }
-    else { if (acc) DG(kPlain, true); else DG(kPlain, false); }
+    if (pro == kRmsNorm) { if (pair) DG(kRmsNorm, kPairSwiGLU); else DG(kRmsNorm, kStore); }
+    else { if (out_mode == kAccum) DG(kPlain, kAccum); else DG(kPlain, kStore); }
 #undef DG
 #undef DGJ
   } else {
     int tiles = 0;
-    for (int i = 0; i < sg.n; i++) {
-      sg.s[i].tile0 = tiles;
-      tiles += (int)cdiv(sg.s[i].rows, 8);
+    if (pair) {
+      tiles = (int)cdiv(sg.s[0].rows, 4);
+    } else {
+      for (int i = 0; i < sg.n; i++) {
+        sg.s[i].tile0 = tiles;
+        tiles += (int)cdiv(sg.s[i].rows, 8);
+      }
     }
-    const size_t shm = sizeof(float) * ((size_t)K + (size_t)K / 32);
     const int gs = m.cfg.group_size;
-#define DW(P, A)                                                                                        \
-  do {                                                                                                  \
-    if (K <= 1024)                                                                                      \
-      hipLaunchKernelGGL((dgemv_w4<P, A, 4, 4>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps);  \
-    else if (K <= 4096)                                                                                 \
-      hipLaunchKernelGGL((dgemv_w4<P, A, 4, 16>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
-    else                                                                                                \
-      hipLaunchKernelGGL((dgemv_w4<P, A, 8, 36>), dim3(tiles), dim3(256), shm, st, sg, K, gs, x0, x1, nw, eps); \
+    const int nchunk = K / 32;
+#define DWU(P, O, U) hipLaunchKernelGGL((dgemv_w4<P, O, U>), dim3(tiles), dim3(256), 0, st, sg, K, gs, x0, nw, eps)
+#define DW(P, O)                      \
+  do {                                \
+    if (nchunk <= 32) DWU(P, O, 1);   \
+    else if (nchunk <= 64) DWU(P, O, 2); \
+    else if (nchunk <= 128) DWU(P, O, 4); \
+    else if (nchunk <= 256) DWU(P, O, 8); \
+    else DWU(P, O, 9);                \
   } while (0)
-    if (pro == kRmsNorm) { if (acc) DW(kRmsNorm, true); else DW(kRmsNorm, false); }
-    else if (pro == kSwiGLU) { if (acc) DW(kSwiGLU, true); else DW(kSwiGLU, false); }
-    else { if (acc) DW(kPlain, true); else DW(kPlain, false); }
+    if (pro == kRmsNorm) { if (pair) DW(kRmsNorm, kPairSwiGLU); else DW(kRmsNorm, kStore); }
+    else { if (out_mode == kAccum) DW(kPlain, kAccum); else DW(kPlain, kStore); }
 #undef DW
+#undef DWU
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
@@ -499,7 +596,7 @@ int enqueue_step(LlamaModel &m) {
                      m.w.token_embedding, m.x, m.state, dim);
   SIMP_HIP(hipGetLastError());
   float *q = m.qkv, *k = m.qkv + dim, *v = m.qkv + dim + kv;
-  float *h1 = m.h13, *h3 = m.h13 + hid;
+  float *g = m.h13;  // silu(h1) * h3
   for (int l = 0; l < L; l++) {
     const int64_t lq = (int64_t)l * dim * dim, lk = (int64_t)l * kv * dim;
     const int64_t lf = (int64_t)l * hid * dim;
@@ -515,7 +612,7 @@ int enqueue_step(LlamaModel &m) {
       s.s[2] = seg_f32(m.w.wv + lk, v, kv);
     }
     s.n = 3;
-    if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_att + (int64_t)l * dim))) return rc;
+    if ((rc = gemv(m, s, dim, kRmsNorm, kStore, m.x, m.w.rms_att + (int64_t)l * dim))) return rc;
     // 2. attention (RoPE, cache store at pos, softmax, V sum), one block per head
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
     hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(kAttnThreads),
@@ -526,30 +623,30 @@ int enqueue_step(LlamaModel &m) {
     s = Segs{};
     s.s[0] = w4 ? seg_w4(m.w.q_wo + lq / 2, m.w.s_wo + lq / gs, m.x, dim) : seg_f32(m.w.wo + lq, m.x, dim);
     s.n = 1;
-    if ((rc = gemv(m, s, dim, kPlain, true, m.xb, nullptr, nullptr))) return rc;
-    // 4. W1 | W3 with the FFN RMSNorm
+    if ((rc = gemv(m, s, dim, kPlain, kAccum, m.xb, nullptr))) return rc;
+    // 4. W1 | W3 with the FFN RMSNorm, rows paired: g = silu(h1) * h3
     s = Segs{};
     if (w4) {
-      s.s[0] = seg_w4(m.w.q_w1 + lf / 2, m.w.s_w1 + lf / gs, h1, hid);
-      s.s[1] = seg_w4(m.w.q_w3 + lf / 2, m.w.s_w3 + lf / gs, h3, hid);
+      s.s[0] = seg_w4(m.w.q_w1 + lf / 2, m.w.s_w1 + lf / gs, g, hid);
+      s.s[1] = seg_w4(m.w.q_w3 + lf / 2, m.w.s_w3 + lf / gs, nullptr, hid);
     } else {
-      s.s[0] = seg_f32(m.w.w1 + lf, h1, hid);
-      s.s[1] = seg_f32(m.w.w3 + lf, h3, hid);
+      s.s[0] = seg_f32(m.w.w1 + lf, g, hid);
+      s.s[1] = seg_f32(m.w.w3 + lf, nullptr, hid);
     }
     s.n = 2;
-    if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_ffn + (int64_t)l * dim))) return rc;
-    // 5. W2 on silu(h1) * h3, accumulated into x
+    if ((rc = gemv(m, s, dim, kRmsNorm, kPairSwiGLU, m.x, m.w.rms_ffn + (int64_t)l * dim))) return rc;
+    // 5. W2 on g, accumulated into x
     s = Segs{};
     s.s[0] = w4 ? seg_w4(m.w.q_w2 + lf / 2, m.w.s_w2 + lf / gs, m.x, dim) : seg_f32(m.w.w2 + lf, m.x, dim);
     s.n = 1;
-    if ((rc = gemv(m, s, hid, kSwiGLU, true, h1, h3, nullptr))) return rc;
+    if ((rc = gemv(m, s, hid, kPlain, kAccum, g, nullptr))) return rc;
   }
   // final RMSNorm + classifier
   Segs s{};
   s.s[0] = w4 ? seg_w4(m.w.q_wcls, m.w.s_wcls, m.logits, (int)c.vocab_size)
               : seg_f32(m.w.wcls, m.logits, (int)c.vocab_size);
   s.n = 1;
-  if ((rc = gemv(m, s, dim, kRmsNorm, false, m.x, nullptr, m.w.rms_final))) return rc;
+  if ((rc = gemv(m, s, dim, kRmsNorm, kStore, m.x, m.w.rms_final))) return rc;
   hipLaunchKernelGGL(argmax_advance_k, dim3(1), dim3(1024), 0, st, m.logits, (int)c.vocab_size,
                      m.state, m.prompt, m.tokens);
   SIMP_HIP(hipGetLastError());

@@ -67,4 +67,33 @@ __device__ __forceinline__ float block_max(float v, float *scratch) {
   return t;
 }
 
+// Byte I of x as float in one v_cvt_f32_ubyte{I} (the compiler would emit a
+// bitfield extract plus ubyte0 for the equivalent shift-and-mask).
+template <int I>
+__device__ __forceinline__ float ubyte(uint32_t x) {
+  float r;
+  if constexpr (I == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (I == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (I == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// Unpacks the 32 nibbles of a 16-byte chunk into u[0..31] (u[k] = nibble k).
+__device__ __forceinline__ void unpack32(uint4 w, float (&u)[32]) {
+  const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t lo = d[i] & 0x0F0F0F0Fu, hi = (d[i] >> 4) & 0x0F0F0F0Fu;
+    u[8 * i + 0] = ubyte<0>(lo);
+    u[8 * i + 1] = ubyte<0>(hi);
+    u[8 * i + 2] = ubyte<1>(lo);
+    u[8 * i + 3] = ubyte<1>(hi);
+    u[8 * i + 4] = ubyte<2>(lo);
+    u[8 * i + 5] = ubyte<2>(hi);
+    u[8 * i + 6] = ubyte<3>(lo);
+    u[8 * i + 7] = ubyte<3>(hi);
+  }
+}
+
 }  // namespace simp
