@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(256)
   __shared__ float ssq[4];
   __shared__ __align__(16) float xw[4][CW][32];
   __shared__ float xsw[4][CW];
-  const int nchunk = K >> 5, cpg = gs >> 5;
+  const int nchunk = K >> 5, cpg = gs >> 5, cps = cpg_log2(cpg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
   int si = 0, row0, rr;
@@ -256,8 +256,10 @@ __global__ void __launch_bounds__(256)
   for (int u = 0; u < UB; u++) {
     const int c = min(g + u * G, nchunk - 1);
     w[u] = *(const uint4 *)(wrow + 16 * c);
-    sc[u] = srow[c / cpg];
+    sc[u] = srow[chunk_group(c, cpg, cps)];
   }
+  // every load above is issued before the x staging below uses any of them
+  __builtin_amdgcn_sched_barrier(0);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < XPL; i++) {

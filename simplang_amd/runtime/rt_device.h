@@ -79,6 +79,16 @@ __device__ __forceinline__ float ubyte(uint32_t x) {
   return r;
 }
 
+// Group index of 32-weight chunk c for a group size of 32 * cpg: a shift when
+// cpg is a power of two (cpg_shift = log2(cpg), else -1), since a 32-bit
+// integer division costs about twenty VALU instructions per use.
+__device__ __forceinline__ int chunk_group(int c, int cpg, int cpg_shift) {
+  return cpg_shift >= 0 ? c >> cpg_shift : c / cpg;
+}
+__device__ __forceinline__ int cpg_log2(int cpg) {
+  return (cpg & (cpg - 1)) == 0 ? __builtin_ctz((unsigned)cpg) : -1;
+}
+
 // Unpacks the 32 nibbles of a 16-byte chunk into u[0..31] (u[k] = nibble k).
 __device__ __forceinline__ void unpack32(uint4 w, float (&u)[32]) {
   const uint32_t d[4] = {w.x, w.y, w.z, w.w};

@@ -22,11 +22,22 @@
 // prologue (LDS), so no per-weight sign handling is needed.  Per-chunk partial
 // dot products are scaled by the group's scale (and zero) and summed in fp32;
 // the 16 lane partials are combined with a butterfly over the lane group.
+#include <type_traits>
+
 #include "rt_device.h"
 #include "rt_internal.h"
 
 namespace simp {
 namespace {
+
+// Calls f(std::integral_constant<int, I>()) for I = B .. E-1 (fully unrolled).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>());
+    static_for<B + 1, E>(f);
+  }
+}
 
 constexpr int kRowsPerBlock = 16;  // 16 lanes per row, 256 threads
 constexpr int kLanesPerRow = 16;
@@ -85,7 +96,7 @@ __global__ void __launch_bounds__(256)
   const int n = min(blockIdx.x * RB + r, N - 1);  // clamped: rows past N compute, never store
   const uint8_t *wrow = W + (int64_t)n * ldw;
   const float *srow = S + (int64_t)n * lds;
-  const int cpg = gs >> 5;
+  const int cpg = gs >> 5, cps = cpg_log2(cpg);
   uint4 w[UB];
   float sc[UB];
   auto load_batch = [&](int c0) {
@@ -93,7 +104,7 @@ __global__ void __launch_bounds__(256)
     for (int u = 0; u < UB; u++) {
       const int c = min(c0 + u * G, nchunk - 1);
       w[u] = *(const uint4 *)(wrow + 16 * c);
-      sc[u] = srow[c / cpg];
+      sc[u] = srow[chunk_group(c, cpg, cps)];
     }
   };
   // the first weight batch is requested before x is staged; the staging
@@ -199,7 +210,7 @@ __global__ void __launch_bounds__(256)
   __shared__ float red[4][RB];
   __shared__ __align__(16) float xw[4][CW][32];
   __shared__ float xsw[4][CW];
-  const int nchunk = K >> 5, cpg = gs >> 5;
+  const int nchunk = K >> 5, cpg = gs >> 5, cps = cpg_log2(cpg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
   const int n = min((int)blockIdx.x * RB + r, N - 1);  // clamped: rows past N never stored
@@ -219,8 +230,10 @@ __global__ void __launch_bounds__(256)
   for (int u = 0; u < UB; u++) {
     const int c = min(g + u * G, nchunk - 1);
     w[u] = *(const uint4 *)(wrow + 16 * c);
-    sc[u] = srow[c / cpg];
+    sc[u] = srow[chunk_group(c, cpg, cps)];
   }
+  // every load above is issued before the x staging below uses any of them
+  __builtin_amdgcn_sched_barrier(0);
   // stage x (float4 slots of chunk j rotated by j: the GW chunks one read touches
   // fall in distinct banks) and the per-chunk sums of x
 #pragma unroll
@@ -265,6 +278,145 @@ __global__ void __launch_bounds__(256)
     O[blockIdx.x * RB + r] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
 }
 
+// Symmetric W4, group size 32, 2 <= M <= 16 x vectors, on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32): C[m][n] = sum_g s[n][g] * sum_{k in g} x[m][k] q[n][k].
+//   * Block = 4 waves, one tile of 16 weight rows each (64 rows), and one part
+//     of at most kW4mMaxG groups of K (gridDim.y parts).  With more than one
+//     part each block writes its partial tile to P[part][M][N] and
+//     w4s_sum_parts adds the parts in order.
+//   * Every load of the block is issued up front: x of the part (staged in LDS
+//     as [k/4][m] float4, so a read of 16 rows x 16 B per lane group covers 256
+//     contiguous bytes), then each lane's weight chunks (lane (n = l%16, kq =
+//     l/16) takes groups 4s + kq of row n) and their scales.  Loads retire in
+//     issue order, so step s computes as soon as its own chunks are in.
+//   * Per step of 4 groups the wave moves its 16 rows x 64 B of chunks through
+//     a small LDS tile (row n's chunk kq in slot kq ^ (n/4), so the dword reads
+//     of one group hit 64 banks): lane (n, kq) then holds dword kq of every
+//     group, i.e. k = 8 kq + j of MFMA j, matching x[m][32g + 8kq + j].
+//   * Per group: eight MFMAs of K = 4 accumulate D = x q (exact nibble values,
+//     fp32 x and accumulation), then acc += s * D.
+constexpr int kW4mRows = 64;  // weight rows per block
+constexpr int kW4mMaxG = 12;  // K groups per block part at most (x of a part: 24 KB of LDS)
+
+// MS = steps of 4 groups per part (4 MS >= the part's groups); every step
+// runs, groups past the part multiply zero x.  Straight-line steps keep each
+// step's chunks in registers (two blocks per CU by LDS: up to 256 VGPRs).
+template <int MS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    w4s_mfma(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
+             const float *__restrict__ X, int64_t ldx, float *__restrict__ O, int64_t ldo,
+             float *__restrict__ P, int M, int N, int K) {
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  constexpr int XPT = MS * 4 * 8 * 16 / 256;  // x float4 per thread
+  __shared__ __align__(16) float4 xl[MS * 4 * 8][16];  // [k/4 within the part][m]
+  __shared__ __align__(16) uint32_t wt[4][2][16 * 16];   // [wave][buf][row*16 + slot*4 + dword]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, kq = lane >> 4;
+  const int ng = K >> 5;
+  const int part = blockIdx.y, nparts = gridDim.y;
+  const int g0 = part * ng / nparts, g1 = (part + 1) * ng / nparts;  // g1 - g0 <= 4 MS
+  const int nk4 = 8 * (g1 - g0);                                     // float4 of x per row
+  const int n = min((int)blockIdx.x * kW4mRows + 16 * wave + ln, N - 1);  // rows past N: never stored
+  // 1. x of the part: thread t -> (m = t % 16, k/4 = t / 16 + 16 i); rows m >= M stay zero
+  const int xm = tid & 15, xc = tid >> 4;
+  const float *xrow = X + (int64_t)min(xm, M - 1) * ldx + 32 * g0;
+  float4 xv[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int c = xc + 16 * i;
+    xv[i] = (xm < M && c < nk4) ? *(const float4 *)(xrow + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // 2. this lane's weight chunks and scales (clamped; groups past g1 are not used)
+  const uint8_t *wrow = W + (int64_t)n * ldw;
+  const float *srow = S + (int64_t)n * lds;
+  // (named registers, not arrays: an array here is moved to LDS by the
+  // compiler's alloca promotion, which serializes the loads)
+  static_assert(MS <= 6, "at most six steps per part");
+  uint4 wv0, wv1, wv2, wv3, wv4, wv5;
+  float sv0, sv1, sv2, sv3, sv4, sv5;
+  auto wv = [&](auto ST) -> uint4 & {
+    constexpr int i = decltype(ST)::value;
+    if constexpr (i == 0) return wv0; else if constexpr (i == 1) return wv1;
+    else if constexpr (i == 2) return wv2; else if constexpr (i == 3) return wv3;
+    else if constexpr (i == 4) return wv4; else return wv5;
+  };
+  auto sv = [&](auto ST) -> float & {
+    constexpr int i = decltype(ST)::value;
+    if constexpr (i == 0) return sv0; else if constexpr (i == 1) return sv1;
+    else if constexpr (i == 2) return sv2; else if constexpr (i == 3) return sv3;
+    else if constexpr (i == 4) return sv4; else return sv5;
+  };
+  static_for<0, MS>([&](auto ST) {
+    const int g = min(g0 + 4 * decltype(ST)::value + kq, ng - 1);
+    wv(ST) = *(const uint4 *)(wrow + 16 * g);
+    sv(ST) = srow[g];
+  });
+  __builtin_amdgcn_sched_barrier(0);  // all loads issued before the staging below waits
+#pragma unroll
+  for (int i = 0; i < XPT; i++) xl[xc + 16 * i][xm] = xv[i];  // zero past the part
+  lds_barrier();
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  const int swz = ln >> 2;
+  static_for<0, MS>([&](auto ST) {  // unrolled: each step's chunk stays in its register
+    constexpr int st = decltype(ST)::value;
+    *(uint4 *)&wt[wave][st & 1][ln * 16 + ((kq ^ swz) << 2)] = wv(ST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's tile is written
+    __builtin_amdgcn_wave_barrier();
+    // the step's four groups as four independent MFMA chains (a dependent
+    // 16x16x4 f32 MFMA waits ~40 cycles for its predecessor; four chains keep
+    // the pipe busy)
+    float xs[4][8];
+    uint32_t d[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int gl = 4 * st + j;  // group within the part
+      const float4 xa = xl[8 * gl + 2 * kq][ln], xb = xl[8 * gl + 2 * kq + 1][ln];
+      xs[j][0] = xa.x; xs[j][1] = xa.y; xs[j][2] = xa.z; xs[j][3] = xa.w;
+      xs[j][4] = xb.x; xs[j][5] = xb.y; xs[j][6] = xb.z; xs[j][7] = xb.w;
+      d[j] = wt[wave][st & 1][ln * 16 + ((j ^ swz) << 2) + kq];
+    }
+    v4f D[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) D[j] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float q = (float)(((int)(d[j] << (28 - 4 * e))) >> 28);  // signed nibble e
+        D[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[j][e], q, D[j], 0, 0, 0);
+      }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float sc = __shfl(sv(ST), ln + 16 * j);  // scale of (row ln, group g0 + 4 st + j)
+      acc = acc + sc * D[j];
+    }
+  });
+  // acc[r] = C[m = 4 kq + r][this wave's row ln] over this block's part of K
+  const int nn = (int)blockIdx.x * kW4mRows + 16 * wave + ln;
+  if (nn < N) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = 4 * kq + r;
+      if (m < M) {
+        if (nparts == 1) O[(int64_t)m * ldo + nn] = acc[r];
+        else P[((int64_t)part * M + m) * N + nn] = acc[r];
+      }
+    }
+  }
+}
+
+// out[m][n] = sum over parts p (in order) of P[p][m][n].
+__global__ void __launch_bounds__(256)
+    w4s_sum_parts(const float *__restrict__ P, int nparts, float *__restrict__ O, int64_t ldo, int M,
+                  int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  float t = 0.f;
+  for (int p = 0; p < nparts; p++) t += P[(int64_t)p * M * N + i];
+  const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+  O[(int64_t)m * ldo + n] = t;
+}
+
 // Reference W4 (unsigned + zero, flat groups), one x vector.  Row i's nibbles
 // start at element offset off + i*cols (a multiple of 32 here).
 __global__ void __launch_bounds__(256)
@@ -280,11 +432,11 @@ __global__ void __launch_bounds__(256)
   const int64_t base = off + (int64_t)i * cols;  // element index of the row start
   const uint8_t *qrow = Q + (base >> 1);
   const int64_t g0 = base / gs;
-  const int cpg = gs >> 5;
+  const int cpg = gs >> 5, cps = cpg_log2(cpg);
   float acc = 0.f;
   for (int c = seg; c < nchunk; c += kLanesPerRow) {
     const uint4 w = *(const uint4 *)(qrow + 16 * c);
-    const int64_t g = g0 + c / cpg;
+    const int64_t g = g0 + chunk_group(c, cpg, cps);
     const float s = S[g], z = Z[g];
     float u[32];
     unpack32(w, u);
@@ -353,6 +505,28 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     const int64_t tot = (int64_t)M * N;
     hipLaunchKernelGGL(w4s_generic, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, W, ldw, S,
                        lds, X, ldx, O, ldo, M, N, K, gs);
+  } else if (M >= 2 && gs == 32) {
+    // several x vectors, groups of 32: fp32 MFMA.  The K parts make about two
+    // blocks per CU; with more than one part the partial tiles go through a
+    // workspace and a second, ordered sum.
+    const int nb = (int)cdiv(N, kW4mRows), ng = K / 32;
+    const int occ = nb >= num_cus() ? 1 : (int)cdiv(2 * num_cus(), nb);
+    const int parts = (int)std::min<int64_t>(ng, std::max<int64_t>(cdiv(ng, kW4mMaxG), occ));
+    float *P = nullptr;
+    if (parts > 1) {
+      int rc = workspace(st, sizeof(float) * (size_t)parts * M * N, (void **)&P, 2);
+      if (rc) return rc;
+    }
+    const int ms = (int)cdiv(cdiv(ng, parts), 4);  // steps for the largest part
+    KernelTimer kt(st, "w4s_mfma");
+#define W4M(MSV) hipLaunchKernelGGL((w4s_mfma<MSV>), dim3((unsigned)nb, (unsigned)parts), dim3(256), 0, st, \
+                                    W, ldw, S, lds, X, ldx, O, ldo, P, M, N, K)
+    if (ms <= 2) W4M(2);
+    else W4M(3);
+#undef W4M
+    if (parts > 1)
+      hipLaunchKernelGGL(w4s_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256)), dim3(256), 0, st, P,
+                         parts, O, ldo, M, N);
   } else if (M == 1 && K / 32 <= 32 * 16) {
     // one x vector: the barrier-free kernel, UB chunks per lane with 32*UB >= K/32
     const int nchunk = K / 32;
