@@ -453,7 +453,8 @@ __device__ __forceinline__ void block_barrier() {
 //   * Rows beyond M (N) load from a clamped in-bounds row; their results are
 //     never stored.
 //   * The MFMA computes C^T tiles (B fragment as the first operand), so a lane
-//     ends with 4 consecutive columns of one row of C: 16-byte stores.
+//     ends with 4 consecutive columns of one row of C: 16-byte nontemporal
+//     stores.
 template <int STAGES, bool AU8>
 __global__ void __launch_bounds__(512)
     gemm_i8_dma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
@@ -566,7 +567,10 @@ __global__ void __launch_bounds__(512)
         const v4i v = acc[i][j] + bias;
         int32_t *dst = C + (int64_t)row * ldc + col;
         if (vec_store) {
-          *(v4i *)dst = v;
+          // streaming store: C is not re-read here, and the all-CU store burst
+          // at a tile's end drains faster without allocating in L2 (measured
+          // 4-5% on the whole kernel at 8192^3)
+          __builtin_nontemporal_store(v, (v4i *)dst);
         } else {
 #pragma unroll
           for (int r = 0; r < 4; r++)
