@@ -329,7 +329,7 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Attention, one 1024-thread block per head (theta <= 0 skips RoPE).  No
+// Attention, one 1024-thread block per head (rope == nullptr: no rotation).  No
 // cross-block communication: a device-scope fence to publish partials between
 // blocks costs an L2 write-back on this multi-XCD part, more than the whole
 // head's work.  Latency is the cost here, so every cache load that depends
@@ -348,7 +348,7 @@ constexpr int kAttnVE = 24;  // V values per thread in registers
 __global__ void __launch_bounds__(kAttnThreads)
     attn_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
            float *__restrict__ out, const StepState *__restrict__ st, int dim, int kv_dim,
-           int n_heads, int n_kv_heads, int hs, float theta) {
+           int n_heads, int n_kv_heads, int hs, const float2 *__restrict__ rope) {
   __shared__ __align__(16) float qs[256];
   __shared__ __align__(16) float kn[256];
   __shared__ __align__(16) float vn[256];
@@ -382,9 +382,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
   // 2. this token's q, k, v (RoPE on q and k)
   for (int j = 2 * threadIdx.x; j < hs; j += 2 * blockDim.x) {
-    const float freq = theta > 0.f ? 1.f / powf(theta, (float)j / (float)hs) : 0.f;
-    const float a = (float)pos * freq;
-    const float fcr = theta > 0.f ? cosf(a) : 1.f, fci = theta > 0.f ? sinf(a) : 0.f;
+    const float2 f = rope ? rope[(int64_t)pos * (hs >> 1) + (j >> 1)] : make_float2(1.f, 0.f);
+    const float fcr = f.x, fci = f.y;
     qs[j] = q[j] * fcr - q[j + 1] * fci;
     qs[j + 1] = q[j] * fci + q[j + 1] * fcr;
     kn[j] = k[j] * fcr - k[j + 1] * fci;
@@ -466,6 +465,20 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
 }
 
+// RoPE factors (cos, sin)(pos * freq_j), freq_j = 1 / theta^(j / head_size)
+// for even j, as stories110M.sl:86-112 computes them at every step; tabulated
+// once per model with the same fp32 expressions, so the values are identical.
+__global__ void __launch_bounds__(256)
+    rope_table_k(float2 *__restrict__ tab, int seq_len, int hs, float theta) {
+  const int half = hs >> 1;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)seq_len * half) return;
+  const int pos = (int)(i / half), j = 2 * (int)(i - (int64_t)pos * half);
+  const float freq = 1.f / powf(theta, (float)j / (float)hs);
+  const float a = (float)pos * freq;
+  tab[i] = make_float2(cosf(a), sinf(a));
+}
+
 __global__ void __launch_bounds__(256)
     embed_k(const float *__restrict__ emb, float *__restrict__ x, const StepState *__restrict__ st,
             int dim) {
@@ -482,7 +495,27 @@ __global__ void __launch_bounds__(1024)
   __shared__ int bi[16];
   float best = -INFINITY;
   int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+  // each thread scans its elements in increasing index order (strict '>' keeps
+  // the first maximum); eight float4 loads are issued before they are compared
+  const int n4 = ((uintptr_t)logits & 15) == 0 ? vocab >> 2 : 0;
+  const float4 *l4 = (const float4 *)logits;
+  for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * blockDim.x) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int i = i0 + u * blockDim.x;
+      v[u] = i < n4 ? l4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int b = 4 * (i0 + u * blockDim.x);
+      if (v[u].x > best) { best = v[u].x; idx = b; }
+      if (v[u].y > best) { best = v[u].y; idx = b + 1; }
+      if (v[u].z > best) { best = v[u].z; idx = b + 2; }
+      if (v[u].w > best) { best = v[u].w; idx = b + 3; }
+    }
+  }
+  for (int i = 4 * n4 + threadIdx.x; i < vocab; i += blockDim.x) {
     const float v = logits[i];
     if (v > best) { best = v; idx = i; }  // strictly greater: first max per thread
   }
@@ -518,6 +551,7 @@ struct LlamaModel {
   // device buffers
   float *x = nullptr, *xb = nullptr, *qkv = nullptr, *h13 = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr;
+  float2 *rope = nullptr;  // [seq_len][head_size / 2] (cos, sin); null when theta <= 0
   StepState *state = nullptr;
   int *prompt = nullptr, *tokens = nullptr;
   hipGraph_t graph = nullptr;
@@ -619,7 +653,7 @@ int enqueue_step(LlamaModel &m) {
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
     hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(kAttnThreads),
                        sizeof(float) * (size_t)c.seq_len, st, m.qkv, kc, vc, m.xb, m.state, dim, kv,
-                       (int)c.n_heads, (int)c.n_kv_heads, hs, c.rope_theta);
+                       (int)c.n_heads, (int)c.n_kv_heads, hs, (const float2 *)m.rope);
     SIMP_HIP(hipGetLastError());
     // 3. Wo, accumulated into x (residual)
     s = Segs{};
@@ -768,6 +802,19 @@ int32_t simp_rt_llama_create(const simp_rt_llama_config *cfg, const simp_rt_llam
     simp_rt_llama_destroy((simp_rt_llama *)m);
     return rc;
   }
+  if (cfg->rope_theta > 0.f) {
+    const int64_t n = cfg->seq_len * (m->hs / 2);
+    if ((rc = alloc((void **)&m->rope, sizeof(float2) * (size_t)n))) {
+      simp_rt_llama_destroy((simp_rt_llama *)m);
+      return rc;
+    }
+    hipLaunchKernelGGL(rope_table_k, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, m->stream, m->rope,
+                       (int)cfg->seq_len, m->hs, cfg->rope_theta);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(m->stream) != hipSuccess) {
+      simp_rt_llama_destroy((simp_rt_llama *)m);
+      return set_error(SIMP_RT_EHIP, "llama_create: RoPE table");
+    }
+  }
   *out = (simp_rt_llama *)m;
   return SIMP_RT_OK;
 }
@@ -779,8 +826,8 @@ int32_t simp_rt_llama_destroy(simp_rt_llama *h) {
   if (m->exec) (void)hipGraphExecDestroy(m->exec);
   if (m->graph) (void)hipGraphDestroy(m->graph);
   for (void *p : {(void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->h13, (void *)m->logits,
-                  (void *)m->kcache, (void *)m->vcache, (void *)m->state, (void *)m->prompt,
-                  (void *)m->tokens})
+                  (void *)m->kcache, (void *)m->vcache, (void *)m->rope, (void *)m->state,
+                  (void *)m->prompt, (void *)m->tokens})
     if (p) (void)hipFree(p);
   delete m;
   return SIMP_RT_OK;
@@ -1089,7 +1136,8 @@ int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim + kvd, kvd, dim, gs, m.off[2] + l * m.dim * kvd, st))) return rc;
     float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
     hipLaunchKernelGGL(attn_k, dim3((unsigned)m.nh), dim3(kAttnThreads), sizeof(float) * (size_t)m.seq,
-                       st, m.qkv, kc, vc, m.xb2, m.state, dim, kvd, (int)m.nh, (int)m.nkv, m.hs, 0.f);
+                       st, m.qkv, kc, vc, m.xb2, m.state, dim, kvd, (int)m.nh, (int)m.nkv, m.hs,
+                       (const float2 *)nullptr);  // llama2_quant.sl applies no RoPE
     SIMP_HIP(hipGetLastError());
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb2, m.xb, dim, dim, gs, m.off[3] + l * m.dim * m.dim, st))) return rc;
     hipLaunchKernelGGL(add_inplace_k, dim3(gd), dim3(256), 0, st, m.x, (const float *)m.xb, dim);
