@@ -79,6 +79,19 @@ __device__ __forceinline__ float ubyte(uint32_t x) {
   return r;
 }
 
+// Streaming (nontemporal) 16-byte loads for data read once per call (weight
+// streams), so they do not displace reused data in the caches.
+__device__ __forceinline__ uint4 ntload16(const void *p) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 ntload_f4(const float4 *p) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 v = __builtin_nontemporal_load((const f32x4 *)p);
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // Group index of 32-weight chunk c for a group size of 32 * cpg: a shift when
 // cpg is a power of two (cpg_shift = log2(cpg), else -1), since a 32-bit
 // integer division costs about twenty VALU instructions per use.
