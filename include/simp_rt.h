@@ -334,6 +334,79 @@ float llama2_quant_forward(
  * reference counterpart). */
 int32_t simp_rt_forward_cache_clear(void);
 
+/* ------------------------------------------------------- model files -- */
+/* llama2.c checkpoint header, as read by
+ * examples/llama2/generate_stories110M.cpp:25-33,143-150 (vocab_size < 0: the
+ * classifier is stored after the other tensors instead of sharing the
+ * embedding table). */
+typedef struct {
+  int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+} simp_rt_ckpt_config;
+int32_t simp_rt_ckpt_read_config(const char *path, simp_rt_ckpt_config *cfg);
+/* Reads the whole fp32 checkpoint (generate_stories110M.cpp:150-191, in the
+ * llama2.c layout: wk/wv of kv_dim rows, legacy RoPE tables skipped before an
+ * unshared classifier) into one device allocation *blob (free it with
+ * simp_rt_free) and points w's fp32 fields into it, ready for
+ * simp_rt_llama_create with SIMP_RT_W_F32. */
+int32_t simp_rt_ckpt_load_f32(const char *path, simp_rt_ckpt_config *cfg, simp_rt_llama_weights *w,
+                              void **blob);
+
+/* Tokenizer file of generate_stories110M.cpp:36-70: max_token_length, then per
+ * token a float score, an int32 length and the bytes. */
+typedef struct simp_rt_tokenizer simp_rt_tokenizer;
+int32_t simp_rt_tokenizer_load(const char *path, int32_t vocab_size, simp_rt_tokenizer **tok);
+/* Tokenizer::decode (generate_stories110M.cpp:64-69): the token's bytes (not
+ * NUL-terminated; *len receives the length), "?" when out of range. */
+const char *simp_rt_tokenizer_decode(const simp_rt_tokenizer *tok, int32_t token, int32_t *len);
+float simp_rt_tokenizer_score(const simp_rt_tokenizer *tok, int32_t token);
+int32_t simp_rt_tokenizer_max_token_length(const simp_rt_tokenizer *tok);
+int32_t simp_rt_tokenizer_free(simp_rt_tokenizer *tok);
+
+/* Token sampling of generate_stories110M.cpp:73-116 on host logits: temperature
+ * 0 is sample_argmax (strict '>' from index 0); otherwise sample_temperature
+ * with a std::mt19937 seeded here (the reference seeds it from
+ * std::random_device).  Returns the token, or a negative status. */
+typedef struct simp_rt_sampler simp_rt_sampler;
+int32_t simp_rt_sampler_create(uint32_t seed, simp_rt_sampler **s);
+int32_t simp_rt_sampler_sample(simp_rt_sampler *s, const float *logits, int32_t n, float temperature);
+int32_t simp_rt_sampler_free(simp_rt_sampler *s);
+
+/* W4 quantizers on the GPU (device arrays, asynchronous on the thread's stream).
+ * _w4u: the reference's quantize_w4 (examples/llama2/bench_llama_quant.cpp:51-93)
+ * over one tensor of n floats: flat groups of group_size (even), q[(n+1)/2]
+ * bytes (low nibble = even index), scales/zeros[ceil(n/group_size)].
+ * _w4s: the symmetric format of simp_rt_matmul_w4s, per row of cols (a multiple
+ * of group_size): scale = max|w|/7 (1 for an all-zero group),
+ * q = clamp(round(w/scale), -8, 7); no reference counterpart. */
+int32_t simp_rt_quantize_w4u(const float *w, int64_t n, int32_t group_size, uint8_t *q, float *scales,
+                             float *zeros);
+int32_t simp_rt_quantize_w4s(const float *w, int64_t rows, int64_t cols, int32_t group_size, uint8_t *q,
+                             float *scales);
+
+/* Packed W4 model files written from a llama2.c checkpoint (offline
+ * quantization; no reference counterpart: the reference quantizes in memory at
+ * start-up, bench_llama_quant.cpp:189-210).  A 64-byte header (magic, the
+ * llama2.c config, group size), then 256-byte-aligned sections.
+ *   "SIMPW4S1" (_w4s_): fp32 embedding and norms, then q and scales of wq, wk,
+ *     wv, wo, w1, w2, w3 and the classifier; _w4s_file_load points the fields
+ *     of a simp_rt_llama_weights, format SIMP_RT_W_W4S, into one device
+ *     allocation.
+ *   "SIMPW4U1" (_w4u_): the arrays of llama2_quant_forward: seven element
+ *     offsets, fp32 embedding, norms and classifier, then qweights, scales and
+ *     zeros of wq..w3 quantized tensor by tensor as the reference does. */
+int32_t simp_rt_w4s_file_write(const char *ckpt_path, const char *out_path, int32_t group_size);
+int32_t simp_rt_w4s_file_load(const char *path, simp_rt_llama_config *cfg, simp_rt_llama_weights *w,
+                              void **blob);
+typedef struct {
+  const float *token_embedding, *rms_att, *rms_ffn, *rms_final, *wcls, *scales, *zeros;
+  const int8_t *qweights;
+  int64_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len, group_size;
+  int64_t qweights_bytes, n_groups;
+  int64_t offsets[7]; /* wq_off .. w3_off of llama2_quant_forward */
+} simp_rt_w4u_model;
+int32_t simp_rt_w4u_file_write(const char *ckpt_path, const char *out_path, int32_t group_size);
+int32_t simp_rt_w4u_file_load(const char *path, simp_rt_w4u_model *m, void **blob);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,14 @@
  *   orc_llama_forward,
  *   orc_llama_quant_forward   -- parity unpinned beyond its parts: the reference
  *                                holds no golden logits (docs/benchmark/llama_results.md:81-95)
+ *   orc_quantize_w4s          -- properties: |dequant - w| <= scale/2 inside the
+ *                                range, the group maximum maps to +-7 exactly,
+ *                                all-zero groups; brute force in numpy
+ *   orc_mt_next               -- the C++ standard's check value: the 10000th draw
+ *                                of std::mt19937 default-seeded (5489) is
+ *                                4123659995 ([rand.predef])
+ *   orc_uniform01f, orc_sample -- equal the library's std::mt19937 /
+ *                                uniform_real_distribution<float> sampler
  */
 #include "oracle.h"
 
@@ -578,4 +586,84 @@ int64_t orc_argmax(const float *logits, int64_t n) {
       best = i;
     }
   return best;
+}
+
+
+/* ---- symmetric W4 quantization (BASELINE format) ---- */
+void orc_quantize_w4s(const float *w, int64_t rows, int64_t cols, int64_t gs, uint8_t *qw,
+                      float *scales) {
+  const int64_t gpr = cols / gs;
+  memset(qw, 0, (size_t)(rows * cols / 2));
+  for (int64_t r = 0; r < rows; r++)
+    for (int64_t g = 0; g < gpr; g++) {
+      const float *src = w + r * cols + g * gs;
+      float amax = 0.f;
+      for (int64_t i = 0; i < gs; i++) amax = fabsf(src[i]) > amax ? fabsf(src[i]) : amax;
+      const float s = amax > 0.f ? amax / 7.0f : 1.0f;
+      scales[r * gpr + g] = s;
+      for (int64_t i = 0; i < gs; i++) {
+        int q = (int)roundf(src[i] / s);
+        q = q < -8 ? -8 : (q > 7 ? 7 : q);
+        const int64_t k = g * gs + i;
+        uint8_t *b = qw + r * (cols / 2) + k / 2;
+        if (k % 2 == 0) *b = (uint8_t)(q & 15);
+        else *b |= (uint8_t)((q & 15) << 4);
+      }
+    }
+}
+
+/* ---- MT19937 and the reference's temperature sampler ---- */
+void orc_mt_seed(orc_mt19937 *g, uint32_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < 624; i++)
+    g->mt[i] = 1812433253u * (g->mt[i - 1] ^ (g->mt[i - 1] >> 30)) + (uint32_t)i;
+  g->idx = 624;
+}
+
+uint32_t orc_mt_next(orc_mt19937 *g) {
+  if (g->idx >= 624) {
+    for (int i = 0; i < 624; i++) {
+      const uint32_t y = (g->mt[i] & 0x80000000u) | (g->mt[(i + 1) % 624] & 0x7fffffffu);
+      g->mt[i] = g->mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    g->idx = 0;
+  }
+  uint32_t y = g->mt[g->idx++];
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
+float orc_uniform01f(orc_mt19937 *g) {
+  const float r = (float)orc_mt_next(g) / 4294967296.0f;
+  return r >= 1.0f ? nextafterf(1.0f, 0.0f) : r;
+}
+
+int64_t orc_sample(const float *logits, int64_t n, float temperature, orc_mt19937 *g) {
+  if (n <= 0) return -1;
+  if (temperature == 0.0f) return orc_argmax(logits, n);
+  float *p = (float *)malloc(sizeof(float) * (size_t)n);
+  for (int64_t i = 0; i < n; i++) p[i] = logits[i] / temperature;
+  float mx = p[0];
+  for (int64_t i = 1; i < n; i++) mx = p[i] > mx ? p[i] : mx;
+  float sum = 0.0f;
+  for (int64_t i = 0; i < n; i++) {
+    p[i] = expf(p[i] - mx);
+    sum += p[i];
+  }
+  for (int64_t i = 0; i < n; i++) p[i] /= sum;
+  const float r = orc_uniform01f(g);
+  float cdf = 0.0f;
+  int64_t tok = n - 1;
+  for (int64_t i = 0; i < n; i++) {
+    cdf += p[i];
+    if (r < cdf) {
+      tok = i;
+      break;
+    }
+  }
+  free(p);
+  return tok;
 }

@@ -190,6 +190,28 @@ void orc_llama_quant_forward(const orc_llama_cfg *cfg, const float *emb, const f
 /* Strict-'>' argmax, first maximum wins (examples/llama2/generate_stories110M.cpp:73-83). */
 int64_t orc_argmax(const float *logits, int64_t n);
 
+/* Symmetric W4 quantization (the BASELINE format, no reference counterpart):
+ * per row of cols, groups of gs: scale = max|w| / 7 (1 for an all-zero group),
+ * q = clamp(round(w / scale), -8, 7), two's-complement nibbles, low = even k. */
+void orc_quantize_w4s(const float *w, int64_t rows, int64_t cols, int64_t gs, uint8_t *qw,
+                      float *scales);
+
+/* MT19937 (Matsumoto & Nishimura 1998; the std::mt19937 of the C++ standard):
+ * state of 624 words, seeded as std::mt19937(seed). */
+typedef struct {
+  uint32_t mt[624];
+  int idx;
+} orc_mt19937;
+void orc_mt_seed(orc_mt19937 *g, uint32_t seed);
+uint32_t orc_mt_next(orc_mt19937 *g);
+/* std::uniform_real_distribution<float>(0, 1) on a 32-bit generator as
+ * libstdc++ implements it (generate_canonical<float, 24>: one draw,
+ * float(x) / 2^32, values >= 1 replaced by the largest float below 1). */
+float orc_uniform01f(orc_mt19937 *g);
+/* sample_temperature of examples/llama2/generate_stories110M.cpp:86-116 on a copy
+ * of logits (argmax for temperature 0, :73-83), one draw from g. */
+int64_t orc_sample(const float *logits, int64_t n, float temperature, orc_mt19937 *g);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,17 @@ _s("orc_matmul_w4s", [_P, _P, _P, _P, _I, _I, _I, _I])
 _s("orc_matmul_w4s_f32", [_P, _P, _P, _P, _I, _I, _I, _I, C.c_int])
 _s("orc_rope", [_P, _P, _I, _I, _I, _I, _F])
 _s("orc_argmax", [_P, _I], C.c_int64)
+_s("orc_quantize_w4s", [_P, _I, _I, _I, _P, _P])
+
+
+class OrcMT(C.Structure):
+    _fields_ = [("mt", C.c_uint32 * 624), ("idx", C.c_int)]
+
+
+_s("orc_mt_seed", [C.POINTER(OrcMT), C.c_uint32])
+_s("orc_mt_next", [C.POINTER(OrcMT)], C.c_uint32)
+_s("orc_uniform01f", [C.POINTER(OrcMT)], C.c_float)
+_s("orc_sample", [_P, _I, C.c_float, C.POINTER(OrcMT)], C.c_int64)
 
 
 class OrcLlamaCfg(C.Structure):
@@ -265,6 +276,34 @@ def quantize_f5(w, gs):
     ze = np.empty(ng, np.float32)
     _o.orc_quantize_f5(_p(w), w.size, gs, _p(qw), _p(sc), _p(ze))
     return qw, sc, ze
+
+
+def quantize_w4s(w, gs):
+    """Symmetric W4 of w [rows, cols]: (q [rows, cols/2] u8, scales [rows, cols/gs])."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    qw = np.empty((rows, cols // 2), np.uint8)
+    sc = np.empty((rows, cols // gs), np.float32)
+    _o.orc_quantize_w4s(_p(w), rows, cols, gs, _p(qw), _p(sc))
+    return qw, sc
+
+
+class MT19937:
+    """std::mt19937 restated (orc_mt_*)."""
+
+    def __init__(self, seed: int):
+        self._g = OrcMT()
+        _o.orc_mt_seed(C.byref(self._g), seed & 0xFFFFFFFF)
+
+    def next(self) -> int:
+        return int(_o.orc_mt_next(C.byref(self._g)))
+
+    def uniform01f(self) -> float:
+        return float(_o.orc_uniform01f(C.byref(self._g)))
+
+    def sample(self, logits, temperature: float) -> int:
+        lg = np.ascontiguousarray(logits, np.float32)
+        return int(_o.orc_sample(_p(lg), lg.size, C.c_float(temperature), C.byref(self._g)))
 
 
 def matmul_w4s(qw, scales, x, gs=32):

@@ -38,4 +38,15 @@ from .host import (  # noqa: F401
     forward_cache_clear,
     W_F32,
     W_W4S,
+    ckpt_read_config,
+    ckpt_load_f32,
+    DeviceModel,
+    Tokenizer,
+    Sampler,
+    quantize_w4u,
+    quantize_w4s,
+    w4s_file_write,
+    w4s_file_load,
+    w4u_file_write,
+    w4u_file_load,
 )

@@ -401,3 +401,198 @@ class Llama:
             self.close()
         except Exception:
             pass
+
+
+# ------------------------------------------------------------- model files
+
+class CkptConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in _CFG_INTS]
+
+
+class W4UModel(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("token_embedding", "rms_att", "rms_ffn", "rms_final",
+                                          "wcls", "scales", "zeros", "qweights")] + [
+        (n, C.c_int64) for n in _CFG_INTS + ("group_size", "qweights_bytes", "n_groups")] + [
+        ("offsets", C.c_int64 * 7)]
+
+
+_sig("simp_rt_ckpt_read_config", [C.c_char_p, C.POINTER(CkptConfig)])
+_sig("simp_rt_ckpt_load_f32", [C.c_char_p, C.POINTER(CkptConfig), C.POINTER(LlamaWeights),
+                               C.POINTER(C.c_void_p)])
+_sig("simp_rt_tokenizer_load", [C.c_char_p, C.c_int32, C.POINTER(C.c_void_p)])
+lib.simp_rt_tokenizer_decode.argtypes = [C.c_void_p, C.c_int32, C.POINTER(C.c_int32)]
+lib.simp_rt_tokenizer_decode.restype = C.POINTER(C.c_char)
+lib.simp_rt_tokenizer_score.argtypes = [C.c_void_p, C.c_int32]
+lib.simp_rt_tokenizer_score.restype = C.c_float
+_sig("simp_rt_tokenizer_max_token_length", [C.c_void_p])
+_sig("simp_rt_tokenizer_free", [C.c_void_p])
+_sig("simp_rt_sampler_create", [C.c_uint32, C.POINTER(C.c_void_p)])
+_sig("simp_rt_sampler_sample", [C.c_void_p, _P, C.c_int32, C.c_float])
+_sig("simp_rt_sampler_free", [C.c_void_p])
+_sig("simp_rt_quantize_w4u", [_P, _I, C.c_int32, _P, _P, _P])
+_sig("simp_rt_quantize_w4s", [_P, _I, _I, C.c_int32, _P, _P])
+_sig("simp_rt_w4s_file_write", [C.c_char_p, C.c_char_p, C.c_int32])
+_sig("simp_rt_w4s_file_load", [C.c_char_p, C.POINTER(LlamaConfig), C.POINTER(LlamaWeights),
+                               C.POINTER(C.c_void_p)])
+_sig("simp_rt_w4u_file_write", [C.c_char_p, C.c_char_p, C.c_int32])
+_sig("simp_rt_w4u_file_load", [C.c_char_p, C.POINTER(W4UModel), C.POINTER(C.c_void_p)])
+_sig("simp_rt_free", [_P])
+_sig("simp_rt_memcpy", [_P, _P, _I])
+
+
+def _b(path) -> bytes:
+    return os.fsencode(path)
+
+
+def ckpt_read_config(path) -> dict:
+    """llama2.c checkpoint header (generate_stories110M.cpp:143-150)."""
+    c = CkptConfig()
+    _check("simp_rt_ckpt_read_config", lib.simp_rt_ckpt_read_config(_b(path), C.byref(c)))
+    return {k: int(getattr(c, k)) for k in _CFG_INTS}
+
+
+class DeviceModel:
+    """Weights loaded into one device allocation (freed by close()).
+
+    ``cfg`` is the engine configuration (keys of simp_rt_llama_config) and
+    ``weights`` maps simp_rt_llama_weights field names to device addresses,
+    so ``Llama(m.cfg, m.weights)`` builds an engine over them."""
+
+    def __init__(self, cfg: dict, weights: dict, blob):
+        self.cfg, self.weights, self._blob = cfg, weights, blob
+
+    def read(self, name: str, count: int, dtype="float32"):
+        """Copies `count` elements of a loaded array to a numpy array."""
+        import numpy as np
+        out = np.empty(count, dtype)
+        if count:
+            _check("simp_rt_memcpy", lib.simp_rt_memcpy(out.ctypes.data, self.weights[name], out.nbytes))
+        return out
+
+    def close(self):
+        if getattr(self, "_blob", None):
+            lib.simp_rt_free(self._blob)
+            self._blob = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def ckpt_load_f32(path) -> DeviceModel:
+    """The whole fp32 checkpoint on the device (generate_stories110M.cpp:150-191)."""
+    c, w, blob = CkptConfig(), LlamaWeights(), C.c_void_p()
+    _check("simp_rt_ckpt_load_f32", lib.simp_rt_ckpt_load_f32(_b(path), C.byref(c), C.byref(w),
+                                                              C.byref(blob)))
+    cfg = {k: abs(int(getattr(c, k))) for k in _CFG_INTS}
+    cfg.update(eps=1e-5, rope_theta=10000.0, weight_format=W_F32, group_size=32)
+    weights = {k: getattr(w, k) for k in _W_NAMES[:12]}
+    return DeviceModel(cfg, weights, blob)
+
+
+def w4s_file_write(ckpt_path, out_path, group_size: int = 32) -> None:
+    _check("simp_rt_w4s_file_write", lib.simp_rt_w4s_file_write(_b(ckpt_path), _b(out_path), group_size))
+
+
+def w4s_file_load(path) -> DeviceModel:
+    c, w, blob = LlamaConfig(), LlamaWeights(), C.c_void_p()
+    _check("simp_rt_w4s_file_load", lib.simp_rt_w4s_file_load(_b(path), C.byref(c), C.byref(w),
+                                                              C.byref(blob)))
+    cfg = {k: int(getattr(c, k)) for k in _CFG_INTS}
+    cfg.update(eps=float(c.eps), rope_theta=float(c.rope_theta),
+               weight_format=int(c.weight_format), group_size=int(c.group_size))
+    weights = {k: getattr(w, k) for k in ("token_embedding", "rms_att", "rms_ffn", "rms_final")
+               + _W_NAMES[12:]}
+    return DeviceModel(cfg, weights, blob)
+
+
+def w4u_file_write(ckpt_path, out_path, group_size: int = 128) -> None:
+    _check("simp_rt_w4u_file_write", lib.simp_rt_w4u_file_write(_b(ckpt_path), _b(out_path), group_size))
+
+
+def w4u_file_load(path) -> DeviceModel:
+    """Arrays of llama2_quant_forward on the device; cfg also holds the sizes
+    and the seven element offsets."""
+    m, blob = W4UModel(), C.c_void_p()
+    _check("simp_rt_w4u_file_load", lib.simp_rt_w4u_file_load(_b(path), C.byref(m), C.byref(blob)))
+    cfg = {k: int(getattr(m, k)) for k in _CFG_INTS + ("group_size", "qweights_bytes", "n_groups")}
+    cfg["offsets"] = [int(v) for v in m.offsets]
+    weights = {k: getattr(m, k) for k in ("token_embedding", "rms_att", "rms_ffn", "rms_final", "wcls",
+                                          "scales", "zeros", "qweights")}
+    return DeviceModel(cfg, weights, blob)
+
+
+class Tokenizer:
+    """Tokenizer file of generate_stories110M.cpp:36-70."""
+
+    def __init__(self, path, vocab_size: int):
+        h = C.c_void_p()
+        _check("simp_rt_tokenizer_load", lib.simp_rt_tokenizer_load(_b(path), vocab_size, C.byref(h)))
+        self._h = h
+
+    def decode(self, token: int) -> bytes:
+        n = C.c_int32()
+        p = lib.simp_rt_tokenizer_decode(self._h, token, C.byref(n))
+        return C.string_at(p, n.value)
+
+    def score(self, token: int) -> float:
+        return float(lib.simp_rt_tokenizer_score(self._h, token))
+
+    @property
+    def max_token_length(self) -> int:
+        return int(lib.simp_rt_tokenizer_max_token_length(self._h))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.simp_rt_tokenizer_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Sampler:
+    """Token sampling of generate_stories110M.cpp:73-116 with a seeded std::mt19937."""
+
+    def __init__(self, seed: int):
+        h = C.c_void_p()
+        _check("simp_rt_sampler_create", lib.simp_rt_sampler_create(seed & 0xFFFFFFFF, C.byref(h)))
+        self._h = h
+
+    def sample(self, logits, temperature: float) -> int:
+        import numpy as np
+        lg = np.ascontiguousarray(logits, np.float32)
+        r = lib.simp_rt_sampler_sample(self._h, lg.ctypes.data, lg.size, C.c_float(temperature))
+        if r < 0:
+            _check("simp_rt_sampler_sample", r)
+        return int(r)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.simp_rt_sampler_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def quantize_w4u(w, group_size, q, scales, zeros) -> None:
+    """Reference quantize_w4 (bench_llama_quant.cpp:51-93) of a device tensor."""
+    _check("simp_rt_quantize_w4u", lib.simp_rt_quantize_w4u(w.data_ptr(), w.numel(), group_size,
+                                                            q.data_ptr(), scales.data_ptr(),
+                                                            zeros.data_ptr()))
+
+
+def quantize_w4s(w, group_size, q, scales) -> None:
+    """Symmetric W4 of a device matrix w [rows, cols]."""
+    rows, cols = w.shape
+    _check("simp_rt_quantize_w4s", lib.simp_rt_quantize_w4s(w.data_ptr(), rows, cols, group_size,
+                                                            q.data_ptr(), scales.data_ptr()))

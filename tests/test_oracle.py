@@ -350,3 +350,25 @@ def test_rope_properties(orc):
     np.testing.assert_allclose(q[0], q0[0] * c - q0[1] * s, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(q[hs], q0[hs] * c - q0[hs + 1] * s, rtol=1e-5, atol=1e-6)
     assert np.allclose(k[dim // 2:], k0[dim // 2:])             # only i < kv_dim rotated
+
+
+def test_quantize_w4s_properties(orc):
+    """Symmetric W4 (BASELINE format): every value within half a step of its
+    dequantized value, the group maximum at +-7, an all-zero group at scale 1,
+    two's-complement nibbles with the even index low."""
+    rng = np.random.default_rng(11)
+    rows, cols, gs = 9, 256, 32
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    w[2, 32:64] = 0.0
+    q, s = orc.quantize_w4s(w, gs)
+    nib = np.stack([q & 15, q >> 4], axis=-1).reshape(rows, cols).astype(np.int32)
+    val = np.where(nib >= 8, nib - 16, nib)
+    sc = np.repeat(s, gs, axis=1)
+    assert val.min() >= -8 and val.max() <= 7
+    assert np.all(np.abs(val * sc - w) <= sc / 2 * (1 + 1e-6))
+    g = np.abs(w).reshape(rows, cols // gs, gs)
+    arg = g.argmax(axis=2)
+    top = np.take_along_axis(val.reshape(rows, cols // gs, gs), arg[..., None], 2)[..., 0]
+    nz = g.max(axis=2) > 0
+    assert np.all(np.abs(top[nz]) == 7)
+    assert s[2, 1] == 1.0 and np.all(val[2, 32:64] == 0)
