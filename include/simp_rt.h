@@ -9,8 +9,10 @@
  *   rank 1 (T[] arrays):       T* alloc, T* aligned, i64 offset, i64 size, i64 stride
  *   rank 2 (tensors):          T* alloc, T* aligned, i64 offset,
  *                              i64 size0, i64 size1, i64 stride0, i64 stride1
- * Elements live at aligned + offset + i*stride0 + j*stride1 (row-major,
- * stride1 must be 1).  `alloc` is carried for ABI fidelity and is not read.
+ *   rank 3 / rank 4:           the same with three / four sizes, then as many strides
+ * Elements live at aligned + offset + i*stride0 + j*stride1 (+ ...) (row-major:
+ * the innermost stride must be 1 and each outer stride must step over the
+ * dimensions inside it).  `alloc` is carried for ABI fidelity and is not read.
  * Scalars follow in the operand order fixed by SimpLang's builtin parser
  * (src/mlir/mlir_codegen.cpp:1388-1531,2068-2292).
  *
@@ -191,6 +193,60 @@ int32_t simp_rt_tensor_matvecmul_f32(
     const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
     const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
     float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* tensor_matmul on f64 tensors: C[M,N] = A[M,K] * B[K,N], C overwritten.
+ * Replaces the general linalg.matmul branch for f64 (ConvertSimpToMemRef.cpp:
+ * 3280-3284; tests/test_tensor_matmul.sl uses f64 tensors). */
+int32_t simp_rt_tensor_matmul_f64(
+    const double *a_alloc, const double *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const double *b_alloc, const double *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    double *c_alloc, double *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* tensor_matmul on rank-3 tensors: C[b] = A[b] x B[b] for A[Bt,M,K], B[Bt,K,N],
+ * C[Bt,M,N], C overwritten.  Replaces the 3-D linalg.batch_matmul case of
+ * TensorMatMulOpLowering (ConvertSimpToMemRef.cpp:3286-3291, into the result the
+ * lowering zero-fills at :2926-2933).  _i8 is s8 x s8 -> i32 (linalg sign-extends). */
+int32_t simp_rt_tensor_batch_matmul_f32(
+    const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2);
+int32_t simp_rt_tensor_batch_matmul_f64(
+    const double *a_alloc, const double *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const double *b_alloc, const double *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    double *c_alloc, double *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2);
+int32_t simp_rt_tensor_batch_matmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2);
+
+/* tensor_matmul of an NHWC tensor by a [C_out, C_in] weight matrix (a fully
+ * connected layer): out[n,h,w,o] = sum_i in[n,h,w,i] * weights[o,i].  Replaces
+ * the 4-D x 2-D case of TensorMatMulOpLowering (ConvertSimpToMemRef.cpp:
+ * 3293-3361: collapse (N,H,W), multiply by the transposed weights, expand).
+ * (N,H,W) of input and output must collapse into one run of rows. */
+int32_t simp_rt_tensor_matmul_nhwc_f32(
+    const float *x_alloc, const float *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_s2,
+    int64_t x_s3, int64_t x_st0, int64_t x_st1, int64_t x_st2, int64_t x_st3,
+    const float *w_alloc, const float *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0,
+    int64_t w_st1,
+    float *y_alloc, float *y, int64_t y_off, int64_t y_s0, int64_t y_s1, int64_t y_s2,
+    int64_t y_s3, int64_t y_st0, int64_t y_st1, int64_t y_st2, int64_t y_st3);
+int32_t simp_rt_tensor_matmul_nhwc_f64(
+    const double *x_alloc, const double *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_s2,
+    int64_t x_s3, int64_t x_st0, int64_t x_st1, int64_t x_st2, int64_t x_st3,
+    const double *w_alloc, const double *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0,
+    int64_t w_st1,
+    double *y_alloc, double *y, int64_t y_off, int64_t y_s0, int64_t y_s1, int64_t y_s2,
+    int64_t y_s3, int64_t y_st0, int64_t y_st1, int64_t y_st2, int64_t y_st3);
 
 /* ------------------------------------------------------ normalisations -- */
 

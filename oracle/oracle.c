@@ -16,6 +16,9 @@
  *                                128) on orc_int4_recipe_inputs; equals the int8
  *                                product of the unpacked nibbles truncated to i16
  *   orc_matmul_f32_acc        -- f64 brute force, KAT 110 (tests/test_tensor_matmul_runner.cpp:39)
+ *   orc_batch_matmul_f32/f64  -- KATs of simptensor/tests/test_matmul_dot.sl:135-199
+ *                                and tests/test_tensor_matmul.sl:66-117; equal
+ *                                orc_matmul_f32_acc batch by batch
  *   orc_rmsnorm/softmax/silu  -- KATs of examples/llama2/kernels/test_*_host.cpp
  *   orc_matmul_quant_f5       -- closed-form KAT of test_quant_roofline.cpp:71-92
  *                                (0x55 bytes, scale .01) + f64 dequant brute force
@@ -267,6 +270,30 @@ void orc_matmul_f32_acc(const float *lhs, const float *rhs, float *out,
       for (int64_t kk = 0; kk < k; kk++) acc += A[i * k + kk] * B[kk * n + j];
       C[i * n + j] = acc;
     }
+}
+
+void orc_batch_matmul_f32(const float *A, const float *B, float *C, int64_t Bt,
+                          int64_t M, int64_t K, int64_t N) {
+  for (int64_t b = 0; b < Bt; b++)
+    for (int64_t i = 0; i < M; i++)
+      for (int64_t j = 0; j < N; j++) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; k++)
+          acc += (double)A[(b * M + i) * K + k] * (double)B[(b * K + k) * N + j];
+        C[(b * M + i) * N + j] = (float)acc;
+      }
+}
+
+void orc_batch_matmul_f64(const double *A, const double *B, double *C, int64_t Bt,
+                          int64_t M, int64_t K, int64_t N) {
+  for (int64_t b = 0; b < Bt; b++)
+    for (int64_t i = 0; i < M; i++)
+      for (int64_t j = 0; j < N; j++) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; k++)
+          acc += A[(b * M + i) * K + k] * B[(b * K + k) * N + j];
+        C[(b * M + i) * N + j] = acc;
+      }
 }
 
 void orc_rmsnorm(const float *in, const float *w, float *out, int64_t size,

@@ -84,6 +84,18 @@ int32_t orc_checksum_i16(const int16_t *C, int64_t n);
 
 /* ------------------------------------------------------------ fp32 ops -- */
 
+/* Rank-3 tensor_matmul: C[b,i,j] = sum_k A[b,i,k] * B[b,k,j] for A[Bt,M,K],
+ * B[Bt,K,N], contiguous, C overwritten (linalg.batch_matmul into the zero-filled
+ * result, src/mlir/lowering/ConvertSimpToMemRef.cpp:2926-2933,3286-3291).  The
+ * sum is taken in double, k increasing, and rounded once.  Pinned by the known
+ * answers of simptensor/tests/test_matmul_dot.sl:135-199 (20.0, 19.0) and
+ * tests/test_tensor_matmul.sl:66-117 (C[0,0,0] = 20 from its fill formulas), and
+ * by agreement with orc_matmul_f32_acc batch by batch. */
+void orc_batch_matmul_f32(const float *A, const float *B, float *C, int64_t Bt,
+                          int64_t M, int64_t K, int64_t N);
+void orc_batch_matmul_f64(const double *A, const double *B, double *C, int64_t Bt,
+                          int64_t M, int64_t K, int64_t N);
+
 /* Array builtin matmul: C += A*B on 1-D arrays viewed as row-major matrices
  * at element offsets (src/mlir/lowering/ConvertSimpToMemRef.cpp:1794-1920,
  * F4).  K is summed in increasing order in fp32 starting from C. */

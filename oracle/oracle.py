@@ -42,6 +42,8 @@ _s("orc_llama_quant_forward", [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _
 _s("orc_int4_recipe_inputs", [_I, _P, _P])
 _s("orc_checksum_i16", [_P, _I], C.c_int32)
 _s("orc_matmul_f32_acc", [_P, _P, _P, _I, _I, _I, _I, _I, _I])
+_s("orc_batch_matmul_f32", [_P, _P, _P, _I, _I, _I, _I])
+_s("orc_batch_matmul_f64", [_P, _P, _P, _I, _I, _I, _I])
 _s("orc_rmsnorm", [_P, _P, _P, _I, _F, _I])
 _s("orc_softmax", [_P, _P, _I, _I, _I])
 _s("orc_silu", [_P, _P, _I])
@@ -235,6 +237,42 @@ def checksum_i32(c) -> int:
 def matmul_f32_acc(lhs, rhs, out, m, k, n, lhs_off=0, rhs_off=0, out_off=0):
     _o.orc_matmul_f32_acc(_p(lhs), _p(rhs), _p(out), m, k, n, lhs_off, rhs_off, out_off)
     return out
+
+
+def batch_matmul(a, b):
+    """Rank-3 ``tensor_matmul``: C[b] = A[b] B[b] (ConvertSimpToMemRef.cpp:3286-3291).
+
+    f32 and f64 go to orc_batch_matmul_*; i8 (s8 x s8 -> i32, linalg's sign
+    extension) runs orc_matmul_i8 on each batch."""
+    if a.ndim != 3 or b.ndim != 3 or a.shape[0] != b.shape[0] or a.shape[2] != b.shape[1]:
+        raise ValueError("batch_matmul: A[Bt,M,K] x B[Bt,K,N] expected")
+    bt, m, k = a.shape
+    n = b.shape[2]
+    if a.dtype == np.int8:
+        c = np.empty((bt, m, n), np.int32)
+        for i in range(bt):
+            c[i] = matmul_i8(np.ascontiguousarray(a[i]), np.ascontiguousarray(b[i]))
+        return c
+    dt = np.float64 if a.dtype == np.float64 else np.float32
+    a = np.ascontiguousarray(a, dt)
+    b = np.ascontiguousarray(b, dt)
+    c = np.empty((bt, m, n), dt)
+    fn = _o.orc_batch_matmul_f64 if dt == np.float64 else _o.orc_batch_matmul_f32
+    fn(_p(a), _p(b), _p(c), bt, m, k, n)
+    return c
+
+
+def matmul_nhwc(x, w):
+    """4-D x 2-D ``tensor_matmul`` (ConvertSimpToMemRef.cpp:3293-3361), in the
+    reference's steps: collapse (N,H,W) to rows, transpose the [C_out, C_in]
+    weights to [C_in, C_out], multiply, expand back."""
+    nb, h, wd, cin = x.shape
+    cout = w.shape[0]
+    if w.shape[1] != cin:
+        raise ValueError("matmul_nhwc: weights must be [C_out, C_in]")
+    rows = np.ascontiguousarray(x).reshape(1, nb * h * wd, cin)
+    wt = np.ascontiguousarray(np.asarray(w).T).reshape(1, cin, cout)
+    return batch_matmul(rows, wt).reshape(nb, h, wd, cout)
 
 
 def rmsnorm(x, w, eps=1e-5, w_off=0, size=None):

@@ -27,6 +27,9 @@ from .host import (  # noqa: F401
     tensor_matmul_f32,
     tensor_matmul_nt_f32,
     tensor_matvecmul_f32,
+    tensor_matmul_f64,
+    tensor_batch_matmul,
+    tensor_matmul_nhwc,
     rmsnorm,
     softmax,
     silu,

@@ -60,6 +60,14 @@ _sig("simp_rt_matmul_f32", _D1 * 3 + [_I] * 6)
 _sig("simp_rt_tensor_matmul_f32", _D2 * 3)
 _sig("simp_rt_tensor_matmul_nt_f32", _D2 * 3)
 _sig("simp_rt_tensor_matvecmul_f32", _D2 * 3)
+_sig("simp_rt_tensor_matmul_f64", _D2 * 3)
+_D3 = [_P, _P, _I] + [_I] * 6
+_D4 = [_P, _P, _I] + [_I] * 8
+for _n in ("simp_rt_tensor_batch_matmul_f32", "simp_rt_tensor_batch_matmul_f64",
+           "simp_rt_tensor_batch_matmul_i8"):
+    _sig(_n, _D3 * 3)
+for _n in ("simp_rt_tensor_matmul_nhwc_f32", "simp_rt_tensor_matmul_nhwc_f64"):
+    _sig(_n, _D4 + _D2 + _D4)
 _sig("simp_rt_rmsnorm", _D1 * 3 + [_I, C.c_double, _I])
 _sig("simp_rt_softmax", _D1 * 2 + [_I, _I, _I])
 _sig("simp_rt_silu", _D1 * 2 + [_I])
@@ -133,6 +141,24 @@ def desc2(x):
     if len(shape) != 2:
         raise ValueError("expected a rank-2 tensor")
     return [p, p, 0, shape[0], shape[1], st0, 1]
+
+
+def descn(x, rank: int):
+    """Rank-``rank`` memref descriptor (alloc, aligned, offset, sizes..., strides...)
+    of a torch tensor or numpy array; strides in elements, the innermost must be 1."""
+    if _is_torch(x):
+        p, shape, strides = x.data_ptr(), tuple(x.shape), tuple(x.stride())
+    else:
+        import numpy as np
+        if not isinstance(x, np.ndarray):
+            raise TypeError(f"unsupported operand type {type(x)}")
+        p, shape = x.ctypes.data, x.shape
+        if any(st % x.itemsize for st in x.strides):
+            raise ValueError("strides must be whole elements")
+        strides = tuple(st // x.itemsize for st in x.strides)
+    if len(shape) != rank:
+        raise ValueError(f"expected a rank-{rank} tensor, got shape {tuple(shape)}")
+    return [p, p, 0, *shape, *strides]
 
 
 def desc1(x):
@@ -301,6 +327,37 @@ def tensor_matvecmul_f32(a, b, c):
     _check("simp_rt_tensor_matvecmul_f32",
            lib.simp_rt_tensor_matvecmul_f32(*desc2(a), *desc2(b), *desc2(c)))
     return c
+
+
+def tensor_matmul_f64(a, b, c):
+    """``tensor_matmul`` on f64 tensors: C = A B, C overwritten."""
+    _check("simp_rt_tensor_matmul_f64",
+           lib.simp_rt_tensor_matmul_f64(*desc2(a), *desc2(b), *desc2(c)))
+    return c
+
+
+_BATCH = {"float32": "f32", "float64": "f64", "int8": "i8"}
+
+
+def tensor_batch_matmul(a, b, c):
+    """Rank-3 ``tensor_matmul``: C[b] = A[b] x B[b] for A[Bt,M,K], B[Bt,K,N]
+    (f32, f64, or s8 x s8 -> i32), C overwritten."""
+    kind = _BATCH.get(str(a.dtype).replace("torch.", ""))
+    if kind is None:
+        raise TypeError(f"tensor_batch_matmul: unsupported dtype {a.dtype}")
+    fn = f"simp_rt_tensor_batch_matmul_{kind}"
+    _check(fn, getattr(lib, fn)(*descn(a, 3), *descn(b, 3), *descn(c, 3)))
+    return c
+
+
+def tensor_matmul_nhwc(x, w, y):
+    """4-D x 2-D ``tensor_matmul``: y[n,h,w,o] = sum_i x[n,h,w,i] w[o,i] (f32 or f64)."""
+    kind = _BATCH.get(str(x.dtype).replace("torch.", ""))
+    if kind not in ("f32", "f64"):
+        raise TypeError(f"tensor_matmul_nhwc: unsupported dtype {x.dtype}")
+    fn = f"simp_rt_tensor_matmul_nhwc_{kind}"
+    _check(fn, getattr(lib, fn)(*descn(x, 4), *desc2(w), *descn(y, 4)))
+    return y
 
 
 def rmsnorm(inp, weight, out, size, epsilon=1e-5, weight_offset=0):

@@ -11,6 +11,7 @@
 // held in registers for the whole kernel, the next row's loads in flight while
 // the current row is reduced.  n > 1 runs an LDS-tiled fp32 GEMM.
 #include <algorithm>
+#include <type_traits>
 
 #include "rt_device.h"
 #include "rt_internal.h"
@@ -74,43 +75,53 @@ __global__ void __launch_bounds__(256)
   if (lane == 0) y[row] = beta != 0.f ? y[row] + s : s;
 }
 
-// C = beta*C + A*B, 64x64 tile per 256 threads, each thread a 4x4 block.
-// BT: B is given transposed, B_T[N,K] (row n holds column n of B).
-template <bool BT>
+__device__ __forceinline__ float fma_t(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ __forceinline__ double fma_t(double a, double b, double c) { return fma(a, b, c); }
+
+// C = beta*C + A*B, 64x64 tile per 256 threads, each thread a 4x4 block; T is
+// float or double.  BT: B is given transposed, B_T[N,K] (row n holds column n
+// of B).  Workgroup x indexes the tiles (n fastest), z the batch: operand
+// bases advance by sa/sb/sc elements per batch.
+template <typename T, bool BT>
 __global__ void __launch_bounds__(256)
-    gemm_f32(const float *__restrict__ A, int64_t lda, const float *__restrict__ B, int64_t ldb,
-             float *__restrict__ C, int64_t ldc, int M, int N, int K, float beta) {
-  __shared__ float sa[16][64 + 1];
-  __shared__ float sb[16][64 + 1];
+    gemm_t(const T *__restrict__ A, int64_t lda, int64_t sa, const T *__restrict__ B, int64_t ldb,
+           int64_t sb, T *__restrict__ C, int64_t ldc, int64_t sc, int M, int N, int K,
+           int tiles_n, T beta) {
+  __shared__ T sa_t[16][64 + 1];
+  __shared__ T sb_t[16][64 + 1];
+  A += blockIdx.z * sa;
+  B += blockIdx.z * sb;
+  C += blockIdx.z * sc;
   const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  float acc[4][4] = {};
+  const int tm = (int)(blockIdx.x / (unsigned)tiles_n), tn = (int)(blockIdx.x % (unsigned)tiles_n);
+  const int m0 = tm * 64, n0 = tn * 64;
+  T acc[4][4] = {};
   for (int k0 = 0; k0 < K; k0 += 16) {
     for (int i = threadIdx.x; i < 16 * 64; i += 256) {
       const int kk = i & 15, mm = i >> 4;  // A tile, k fastest
       const int gm = m0 + mm, gk = k0 + kk;
-      sa[kk][mm] = (gm < M && gk < K) ? A[(int64_t)gm * lda + gk] : 0.f;
+      sa_t[kk][mm] = (gm < M && gk < K) ? A[(int64_t)gm * lda + gk] : T(0);
       if constexpr (BT) {
         const int gn = n0 + mm;  // B_T tile, k fastest (rows of B_T are contiguous in k)
-        sb[kk][mm] = (gn < N && gk < K) ? B[(int64_t)gn * ldb + gk] : 0.f;
+        sb_t[kk][mm] = (gn < N && gk < K) ? B[(int64_t)gn * ldb + gk] : T(0);
       } else {
         const int nn = i & 63, kb = i >> 6;  // B tile, n fastest
         const int gn = n0 + nn, gk2 = k0 + kb;
-        sb[kb][nn] = (gn < N && gk2 < K) ? B[(int64_t)gk2 * ldb + gn] : 0.f;
+        sb_t[kb][nn] = (gn < N && gk2 < K) ? B[(int64_t)gk2 * ldb + gn] : T(0);
       }
     }
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < 16; kk++) {
-      float av[4], bv[4];
+      T av[4], bv[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) av[i] = sa[kk][ty * 4 + i];
+      for (int i = 0; i < 4; i++) av[i] = sa_t[kk][ty * 4 + i];
 #pragma unroll
-      for (int j = 0; j < 4; j++) bv[j] = sb[kk][tx * 4 + j];
+      for (int j = 0; j < 4; j++) bv[j] = sb_t[kk][tx * 4 + j];
 #pragma unroll
       for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        for (int j = 0; j < 4; j++) acc[i][j] = fma_t(av[i], bv[j], acc[i][j]);
     }
     __syncthreads();
   }
@@ -120,10 +131,31 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < 4; j++) {
       const int gm = m0 + ty * 4 + i, gn = n0 + tx * 4 + j;
       if (gm < M && gn < N) {
-        float *c = C + (int64_t)gm * ldc + gn;
-        *c = beta != 0.f ? *c + acc[i][j] : acc[i][j];
+        T *c = C + (int64_t)gm * ldc + gn;
+        *c = beta != T(0) ? *c + acc[i][j] : acc[i][j];
       }
     }
+}
+
+// Batched launch of gemm_t: `batch` products, operand bases `sa`/`sb`/`sc`
+// elements apart.  The batch goes on grid z in chunks of at most 65535.
+template <typename T, bool BT>
+int launch_gemm_t(const T *A, int64_t lda, int64_t sa, const T *B, int64_t ldb, int64_t sb, T *C,
+                  int64_t ldc, int64_t sc, int M, int N, int K, int64_t batch, T beta,
+                  hipStream_t st) {
+  if (M == 0 || N == 0 || batch == 0) return SIMP_RT_OK;
+  const int64_t tiles_n = cdiv(N, 64), tiles = cdiv(M, 64) * tiles_n;
+  if (tiles > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "gemm: %lld output tiles exceed one launch",
+                     (long long)tiles);
+  for (int64_t b0 = 0; b0 < batch; b0 += 65535) {
+    const unsigned nb = (unsigned)std::min<int64_t>(65535, batch - b0);
+    hipLaunchKernelGGL((gemm_t<T, BT>), dim3((unsigned)tiles, 1, nb), dim3(256), 0, st,
+                       A + b0 * sa, lda, sa, B + b0 * sb, ldb, sb, C + b0 * sc, ldc, sc, M, N, K,
+                       (int)tiles_n, beta);
+    SIMP_HIP(hipGetLastError());
+  }
+  return SIMP_RT_OK;
 }
 
 // y[0..rows) = beta*y + W x: W rows of lda floats, x and y contiguous.
@@ -159,10 +191,7 @@ int launch_matmul_f32(const float *A, int64_t lda, const float *B, int64_t ldb, 
   if (M == 0 || N == 0) return SIMP_RT_OK;
   // column vector operand (B[k*ldb], ldb == 1) and a contiguous C column: GEMV
   if (N == 1 && ldb == 1 && ldc == 1) return launch_gemv_f32(A, lda, B, C, M, K, beta, st);
-  dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
-  hipLaunchKernelGGL(gemm_f32<false>, grid, dim3(256), 0, st, A, lda, B, ldb, C, ldc, M, N, K, beta);
-  SIMP_HIP(hipGetLastError());
-  return SIMP_RT_OK;
+  return launch_gemm_t<float, false>(A, lda, 0, B, ldb, 0, C, ldc, 0, M, N, K, 1, beta, st);
 }
 
 namespace {
@@ -172,10 +201,7 @@ int launch_matmul_nt_f32(const float *A, int64_t lda, const float *BT, int64_t l
                          int64_t ldc, int M, int N, int K, hipStream_t st) {
   if (M == 0 || N == 0) return SIMP_RT_OK;
   if (M == 1) return launch_gemv_f32(BT, ldb, A, C, N, K, 0.f, st);
-  dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
-  hipLaunchKernelGGL(gemm_f32<true>, grid, dim3(256), 0, st, A, lda, BT, ldb, C, ldc, M, N, K, 0.f);
-  SIMP_HIP(hipGetLastError());
-  return SIMP_RT_OK;
+  return launch_gemm_t<float, true>(A, lda, 0, BT, ldb, 0, C, ldc, 0, M, N, K, 1, 0.f, st);
 }
 }  // namespace
 
@@ -221,6 +247,113 @@ int tensor_f32_entry(const char *name, const float *a_alloc, const float *a, int
   if (rc) return rc;
   Operand *ops[] = {&oa, &ob, &oc};
   return finish(ops, 3);
+}
+
+// Shared body of the rank-3 entry points: C[b] = A[b] x B[b] for every batch b,
+// A[Bt,M,K], B[Bt,K,N], C[Bt,M,N], C overwritten (linalg.batch_matmul into a
+// zero-filled result, ConvertSimpToMemRef.cpp:2926-2933,3286-3291).
+template <typename T>
+int batch_entry(const char *name, const T *a, int64_t a_off, const int64_t *as, const int64_t *ast,
+                const T *b, int64_t b_off, const int64_t *bs, const int64_t *bst, T *c,
+                int64_t c_off, const int64_t *cs, const int64_t *cst) {
+  int rc;
+  int64_t an, bn, cn;
+  if ((rc = check_descn("A", a, a_off, 3, as, ast, &an))) return rc;
+  if ((rc = check_descn("B", b, b_off, 3, bs, bst, &bn))) return rc;
+  if ((rc = check_descn("C", c, c_off, 3, cs, cst, &cn))) return rc;
+  const int64_t Bt = as[0], M = as[1], K = as[2], N = bs[2];
+  if (bs[0] != Bt || bs[1] != K || cs[0] != Bt || cs[1] != M || cs[2] != N)
+    return set_error(SIMP_RT_EINVAL,
+                     "%s: shape mismatch A[%lld,%lld,%lld] B[%lld,%lld,%lld] C[%lld,%lld,%lld]",
+                     name, (long long)as[0], (long long)as[1], (long long)as[2], (long long)bs[0],
+                     (long long)bs[1], (long long)bs[2], (long long)cs[0], (long long)cs[1],
+                     (long long)cs[2]);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  if (Bt == 0 || M == 0 || N == 0) return SIMP_RT_OK;
+  Operand oa, ob, oc;
+  if ((rc = oa.bind(a + a_off, sizeof(T) * (size_t)an, Operand::kIn, "A"))) return rc;
+  if ((rc = ob.bind(b + b_off, sizeof(T) * (size_t)bn, Operand::kIn, "B"))) return rc;
+  if ((rc = oc.bind(c + c_off, sizeof(T) * (size_t)cn, Operand::kOut, "C"))) return rc;
+  const T *da = (const T *)oa.dev(), *db = (const T *)ob.dev();
+  T *dc = (T *)oc.dev();
+  bool done = false;
+  if constexpr (std::is_same<T, float>::value) {
+    if (Bt == 1) {  // one product: the rank-2 dispatch (GEMV for a column B)
+      rc = launch_matmul_f32(da, ast[1], db, bst[1], dc, cst[1], (int)M, (int)N, (int)K, 0.f,
+                             cur_stream());
+      done = true;
+    }
+  }
+  if (!done)
+    rc = launch_gemm_t<T, false>(da, ast[1], ast[0], db, bst[1], bst[0], dc, cst[1], cst[0],
+                                 (int)M, (int)N, (int)K, Bt, T(0), cur_stream());
+  if (rc) return rc;
+  Operand *ops[] = {&oa, &ob, &oc};
+  return finish(ops, 3);
+}
+
+// Shared body of the rank-4 entry points: out[n,h,w,:] = W[C_out,C_in] x
+// in[n,h,w,:] (ConvertSimpToMemRef.cpp:3293-3361: collapse (N,H,W), multiply by
+// the transposed weights, expand back).  The collapse needs the three outer
+// dimensions of `in` and `out` to be one run of rows (stride0 = H*stride1,
+// stride1 = W*stride2), as memref.collapse_shape does.
+template <typename T>
+int nhwc_entry(const char *name, const T *x, int64_t x_off, const int64_t *xs, const int64_t *xst,
+               const T *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0,
+               int64_t w_st1, T *y, int64_t y_off, const int64_t *ys, const int64_t *yst) {
+  int rc;
+  int64_t xn, yn;
+  if ((rc = check_descn("input", x, x_off, 4, xs, xst, &xn))) return rc;
+  if ((rc = check_desc2("weights", w, w_off, w_s0, w_s1, w_st0, w_st1))) return rc;
+  if ((rc = check_descn("output", y, y_off, 4, ys, yst, &yn))) return rc;
+  const int64_t Cin = xs[3], Cout = w_s0;
+  if (w_s1 != Cin || ys[0] != xs[0] || ys[1] != xs[1] || ys[2] != xs[2] || ys[3] != Cout)
+    return set_error(SIMP_RT_EINVAL,
+                     "%s: shape mismatch input[%lld,%lld,%lld,%lld] weights[%lld,%lld] "
+                     "output[%lld,%lld,%lld,%lld]",
+                     name, (long long)xs[0], (long long)xs[1], (long long)xs[2], (long long)xs[3],
+                     (long long)w_s0, (long long)w_s1, (long long)ys[0], (long long)ys[1],
+                     (long long)ys[2], (long long)ys[3]);
+  const int64_t rows = xs[0] * xs[1] * xs[2];
+  if (rows == 0 || Cout == 0) return SIMP_RT_OK;
+  auto collapsible = [](const int64_t *sz, const int64_t *st) {
+    return (sz[0] == 1 || st[0] == sz[1] * st[1]) && (sz[1] == 1 || st[1] == sz[2] * st[2]);
+  };
+  if (!collapsible(xs, xst) || !collapsible(ys, yst))
+    return set_error(SIMP_RT_EINVAL, "%s: (N,H,W) of input/output do not collapse to one row run",
+                     name);
+  if (rows > INT32_MAX || Cout > INT32_MAX || Cin > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  Operand ox, ow, oy;
+  const size_t wn = Cin ? (size_t)((w_s0 - 1) * w_st0 + w_s1) : 0;
+  if ((rc = ox.bind(x + x_off, sizeof(T) * (size_t)xn, Operand::kIn, "input"))) return rc;
+  if ((rc = ow.bind(w + w_off, sizeof(T) * wn, Operand::kIn, "weights"))) return rc;
+  if ((rc = oy.bind(y + y_off, sizeof(T) * (size_t)yn, Operand::kOut, "output"))) return rc;
+  // collapsed row pitch: the W-dimension stride (N, H and W step in whole rows)
+  const T *dx = (const T *)ox.dev(), *dw = (const T *)ow.dev();
+  T *dy = (T *)oy.dev();
+  if constexpr (std::is_same<T, float>::value)
+    rc = launch_matmul_nt_f32(dx, xst[2], dw, w_st0, dy, yst[2], (int)rows, (int)Cout, (int)Cin,
+                              cur_stream());
+  else
+    rc = launch_gemm_t<T, true>(dx, xst[2], 0, dw, w_st0, 0, dy, yst[2], 0, (int)rows, (int)Cout,
+                                (int)Cin, 1, T(0), cur_stream());
+  if (rc) return rc;
+  Operand *ops[] = {&ox, &ow, &oy};
+  return finish(ops, 3);
+}
+
+// tensor_matmul on f64 tensors (the general linalg.matmul branch, :3280-3284).
+int f64_entry(const double *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0,
+              int64_t a_st1, const double *b, int64_t b_off, int64_t b_s0, int64_t b_s1,
+              int64_t b_st0, int64_t b_st1, double *c, int64_t c_off, int64_t c_s0, int64_t c_s1,
+              int64_t c_st0, int64_t c_st1) {
+  const int64_t as[3] = {1, a_s0, a_s1}, ast[3] = {a_s0 * a_st0, a_st0, a_st1};
+  const int64_t bs[3] = {1, b_s0, b_s1}, bst[3] = {b_s0 * b_st0, b_st0, b_st1};
+  const int64_t cs[3] = {1, c_s0, c_s1}, cst[3] = {c_s0 * c_st0, c_st0, c_st1};
+  return batch_entry<double>("tensor_matmul_f64", a, a_off, as, ast, b, b_off, bs, bst, c, c_off,
+                             cs, cst);
 }
 }  // namespace
 }  // namespace simp
@@ -283,6 +416,73 @@ int32_t simp_rt_tensor_matvecmul_f32(
   return tensor_f32_entry<false>("tensor_matvecmul_f32", a_alloc, a, a_off, a_s0, a_s1, a_st0,
                                  a_st1, b_alloc, b, b_off, b_s0, b_s1, b_st0, b_st1, c_alloc, c,
                                  c_off, c_s0, c_s1, c_st0, c_st1);
+}
+
+int32_t simp_rt_tensor_batch_matmul_f32(
+    const float *a_alloc, const float *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const float *b_alloc, const float *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    float *c_alloc, float *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  const int64_t as[3] = {a_s0, a_s1, a_s2}, ast[3] = {a_st0, a_st1, a_st2};
+  const int64_t bs[3] = {b_s0, b_s1, b_s2}, bst[3] = {b_st0, b_st1, b_st2};
+  const int64_t cs[3] = {c_s0, c_s1, c_s2}, cst[3] = {c_st0, c_st1, c_st2};
+  return batch_entry<float>("tensor_batch_matmul_f32", a, a_off, as, ast, b, b_off, bs, bst, c,
+                            c_off, cs, cst);
+}
+
+int32_t simp_rt_tensor_batch_matmul_f64(
+    const double *a_alloc, const double *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const double *b_alloc, const double *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    double *c_alloc, double *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  const int64_t as[3] = {a_s0, a_s1, a_s2}, ast[3] = {a_st0, a_st1, a_st2};
+  const int64_t bs[3] = {b_s0, b_s1, b_s2}, bst[3] = {b_st0, b_st1, b_st2};
+  const int64_t cs[3] = {c_s0, c_s1, c_s2}, cst[3] = {c_st0, c_st1, c_st2};
+  return batch_entry<double>("tensor_batch_matmul_f64", a, a_off, as, ast, b, b_off, bs, bst, c,
+                             c_off, cs, cst);
+}
+
+int32_t simp_rt_tensor_matmul_f64(
+    const double *a_alloc, const double *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const double *b_alloc, const double *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    double *c_alloc, double *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  return f64_entry(a, a_off, a_s0, a_s1, a_st0, a_st1, b, b_off, b_s0, b_s1, b_st0, b_st1, c,
+                   c_off, c_s0, c_s1, c_st0, c_st1);
+}
+
+int32_t simp_rt_tensor_matmul_nhwc_f32(
+    const float *x_alloc, const float *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_s2,
+    int64_t x_s3, int64_t x_st0, int64_t x_st1, int64_t x_st2, int64_t x_st3,
+    const float *w_alloc, const float *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0,
+    int64_t w_st1,
+    float *y_alloc, float *y, int64_t y_off, int64_t y_s0, int64_t y_s1, int64_t y_s2,
+    int64_t y_s3, int64_t y_st0, int64_t y_st1, int64_t y_st2, int64_t y_st3) {
+  (void)x_alloc; (void)w_alloc; (void)y_alloc;
+  const int64_t xs[4] = {x_s0, x_s1, x_s2, x_s3}, xst[4] = {x_st0, x_st1, x_st2, x_st3};
+  const int64_t ys[4] = {y_s0, y_s1, y_s2, y_s3}, yst[4] = {y_st0, y_st1, y_st2, y_st3};
+  return nhwc_entry<float>("tensor_matmul_nhwc_f32", x, x_off, xs, xst, w, w_off, w_s0, w_s1,
+                           w_st0, w_st1, y, y_off, ys, yst);
+}
+
+int32_t simp_rt_tensor_matmul_nhwc_f64(
+    const double *x_alloc, const double *x, int64_t x_off, int64_t x_s0, int64_t x_s1, int64_t x_s2,
+    int64_t x_s3, int64_t x_st0, int64_t x_st1, int64_t x_st2, int64_t x_st3,
+    const double *w_alloc, const double *w, int64_t w_off, int64_t w_s0, int64_t w_s1, int64_t w_st0,
+    int64_t w_st1,
+    double *y_alloc, double *y, int64_t y_off, int64_t y_s0, int64_t y_s1, int64_t y_s2,
+    int64_t y_s3, int64_t y_st0, int64_t y_st1, int64_t y_st2, int64_t y_st3) {
+  (void)x_alloc; (void)w_alloc; (void)y_alloc;
+  const int64_t xs[4] = {x_s0, x_s1, x_s2, x_s3}, xst[4] = {x_st0, x_st1, x_st2, x_st3};
+  const int64_t ys[4] = {y_s0, y_s1, y_s2, y_s3}, yst[4] = {y_st0, y_st1, y_st2, y_st3};
+  return nhwc_entry<double>("tensor_matmul_nhwc_f64", x, x_off, xs, xst, w, w_off, w_s0, w_s1,
+                            w_st0, w_st1, y, y_off, ys, yst);
 }
 
 }  // extern "C"

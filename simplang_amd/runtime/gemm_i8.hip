@@ -81,7 +81,7 @@ template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8, bool ATO
 __global__ void __launch_bounds__(WGM *WGN * 64)
     gemm_i8_mfma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
                  int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
-                 int tiles_m, int tiles_n, int k_span) {
+                 int tiles_m, int tiles_n, int k_span, int64_t sa, int64_t sb, int64_t sc) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int FM = WM / 32, FN = WN / 32;
@@ -96,6 +96,9 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   __shared__ uint4 sA[2][KC * BM];
   __shared__ uint4 sB[2][KC * BN];
 
+  A += blockIdx.z * sa;  // batch z of a batched product (0 strides otherwise)
+  B += blockIdx.z * sb;
+  C += blockIdx.z * sc;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
   int tm, tn;
@@ -668,26 +671,35 @@ __global__ void __launch_bounds__(256)
 }
 
 // Correctness fallback for shapes the MFMA path cannot load with aligned
-// vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).
+// vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).  Rows
+// stride over grid y; z is the batch.
 template <bool BNK, bool AU8>
 __global__ void __launch_bounds__(256)
     gemm_i8_generic(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
-                    int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K) {
+                    int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+                    int64_t sa, int64_t sb, int64_t sc) {
+  A += blockIdx.z * sa;
+  B += blockIdx.z * sb;
+  C += blockIdx.z * sc;
   const int col = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (row >= M || col >= N) return;
-  uint32_t s = 0;
-  for (int k = 0; k < K; k++) {
-    const int32_t a = AU8 ? (int32_t)(uint8_t)A[(int64_t)row * lda + k]
-                          : (int32_t)A[(int64_t)row * lda + k];
-    const int32_t b = BNK ? (int32_t)B[(int64_t)col * ldb + k] : (int32_t)B[(int64_t)k * ldb + col];
-    s += (uint32_t)(a * b);
+  if (col >= N) return;
+  for (int row = blockIdx.y * 4 + (threadIdx.x >> 6); row < M; row += gridDim.y * 4) {
+    uint32_t s = 0;
+    for (int k = 0; k < K; k++) {
+      const int32_t a = AU8 ? (int32_t)(uint8_t)A[(int64_t)row * lda + k]
+                            : (int32_t)A[(int64_t)row * lda + k];
+      const int32_t b =
+          BNK ? (int32_t)B[(int64_t)col * ldb + k] : (int32_t)B[(int64_t)k * ldb + col];
+      s += (uint32_t)(a * b);
+    }
+    C[(int64_t)row * ldc + col] = (int32_t)s;
   }
-  C[(int64_t)row * ldc + col] = (int32_t)s;
 }
 
+// C[z][r, c] = 0 for r < M, c < N (z: batch, sc elements apart).
 __global__ void __launch_bounds__(256)
-    fill_i32_2d(int32_t *__restrict__ C, int64_t ldc, int M, int N) {
+    fill_i32_2d(int32_t *__restrict__ C, int64_t ldc, int M, int N, int64_t sc) {
+  C += blockIdx.z * sc;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)M * N) return;
   const int64_t r = i / N, c = i - r * N;
@@ -702,6 +714,8 @@ struct GemmArgs {
   int32_t *C;
   int64_t ldc;
   int M, N, K;
+  int batch = 1;                   // products on grid z (at most 65535)
+  int64_t sa = 0, sb = 0, sc = 0;  // element distance between consecutive products
 };
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8>
@@ -711,19 +725,19 @@ int launch_mfma(const GemmArgs &g, int splits, hipStream_t st) {
   splits = std::max(1, std::min(splits, nkt));
   const int k_span = (int)cdiv(nkt, splits) * BK;
   splits = (int)cdiv(g.K, k_span);
-  dim3 grid(tiles_m * tiles_n, splits), block(WGM * WGN * 64);
+  dim3 grid(tiles_m * tiles_n, splits, g.batch), block(WGM * WGN * 64);
   KernelTimer kt(st, "gemm_i8_mfma");
   if (splits > 1) {
     const int64_t tot = (int64_t)g.M * g.N;
-    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C, g.ldc,
-                       g.M, g.N);
+    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256), 1, g.batch), dim3(256), 0, st,
+                       g.C, g.ldc, g.M, g.N, g.sc);
     hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, BK, WGM, WGN, BNK, AU8, true>), grid, block, 0, st,
                        g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tiles_m, tiles_n,
-                       k_span);
+                       k_span, g.sa, g.sb, g.sc);
   } else {
     hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, BK, WGM, WGN, BNK, AU8, false>), grid, block, 0,
                        st, g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tiles_m, tiles_n,
-                       k_span);
+                       k_span, g.sa, g.sb, g.sc);
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
@@ -731,27 +745,44 @@ int launch_mfma(const GemmArgs &g, int splits, hipStream_t st) {
 
 template <bool BNK, bool AU8>
 int dispatch(const GemmArgs &g, hipStream_t st) {
-  if (g.M == 0 || g.N == 0) return SIMP_RT_OK;
-  if (g.K == 0) {
-    const int64_t tot = (int64_t)g.M * g.N;
-    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C, g.ldc,
-                       g.M, g.N);
-    SIMP_HIP(hipGetLastError());
-    return SIMP_RT_OK;
-  }
-  const bool a_ok = g.K % 16 == 0 && g.lda % 16 == 0 && ((uintptr_t)g.A & 15) == 0;
-  const bool b_ok = BNK ? (g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0)
-                        : (g.N % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.B & 3) == 0);
-  if (!a_ok || !b_ok) {
-    dim3 grid((unsigned)cdiv(g.N, 64), (unsigned)cdiv(g.M, 4));
-    hipLaunchKernelGGL((gemm_i8_generic<BNK, AU8>), grid, dim3(256), 0, st, g.A, g.lda, g.B,
-                       g.ldb, g.C, g.ldc, g.M, g.N, g.K);
-    SIMP_HIP(hipGetLastError());
-    return SIMP_RT_OK;
-  }
+  if (g.M == 0 || g.N == 0 || g.batch == 0) return SIMP_RT_OK;
   const int64_t cus = num_cus();
   auto tiles = [&](int bm, int bn) { return cdiv(g.M, bm) * cdiv(g.N, bn); };
-  if (tiles(256, 256) >= cus && g.N % 16 == 0) {
+  if (g.batch > 1 && tiles(256, 256) >= cus) {
+    // each product fills the chip alone: one dispatch per product, in stream order
+    for (int b = 0; b < g.batch; b++) {
+      GemmArgs h = g;
+      h.A += b * g.sa;
+      h.B += b * g.sb;
+      h.C += b * g.sc;
+      h.batch = 1;
+      h.sa = h.sb = h.sc = 0;
+      int rc = dispatch<BNK, AU8>(h, st);
+      if (rc) return rc;
+    }
+    return SIMP_RT_OK;
+  }
+  if (g.K == 0) {
+    const int64_t tot = (int64_t)g.M * g.N;
+    hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256), 1, g.batch), dim3(256), 0, st,
+                       g.C, g.ldc, g.M, g.N, g.sc);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
+  const bool a_ok = g.K % 16 == 0 && g.lda % 16 == 0 && ((uintptr_t)g.A & 15) == 0 &&
+                    g.sa % 16 == 0;
+  const bool b_ok = BNK ? (g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0 && g.sb % 16 == 0)
+                        : (g.N % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.B & 3) == 0 &&
+                           g.sb % 4 == 0);
+  if (!a_ok || !b_ok) {
+    dim3 grid((unsigned)cdiv(g.N, 64), (unsigned)std::min<int64_t>(cdiv(g.M, 4), 65535),
+              g.batch);
+    hipLaunchKernelGGL((gemm_i8_generic<BNK, AU8>), grid, dim3(256), 0, st, g.A, g.lda, g.B,
+                       g.ldb, g.C, g.ldc, g.M, g.N, g.K, g.sa, g.sb, g.sc);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
+  if (g.batch == 1 && tiles(256, 256) >= cus && g.N % 16 == 0) {
     // Workspace: [colsum: N int32, 256-byte aligned][B_T: N x K bytes when B is [K,N]]
     GemmArgs h = g;
     const size_t cs_bytes = AU8 ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
@@ -764,7 +795,7 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       int8_t *bt = (int8_t *)ws + cs_bytes;
       if (AU8)
         hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
-                           (int64_t)g.N, 1, g.N);
+                           (int64_t)g.N, 1, g.N, (int64_t)0);
       KernelTimer kt(st, "transpose_i8");
       hipLaunchKernelGGL(transpose_i8<KT>, dim3((unsigned)cdiv(g.N, 128), (unsigned)cdiv(g.K, KT)),
                          dim3(256), 0, st, g.B, g.ldb, bt, g.K, g.N, colsum);
@@ -791,13 +822,13 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     SIMP_HIP(hipGetLastError());
     return SIMP_RT_OK;
   }
-  if (tiles(128, 128) >= cus) return launch_mfma<128, 128, 128, 2, 2, BNK, AU8>(g, 1, st);
+  if (tiles(128, 128) * g.batch >= cus) return launch_mfma<128, 128, 128, 2, 2, BNK, AU8>(g, 1, st);
   if (g.M > 32) {
-    const int64_t t = tiles(64, 64);
+    const int64_t t = tiles(64, 64) * g.batch;
     const int s = (int)std::min<int64_t>(cdiv(2 * cus, t), 16);
     return launch_mfma<64, 64, 128, 2, 2, BNK, AU8>(g, t >= cus ? 1 : s, st);
   }
-  const int64_t t = tiles(32, 64);
+  const int64_t t = tiles(32, 64) * g.batch;
   const int s = (int)std::min<int64_t>(cdiv(2 * cus, t), 16);
   return launch_mfma<32, 64, 128, 1, 2, BNK, AU8>(g, t >= cus ? 1 : s, st);
 }
@@ -910,6 +941,47 @@ int gemm_entry(const char *name, const void *a, int64_t a_off, int64_t a_s0, int
   return finish(ops, 3);
 }
 
+// Rank-3 s8 x s8 -> i32: C[b] = A[b] x B[b] for every batch b (linalg.batch_matmul
+// on i8 operands into the zero-filled i32 result, ConvertSimpToMemRef.cpp:
+// 2926-2933,3286-3291; linalg sign-extends both operands).
+int batch_i8_entry(const int8_t *a, int64_t a_off, const int64_t *as, const int64_t *ast,
+                   const int8_t *b, int64_t b_off, const int64_t *bs, const int64_t *bst,
+                   int32_t *c, int64_t c_off, const int64_t *cs, const int64_t *cst) {
+  const char *name = "tensor_batch_matmul_i8";
+  int rc;
+  int64_t an, bn, cn;
+  if ((rc = check_descn("A", a, a_off, 3, as, ast, &an))) return rc;
+  if ((rc = check_descn("B", b, b_off, 3, bs, bst, &bn))) return rc;
+  if ((rc = check_descn("C", c, c_off, 3, cs, cst, &cn))) return rc;
+  const int64_t Bt = as[0], M = as[1], K = as[2], N = bs[2];
+  if (bs[0] != Bt || bs[1] != K || cs[0] != Bt || cs[1] != M || cs[2] != N)
+    return set_error(SIMP_RT_EINVAL,
+                     "%s: shape mismatch A[%lld,%lld,%lld] B[%lld,%lld,%lld] C[%lld,%lld,%lld]",
+                     name, (long long)as[0], (long long)as[1], (long long)as[2], (long long)bs[0],
+                     (long long)bs[1], (long long)bs[2], (long long)cs[0], (long long)cs[1],
+                     (long long)cs[2]);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  if (Bt == 0 || M == 0 || N == 0) return SIMP_RT_OK;
+  Operand oa, ob, oc;
+  if ((rc = oa.bind(a + a_off, (size_t)an, Operand::kIn, "A"))) return rc;
+  if ((rc = ob.bind(b + b_off, (size_t)bn, Operand::kIn, "B"))) return rc;
+  if ((rc = oc.bind(c + c_off, 4 * (size_t)cn, Operand::kOut, "C"))) return rc;
+  const int8_t *da = (const int8_t *)oa.dev(), *db = (const int8_t *)ob.dev();
+  int32_t *dc = (int32_t *)oc.dev();
+  for (int64_t b0 = 0; b0 < Bt; b0 += 65535) {  // grid z holds at most 65535 products
+    GemmArgs g{da + b0 * ast[0], ast[1], db + b0 * bst[0], bst[1], dc + b0 * cst[0], cst[1],
+               (int)M, (int)N, (int)K};
+    g.batch = (int)std::min<int64_t>(65535, Bt - b0);
+    g.sa = ast[0];
+    g.sb = bst[0];
+    g.sc = cst[0];
+    if ((rc = dispatch<false, false>(g, cur_stream()))) return rc;
+  }
+  Operand *ops[] = {&oa, &ob, &oc};
+  return finish(ops, 3);
+}
+
 }  // namespace
 }  // namespace simp
 
@@ -963,6 +1035,20 @@ int32_t simp_rt_tensor_matvecmul_i8(
   return gemm_entry<false, false>("tensor_matvecmul_i8", a, a_off, a_s0, a_s1, a_st0, a_st1, b,
                                   b_off, b_s0, b_s1, b_st0, b_st1, c, c_off, c_s0, c_s1, c_st0,
                                   c_st1);
+}
+
+int32_t simp_rt_tensor_batch_matmul_i8(
+    const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+    int64_t a_st0, int64_t a_st1, int64_t a_st2,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_s2,
+    int64_t b_st0, int64_t b_st1, int64_t b_st2,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+    int64_t c_st0, int64_t c_st1, int64_t c_st2) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  const int64_t as[3] = {a_s0, a_s1, a_s2}, ast[3] = {a_st0, a_st1, a_st2};
+  const int64_t bs[3] = {b_s0, b_s1, b_s2}, bst[3] = {b_st0, b_st1, b_st2};
+  const int64_t cs[3] = {c_s0, c_s1, c_s2}, cst[3] = {c_st0, c_st1, c_st2};
+  return batch_i8_entry(a, a_off, as, ast, b, b_off, bs, bst, c, c_off, cs, cst);
 }
 
 int32_t simp_rt_tensor_matmul_i4(

@@ -230,6 +230,33 @@ int check_desc2(const char *name, const void *aligned, int64_t off, int64_t s0,
   return SIMP_RT_OK;
 }
 
+int check_descn(const char *name, const void *aligned, int64_t off, int rank,
+                const int64_t *sizes, const int64_t *strides, int64_t *span) {
+  *span = 0;
+  if (off < 0) return set_error(SIMP_RT_EINVAL, "%s: negative offset", name);
+  bool empty = false;
+  for (int i = 0; i < rank; i++) {
+    if (sizes[i] < 0) return set_error(SIMP_RT_EINVAL, "%s: negative size", name);
+    empty |= sizes[i] == 0;
+  }
+  if (empty) return SIMP_RT_OK;
+  if (!aligned) return set_error(SIMP_RT_EINVAL, "%s: null pointer", name);
+  if (strides[rank - 1] != 1)
+    return set_error(SIMP_RT_EINVAL, "%s: inner stride %lld != 1 (row-major required)", name,
+                     (long long)strides[rank - 1]);
+  int64_t inner = sizes[rank - 1];  // span of the levels inside level i
+  for (int i = rank - 2; i >= 0; i--) {
+    if (strides[i] < inner)
+      return set_error(SIMP_RT_EINVAL, "%s: stride %d (%lld) < span %lld of the dimensions inside it",
+                       name, i, (long long)strides[i], (long long)inner);
+    if (sizes[i] - 1 > (INT64_MAX - inner) / strides[i])
+      return set_error(SIMP_RT_EINVAL, "%s: extent overflows", name);
+    inner += (sizes[i] - 1) * strides[i];
+  }
+  *span = inner;
+  return SIMP_RT_OK;
+}
+
 int check_desc1(const char *name, const void *aligned, int64_t off, int64_t size,
                 int64_t stride) {
   if (size < 0 || off < 0) return set_error(SIMP_RT_EINVAL, "%s: negative size or offset", name);

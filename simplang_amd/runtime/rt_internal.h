@@ -67,6 +67,11 @@ int check_desc2(const char *name, const void *aligned, int64_t off, int64_t s0,
                 int64_t s1, int64_t st0, int64_t st1);
 int check_desc1(const char *name, const void *aligned, int64_t off, int64_t size,
                 int64_t stride);
+// Rank-n descriptor (n <= 4): innermost stride 1, each outer stride at least the
+// span of the level inside it (no two elements alias).  *span receives the
+// element extent from the first to one past the last element (0 when empty).
+int check_descn(const char *name, const void *aligned, int64_t off, int rank,
+                const int64_t *sizes, const int64_t *strides, int64_t *span);
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

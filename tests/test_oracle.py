@@ -372,3 +372,64 @@ def test_quantize_w4s_properties(orc):
     nz = g.max(axis=2) > 0
     assert np.all(np.abs(top[nz]) == 7)
     assert s[2, 1] == 1.0 and np.all(val[2, 32:64] == 0)
+
+
+# ------------------------------------------------------ rank-3 / rank-4 --
+# Known answers of simptensor/tests/test_matmul_dot.sl:135-290 and
+# tests/test_tensor_matmul.sl:66-117.
+
+def test_batch_matmul_kats(orc):
+    a = np.arange(1, 13, dtype=np.float32).reshape(2, 2, 3)
+    b = np.tile(np.array([1, 0, 0, 1, 1, 1], np.float32), 2).reshape(2, 3, 2)
+    c = orc.batch_matmul(a, b)
+    assert c[0, 0, 0] + c[1, 0, 0] == 20.0            # test_matmul_dot.sl:135-161
+    eye = np.eye(3, dtype=np.float32)
+    a = np.stack([eye, 2 * eye, 3 * eye])
+    b = np.stack([5 * eye, 4 * eye, 2 * eye])
+    c = orc.batch_matmul(a, b)
+    assert c[0, 0, 0] + c[1, 1, 1] + c[2, 2, 2] == 19.0  # :164-199
+    assert np.count_nonzero(c) == 9                   # diagonal products only
+    # tests/test_tensor_matmul.sl:66-117 (f64): A[b,i,j] = (b+1)(i+j), B[b,i,j] = (b+1)(i+1)
+    bb, ii, jj = np.meshgrid(np.arange(2), np.arange(3), np.arange(4), indexing="ij")
+    A = ((bb + 1) * (ii + jj)).astype(np.float64)
+    bb, ii, jj = np.meshgrid(np.arange(2), np.arange(4), np.arange(3), indexing="ij")
+    B = ((bb + 1) * (ii + 1)).astype(np.float64)
+    c = orc.batch_matmul(A, B)
+    assert c[0, 0, 0] == 20.0                         # sum_j j (j+1), j < 4
+    assert c[1, 2, 1] == 4 * sum((2 + j) * (j + 1) for j in range(4))
+
+
+def test_batch_matmul_equals_2d_per_batch(orc):
+    bt, m, k, n = 3, 7, 13, 5
+    a = RNG.standard_normal((bt, m, k)).astype(np.float32)
+    b = RNG.standard_normal((bt, k, n)).astype(np.float32)
+    c = orc.batch_matmul(a, b)
+    for i in range(bt):
+        ref = np.zeros(m * n, np.float32)
+        orc.matmul_f32_acc(a[i].ravel(), b[i].ravel(), ref, m, k, n)
+        np.testing.assert_allclose(c[i].ravel(), ref, rtol=1e-5, atol=1e-5)
+    c64 = orc.batch_matmul(a.astype(np.float64), b.astype(np.float64))
+    np.testing.assert_allclose(c64, np.matmul(a.astype(np.float64), b.astype(np.float64)),
+                               rtol=1e-13, atol=1e-13)
+
+
+def test_batch_matmul_i8_vs_int64(orc):
+    a = RNG.integers(-128, 128, (4, 9, 70), dtype=np.int8)
+    b = RNG.integers(-128, 128, (4, 70, 11), dtype=np.int8)
+    c = orc.batch_matmul(a, b)
+    assert c.dtype == np.int32
+    assert (c == np.matmul(a.astype(np.int64), b.astype(np.int64))).all()
+
+
+def test_matmul_nhwc_kats(orc):
+    x = np.arange(1, 25, dtype=np.float32).reshape(2, 2, 2, 3)
+    w = np.array([[1, 0, 0], [0, 1, 0], [0, 0, 1], [.5, .5, .5]], np.float32)
+    y = orc.matmul_nhwc(x, w)
+    assert y.shape == (2, 2, 2, 4)
+    assert y[0, 0, 0, 0] + y[0, 0, 0, 3] == 4.0       # test_matmul_dot.sl:204-236
+    assert (y[..., :3] == x).all()                    # identity rows pass channels through
+    x = np.repeat(np.arange(1, 19, dtype=np.float32), 2).reshape(2, 3, 3, 2)
+    w = np.array([[1, 1], [2, 2], [3, 3]], np.float32)
+    y = orc.matmul_nhwc(x, w)
+    assert y[0, 0, 0, 0] + y[0, 0, 0, 1] + y[0, 0, 0, 2] == 12.0  # :239-268
+    assert y[1, 2, 2, 2] == 3 * 2 * 18
