@@ -331,10 +331,11 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Attention, one 1024-thread block per head (rope == nullptr: no rotation).  No
-// cross-block communication: a device-scope fence to publish partials between
-// blocks costs an L2 write-back on this multi-XCD part, more than the whole
-// head's work.  Latency is the cost here, so every cache load that depends
+// Attention, one 1024-thread block per head (rope == nullptr: no rotation), for
+// head sizes attn_split_k does not take.  No cross-block communication: a
+// device-scope fence to publish partials between blocks costs an L2 write-back
+// on this multi-XCD part, more than the whole head's work.  Latency is the
+// cost here, so every cache load that depends
 // only on pos is issued first, into registers: the K rows of the first 256
 // positions (4 lanes per position, a quarter of the head dimension each, as
 // float4) and up to kAttnVE V values per thread (thread (d, p) holds
@@ -467,6 +468,242 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
 }
 
+// Attention split over positions (head_size % 4 == 0, head_size <= 128):
+// block (h, s) of 256 threads takes positions [64 s, 64 s + 64) of head h, so
+// a long context spreads over up to seq_len / 64 CUs per head instead of one.
+// Each block issues its chunk's K rows (4 lanes per position, float4) and V
+// rows (thread (d4, pg) holds float4 d4 of positions pg, pg + P, ...) before
+// anything else, then applies RoPE to q (and to the new k for the chunk that
+// holds pos; the first head of each kv head stores k, v at pos), takes the
+// chunk's scores, a chunk-local softmax (max m_s, sum l_s) and the V sum o_s.
+// A single chunk (pos < 64) writes out = o / l directly; otherwise (o_s, m_s,
+// l_s) go to ws[h][s] and attn_combine_k forms
+//   out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s,  M = max_s m_s,
+// which equals the one-pass softmax-weighted sum up to rounding.  (Combining in
+// the last chunk's block instead, after a count of the others in a global
+// counter, measured ~4 us slower than the separate kernel: the agent-scope
+// round trips cost more than a launch.)
+constexpr int kAttnTP = 64;
+__global__ void __launch_bounds__(256)
+    attn_split_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
+                 float *__restrict__ out, float *__restrict__ ws,
+                 const StepState *__restrict__ st, int dim, int kv_dim, int n_heads,
+                 int n_kv_heads, int hs, const float2 *__restrict__ rope, int max_splits) {
+  constexpr int TP = kAttnTP, LPP = 256 / TP, KF = 32 / LPP;  // lanes per position, K float4 per lane
+  __shared__ __align__(16) float qs[128];
+  __shared__ __align__(16) float kn[128];
+  __shared__ __align__(16) float vn[128];
+  __shared__ float att[TP];
+  __shared__ __align__(16) float4 red[256];
+  __shared__ float ml[2];
+  const int h = blockIdx.x, s = blockIdx.y;
+  const int pos = st->pos;
+  const int t0 = s * TP;
+  if (t0 > pos) return;  // uniform per block
+  const int nloc = min(TP, pos + 1 - t0);
+  const int nsplit = pos / TP + 1;
+  const int kvh = h * n_kv_heads / n_heads;
+  const float *kbase = kc + kvh * hs, *vbase = vc + kvh * hs;
+  const int hs4 = hs >> 2;
+  // 1. cache loads of the chunk (rows t < pos only)
+  const int lt = threadIdx.x / LPP, sub = threadIdx.x % LPP;
+  float4 kr[KF];
+  {
+    const int t = t0 + lt;
+    const float4 *krow = (const float4 *)(kbase + (int64_t)t * kv_dim);
+#pragma unroll
+    for (int i = 0; i < KF; i++) {
+      const int j = sub + LPP * i;
+      kr[i] = (j < hs4 && t < pos) ? krow[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const int P = 256 / hs4;  // position groups of the V sum (8 * P >= TP)
+  const int d4 = threadIdx.x % hs4, pg = threadIdx.x / hs4;
+  float4 vv[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int tl = pg + e * P, t = t0 + tl;
+    vv[e] = (pg < P && tl < TP && t < pos) ? ((const float4 *)(vbase + (int64_t)t * kv_dim))[d4]
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // 2. q (and, in the chunk holding pos, the new k and v) with RoPE
+  const float *q = qkv + h * hs, *k = qkv + dim + kvh * hs, *v = qkv + dim + kv_dim + kvh * hs;
+  const bool has_pos = pos < t0 + TP;
+  for (int j = 2 * threadIdx.x; j < hs; j += 512) {
+    const float2 f = rope ? rope[(int64_t)pos * (hs >> 1) + (j >> 1)] : make_float2(1.f, 0.f);
+    qs[j] = q[j] * f.x - q[j + 1] * f.y;
+    qs[j + 1] = q[j] * f.y + q[j + 1] * f.x;
+    if (has_pos) {
+      kn[j] = k[j] * f.x - k[j + 1] * f.y;
+      kn[j + 1] = k[j] * f.y + k[j + 1] * f.x;
+      vn[j] = v[j];
+      vn[j + 1] = v[j + 1];
+    }
+  }
+  __syncthreads();
+  const bool writer = h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh;
+  if (has_pos && writer)
+    for (int j = threadIdx.x; j < hs; j += 256) {
+      kc[(int64_t)pos * kv_dim + kvh * hs + j] = kn[j];
+      vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
+    }
+  // 3. scores of the chunk
+  const float inv_scale = 1.f / sqrtf((float)hs);
+  const float4 *q4 = (const float4 *)qs;
+  {
+    float sacc = 0.f;
+    const int t = t0 + lt;
+    if (lt < nloc) {
+      if (t < pos) {
+#pragma unroll
+        for (int i = 0; i < KF; i++) {
+          const int j = sub + LPP * i;
+          if (j < hs4) {
+            const float4 a = kr[i], b = q4[j];
+            sacc = fmaf(a.x, b.x, sacc);
+            sacc = fmaf(a.y, b.y, sacc);
+            sacc = fmaf(a.z, b.z, sacc);
+            sacc = fmaf(a.w, b.w, sacc);
+          }
+        }
+      } else {
+        const float4 *kn4 = (const float4 *)kn;
+        for (int j = sub; j < hs4; j += LPP) {
+          const float4 a = kn4[j], b = q4[j];
+          sacc = fmaf(a.x, b.x, sacc);
+          sacc = fmaf(a.y, b.y, sacc);
+          sacc = fmaf(a.z, b.z, sacc);
+          sacc = fmaf(a.w, b.w, sacc);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < LPP; o <<= 1) sacc += __shfl_xor(sacc, o);
+    if (sub == 0) att[lt] = lt < nloc ? sacc * inv_scale : -INFINITY;
+  }
+  __syncthreads();
+  // 4. chunk softmax (one wave: TP == 64 lanes)
+  if (threadIdx.x < 64) {
+    const float a = att[threadIdx.x];
+    const float m = wave_max(a);
+    const float e = (int)threadIdx.x < nloc ? expf(a - m) : 0.f;
+    const float l = wave_sum(e);
+    att[threadIdx.x] = e;
+    if (threadIdx.x == 0) {
+      ml[0] = m;
+      ml[1] = l;
+    }
+  }
+  __syncthreads();
+  // 5. V sum of the chunk; the P partitions added through LDS
+  if (pg < P) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int tl = pg + e * P;
+      if (tl < nloc) {
+        const float4 x = t0 + tl == pos ? ((const float4 *)vn)[d4] : vv[e];
+        const float a = att[tl];
+        o.x = fmaf(a, x.x, o.x);
+        o.y = fmaf(a, x.y, o.y);
+        o.z = fmaf(a, x.z, o.z);
+        o.w = fmaf(a, x.w, o.w);
+      }
+    }
+    red[pg * hs4 + d4] = o;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < hs4) {
+    float4 sum = red[threadIdx.x];
+    for (int pp = 1; pp < P; pp++) {
+      const float4 x = red[pp * hs4 + threadIdx.x];
+      sum.x += x.x;
+      sum.y += x.y;
+      sum.z += x.z;
+      sum.w += x.w;
+    }
+    if (nsplit == 1) {
+      const float il = 1.f / ml[1];
+      ((float4 *)(out + h * hs))[threadIdx.x] =
+          make_float4(sum.x * il, sum.y * il, sum.z * il, sum.w * il);
+    } else {
+      float *w = ws + ((int64_t)h * max_splits + s) * (hs + 4);
+      ((float4 *)w)[threadIdx.x] = sum;
+      if (threadIdx.x == 0) {
+        w[hs] = ml[0];
+        w[hs + 1] = ml[1];
+      }
+    }
+  }
+}
+
+// Combines the chunks of attn_split_k (nothing to do when pos < 64).
+__global__ void __launch_bounds__(128)
+    attn_combine_k(const float *__restrict__ ws, float *__restrict__ out,
+                   const StepState *__restrict__ st, int hs, int max_splits) {
+  const int h = blockIdx.x, nsplit = st->pos / kAttnTP + 1;
+  if (nsplit == 1) return;
+  const float *w = ws + (int64_t)h * max_splits * (hs + 4);
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; s++) M = fmaxf(M, w[s * (hs + 4) + hs]);
+  float L = 0.f;
+  for (int s = 0; s < nsplit; s++) L += expf(w[s * (hs + 4) + hs] - M) * w[s * (hs + 4) + hs + 1];
+  const float il = 1.f / L;
+  for (int d = threadIdx.x; d < hs; d += 128) {
+    float o = 0.f;
+    for (int s = 0; s < nsplit; s++) o = fmaf(expf(w[s * (hs + 4) + hs] - M), w[s * (hs + 4) + d], o);
+    out[h * hs + d] = o * il;
+  }
+}
+
+// How a step computes attention, chosen on the host from pos (the graph of a
+// step is captured once per mode):
+//   kAttnOne    one 1024-thread block per head
+//   kAttnChunk  attn_split_k alone: pos < 64, one chunk per head, written directly
+//   kAttnSplit  attn_split_k over all chunks + attn_combine_k
+enum AttnMode { kAttnOne = 0, kAttnChunk = 1, kAttnSplit = 2 };
+
+// Workspace floats of the split attention (0: the split kernel is not used).
+int64_t attn_ws_floats(int64_t n_heads, int64_t seq_len, int hs) {
+  if (hs % 4 != 0 || hs > 128) return 0;
+  return n_heads * cdiv(seq_len, kAttnTP) * (hs + 4);
+}
+
+// The mode for a step at pos: the split kernel alone while one chunk covers the
+// context, then the one-block kernel up to `split_from`, then split + combine.
+// split_from is where split + combine measured faster on MI355X (26/12 layers,
+// cold caches): for 32 heads of 100 from pos 64 on (pos 160: 7.8 vs 8.5 us,
+// pos 511: 11.5 vs 27.5 us per layer), for 12 heads of 64 from about 480 (pos
+// 300: 9.3 vs 8.6, pos 700: 13.1 vs 16.5).  Fewer heads leave the one-block
+// kernel more CUs per head, so it keeps up longer.
+int attn_mode(int64_t pos, bool have_ws, int64_t n_heads) {
+  if (!have_ws) return kAttnOne;
+  if (pos < kAttnTP) return kAttnChunk;
+  const int64_t split_from = n_heads >= 32 ? kAttnTP : 480;
+  return pos >= split_from ? kAttnSplit : kAttnOne;
+}
+
+// One decode step's attention for one layer (cache rows [seq_len, kv_dim]).
+int launch_attention(int mode, const float *qkv, float *kc, float *vc, float *out, float *ws,
+                     const StepState *state, int dim, int kv_dim, int n_heads, int n_kv_heads,
+                     int hs, const float2 *rope, int64_t seq_len, hipStream_t st) {
+  if (mode == kAttnOne) {
+    hipLaunchKernelGGL(attn_k, dim3((unsigned)n_heads), dim3(kAttnThreads),
+                       sizeof(float) * (size_t)seq_len, st, qkv, kc, vc, out, state, dim, kv_dim,
+                       n_heads, n_kv_heads, hs, rope);
+  } else {
+    const int splits = (int)cdiv(seq_len, kAttnTP);
+    hipLaunchKernelGGL(attn_split_k, dim3((unsigned)n_heads, (unsigned)(mode == kAttnChunk ? 1 : splits)),
+                       dim3(256), 0, st, qkv, kc, vc, out, ws, state, dim, kv_dim, n_heads,
+                       n_kv_heads, hs, rope, splits);
+    if (mode == kAttnSplit)
+      hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128), 0, st,
+                         (const float *)ws, out, state, hs, splits);
+  }
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
 // RoPE factors (cos, sin)(pos * freq_j), freq_j = 1 / theta^(j / head_size)
 // for even j, as stories110M.sl:86-112 computes them at every step; tabulated
 // once per model with the same fp32 expressions, so the values are identical.
@@ -554,10 +791,11 @@ struct LlamaModel {
   float *x = nullptr, *xb = nullptr, *qkv = nullptr, *h13 = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr;
   float2 *rope = nullptr;  // [seq_len][head_size / 2] (cos, sin); null when theta <= 0
+  float *attn_ws = nullptr;  // split-attention partials; null: one block per head
   StepState *state = nullptr;
   int *prompt = nullptr, *tokens = nullptr;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph[3] = {};  // one step, per attention mode (AttnMode)
+  hipGraphExec_t exec[3] = {};
 };
 
 namespace {
@@ -623,7 +861,8 @@ Seg seg_f32(const float *W, float *out, int rows) { return Seg{W, nullptr, out, 
 Seg seg_w4(const uint8_t *W, const float *S, float *out, int rows) { return Seg{W, S, out, rows, 0}; }
 
 // Enqueues one decode step (token and pos read from the device state).
-int enqueue_step(LlamaModel &m) {
+// attn: the AttnMode of the step's position.
+int enqueue_step(LlamaModel &m, int attn) {
   const auto &c = m.cfg;
   const int dim = (int)c.dim, hid = (int)c.hidden_dim, kv = m.kv_dim, hs = m.hs;
   const int L = (int)c.n_layers, gs = c.group_size;
@@ -653,10 +892,10 @@ int enqueue_step(LlamaModel &m) {
     if ((rc = gemv(m, s, dim, kRmsNorm, kStore, m.x, m.w.rms_att + (int64_t)l * dim))) return rc;
     // 2. attention (RoPE, cache store at pos, softmax, V sum), one block per head
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
-    hipLaunchKernelGGL(attn_k, dim3((unsigned)c.n_heads), dim3(kAttnThreads),
-                       sizeof(float) * (size_t)c.seq_len, st, m.qkv, kc, vc, m.xb, m.state, dim, kv,
-                       (int)c.n_heads, (int)c.n_kv_heads, hs, (const float2 *)m.rope);
-    SIMP_HIP(hipGetLastError());
+    if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb, m.attn_ws, m.state, dim, kv,
+                               (int)c.n_heads,
+                               (int)c.n_kv_heads, hs, (const float2 *)m.rope, c.seq_len, st)))
+      return rc;
     // 3. Wo, accumulated into x (residual)
     s = Segs{};
     s.s[0] = w4 ? seg_w4(m.w.q_wo + lq / 2, m.w.s_wo + lq / gs, m.x, dim) : seg_f32(m.w.wo + lq, m.x, dim);
@@ -804,6 +1043,16 @@ int32_t simp_rt_llama_create(const simp_rt_llama_config *cfg, const simp_rt_llam
     simp_rt_llama_destroy((simp_rt_llama *)m);
     return rc;
   }
+  if (const int64_t wsf = attn_ws_floats(cfg->n_heads, cfg->seq_len, m->hs)) {
+    if ((rc = alloc((void **)&m->attn_ws, sizeof(float) * (size_t)wsf))) {
+      simp_rt_llama_destroy((simp_rt_llama *)m);
+      return rc;
+    }
+    if (hipMemset(m->attn_ws, 0, sizeof(float) * (size_t)wsf) != hipSuccess) {
+      simp_rt_llama_destroy((simp_rt_llama *)m);
+      return set_error(SIMP_RT_EHIP, "llama_create: attention workspace");
+    }
+  }
   if (cfg->rope_theta > 0.f) {
     const int64_t n = cfg->seq_len * (m->hs / 2);
     if ((rc = alloc((void **)&m->rope, sizeof(float2) * (size_t)n))) {
@@ -825,10 +1074,13 @@ int32_t simp_rt_llama_destroy(simp_rt_llama *h) {
   auto *m = (LlamaModel *)h;
   if (!m) return SIMP_RT_OK;
   (void)hipStreamSynchronize(m->stream);
-  if (m->exec) (void)hipGraphExecDestroy(m->exec);
-  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (int i = 0; i < 3; i++) {
+    if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
+    if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
+  }
   for (void *p : {(void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->h13, (void *)m->logits,
-                  (void *)m->kcache, (void *)m->vcache, (void *)m->rope, (void *)m->state,
+                  (void *)m->kcache, (void *)m->vcache, (void *)m->rope, (void *)m->attn_ws,
+                  (void *)m->state,
                   (void *)m->prompt, (void *)m->tokens})
     if (p) (void)hipFree(p);
   delete m;
@@ -844,7 +1096,7 @@ int32_t simp_rt_llama_forward(simp_rt_llama *h, int64_t token, int64_t pos, floa
   m->stream = cur_stream();
   StepState s{(int)token, (int)pos, 0, 0};
   SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->stream));
-  int rc = enqueue_step(*m);
+  int rc = enqueue_step(*m, attn_mode(pos, m->attn_ws != nullptr, m->cfg.n_heads));
   if (rc) return rc;
   if (logits) {
     Operand ol;
@@ -877,28 +1129,34 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
   SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, st));
   int rc;
   const int64_t steps = total - 1;  // the last sampled token needs no forward pass
+  // step i runs at pos i
+  auto mode_of = [&](int64_t i) { return attn_mode(i, m->attn_ws != nullptr, m->cfg.n_heads); };
   if (use_graph) {
-    if (!m->exec) {
+    auto capture = [&](int mode) -> int {
+      if (m->exec[mode]) return SIMP_RT_OK;
       SIMP_HIP(hipStreamSynchronize(st));
       hipStream_t cap;
       SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
       hipStream_t saved = m->stream;
       m->stream = cap;
       SIMP_HIP(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal));
-      rc = enqueue_step(*m);
+      int rc2 = enqueue_step(*m, mode);
       hipGraph_t g = nullptr;
       hipError_t e = hipStreamEndCapture(cap, &g);
       m->stream = saved;
       (void)hipStreamDestroy(cap);
-      if (rc) return rc;
+      if (rc2) return rc2;
       if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-      m->graph = g;
-      SIMP_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
-    }
-    for (int64_t i = 0; i < steps; i++) SIMP_HIP(hipGraphLaunch(m->exec, st));
+      m->graph[mode] = g;
+      SIMP_HIP(hipGraphInstantiate(&m->exec[mode], g, nullptr, nullptr, 0));
+      return SIMP_RT_OK;
+    };
+    for (int64_t i = 0; i < steps; i++)  // capture every mode the run needs up front
+      if ((rc = capture(mode_of(i)))) return rc;
+    for (int64_t i = 0; i < steps; i++) SIMP_HIP(hipGraphLaunch(m->exec[mode_of(i)], st));
   } else {
     for (int64_t i = 0; i < steps; i++)
-      if ((rc = enqueue_step(*m))) return rc;
+      if ((rc = enqueue_step(*m, mode_of(i)))) return rc;
   }
   SIMP_HIP(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, st));
   SIMP_HIP(hipStreamSynchronize(st));
@@ -1095,14 +1353,15 @@ struct QuantModel {
   const float *emb, *rms_att, *rms_ffn, *rms_final, *wcls, *scales, *zeros;
   const uint8_t *qw;
   float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *qkv = nullptr, *hb = nullptr, *hb2 = nullptr,
-        *logits = nullptr, *kc = nullptr, *vc = nullptr;
+        *logits = nullptr, *kc = nullptr, *vc = nullptr, *attn_ws = nullptr;
   StepState *state = nullptr;
   std::vector<const void *> registered;
 };
 
 void quant_free(QuantModel &m) {
   for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.xb2, (void *)m.qkv, (void *)m.hb,
-                  (void *)m.hb2, (void *)m.logits, (void *)m.kc, (void *)m.vc, (void *)m.state})
+                  (void *)m.hb2, (void *)m.logits, (void *)m.kc, (void *)m.vc, (void *)m.attn_ws,
+                  (void *)m.state})
     if (p) (void)hipFree(p);
   for (const void *p : m.registered) (void)simp_rt_unregister(p);
 }
@@ -1120,6 +1379,11 @@ int quant_alloc(QuantModel &m) {
   }
   if (hipMalloc((void **)&m.state, sizeof(StepState)) != hipSuccess)
     return set_error(SIMP_RT_ENOMEM, "llama2_quant_forward: device buffers");
+  if (const int64_t wsf = attn_ws_floats(m.nh, m.seq, m.hs)) {
+    if (hipMalloc((void **)&m.attn_ws, sizeof(float) * (size_t)wsf) != hipSuccess)
+      return set_error(SIMP_RT_ENOMEM, "llama2_quant_forward: device buffers");
+    SIMP_HIP(hipMemset(m.attn_ws, 0, sizeof(float) * (size_t)wsf));
+  }
   return SIMP_RT_OK;
 }
 
@@ -1137,10 +1401,10 @@ int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim, kvd, dim, gs, m.off[1] + l * m.dim * kvd, st))) return rc;
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim + kvd, kvd, dim, gs, m.off[2] + l * m.dim * kvd, st))) return rc;
     float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
-    hipLaunchKernelGGL(attn_k, dim3((unsigned)m.nh), dim3(kAttnThreads), sizeof(float) * (size_t)m.seq,
-                       st, m.qkv, kc, vc, m.xb2, m.state, dim, kvd, (int)m.nh, (int)m.nkv, m.hs,
-                       (const float2 *)nullptr);  // llama2_quant.sl applies no RoPE
-    SIMP_HIP(hipGetLastError());
+    if ((rc = launch_attention(attn_mode(pos, m.attn_ws != nullptr, m.nh), m.qkv, kc, vc, m.xb2,
+                               m.attn_ws, m.state, dim, kvd, (int)m.nh,
+                               (int)m.nkv, m.hs, nullptr, m.seq, st)))  // llama2_quant.sl: no RoPE
+      return rc;
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb2, m.xb, dim, dim, gs, m.off[3] + l * m.dim * m.dim, st))) return rc;
     hipLaunchKernelGGL(add_inplace_k, dim3(gd), dim3(256), 0, st, m.x, (const float *)m.xb, dim);
     if ((rc = launch_rmsnorm(m.x, m.rms_ffn + l * dim, m.xb, dim, eps, st))) return rc;

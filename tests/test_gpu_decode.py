@@ -65,6 +65,34 @@ def test_small_gqa_logits_and_greedy(dev, orc, fmt):
     assert np.array_equal(got, want)
 
 
+LONG = dict(dim=400, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=512,
+            seq_len=512, eps=1e-5, rope_theta=10000.0, weight_format=0, group_size=32)
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_long_context_split_attention(dev, orc, fmt):
+    """Context up to 511 (head size 100 or 96, GQA): from position 192 the step takes
+    the attention split over 64-position chunks; logits at every position of a
+    300-token prompt, then 480 greedy tokens with and without the graph."""
+    cfg = dict(LONG, weight_format=fmt, dim=400 if fmt == 0 else 384)  # head size 100 / 96
+    w = make_model(cfg, dev, seed=11 + fmt)
+    rng = np.random.default_rng(20 + fmt)
+    print(f"[decode] long context fmt {fmt} logits", flush=True)
+    _check_logits(dev, orc, cfg, w, rng.integers(0, cfg["vocab_size"], 300).astype(np.int32))
+    prompt = rng.integers(0, cfg["vocab_size"], 8).astype(np.int32)
+    m = sa.Llama(cfg, w)
+    print(f"[decode] long context fmt {fmt} greedy", flush=True)
+    got = m.generate(prompt, 480, use_graph=True)
+    got_eager = m.generate(prompt, 480, use_graph=False)
+    m.close()
+    want, margins = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 480)
+    assert np.array_equal(got, got_eager)
+    if not np.array_equal(got, want):
+        i = int(np.argmax(got != want))
+        print("first divergence at", i, "oracle top-2 margin", margins[i - len(prompt)])
+    assert np.array_equal(got, want)
+
+
 def test_110m_f32_greedy_256(dev, orc):
     """32-token random prompt, 256 greedy tokens."""
     cfg = CFG_110M

@@ -94,13 +94,14 @@ QCFG = dict(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=4, vocab_
             seq_len=16)
 
 
-def _quant_model(orc, seed, gs=128):
+def _quant_model(orc, seed, gs=128, cfg=None):
     """Arrays of llama2_quant_forward built the way bench_llama_quant.cpp:157-209
     builds them: random fp32 matrices quantized with the reference quantizer
     into one flat qweights array, offsets in elements."""
+    cfg = cfg or QCFG
     rng = np.random.default_rng(seed)
-    d, h, L, V, S = (QCFG[k] for k in ("dim", "hidden_dim", "n_layers", "vocab_size", "seq_len"))
-    kv = d * QCFG["n_kv_heads"] // QCFG["n_heads"]
+    d, h, L, V, S = (cfg[k] for k in ("dim", "hidden_dim", "n_layers", "vocab_size", "seq_len"))
+    kv = d * cfg["n_kv_heads"] // cfg["n_heads"]
     r = lambda *s: (rng.standard_normal(s) * 0.05).astype(np.float32)
     mats = [r(L, d, d), r(L, kv, d), r(L, kv, d), r(L, d, d), r(L, h, d), r(L, d, h), r(L, h, d)]
     qs, ss, zs, offs, at = [], [], [], [], 0
@@ -113,7 +114,7 @@ def _quant_model(orc, seed, gs=128):
               "qweights": np.concatenate(qs).view(np.int8), "scales": np.concatenate(ss),
               "zeros": np.concatenate(zs)}
     for k, n in (("x", d), ("xb", d), ("xb2", d), ("q", d), ("k", kv), ("v", kv),
-                 ("att", QCFG["n_heads"] * S), ("att_soft", QCFG["n_heads"] * S), ("hb", h),
+                 ("att", cfg["n_heads"] * S), ("att_soft", cfg["n_heads"] * S), ("hb", h),
                  ("hb_silu", h), ("hb2", h), ("logits", V), ("key_cache", L * S * kv),
                  ("value_cache", L * S * kv)):
         arrays[k] = np.zeros(n, np.float32)
@@ -144,4 +145,30 @@ def test_llama2_quant_forward_host_arrays(dev, orc):
     bad = dict(arrays, scales=arrays["scales"][:5])
     with pytest.raises(sa.SimpRTError):
         sa.llama2_quant_forward(bad, 0, 0, *dims, gs, offs)
+    sa.forward_cache_clear()
+
+
+@pytest.mark.parametrize("heads", [4, 32])
+def test_llama2_quant_forward_long_context(dev, orc, heads):
+    """Positions 0..259 through every attention mode of the step: one 64-position
+    chunk (pos < 64), then the one-block kernel (4 heads) or the split over
+    chunks with the combine kernel (32 heads)."""
+    gs = 128
+    cfg = dict(QCFG, seq_len=260) if heads == 4 else dict(QCFG, dim=256, n_heads=32,
+                                                           n_kv_heads=8, seq_len=260)
+    arrays, offs = _quant_model(orc, 23, gs, cfg)
+    o = orc.LlamaQuantOracle(cfg, {k: arrays[k] for k in ("token_emb", "rms_att_w", "rms_ffn_w",
+                                                          "rms_final_w", "wcls", "scales",
+                                                          "zeros")} |
+                             {"qweights": arrays["qweights"].view(np.uint8)}, gs, offs)
+    dims = tuple(cfg[k] for k in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
+                                  "vocab_size", "seq_len"))
+    toks = np.random.default_rng(5).integers(0, cfg["vocab_size"], cfg["seq_len"])
+    print("[quant-export] long context", flush=True)
+    for pos, t in enumerate(toks):
+        sa.llama2_quant_forward(arrays, int(t), pos, *dims, gs, offs)
+        want = o.forward(int(t), pos).astype(np.float64)
+        if pos % 17 == 0 or pos >= 188:
+            got = arrays["logits"].astype(np.float64)
+            assert np.abs(got - want).max() <= TOL * np.abs(want).max(), pos
     sa.forward_cache_clear()
