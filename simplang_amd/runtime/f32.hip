@@ -137,6 +137,233 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// ---------------------------------------------------------------- MFMA path
+// fp32 GEMM on v_mfma_f32_16x16x4_f32.  Block tile BM x BN (WGM x WGN waves,
+// each (BM/WGM) x (BN/WGN) in 16x16 MFMA tiles), K in steps of 16 through a
+// double-buffered LDS tile filled from registers (the next step's global loads
+// are in flight while the current step's MFMAs run).  Within a 16-wide K step,
+// lane group g = lane/16 takes k = 4g..4g+3 over the four MFMAs, so each lane
+// reads its A (and B_T) operands as one float4 from k-contiguous LDS rows; B
+// given as [K,N] stays n-contiguous in LDS and is read as four floats.
+// grid: x = output tiles (n fastest), y = K splits, z = batch.  With one split
+// the result goes to C (beta 0: overwrite, 1: accumulate); with several, each
+// split writes its own partial slice P[z][split][M][N] for gemm_f32_sum_parts.
+// Requirements (checked by the dispatch): K, lda (and ldb for B_T) multiples of
+// 4, N and ldb multiples of 4 for B[K,N], 16-byte aligned bases and batch strides.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int BM, int BN, int WGM, int WGN, bool BT>
+__global__ void __launch_bounds__(WGM *WGN * 64)
+    gemm_f32_mfma(const float *__restrict__ A, int64_t lda, int64_t sa, const float *__restrict__ B,
+                  int64_t ldb, int64_t sb, float *__restrict__ C, int64_t ldc, int64_t sc,
+                  float *__restrict__ P, int M, int N, int K, int tiles_n, int k_span, float beta) {
+  constexpr int NT = WGM * WGN * 64, BK = 16;
+  constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
+  constexpr int LDA = BK + 4;                  // k-contiguous rows (A, and B_T)
+  constexpr int LDB = BT ? BK + 4 : BN + 4;    // B[K,N]: n-contiguous rows
+  constexpr int A_TOT = BM * BK / 4, A_PER = (A_TOT + NT - 1) / NT;
+  constexpr int B_TOT = BN * BK / 4, B_PER = (B_TOT + NT - 1) / NT;
+  __shared__ __align__(16) float As[2][BM * LDA];
+  __shared__ __align__(16) float Bs[2][BT ? BN * LDB : BK * LDB];
+
+  A += blockIdx.z * sa;
+  B += blockIdx.z * sb;
+  C += blockIdx.z * sc;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int tm = (int)(blockIdx.x / (unsigned)tiles_n), tn = (int)(blockIdx.x % (unsigned)tiles_n);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = blockIdx.y * k_span, kend = min(K, kbeg + k_span);
+  const int nk = kbeg < kend ? (kend - kbeg + BK - 1) / BK : 0;
+
+  float4 ra[A_PER], rb[B_PER];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (A_TOT % NT == 0 || c < A_TOT) {
+        const int m = c >> 2, gm = m0 + m, gk = k0 + 4 * (c & 3);
+        if (gm < M && gk < kend) v = *(const float4 *)(A + (int64_t)gm * lda + gk);
+      }
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const int c = tid + i * NT;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (B_TOT % NT == 0 || c < B_TOT) {
+        if constexpr (BT) {
+          const int n = c >> 2, gn = n0 + n, gk = k0 + 4 * (c & 3);
+          if (gn < N && gk < kend) v = *(const float4 *)(B + (int64_t)gn * ldb + gk);
+        } else {
+          const int kr = c / (BN / 4), gk = k0 + kr, gn = n0 + 4 * (c % (BN / 4));
+          if (gk < kend && gn < N) v = *(const float4 *)(B + (int64_t)gk * ldb + gn);
+        }
+      }
+      rb[i] = v;
+    }
+  };
+  auto store = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const int c = tid + i * NT;
+      if (A_TOT % NT == 0 || c < A_TOT) *(float4 *)&As[st][(c >> 2) * LDA + 4 * (c & 3)] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const int c = tid + i * NT;
+      if (B_TOT % NT == 0 || c < B_TOT) {
+        if constexpr (BT) *(float4 *)&Bs[st][(c >> 2) * LDB + 4 * (c & 3)] = rb[i];
+        else *(float4 *)&Bs[st][(c / (BN / 4)) * LDB + 4 * (c % (BN / 4))] = rb[i];
+      }
+    }
+  };
+
+  v4f acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    load(kbeg);
+    store(0);
+    __syncthreads();
+  }
+  for (int kt = 0; kt < nk; kt++) {
+    const int st = kt & 1;
+    if (kt + 1 < nk) load(kbeg + (kt + 1) * BK);
+    float4 a[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) a[i] = *(const float4 *)&As[st][(wm0 + 16 * i + r16) * LDA + 4 * g];
+    float b[FN][4];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      if constexpr (BT) {
+        const float4 v = *(const float4 *)&Bs[st][(wn0 + 16 * j + r16) * LDB + 4 * g];
+        b[j][0] = v.x; b[j][1] = v.y; b[j][2] = v.z; b[j][3] = v.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) b[j][q] = Bs[st][(4 * g + q) * LDB + wn0 + 16 * j + r16];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const float av = q == 0 ? a[i].x : q == 1 ? a[i].y : q == 2 ? a[i].z : a[i].w;
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[j][q], acc[i][j], 0, 0, 0);
+      }
+    if (kt + 1 < nk) {
+      store(st ^ 1);  // the other buffer was last read before the previous barrier
+      __syncthreads();
+    }
+  }
+  // D layout: lane holds rows 4g + r (r < 4) of column r16 of each 16x16 tile
+  float *Pz = P ? P + ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * M * N : nullptr;
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn0 + 16 * j + r16;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int row = m0 + wm0 + 16 * i + 4 * g + r;
+        if (row < M && col < N) {
+          const float v = acc[i][j][r];
+          if (Pz) {
+            Pz[(int64_t)row * N + col] = v;
+          } else {
+            float *c = C + (int64_t)row * ldc + col;
+            *c = beta != 0.f ? *c + v : v;
+          }
+        }
+      }
+    }
+}
+
+// C[z] = beta*C[z] + sum_s P[z][s] (s increasing: deterministic).
+__global__ void __launch_bounds__(256)
+    gemm_f32_sum_parts(const float *__restrict__ P, float *__restrict__ C, int64_t ldc, int64_t sc,
+                       int M, int N, int parts, float beta) {
+  const int64_t mn = (int64_t)M * N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= mn) return;
+  const float *p = P + (int64_t)blockIdx.z * parts * mn + i;
+  float v = 0.f;
+  for (int s = 0; s < parts; s++) v += p[s * mn];
+  const int64_t r = i / N, c = i - r * N;
+  float *o = C + blockIdx.z * sc + r * ldc + c;
+  *o = beta != 0.f ? *o + v : v;
+}
+
+template <int BM, int BN, int WGM, int WGN, bool BT>
+int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int64_t ldb,
+                    int64_t sb, float *C, int64_t ldc, int64_t sc, int M, int N, int K, int batch,
+                    float beta, hipStream_t st) {
+  const int64_t tiles_n = cdiv(N, BN), tiles = cdiv(M, BM) * tiles_n;
+  if (tiles > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "gemm: %lld output tiles exceed one launch",
+                     (long long)tiles);
+  // split K until there are about four blocks per CU: each split at least 64
+  // deep, the partials no larger than the operands (they are written and read
+  // once more) and within 1 GiB
+  const int64_t cus = num_cus(), nkt = cdiv(K, 16);
+  int64_t splits = 1;
+  if (tiles * batch < 4 * cus && K >= 512) {
+    const int64_t mn = (int64_t)M * N, ops = (int64_t)M * K + (int64_t)K * N;
+    splits = std::min<int64_t>(std::min<int64_t>(cdiv(4 * cus, tiles * batch), 32), nkt / 4);
+    splits = std::min<int64_t>(splits, ops / std::max<int64_t>(mn, 1));
+    while (splits > 1 && (int64_t)batch * splits * mn * 4 > (int64_t(1) << 30)) splits--;
+    splits = std::max<int64_t>(splits, 1);
+  }
+  const int k_span = (int)(cdiv(nkt, splits) * 16);
+  splits = cdiv(K, k_span);
+  float *P = nullptr;
+  if (splits > 1) {
+    int rc = workspace(st, sizeof(float) * (size_t)batch * splits * M * N, (void **)&P, 3);
+    if (rc) return rc;
+  }
+  KernelTimer kt(st, "gemm_f32_mfma");
+  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, WGM, WGN, BT>),
+                     dim3((unsigned)tiles, (unsigned)splits, (unsigned)batch), dim3(WGM * WGN * 64),
+                     0, st, A, lda, sa, B, ldb, sb, C, ldc, sc, P, M, N, K, (int)tiles_n, k_span,
+                     beta);
+  SIMP_HIP(hipGetLastError());
+  if (splits > 1) {
+    hipLaunchKernelGGL(gemm_f32_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256), 1, (unsigned)batch),
+                       dim3(256), 0, st, (const float *)P, C, ldc, sc, M, N, (int)splits, beta);
+    SIMP_HIP(hipGetLastError());
+  }
+  return SIMP_RT_OK;
+}
+
+// fp32 GEMM dispatch on the MFMA path (returns 1 when the operands do not meet
+// its requirements, for the caller's SIMT fallback).
+template <bool BT>
+int dispatch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int64_t ldb,
+                      int64_t sb, float *C, int64_t ldc, int64_t sc, int M, int N, int K, int batch,
+                      float beta, hipStream_t st) {
+  auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+  const bool ok = K % 4 == 0 && lda % 4 == 0 && sa % 4 == 0 && sb % 4 == 0 && al(A) && al(B) &&
+                  (BT ? ldb % 4 == 0 : (N % 4 == 0 && ldb % 4 == 0)) && K > 0;
+  if (!ok) return 1;
+  const int64_t cus = num_cus();
+  auto tiles = [&](int bm, int bn) { return cdiv(M, bm) * cdiv(N, bn) * batch; };
+  if (M <= 16)
+    return launch_mfma_f32<16, 256, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+  if (M <= 32)
+    return launch_mfma_f32<32, 128, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+  if (tiles(128, 128) >= cus)
+    return launch_mfma_f32<128, 128, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+  return launch_mfma_f32<64, 64, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+}
+
 // Batched launch of gemm_t: `batch` products, operand bases `sa`/`sb`/`sc`
 // elements apart.  The batch goes on grid z in chunks of at most 65535.
 template <typename T, bool BT>
@@ -144,6 +371,13 @@ int launch_gemm_t(const T *A, int64_t lda, int64_t sa, const T *B, int64_t ldb, 
                   int64_t ldc, int64_t sc, int M, int N, int K, int64_t batch, T beta,
                   hipStream_t st) {
   if (M == 0 || N == 0 || batch == 0) return SIMP_RT_OK;
+  if constexpr (std::is_same<T, float>::value) {
+    if (batch <= 65535) {
+      const int rc = dispatch_mfma_f32<BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, (int)batch,
+                                           beta, st);
+      if (rc != 1) return rc;
+    }
+  }
   const int64_t tiles_n = cdiv(N, 64), tiles = cdiv(M, 64) * tiles_n;
   if (tiles > INT32_MAX)
     return set_error(SIMP_RT_EUNSUPPORTED, "gemm: %lld output tiles exceed one launch",
