@@ -12,12 +12,12 @@ with HIP events on the stream they run on (simp_rt_timing), so ``achieved`` is
 2*M*N*K over that kernel's average launch time.
 
 Also reported on the same line: the configs[1] sweep (TOPS per shape), the W4
-GEMV and decode sections, and the CPU baseline -- the oracle's restatement of
+GEMV, fp32 GEMM and decode sections, and the CPU baseline -- the oracle's restatement of
 the reference's VNNI kernel timed on this host's cores on a bounded row-block
 sample of the same 8192^3 problem.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-sweep] [--no-cpu]
-                    [--only gemm|w4|decode|copy]
+                    [--only gemm|w4|f32|decode|copy]
 
 ``--only copy`` times a plain 256 MiB device copy (the calibration run for the
 rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and prints its own JSON line.
@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "int8 GEMM TOPS (% MFMA peak); W4 decode tokens/s + HBM GB/s (1 GPU)"
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
+FP32_PEAK_TFS = 157.3    # MI355X dense fp32 MFMA
 HBM_PEAK_GBS = 8000.0
 
 
@@ -150,6 +151,31 @@ def w4_bench(dev, stream):
     return out
 
 
+def f32_bench(dev, stream):
+    """fp32 tensor_matmul (row a5) on prefill-shaped and square problems, and the
+    rank-3 batched product; inputs N(0,1) resident in HBM, HIP-graph replay."""
+    import torch
+    import simplang_amd as sa
+    out = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    for (bt, M, K, N) in ((1, 8, 2048, 2048), (1, 128, 2048, 8192), (1, 512, 2048, 2048),
+                          (1, 4096, 4096, 4096), (32, 512, 128, 512)):
+        shape = (bt, M, K) if bt > 1 else (M, K)
+        a = torch.randn(shape, device=dev, generator=g)
+        b = torch.randn((bt, K, N) if bt > 1 else (K, N), device=dev, generator=g)
+        c = torch.empty((bt, M, N) if bt > 1 else (M, N), device=dev)
+        fn = sa.tensor_batch_matmul if bt > 1 else sa.tensor_matmul_f32
+        reps = 5 if M * N * K * bt >= 2**34 else 20
+        t = graph_time_ms([lambda: fn(a, b, c)] * reps, stream)
+        tfs = 2.0 * bt * M * N * K / (t * 1e-3) / 1e12
+        out.append({"batch": bt, "M": M, "K": K, "N": N, "us": round(t * 1e3, 2),
+                    "TFs": round(tfs, 1), "frac_fp32_peak": round(tfs / FP32_PEAK_TFS, 3)})
+        del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_bench(dev, stream, with_cpu=True):
     """Greedy decode tok/s, BASELINE configs[3] (110M fp32) and configs[4]
     (3B W4): random-init weights, random prompt of 32 tokens, then 256 / 128
@@ -221,7 +247,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "w4", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "w4", "f32", "decode", "copy"], default=None,
                     help="run one section (for profiling); the JSON line is still printed")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -300,6 +326,7 @@ def main():
         torch.cuda.empty_cache()
 
     w4 = w4_bench(dev, stream) if args.only == "w4" or (args.only is None and not args.no_sweep) else []
+    f32 = f32_bench(dev, stream) if args.only == "f32" or (args.only is None and not args.no_sweep) else []
     decode = [] if args.no_decode else decode_bench(dev, stream, with_cpu=not args.no_cpu)
 
     cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baseline(n)
@@ -327,6 +354,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "w4_gemv": w4,
+        "f32_gemm": f32,
         "decode": decode,
     }
     print(json.dumps(line), flush=True)

@@ -139,9 +139,9 @@ __global__ void __launch_bounds__(256)
 
 // ---------------------------------------------------------------- MFMA path
 // fp32 GEMM on v_mfma_f32_16x16x4_f32.  Block tile BM x BN (WGM x WGN waves,
-// each (BM/WGM) x (BN/WGN) in 16x16 MFMA tiles), K in steps of 16 through a
+// each (BM/WGM) x (BN/WGN) in 16x16 MFMA tiles), K in steps of BK through a
 // double-buffered LDS tile filled from registers (the next step's global loads
-// are in flight while the current step's MFMAs run).  Within a 16-wide K step,
+// are in flight while the current step's MFMAs run).  Within each 16 of K,
 // lane group g = lane/16 takes k = 4g..4g+3 over the four MFMAs, so each lane
 // reads its A (and B_T) operands as one float4 from k-contiguous LDS rows; B
 // given as [K,N] stays n-contiguous in LDS and is read as four floats.
@@ -152,16 +152,18 @@ __global__ void __launch_bounds__(256)
 // 4, N and ldb multiples of 4 for B[K,N], 16-byte aligned bases and batch strides.
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-template <int BM, int BN, int WGM, int WGN, bool BT>
+template <int BM, int BN, int WGM, int WGN, bool BT, int BK = 16>
 __global__ void __launch_bounds__(WGM *WGN * 64)
     gemm_f32_mfma(const float *__restrict__ A, int64_t lda, int64_t sa, const float *__restrict__ B,
                   int64_t ldb, int64_t sb, float *__restrict__ C, int64_t ldc, int64_t sc,
                   float *__restrict__ P, int M, int N, int K, int tiles_n, int k_span, float beta) {
-  constexpr int NT = WGM * WGN * 64, BK = 16;
+  constexpr int NT = WGM * WGN * 64;
+  static_assert(BK % 16 == 0, "K step");
   constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
   constexpr int LDA = BK + 4;                  // k-contiguous rows (A, and B_T)
   constexpr int LDB = BT ? BK + 4 : BN + 4;    // B[K,N]: n-contiguous rows
+  constexpr int KQ = BK / 4;                   // float4 per k-contiguous row
   constexpr int A_TOT = BM * BK / 4, A_PER = (A_TOT + NT - 1) / NT;
   constexpr int B_TOT = BN * BK / 4, B_PER = (B_TOT + NT - 1) / NT;
   __shared__ __align__(16) float As[2][BM * LDA];
@@ -185,7 +187,7 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
       const int c = tid + i * NT;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (A_TOT % NT == 0 || c < A_TOT) {
-        const int m = c >> 2, gm = m0 + m, gk = k0 + 4 * (c & 3);
+        const int m = c / KQ, gm = m0 + m, gk = k0 + 4 * (c % KQ);
         if (gm < M && gk < kend) v = *(const float4 *)(A + (int64_t)gm * lda + gk);
       }
       ra[i] = v;
@@ -196,7 +198,7 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (B_TOT % NT == 0 || c < B_TOT) {
         if constexpr (BT) {
-          const int n = c >> 2, gn = n0 + n, gk = k0 + 4 * (c & 3);
+          const int n = c / KQ, gn = n0 + n, gk = k0 + 4 * (c % KQ);
           if (gn < N && gk < kend) v = *(const float4 *)(B + (int64_t)gn * ldb + gk);
         } else {
           const int kr = c / (BN / 4), gk = k0 + kr, gn = n0 + 4 * (c % (BN / 4));
@@ -210,13 +212,13 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
       const int c = tid + i * NT;
-      if (A_TOT % NT == 0 || c < A_TOT) *(float4 *)&As[st][(c >> 2) * LDA + 4 * (c & 3)] = ra[i];
+      if (A_TOT % NT == 0 || c < A_TOT) *(float4 *)&As[st][(c / KQ) * LDA + 4 * (c % KQ)] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
       const int c = tid + i * NT;
       if (B_TOT % NT == 0 || c < B_TOT) {
-        if constexpr (BT) *(float4 *)&Bs[st][(c >> 2) * LDB + 4 * (c & 3)] = rb[i];
+        if constexpr (BT) *(float4 *)&Bs[st][(c / KQ) * LDB + 4 * (c % KQ)] = rb[i];
         else *(float4 *)&Bs[st][(c / (BN / 4)) * LDB + 4 * (c % (BN / 4))] = rb[i];
       }
     }
@@ -236,29 +238,33 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   for (int kt = 0; kt < nk; kt++) {
     const int st = kt & 1;
     if (kt + 1 < nk) load(kbeg + (kt + 1) * BK);
-    float4 a[FM];
 #pragma unroll
-    for (int i = 0; i < FM; i++) a[i] = *(const float4 *)&As[st][(wm0 + 16 * i + r16) * LDA + 4 * g];
-    float b[FN][4];
+    for (int kk = 0; kk < BK; kk += 16) {
+      float4 a[FM];
 #pragma unroll
-    for (int j = 0; j < FN; j++) {
-      if constexpr (BT) {
-        const float4 v = *(const float4 *)&Bs[st][(wn0 + 16 * j + r16) * LDB + 4 * g];
-        b[j][0] = v.x; b[j][1] = v.y; b[j][2] = v.z; b[j][3] = v.w;
-      } else {
+      for (int i = 0; i < FM; i++)
+        a[i] = *(const float4 *)&As[st][(wm0 + 16 * i + r16) * LDA + kk + 4 * g];
+      float b[FN][4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) b[j][q] = Bs[st][(4 * g + q) * LDB + wn0 + 16 * j + r16];
+      for (int j = 0; j < FN; j++) {
+        if constexpr (BT) {
+          const float4 v = *(const float4 *)&Bs[st][(wn0 + 16 * j + r16) * LDB + kk + 4 * g];
+          b[j][0] = v.x; b[j][1] = v.y; b[j][2] = v.z; b[j][3] = v.w;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; q++) b[j][q] = Bs[st][(kk + 4 * g + q) * LDB + wn0 + 16 * j + r16];
+        }
       }
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+          const float av = q == 0 ? a[i].x : q == 1 ? a[i].y : q == 2 ? a[i].z : a[i].w;
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[j][q], acc[i][j], 0, 0, 0);
+        }
     }
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-      for (int i = 0; i < FM; i++) {
-        const float av = q == 0 ? a[i].x : q == 1 ? a[i].y : q == 2 ? a[i].z : a[i].w;
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[j][q], acc[i][j], 0, 0, 0);
-      }
     if (kt + 1 < nk) {
       store(st ^ 1);  // the other buffer was last read before the previous barrier
       __syncthreads();
@@ -302,7 +308,7 @@ __global__ void __launch_bounds__(256)
   *o = beta != 0.f ? *o + v : v;
 }
 
-template <int BM, int BN, int WGM, int WGN, bool BT>
+template <int BM, int BN, int WGM, int WGN, bool BT, int BK = 16>
 int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int64_t ldb,
                     int64_t sb, float *C, int64_t ldc, int64_t sc, int M, int N, int K, int batch,
                     float beta, hipStream_t st) {
@@ -330,7 +336,7 @@ int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int
     if (rc) return rc;
   }
   KernelTimer kt(st, "gemm_f32_mfma");
-  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, WGM, WGN, BT>),
+  hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, WGM, WGN, BT, BK>),
                      dim3((unsigned)tiles, (unsigned)splits, (unsigned)batch), dim3(WGM * WGN * 64),
                      0, st, A, lda, sa, B, ldb, sb, C, ldc, sc, P, M, N, K, (int)tiles_n, k_span,
                      beta);
@@ -360,7 +366,7 @@ int dispatch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, i
   if (M <= 32)
     return launch_mfma_f32<32, 128, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   if (tiles(128, 128) >= cus)
-    return launch_mfma_f32<128, 128, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+    return launch_mfma_f32<128, 128, 2, 2, BT, 32>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   return launch_mfma_f32<64, 64, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
 }
 
