@@ -213,6 +213,69 @@ def decode_bench(dev, stream, with_cpu=True):
     return out
 
 
+def llama32_bench(dev, with_cpu=True):
+    """llama32_forward (examples/llama2/llama32_1b_int8_tensor.sl) at the
+    LLaMA-3.2-1B shape of bench_llama32_1b_int8.cpp:17-25 with its init (int8
+    uniform [-64,63], fp32 uniform +-0.01), arrays resident on the device: ms per
+    call at the reference bench's positions and a 64-token loop from pos 128
+    (bench_llama32_1b_int8.cpp:240-315).  Every call is a full token (16 layers
+    of int8 GEMVs over 0.97 GB plus the 1.05 GB fp32 classifier)."""
+    import numpy as np
+    import torch
+    import simplang_amd as sa
+    D, H, L, NH, NKV, V, S, HD = 2048, 8192, 16, 32, 8, 128256, 4096, 64
+    kv = NKV * HD
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    i8 = lambda n: torch.randint(-64, 64, (n,), dtype=torch.int8, device=dev, generator=g)
+    f32 = lambda n: (torch.rand((n,), device=dev, generator=g) * 0.02 - 0.01)
+    a = {"x_i8": i8(D), "rms_att_w": f32(L * D), "rms_ffn_w": f32(L * D), "rms_final_w": f32(D),
+         "wq_t": i8(L * D * D), "wk_t": i8(L * kv * D), "wv_t": i8(L * kv * D),
+         "wo_t": i8(L * D * D), "w1_t": i8(L * H * D), "w2_t": i8(L * D * H),
+         "w3_t": i8(L * H * D), "wcls": f32(V * D),
+         "x_fp32": torch.zeros(D, device=dev), "xb_fp32": torch.zeros(D, device=dev),
+         "logits": torch.zeros(V, device=dev), "xb_i8": torch.zeros(D, dtype=torch.int8, device=dev),
+         "k_cache": torch.zeros(L * S * kv, dtype=torch.int8, device=dev),
+         "v_cache": torch.zeros(L * S * kv, dtype=torch.int8, device=dev),
+         "att_scores": torch.zeros(NH * S, device=dev), "att_probs": torch.zeros(NH * S, device=dev),
+         "attn_out": torch.zeros(D, dtype=torch.int32, device=dev),
+         "ffn_hb": torch.zeros(H, dtype=torch.int8, device=dev)}
+    dims = (D, H, L, NH, NKV, V, S, HD)
+    wbytes = L * (2 * D * D + 2 * kv * D + 3 * H * D) + 4 * V * D
+    for _ in range(2):
+        sa.llama32_forward(a, 0, *dims)
+    per_pos = []
+    for pos in (0, 127, 511, 1023, 2047, 4095):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            sa.llama32_forward(a, pos, *dims)
+        ms = (time.perf_counter() - t0) / 5 * 1e3
+        byts = wbytes + 2 * L * (pos + 1) * kv
+        per_pos.append({"pos": pos, "ms": round(ms, 3), "GBs": round(byts / ms / 1e6, 1)})
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(64):
+        sa.llama32_forward(a, 128 + i, *dims)
+    el = time.perf_counter() - t0
+    rec = {"model": "llama32-1B int8 (llama32_forward)", "positions": per_pos,
+           "loop_64_from_128": {"tok_s": round(64 / el, 1), "ms_per_token": round(el / 64 * 1e3, 3),
+                                "GBs": round((wbytes + 2 * L * 160 * kv) * 64 / el / 1e9, 1)}}
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        host = {k: v.cpu().numpy() for k, v in a.items()}
+        t0 = time.perf_counter()
+        oracle.llama32_int8_forward(host, 0, *dims)
+        rec["cpu_baseline"] = {"tok_s": round(1 / (time.perf_counter() - t0), 3), "cores": 1,
+                               "kind": "port", "sample": "one call of the oracle's restatement at pos 0"}
+        del host
+    sa.forward_cache_clear()
+    del a
+    torch.cuda.empty_cache()
+    return rec
+
+
 def decode_cpu(cfg, w, prompt, steps):
     """The oracle's restatement of the decode step on the host cores (OpenMP
     GEMVs, double accumulation), timed over a few steps."""
@@ -328,6 +391,8 @@ def main():
     w4 = w4_bench(dev, stream) if args.only == "w4" or (args.only is None and not args.no_sweep) else []
     f32 = f32_bench(dev, stream) if args.only == "f32" or (args.only is None and not args.no_sweep) else []
     decode = [] if args.no_decode else decode_bench(dev, stream, with_cpu=not args.no_cpu)
+    if not args.no_decode:
+        decode.append(llama32_bench(dev, with_cpu=not args.no_cpu))
 
     cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baseline(n)
 

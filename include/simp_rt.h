@@ -386,6 +386,32 @@ float llama2_quant_forward(
     int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
     int64_t vocab_size, int64_t seq_len, int64_t group_size, int64_t wq_off, int64_t wk_off,
     int64_t wv_off, int64_t wo_off, int64_t w1_off, int64_t w2_off, int64_t w3_off);
+/* The int8 LLaMA-3.2 program's entry point, byte-identical signature (i8[], f32[]
+ * and i32[] rank-1 descriptors, then pos and the eight i64 dims).  Replaces
+ * llama32_forward (examples/llama2/llama32_1b_int8_tensor.sl:16-305) as bound by
+ * examples/llama2/bench_llama32_1b_int8.cpp:36-61,124.  The program's
+ * arithmetic: int8 weights pre-transposed for tensor_matmul_nt, activations
+ * quantized as xb*127 clamped and truncated, int8 KV cache of (i32 / 256),
+ * fixed-point rescales by 1/256 and 1/65536, fp32 norms, softmax and classifier;
+ * the program's RoPE loop discards its results and is not run.  Dims come from
+ * the arguments (the program hard-codes 2048/512/8192, deviation D4); dim and
+ * hidden_dim and head_dim must be multiples of 16 and the int8 weights
+ * 16-byte aligned.
+ * The KV cache is kept on the device and the rows at pos are copied back into
+ * k_cache / v_cache; logits, x_fp32 and xb_fp32 are written; xb_i8,
+ * att_scores, att_probs, attn_out and ffn_hb are left untouched.  Weights and
+ * errors as for stories110M_forward. */
+#define SIMP_RT_DESC_I32(n) int32_t *n##_alloc, int32_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+float llama32_forward(
+    SIMP_RT_DESC_I8(x_i8), SIMP_RT_DESC_F32(rms_att_w), SIMP_RT_DESC_F32(rms_ffn_w),
+    SIMP_RT_DESC_F32(rms_final_w), SIMP_RT_DESC_I8(wq_t), SIMP_RT_DESC_I8(wk_t),
+    SIMP_RT_DESC_I8(wv_t), SIMP_RT_DESC_I8(wo_t), SIMP_RT_DESC_I8(w1_t), SIMP_RT_DESC_I8(w2_t),
+    SIMP_RT_DESC_I8(w3_t), SIMP_RT_DESC_F32(wcls), SIMP_RT_DESC_F32(x_fp32),
+    SIMP_RT_DESC_F32(xb_fp32), SIMP_RT_DESC_F32(logits), SIMP_RT_DESC_I8(xb_i8),
+    SIMP_RT_DESC_I8(k_cache), SIMP_RT_DESC_I8(v_cache), SIMP_RT_DESC_F32(att_scores),
+    SIMP_RT_DESC_F32(att_probs), SIMP_RT_DESC_I32(attn_out), SIMP_RT_DESC_I8(ffn_hb), int64_t pos,
+    int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
+    int64_t vocab_size, int64_t max_seq_len, int64_t head_dim);
 /* Frees the engines and device mirrors the model-level exports created (no
  * reference counterpart). */
 int32_t simp_rt_forward_cache_clear(void);

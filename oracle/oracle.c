@@ -26,7 +26,8 @@
  *   orc_rope                  -- pos 0 identity, rotation preserves pair norms,
  *                                closed-form angle for pair 0
  *   orc_llama_forward,
- *   orc_llama_quant_forward   -- parity unpinned beyond its parts: the reference
+ *   orc_llama_quant_forward,
+ *   orc_llama32_int8_forward  -- parity unpinned beyond its parts: the reference
  *                                holds no golden logits (docs/benchmark/llama_results.md:81-95)
  *   orc_quantize_w4s          -- properties: |dequant - w| <= scale/2 inside the
  *                                range, the group maximum maps to +-7 exactly,
@@ -536,6 +537,108 @@ void orc_llama_forward(const orc_llama_cfg *c, const orc_llama_weights *w,
   gemv(c, w->wcls, w->q_wcls, w->s_wcls, xb, logits, c->vocab, dim);
   free(x); free(xb); free(xb2); free(q); free(kk); free(vv);
   free(hb); free(hb2); free(att); free(att_soft);
+}
+
+/* ----------------------------------------------- llama32_forward (int8) -- */
+
+/* (i8) of an fp32 value as x86 code lowers it: cvttss2si to i32 (0x80000000 for
+ * NaN and out-of-range), then the low byte. */
+static int8_t l32_fptosi_i8(float v) {
+  if (!(v > -2147483648.0f && v < 2147483648.0f)) return 0;
+  return (int8_t)(uint8_t)(uint32_t)(int32_t)v;
+}
+
+/* val = v * 127.0; clamp to [-128, 127]; (i8)val (llama32_1b_int8_tensor.sl:90-96) */
+static int8_t l32_quant127(float v) {
+  float val = v * 127.0f;
+  if (val > 127.0f) val = 127.0f;
+  if (val < -128.0f) val = -128.0f;
+  return (int8_t)(int32_t)val;
+}
+
+/* y[n] = sum_k x[k] * w[n*K + k], i8 x i8 -> i32 with wraparound
+ * (tensor_matmul_nt on [1,K] x [N,K], ConvertSimpToMemRef.cpp:3373-3486). */
+static void l32_mv_nt(const int8_t *x, const int8_t *w, int64_t N, int64_t K, int32_t *y) {
+  for (int64_t n = 0; n < N; n++) {
+    uint32_t acc = 0;
+    for (int64_t k = 0; k < K; k++) acc += (uint32_t)((int32_t)x[k] * (int32_t)w[n * K + k]);
+    y[n] = (int32_t)acc;
+  }
+}
+
+float orc_llama32_int8_forward(const orc_llama_cfg *c, int64_t hs, const int8_t *x_i8,
+                               const float *rms_att, const float *rms_ffn,
+                               const float *rms_final, const int8_t *wq, const int8_t *wk,
+                               const int8_t *wv, const int8_t *wo, const int8_t *w1,
+                               const int8_t *w2, const int8_t *w3, const float *wcls,
+                               float *x, float *xb, float *logits, int8_t *xb_i8,
+                               int8_t *kc, int8_t *vc, float *att_scores, float *att_probs,
+                               int32_t *attn_out, int8_t *ffn_hb, int64_t pos) {
+  const int64_t dim = c->dim, hid = c->hidden, L = c->n_layers, nh = c->n_heads;
+  const int64_t S = c->seq_len, kv = c->n_kv_heads * hs, n_rep = nh / c->n_kv_heads;
+  const int64_t seq_len = pos + 1;
+  int32_t *Q = malloc(sizeof(int32_t) * dim), *K = malloc(sizeof(int32_t) * kv);
+  int32_t *V = malloc(sizeof(int32_t) * kv), *D = malloc(sizeof(int32_t) * dim);
+  int32_t *G = malloc(sizeof(int32_t) * hid), *U = malloc(sizeof(int32_t) * hid);
+  for (int64_t i = 0; i < dim; i++) x[i] = (float)x_i8[i] * 1.0f;           /* :79-83 */
+  for (int64_t l = 0; l < L; l++) {
+    orc_rmsnorm(x, rms_att, xb, dim, 1e-5f, l * dim);                      /* :93 */
+    for (int64_t i = 0; i < dim; i++) xb_i8[i] = l32_quant127(xb[i]);      /* :96-102 */
+    l32_mv_nt(xb_i8, wq + l * dim * dim, dim, dim, Q);                     /* :104-121 */
+    l32_mv_nt(xb_i8, wk + l * kv * dim, kv, dim, K);
+    l32_mv_nt(xb_i8, wv + l * kv * dim, kv, dim, V);
+    const int64_t co = l * S * kv + pos * kv;                              /* :142-151 */
+    for (int64_t i = 0; i < kv; i++) {
+      kc[co + i] = (int8_t)(uint8_t)(uint64_t)((int64_t)K[i] / 256);
+      vc[co + i] = (int8_t)(uint8_t)(uint64_t)((int64_t)V[i] / 256);
+    }
+    for (int64_t i = 0; i < dim; i++) attn_out[i] = 0;                    /* :155-159 */
+    for (int64_t h = 0; h < nh; h++) {                                     /* :161-204 */
+      const int64_t qo = h * hs, kho = (h / n_rep) * hs;
+      for (int64_t t = 0; t < seq_len; t++) {
+        float score = 0.0f;
+        const int8_t *kp = kc + l * S * kv + t * kv + kho;
+        for (int64_t d = 0; d < hs; d++) score = score + (float)Q[qo + d] * 1.0f * ((float)kp[d] * 1.0f);
+        score = score / 8.0f;
+        att_scores[h * S + t] = score;
+      }
+      orc_softmax(att_scores, att_probs, seq_len, h * S, h * S);
+      for (int64_t d = 0; d < hs; d++) {
+        float val = 0.0f;
+        for (int64_t t = 0; t < seq_len; t++)
+          val = val + att_probs[h * S + t] * ((float)vc[l * S * kv + t * kv + kho + d] * 1.0f);
+        attn_out[qo + d] = (int32_t)val;
+      }
+    }
+    for (int64_t i = 0; i < dim; i++) {                                    /* :208-216 */
+      float val = (float)attn_out[i] * 1.0f / 256.0f;
+      if (val > 127.0f) val = 127.0f;
+      if (val < -128.0f) val = -128.0f;
+      xb_i8[i] = (int8_t)(int32_t)val;
+    }
+    l32_mv_nt(xb_i8, wo + l * dim * dim, dim, dim, D);                    /* :218-222 */
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + (float)D[i] * 1.0f / 65536.0f;  /* :225-229 */
+    orc_rmsnorm(x, rms_ffn, xb, dim, 1e-5f, l * dim);                      /* :232 */
+    for (int64_t i = 0; i < dim; i++) xb_i8[i] = l32_quant127(xb[i]);      /* :235-242 */
+    l32_mv_nt(xb_i8, w1 + l * hid * dim, hid, dim, G);                     /* :245-256 */
+    l32_mv_nt(xb_i8, w3 + l * hid * dim, hid, dim, U);
+    for (int64_t i = 0; i < hid; i++) {                                    /* :258-267 */
+      const float gate_f = (float)G[i] * 1.0f / 65536.0f;
+      const float silu = gate_f / (1.0f + expf(0.0f - gate_f));
+      const float up_f = (float)U[i] * 1.0f / 65536.0f;
+      ffn_hb[i] = l32_fptosi_i8(silu * up_f * 127.0f);
+    }
+    l32_mv_nt(ffn_hb, w2 + l * dim * hid, dim, hid, D);                   /* :269-272 */
+    for (int64_t i = 0; i < dim; i++) x[i] = x[i] + (float)D[i] * 1.0f / 65536.0f;  /* :275-279 */
+  }
+  orc_rmsnorm(x, rms_final, xb, dim, 1e-5f, 0);                            /* :287 */
+  for (int64_t i = 0; i < c->vocab; i++) {                                 /* :292-302 */
+    float sum = 0.0f;
+    for (int64_t j = 0; j < dim; j++) sum = sum + wcls[i * dim + j] * xb[j];
+    logits[i] = sum;
+  }
+  free(Q); free(K); free(V); free(D); free(G); free(U);
+  return logits[0];
 }
 
 void orc_llama_quant_forward(const orc_llama_cfg *c, const float *emb, const float *rms_att,

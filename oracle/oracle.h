@@ -199,6 +199,33 @@ void orc_llama_quant_forward(const orc_llama_cfg *cfg, const float *emb, const f
                              int64_t gs, const int64_t off[7], float *key_cache,
                              float *value_cache, int64_t token, int64_t pos, float *logits);
 
+/* One call of llama32_forward, the int8 LLaMA-3.2 program
+ * examples/llama2/llama32_1b_int8_tensor.sl:16-305 (as bound by
+ * examples/llama2/bench_llama32_1b_int8.cpp:36-61), statement by statement with
+ * SimpLang's typing (float literals f32, integer literals i64,
+ * src/mlir/mlir_codegen.cpp:305-390,608-625): x = (float)x_i8; per layer
+ * rmsnorm, xb*127 clamped to [-128,127] and truncated to i8, Q/K/V =
+ * tensor_matmul_nt (i8 x i8 -> i32), no RoPE (the program computes factors and
+ * discards them, :123-140), K/V cached as (i8)(v / 256) (i64 division, integer
+ * truncation), per head scores sum_d (float)Q * (float)k / 8 (fp32, in order),
+ * softmax, attn_out = (i32) sum_t p * v, Wo on (i8)clamp(attn_out / 256), x +=
+ * Wo / 65536, FFN rmsnorm, Gate/Up on the re-quantized xb (the program's xb_mat
+ * views xb_i8), ffn_hb = (i8)(silu(g/65536) * (u/65536) * 127) with the x86
+ * lowering of an out-of-range conversion (truncate to i32, keep the low byte;
+ * NaN or beyond i32 gives 0), x += Down / 65536, final rmsnorm, fp32 classifier.
+ * cfg: dim, hidden, n_layers, n_heads, n_kv_heads, vocab, seq_len (max_seq_len);
+ * head_dim given separately (kv_dim = n_kv_heads * head_dim).  Every array of
+ * the program is written as the program writes it.  Returns logits[0]. */
+float orc_llama32_int8_forward(const orc_llama_cfg *cfg, int64_t head_dim, const int8_t *x_i8,
+                               const float *rms_att, const float *rms_ffn,
+                               const float *rms_final, const int8_t *wq, const int8_t *wk,
+                               const int8_t *wv, const int8_t *wo, const int8_t *w1,
+                               const int8_t *w2, const int8_t *w3, const float *wcls,
+                               float *x, float *xb, float *logits, int8_t *xb_i8,
+                               int8_t *k_cache, int8_t *v_cache, float *att_scores,
+                               float *att_probs, int32_t *attn_out, int8_t *ffn_hb,
+                               int64_t pos);
+
 /* Strict-'>' argmax, first maximum wins (examples/llama2/generate_stories110M.cpp:73-83). */
 int64_t orc_argmax(const float *logits, int64_t n);
 

@@ -109,6 +109,29 @@ class LlamaOracle:
                              self.vc.ctypes.data, token, pos, logits.ctypes.data)
         return logits
 
+_s("orc_llama32_int8_forward", [_P, _I] + [_P] * 22 + [_I], C.c_float)
+
+LLAMA32_ARRAYS = ("x_i8", "rms_att_w", "rms_ffn_w", "rms_final_w", "wq_t", "wk_t", "wv_t",
+                  "wo_t", "w1_t", "w2_t", "w3_t", "wcls", "x_fp32", "xb_fp32", "logits", "xb_i8",
+                  "k_cache", "v_cache", "att_scores", "att_probs", "attn_out", "ffn_hb")
+
+
+def llama32_int8_forward(arrays: dict, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                         vocab_size, max_seq_len, head_dim) -> float:
+    """orc_llama32_int8_forward over numpy arrays named as llama32_forward's
+    parameters (contiguous, the program's dtypes); writes them as the program
+    does and returns logits[0]."""
+    c = OrcLlamaCfg(dim=dim, hidden=hidden_dim, n_layers=n_layers, n_heads=n_heads,
+                    n_kv_heads=n_kv_heads, vocab=vocab_size, seq_len=max_seq_len, eps=1e-5,
+                    theta=0.0, w4=0, gs=32)
+    for name in LLAMA32_ARRAYS:
+        a = arrays[name]
+        if not (isinstance(a, np.ndarray) and a.flags["C_CONTIGUOUS"]):
+            raise ValueError(f"{name} must be a contiguous numpy array")
+    return _o.orc_llama32_int8_forward(C.byref(c), head_dim,
+                                       *[arrays[n].ctypes.data for n in LLAMA32_ARRAYS], pos)
+
+
 class LlamaQuantOracle:
     """orc_llama_quant_forward (llama2_quant.sl) over numpy arrays named as the
     program's parameters; keeps its own KV cache."""

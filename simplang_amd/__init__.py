@@ -38,6 +38,7 @@ from .host import (  # noqa: F401
     Llama,
     stories110M_forward,
     llama2_quant_forward,
+    llama32_forward,
     forward_cache_clear,
     W_F32,
     W_W4S,

@@ -86,6 +86,8 @@ lib.stories110M_forward.argtypes = [_P, _P, _I, _I, _I] * 25 + [_I] * 9
 lib.stories110M_forward.restype = C.c_float
 lib.llama2_quant_forward.argtypes = [_P, _P, _I, _I, _I] * 22 + [_I] * 17
 lib.llama2_quant_forward.restype = C.c_float
+lib.llama32_forward.argtypes = [_P, _P, _I, _I, _I] * 22 + [_I] * 9
+lib.llama32_forward.restype = C.c_float
 _sig("simp_rt_timing_query", [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_int64)])
 
 
@@ -256,6 +258,27 @@ def llama2_quant_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_
         msg = lib.simp_rt_last_error().decode()
         if msg:
             raise SimpRTError("llama2_quant_forward", -1, msg)
+    return r
+
+
+LLAMA32_ARRAYS = ("x_i8", "rms_att_w", "rms_ffn_w", "rms_final_w", "wq_t", "wk_t", "wv_t",
+                  "wo_t", "w1_t", "w2_t", "w3_t", "wcls", "x_fp32", "xb_fp32", "logits", "xb_i8",
+                  "k_cache", "v_cache", "att_scores", "att_probs", "attn_out", "ffn_hb")
+
+
+def llama32_forward(arrays: dict, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                    vocab_size, max_seq_len, head_dim) -> float:
+    """``llama32_forward`` of examples/llama2/llama32_1b_int8_tensor.sl, called as
+    bench_llama32_1b_int8.cpp calls it: ``arrays`` maps the program's parameter
+    names (LLAMA32_ARRAYS) to 1-D arrays (i8 / f32 / i32).  Returns logits[0]
+    (NaN on error, with the message in simp_rt_last_error)."""
+    args = []
+    for name in LLAMA32_ARRAYS:
+        args += desc1(arrays[name])
+    r = lib.llama32_forward(*args, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                            vocab_size, max_seq_len, head_dim)
+    if r != r:
+        raise SimpRTError("llama32_forward", -1, lib.simp_rt_last_error().decode())
     return r
 
 

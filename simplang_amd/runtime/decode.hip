@@ -1184,6 +1184,8 @@ struct ForwardEntry {
 std::mutex g_fwd_mu;
 std::map<std::vector<int64_t>, ForwardEntry> g_fwd;
 
+}  // namespace
+
 int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *name,
                   std::vector<const void *> &registered) {
   if (device_view(p, bytes, dev, name) == SIMP_RT_OK) return SIMP_RT_OK;
@@ -1193,7 +1195,6 @@ int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *nam
   return device_view(p, bytes, dev, name);
 }
 
-}  // namespace
 }  // namespace simp
 
 extern "C" {
@@ -1561,6 +1562,7 @@ int32_t simp_rt_forward_cache_clear(void) {
     quant_free(kv.second);
   }
   g_qfwd.clear();
+  l32_cache_clear();
   return SIMP_RT_OK;
 }
 

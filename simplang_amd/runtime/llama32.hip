@@ -1,0 +1,523 @@
+// llama32.hip -- llama32_forward: the int8 LLaMA-3.2 program
+// (examples/llama2/llama32_1b_int8_tensor.sl:16-305, bound by
+// examples/llama2/bench_llama32_1b_int8.cpp:36-61,201-230) as a model-level
+// export with the compiled program's signature.
+//
+// The program's arithmetic, with SimpLang's typing (float literals f32,
+// integer literals i64): x = (float)x_i8; per layer an RMSNorm, xb*127 clamped
+// and truncated to i8, Q/K/V = tensor_matmul_nt (i8 x i8 -> i32), K/V cached as
+// (i8)(v / 256), per head fp32 scores / 8, softmax, attn_out = (i32) sum p*v,
+// Wo on (i8)clamp(attn_out / 256), x += Wo / 65536, FFN RMSNorm, Gate/Up on the
+// re-quantized xb, ffn_hb = (i8)(silu(g/65536) * (u/65536) * 127), x += Down /
+// 65536, final RMSNorm and an fp32 classifier.  The RoPE loop of the program
+// discards its results (:123-140) and is not run.
+//
+// Kernels per layer: norm+quantize, one int8 GEMV over Wq|Wk|Wv with the K/V
+// cache store fused, attention (one block per head), Wo GEMV adding into x,
+// norm+quantize, one paired W1|W3 GEMV writing ffn_hb, W2 GEMV adding into x.
+// The int8 GEMVs are HBM-bound: each wave reads whole rows of W_t as 1 KB
+// coalesced lines, x sits in registers, v_dot4_i32_i8 accumulates exactly, so
+// every integer the program computes is reproduced bit for bit.
+//
+// State: the KV cache lives on the device (authoritative across calls); each
+// call writes the new row of every layer back to the caller's k_cache/v_cache,
+// and writes logits, x_fp32 and xb_fp32.  att_scores, att_probs, attn_out,
+// xb_i8 and ffn_hb are the program's per-layer scratch and are not written.
+#include <algorithm>
+#include <cmath>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "rt_device.h"
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+enum L32Out { kL32QKV = 0, kL32Resid = 1, kL32Pair = 2 };
+
+// (i8) of an fp32 value as the reference's x86 build lowers fptosi to i8:
+// truncate to i32 (0x80000000 for NaN or out of range), keep the low byte.
+__device__ __forceinline__ int8_t l32_fptosi_i8(float v) {
+  if (!(v > -2147483648.0f && v < 2147483648.0f)) return 0;
+  return (int8_t)(uint8_t)(uint32_t)(int32_t)v;
+}
+
+// val = v * 127; clamp to [-128, 127]; (i8)val (:96-102, :235-242)
+__device__ __forceinline__ int8_t l32_quant127(float v) {
+  float val = v * 127.0f;
+  val = val > 127.0f ? 127.0f : val;
+  val = val < -128.0f ? -128.0f : val;
+  return (int8_t)(int32_t)val;
+}
+
+__device__ __forceinline__ int32_t dot16(uint4 a, uint4 b, int32_t acc) {
+  acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
+  return acc;
+}
+
+__device__ __forceinline__ int32_t wave_isum(int32_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// x = (float)x_i8 (:79-83)
+__global__ void __launch_bounds__(256)
+    l32_embed_k(const int8_t *__restrict__ xi, float *__restrict__ x, int dim) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < dim) x[i] = (float)xi[i];
+}
+
+// RMSNorm (the rmsnorm builtin: (x / sqrt(sum x^2 / n + eps)) * w) of x into xb,
+// and, when xq is given, its i8 quantization.  One 1024-thread block.
+__global__ void __launch_bounds__(1024)
+    l32_norm_k(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ xb,
+               int8_t *__restrict__ xq, int dim, float eps) {
+  __shared__ float scratch[16];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < dim; i += 1024) ss = fmaf(x[i], x[i], ss);
+  ss = block_sum(ss, scratch);
+  const float rms = sqrtf(ss / (float)dim + eps);
+  for (int i = threadIdx.x; i < dim; i += 1024) {
+    const float v = (x[i] / rms) * w[i];
+    if (xb) xb[i] = v;
+    if (xq) xq[i] = l32_quant127(v);
+  }
+}
+
+// Rows of up to three int8 matrices W_t[rows, K] against x[K] (i8, K % 16 == 0),
+// R rows per wave, C 16-byte chunks per lane (K <= 1024 * C).
+//   kL32QKV   rows of s0 -> q[r] (i32); of s1 -> krow[r] = (i8)(acc / 256);
+//             of s2 -> vrow[r] = (i8)(acc / 256)           (:104-121, :142-151)
+//   kL32Resid rows of s0 -> x[r] += (float)acc / 65536     (:225-229, :275-279)
+//   kL32Pair  row r of s0 (W1) and of s1 (W3): hb[r] = (i8)(silu(g / 65536) *
+//             (u / 65536) * 127)                            (:245-267)
+struct L32Segs {
+  const int8_t *w[3];
+  int rows[3];
+};
+
+template <int C, int R, int MODE>
+__global__ void __launch_bounds__(256)
+    l32_gemv_k(L32Segs sg, const int8_t *__restrict__ xq, int K, int32_t *__restrict__ q,
+               int8_t *__restrict__ krow, int8_t *__restrict__ vrow, float *__restrict__ x,
+               int8_t *__restrict__ hb) {
+  constexpr int NM = MODE == kL32Pair ? 2 : 1;  // matrices read per row
+  const int lane = threadIdx.x & 63;
+  const int total = MODE == kL32QKV ? sg.rows[0] + sg.rows[1] + sg.rows[2] : sg.rows[0];
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= total) return;  // uniform per wave
+  const int nch = K >> 4;
+  uint4 xv[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    const int c = lane + 64 * j;
+    xv[j] = c < nch ? *(const uint4 *)(xq + 16 * c) : make_uint4(0, 0, 0, 0);
+  }
+  uint4 wv[NM][R][C];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int row = min(row0 + r, total - 1);
+    const int8_t *base[NM];
+    if constexpr (MODE == kL32QKV) {
+      const int s = row < sg.rows[0] ? 0 : (row < sg.rows[0] + sg.rows[1] ? 1 : 2);
+      const int rr = s == 0 ? row : (s == 1 ? row - sg.rows[0] : row - sg.rows[0] - sg.rows[1]);
+      base[0] = sg.w[s] + (int64_t)rr * K;
+    } else {
+#pragma unroll
+      for (int mtx = 0; mtx < NM; mtx++) base[mtx] = sg.w[mtx] + (int64_t)row * K;
+    }
+#pragma unroll
+    for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+      for (int j = 0; j < C; j++) {
+        const int c = lane + 64 * j;
+        wv[mtx][r][j] = c < nch ? *(const uint4 *)(base[mtx] + 16 * c) : make_uint4(0, 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    int32_t acc[NM];
+#pragma unroll
+    for (int mtx = 0; mtx < NM; mtx++) {
+      int32_t a = 0;
+#pragma unroll
+      for (int j = 0; j < C; j++) a = dot16(wv[mtx][r][j], xv[j], a);
+      acc[mtx] = wave_isum(a);
+    }
+    const int row = row0 + r;
+    if (lane != 0 || row >= total) continue;
+    if constexpr (MODE == kL32QKV) {
+      if (row < sg.rows[0]) q[row] = acc[0];
+      else if (row < sg.rows[0] + sg.rows[1]) krow[row - sg.rows[0]] = (int8_t)(uint8_t)(uint32_t)(acc[0] / 256);
+      else vrow[row - sg.rows[0] - sg.rows[1]] = (int8_t)(uint8_t)(uint32_t)(acc[0] / 256);
+    } else if constexpr (MODE == kL32Resid) {
+      x[row] = x[row] + (float)acc[0] / 65536.0f;
+    } else {
+      const float gate_f = (float)acc[0] / 65536.0f;
+      const float silu = gate_f / (1.0f + expf(0.0f - gate_f));
+      const float up_f = (float)acc[1] / 65536.0f;
+      hb[row] = l32_fptosi_i8(silu * up_f * 127.0f);
+    }
+  }
+}
+
+// Attention of one layer, one block per head (:161-216).  Scores: one thread
+// per position, the program's order and operations within a position (fp32
+// product then sum, no fused multiply-add), / 8; four positions per thread
+// are loaded before any is summed.  Softmax over pos + 1 scores.  V sum: a
+// thread takes 16 consecutive d of every P-th position (four rows in flight),
+// partitions added in order.  attn_out = (i32) sum; xq = its i8 quantization
+// (float)attn_out / 256, clamped.  Head size and kv_dim multiples of 16.
+// LDS: head_size + pos + 1 floats (dynamic, at most 47 KB) + 16 KB.
+__global__ void __launch_bounds__(256)
+    l32_attn_k(const int32_t *__restrict__ Q, const int8_t *__restrict__ kc,
+               const int8_t *__restrict__ vc, int32_t *__restrict__ attn_out,
+               int8_t *__restrict__ xq, int pos, int kv, int hs, int n_rep) {
+  extern __shared__ float sm[];
+  __shared__ float red[4096];
+  __shared__ float scratch[16];
+  constexpr int U = 4;
+  const int h = blockIdx.x, kho = (h / n_rep) * hs, n = pos + 1;
+  const int hc = hs >> 4;  // 16-byte chunks per row
+  float *qf = sm, *att = sm + hs;
+  for (int d = threadIdx.x; d < hs; d += 256) qf[d] = (float)Q[h * hs + d];
+  __syncthreads();
+  for (int t0 = threadIdx.x; t0 < n; t0 += 256 * U) {
+    float score[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) score[u] = 0.f;
+    for (int c = 0; c < hc; c++) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int t = min(t0 + 256 * u, n - 1);
+        v[u] = *(const uint4 *)(kc + (int64_t)t * kv + kho + 16 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const float kf = (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)));
+          score[u] = __fadd_rn(score[u], __fmul_rn(qf[16 * c + e], kf));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (t0 + 256 * u < n) att[t0 + 256 * u] = score[u] / 8.0f;
+  }
+  __syncthreads();
+  float m = -INFINITY;
+  for (int t = threadIdx.x; t < n; t += 256) m = fmaxf(m, att[t]);
+  m = block_max(m, scratch);
+  float l = 0.f;
+  for (int t = threadIdx.x; t < n; t += 256) {
+    const float e = expf(att[t] - m);
+    att[t] = e;
+    l += e;
+  }
+  l = block_sum(l, scratch);
+  for (int t = threadIdx.x; t < n; t += 256) att[t] = att[t] / l;
+  __syncthreads();
+  const int P = 256 / hc;  // position partitions (hs <= 256: P >= 16)
+  const int c = threadIdx.x % hc, p = threadIdx.x / hc;
+  if (p < P) {
+    float acc[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[e] = 0.f;
+    for (int t0 = p; t0 < n; t0 += P * U) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int t = min(t0 + P * u, n - 1);
+        v[u] = *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        if (t0 + P * u >= n) break;
+        const float a = att[t0 + P * u];
+        const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+          acc[e] = __fadd_rn(acc[e], __fmul_rn(a, (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)))));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) red[p * hs + 16 * c + e] = acc[e];
+  }
+  __syncthreads();
+  for (int dd = threadIdx.x; dd < hs; dd += 256) {
+    float v = red[dd];
+    for (int pp = 1; pp < P; pp++) v = __fadd_rn(v, red[pp * hs + dd]);
+    const int32_t a = (int32_t)v;
+    attn_out[h * hs + dd] = a;
+    float s = (float)a * 1.0f / 256.0f;
+    s = s > 127.0f ? 127.0f : s;
+    s = s < -128.0f ? -128.0f : s;
+    xq[h * hs + dd] = (int8_t)(int32_t)s;
+  }
+}
+
+struct L32Model {
+  int64_t dim, hid, L, nh, nkv, V, S, hs, kv;
+  const float *rms_att, *rms_ffn, *rms_final, *wcls;
+  const int8_t *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+  float *x = nullptr, *xb = nullptr, *logits = nullptr;
+  int8_t *xi = nullptr, *xq = nullptr, *hq = nullptr, *kc = nullptr, *vc = nullptr;
+  int32_t *q = nullptr, *attn = nullptr;
+  std::vector<const void *> registered;
+};
+
+void l32_free(L32Model &m) {
+  for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.logits, (void *)m.xi, (void *)m.xq,
+                  (void *)m.hq, (void *)m.kc, (void *)m.vc, (void *)m.q, (void *)m.attn})
+    if (p) (void)hipFree(p);
+  for (const void *p : m.registered) (void)simp_rt_unregister(p);
+}
+
+int l32_alloc(L32Model &m) {
+  const size_t cache = (size_t)(m.L * m.S * m.kv);
+  struct B { void **p; size_t bytes; };
+  const B bufs[] = {{(void **)&m.x, 4 * (size_t)m.dim},    {(void **)&m.xb, 4 * (size_t)m.dim},
+                    {(void **)&m.logits, 4 * (size_t)m.V}, {(void **)&m.xi, (size_t)m.dim},
+                    {(void **)&m.xq, (size_t)m.dim},       {(void **)&m.hq, (size_t)m.hid},
+                    {(void **)&m.kc, cache},               {(void **)&m.vc, cache},
+                    {(void **)&m.q, 4 * (size_t)m.dim},    {(void **)&m.attn, 4 * (size_t)m.dim}};
+  for (const B &b : bufs) {
+    if (hipMalloc(b.p, std::max<size_t>(b.bytes, 16)) != hipSuccess)
+      return set_error(SIMP_RT_ENOMEM, "llama32_forward: device buffers");
+    SIMP_HIP(hipMemset(*b.p, 0, b.bytes));
+  }
+  return SIMP_RT_OK;
+}
+
+// One int8 GEMV launch: C chunks per lane from K, R rows per wave.
+template <int MODE>
+int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, int8_t *krow,
+             int8_t *vrow, float *x, int8_t *hb, hipStream_t st) {
+  const int C = (int)cdiv(K / 16, 64);
+  const int R = MODE == kL32Pair ? 1 : 2;
+  const unsigned grid = (unsigned)cdiv(total, 4 * R);
+#define L32G(CC)                                                                              \
+  case CC:                                                                                    \
+    hipLaunchKernelGGL((l32_gemv_k<CC, (MODE == kL32Pair ? 1 : 2), MODE>), dim3(grid),        \
+                       dim3(256), 0, st, sg, xq, K, q, krow, vrow, x, hb);                    \
+    break;
+  switch (C) {
+    L32G(1) L32G(2) L32G(4) L32G(8) L32G(16)
+    default:
+      return set_error(SIMP_RT_EUNSUPPORTED, "llama32_forward: K=%d per matrix row", K);
+  }
+#undef L32G
+  (void)R;
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
+  const int dim = (int)m.dim, hid = (int)m.hid, kv = (int)m.kv;
+  const float eps = 1e-5f;  // the program's 0.00001 (:93, :232, :287)
+  hipLaunchKernelGGL(l32_embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st,
+                     (const int8_t *)m.xi, m.x, dim);
+  int rc;
+  const size_t attn_lds = sizeof(float) * (size_t)(m.hs + pos + 1);
+  for (int64_t l = 0; l < m.L; l++) {
+    int8_t *kc = m.kc + l * m.S * kv, *vc = m.vc + l * m.S * kv;
+    hipLaunchKernelGGL(l32_norm_k, dim3(1), dim3(1024), 0, st, (const float *)m.x,
+                       m.rms_att + l * dim, (float *)nullptr, m.xq, dim, eps);
+    L32Segs s{};
+    s.w[0] = m.wq + l * m.dim * m.dim;
+    s.w[1] = m.wk + l * m.kv * m.dim;
+    s.w[2] = m.wv + l * m.kv * m.dim;
+    s.rows[0] = dim;
+    s.rows[1] = kv;
+    s.rows[2] = kv;
+    if ((rc = l32_gemv<kL32QKV>(s, dim + 2 * kv, dim, m.xq, m.q, kc + pos * kv, vc + pos * kv,
+                                nullptr, nullptr, st)))
+      return rc;
+    hipLaunchKernelGGL(l32_attn_k, dim3((unsigned)m.nh), dim3(256), attn_lds, st,
+                       (const int32_t *)m.q, (const int8_t *)kc, (const int8_t *)vc, m.attn, m.xq,
+                       (int)pos, kv, (int)m.hs, (int)(m.nh / m.nkv));
+    s = L32Segs{};
+    s.w[0] = m.wo + l * m.dim * m.dim;
+    s.rows[0] = dim;
+    if ((rc = l32_gemv<kL32Resid>(s, dim, dim, m.xq, nullptr, nullptr, nullptr, m.x, nullptr, st)))
+      return rc;
+    hipLaunchKernelGGL(l32_norm_k, dim3(1), dim3(1024), 0, st, (const float *)m.x,
+                       m.rms_ffn + l * dim, (float *)nullptr, m.xq, dim, eps);
+    s = L32Segs{};
+    s.w[0] = m.w1 + l * m.hid * m.dim;
+    s.w[1] = m.w3 + l * m.hid * m.dim;
+    s.rows[0] = hid;
+    if ((rc = l32_gemv<kL32Pair>(s, hid, dim, m.xq, nullptr, nullptr, nullptr, nullptr, m.hq, st)))
+      return rc;
+    s = L32Segs{};
+    s.w[0] = m.w2 + l * m.dim * m.hid;
+    s.rows[0] = dim;
+    if ((rc = l32_gemv<kL32Resid>(s, dim, hid, m.hq, nullptr, nullptr, nullptr, m.x, nullptr, st)))
+      return rc;
+  }
+  hipLaunchKernelGGL(l32_norm_k, dim3(1), dim3(1024), 0, st, (const float *)m.x, m.rms_final,
+                     m.xb, (int8_t *)nullptr, dim, eps);
+  SIMP_HIP(hipGetLastError());
+  return launch_matmul_f32(m.wcls, dim, m.xb, 1, m.logits, 1, (int)m.V, 1, dim, 0.f, st);
+}
+
+std::mutex g_l32_mu;
+std::map<std::vector<int64_t>, L32Model> g_l32;
+
+}  // namespace
+
+void l32_cache_clear() {
+  std::lock_guard<std::mutex> lk(g_l32_mu);
+  if (!g_l32.empty()) (void)hipDeviceSynchronize();
+  for (auto &kv : g_l32) l32_free(kv.second);
+  g_l32.clear();
+}
+
+}  // namespace simp
+
+using namespace simp;
+
+extern "C" {
+
+#define SIMP_DESC_F32(n) float *n##_alloc, float *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+#define SIMP_DESC_I8(n) int8_t *n##_alloc, int8_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+#define SIMP_DESC_I32(n) int32_t *n##_alloc, int32_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
+
+float llama32_forward(
+    SIMP_DESC_I8(x_i8), SIMP_DESC_F32(rms_att_w), SIMP_DESC_F32(rms_ffn_w),
+    SIMP_DESC_F32(rms_final_w), SIMP_DESC_I8(wq_t), SIMP_DESC_I8(wk_t), SIMP_DESC_I8(wv_t),
+    SIMP_DESC_I8(wo_t), SIMP_DESC_I8(w1_t), SIMP_DESC_I8(w2_t), SIMP_DESC_I8(w3_t),
+    SIMP_DESC_F32(wcls), SIMP_DESC_F32(x_fp32), SIMP_DESC_F32(xb_fp32), SIMP_DESC_F32(logits),
+    SIMP_DESC_I8(xb_i8), SIMP_DESC_I8(k_cache), SIMP_DESC_I8(v_cache), SIMP_DESC_F32(att_scores),
+    SIMP_DESC_F32(att_probs), SIMP_DESC_I32(attn_out), SIMP_DESC_I8(ffn_hb), int64_t pos,
+    int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
+    int64_t vocab_size, int64_t max_seq_len, int64_t head_dim) {
+  const float nan = std::numeric_limits<float>::quiet_NaN();
+  (void)xb_i8; (void)att_scores; (void)att_probs; (void)attn_out; (void)ffn_hb;
+  (void)xb_i8_alloc; (void)att_scores_alloc; (void)att_probs_alloc; (void)attn_out_alloc;
+  (void)ffn_hb_alloc;
+  auto fail = [&](const char *msg) {
+    set_error(SIMP_RT_EINVAL, "llama32_forward: %s", msg);
+    return nan;
+  };
+  if (dim <= 0 || hidden_dim <= 0 || n_layers <= 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+      vocab_size <= 0 || max_seq_len <= 0 || head_dim <= 0 || n_heads % n_kv_heads ||
+      n_heads * head_dim != dim)
+    return fail("bad model dimensions (n_heads * head_dim must equal dim)");
+  if (dim % 16 || hidden_dim % 16 || head_dim % 16 || head_dim > 256 || dim > 16384 ||
+      hidden_dim > 16384 ||
+      4 * (head_dim + max_seq_len) > 47 * 1024)
+    return fail("dim, hidden_dim and head_dim must be multiples of 16 (dim, hidden_dim <= "
+                "16384, head_dim <= 256), head_dim + max_seq_len <= 12032");
+  if (pos < 0 || pos >= max_seq_len) return fail("pos out of range");
+  const int64_t L = n_layers, D = dim, H = hidden_dim, kv = n_kv_heads * head_dim;
+  struct In { const void *p; int64_t off, size, stride, need; size_t esz; const char *name; };
+  const In ins[] = {
+      {rms_att_w, rms_att_w_off, rms_att_w_size, rms_att_w_stride, L * D, 4, "rms_att_w"},
+      {rms_ffn_w, rms_ffn_w_off, rms_ffn_w_size, rms_ffn_w_stride, L * D, 4, "rms_ffn_w"},
+      {rms_final_w, rms_final_w_off, rms_final_w_size, rms_final_w_stride, D, 4, "rms_final_w"},
+      {wcls, wcls_off, wcls_size, wcls_stride, vocab_size * D, 4, "wcls"},
+      {wq_t, wq_t_off, wq_t_size, wq_t_stride, L * D * D, 1, "wq_t"},
+      {wk_t, wk_t_off, wk_t_size, wk_t_stride, L * kv * D, 1, "wk_t"},
+      {wv_t, wv_t_off, wv_t_size, wv_t_stride, L * kv * D, 1, "wv_t"},
+      {wo_t, wo_t_off, wo_t_size, wo_t_stride, L * D * D, 1, "wo_t"},
+      {w1_t, w1_t_off, w1_t_size, w1_t_stride, L * H * D, 1, "w1_t"},
+      {w2_t, w2_t_off, w2_t_size, w2_t_stride, L * D * H, 1, "w2_t"},
+      {w3_t, w3_t_off, w3_t_size, w3_t_stride, L * H * D, 1, "w3_t"},
+      {x_i8, x_i8_off, x_i8_size, x_i8_stride, D, 1, "x_i8"},
+      {x_fp32, x_fp32_off, x_fp32_size, x_fp32_stride, D, 4, "x_fp32"},
+      {xb_fp32, xb_fp32_off, xb_fp32_size, xb_fp32_stride, D, 4, "xb_fp32"},
+      {logits, logits_off, logits_size, logits_stride, vocab_size, 4, "logits"},
+      {k_cache, k_cache_off, k_cache_size, k_cache_stride, L * max_seq_len * kv, 1, "k_cache"},
+      {v_cache, v_cache_off, v_cache_size, v_cache_stride, L * max_seq_len * kv, 1, "v_cache"}};
+  for (const In &a : ins) {
+    if (check_desc1(a.name, a.p, a.off, a.size, a.stride)) return nan;
+    if (a.size < a.need) {
+      set_error(SIMP_RT_EINVAL, "llama32_forward: %s has %lld elements, needs %lld", a.name,
+                (long long)a.size, (long long)a.need);
+      return nan;
+    }
+  }
+  constexpr int NW = 11;  // weight arrays: ins[0..10]
+  const void *wp[NW];
+  for (int i = 0; i < NW; i++) wp[i] = (const char *)ins[i].p + ins[i].esz * (size_t)ins[i].off;
+  std::vector<int64_t> key = {dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size,
+                              max_seq_len, head_dim};
+  for (int i = 0; i < NW; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
+  hipStream_t st = cur_stream();
+  L32Model *m = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_l32_mu);
+    auto it = g_l32.find(key);
+    if (it == g_l32.end()) {
+      L32Model nm;
+      nm.dim = D; nm.hid = H; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
+      nm.V = vocab_size; nm.S = max_seq_len; nm.hs = head_dim; nm.kv = kv;
+      const void *d[NW];
+      for (int i = 0; i < NW; i++)
+        if (dev_or_mirror(wp[i], ins[i].esz * (size_t)ins[i].need, &d[i], ins[i].name,
+                          nm.registered)) {
+          l32_free(nm);
+          return nan;
+        }
+      nm.rms_att = (const float *)d[0]; nm.rms_ffn = (const float *)d[1];
+      nm.rms_final = (const float *)d[2]; nm.wcls = (const float *)d[3];
+      nm.wq = (const int8_t *)d[4]; nm.wk = (const int8_t *)d[5]; nm.wv = (const int8_t *)d[6];
+      nm.wo = (const int8_t *)d[7]; nm.w1 = (const int8_t *)d[8]; nm.w2 = (const int8_t *)d[9];
+      nm.w3 = (const int8_t *)d[10];
+      for (int i = 4; i < NW; i++)
+        if ((uintptr_t)d[i] & 15) {
+          l32_free(nm);
+          return fail("int8 weight arrays must start 16-byte aligned (offset included)");
+        }
+      if (l32_alloc(nm)) {
+        l32_free(nm);
+        return nan;
+      }
+      it = g_l32.emplace(key, std::move(nm)).first;
+    }
+    m = &it->second;
+  }
+  hipError_t e = hipMemcpyAsync(m->xi, x_i8 + x_i8_off, (size_t)D, hipMemcpyDefault, st);
+  if (e != hipSuccess) {
+    hip_fail(e, "llama32_forward: input copy");
+    return nan;
+  }
+  if (l32_step(*m, pos, st)) return nan;
+  const size_t pitch = (size_t)(max_seq_len * kv), row = (size_t)kv, at = (size_t)(pos * kv);
+  e = hipMemcpyAsync(logits + logits_off, m->logits, 4 * (size_t)vocab_size, hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(x_fp32 + x_fp32_off, m->x, 4 * (size_t)D, hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(xb_fp32 + xb_fp32_off, m->xb, 4 * (size_t)D, hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(k_cache + k_cache_off + at, pitch, m->kc + at, pitch, row, (size_t)L,
+                         hipMemcpyDefault, st);
+  if (e == hipSuccess)
+    e = hipMemcpy2DAsync(v_cache + v_cache_off + at, pitch, m->vc + at, pitch, row, (size_t)L,
+                         hipMemcpyDefault, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    hip_fail(e, "llama32_forward: result copies");
+    return nan;
+  }
+  float l0 = nan;
+  if (hipMemcpy(&l0, logits + logits_off, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
+  return l0;
+}
+
+#undef SIMP_DESC_F32
+#undef SIMP_DESC_I8
+#undef SIMP_DESC_I32
+
+}  // extern "C"

@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "simp_rt.h"
 
@@ -57,6 +58,15 @@ class Operand {
 // Device address of a caller range that must already be device-resident
 // (device memory, or inside a simp_rt_register'd range); no staging.
 int device_view(const void *p, size_t bytes, const void **dev, const char *name);
+
+// Device address of a model-level export's weight array: device memory is used
+// in place; host memory is registered once as an immutable mirror (appended
+// to `registered`, for simp_rt_unregister when the export's engine is freed).
+int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *name,
+                  std::vector<const void *> &registered);
+
+// Frees the engines of llama32_forward (part of simp_rt_forward_cache_clear).
+void l32_cache_clear();
 
 // Finishes an entry point: commits staged outputs and, when anything was
 // staged, waits for the stream so host buffers are valid on return.

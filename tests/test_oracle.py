@@ -433,3 +433,79 @@ def test_matmul_nhwc_kats(orc):
     y = orc.matmul_nhwc(x, w)
     assert y[0, 0, 0, 0] + y[0, 0, 0, 1] + y[0, 0, 0, 2] == 12.0  # :239-268
     assert y[1, 2, 2, 2] == 3 * 2 * 18
+
+
+# ---------------------------------------------------------- llama32 (int8) --
+
+def _l32_dims(cfg):
+    from _llama32 import DIMS
+    return [cfg[k] for k in DIMS]
+
+
+def test_llama32_zero_weights_closed_form(orc):
+    """All-zero int8 layer weights: every projection is 0, the residual stream
+    stays x = (float)x_i8 and logits = wcls . rmsnorm(x) (numpy, float64)."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg = dict(CFG_SMALL, n_layers=2)
+    a = make_arrays(cfg, seed=9, wide=True)
+    for k in ("wq_t", "wk_t", "wv_t", "wo_t", "w1_t", "w2_t", "w3_t"):
+        a[k][:] = 0
+    r = orc.llama32_int8_forward(a, 3, *_l32_dims(cfg))
+    x = a["x_i8"].astype(np.float64)
+    assert np.array_equal(a["x_fp32"], a["x_i8"].astype(np.float32))
+    xb = x / np.sqrt((x * x).mean() + 1e-5) * a["rms_final_w"]
+    lg = a["wcls"].reshape(cfg["vocab_size"], cfg["dim"]).astype(np.float64) @ xb
+    np.testing.assert_allclose(a["logits"], lg, rtol=1e-4, atol=1e-4 * np.abs(lg).max())
+    assert r == a["logits"][0]
+    assert not a["k_cache"].any() and not a["ffn_hb"].any()
+
+
+def test_llama32_first_layer_cache_rows(orc):
+    """Layer 0's K/V rows at pos are (i8)((xb_i8 . W_t row) / 256) with xb_i8 the
+    quantized attention RMSNorm of x_i8: recomputed in float64 / int64, equal
+    except where xb*127 lies within 1e-4 of an integer (fp32 rounding)."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg = dict(CFG_SMALL, n_layers=1)
+    a = make_arrays(cfg, seed=10, wide=True)
+    pos = 5
+    orc.llama32_int8_forward(a, pos, *_l32_dims(cfg))
+    D, kv = cfg["dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    x = a["x_i8"].astype(np.float64)
+    v = x / np.sqrt((x * x).mean() + 1e-5) * a["rms_att_w"][:D] * 127.0
+    near = (np.abs(v - np.round(v)) < 1e-4) & (v != np.round(v))
+    assert not near.any()                                 # no quantization tie in this draw
+    xq = np.trunc(np.clip(v, -128, 127)).astype(np.int64)
+    for name, w in (("k_cache", "wk_t"), ("v_cache", "wv_t")):
+        acc = a[w].reshape(kv, D).astype(np.int64) @ xq
+        want = (np.trunc(acc / 256.0).astype(np.int64) & 0xFF).astype(np.uint8).view(np.int8)
+        got = a[name].reshape(cfg["max_seq_len"], kv)[pos]
+        assert np.array_equal(got, want), name
+
+
+def test_llama32_attention_is_inert(orc):
+    """attn_out = (i32) of a convex combination of int8 values, so |attn_out| <=
+    128 and (float)attn_out / 256 truncates to 0: Wo sees a zero vector and
+    cannot change the logits (a property of the program's fixed-point scales)."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg = CFG_SMALL
+    a = make_arrays(cfg, seed=11, wide=True)
+    b = {k: v.copy() for k, v in a.items()}
+    b["wo_t"][:] = np.random.default_rng(12).integers(-128, 128, b["wo_t"].size, dtype=np.int8)
+    for pos in range(3):
+        orc.llama32_int8_forward(a, pos, *_l32_dims(cfg))
+        orc.llama32_int8_forward(b, pos, *_l32_dims(cfg))
+    assert np.abs(a["attn_out"]).max() <= 128
+    assert np.array_equal(a["logits"], b["logits"])
+
+
+def test_llama32_fptosi_wraps_like_x86(orc):
+    """ffn_hb = (i8)(silu(g)*u*127) keeps the low byte of the i32 truncation
+    (the program does not clamp there): out-of-range values wrap."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg = dict(CFG_SMALL, n_layers=1)
+    a = make_arrays(cfg, seed=13, wide=True)
+    a["rms_ffn_w"][:] = 4.0                                # large activations into W1/W3
+    orc.llama32_int8_forward(a, 0, *_l32_dims(cfg))
+    hb = a["ffn_hb"].astype(np.int64)
+    assert np.unique(hb).size > 100                       # wrapped values cover the byte range
+    assert np.isin(hb, (-128, 127)).mean() < 0.05         # a clamp would pile them up at the ends
