@@ -22,22 +22,13 @@
 // prologue (LDS), so no per-weight sign handling is needed.  Per-chunk partial
 // dot products are scaled by the group's scale (and zero) and summed in fp32;
 // the 16 lane partials are combined with a butterfly over the lane group.
-#include <type_traits>
-
+// Several x vectors (2 <= M <= 16, groups of 32) run on f16 MFMA instead
+// (w4s_h16): nibbles as exact f16 subnormals, x split exactly into f16 hi+lo.
 #include "rt_device.h"
 #include "rt_internal.h"
 
 namespace simp {
 namespace {
-
-// Calls f(std::integral_constant<int, I>()) for I = B .. E-1 (fully unrolled).
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>());
-    static_for<B + 1, E>(f);
-  }
-}
 
 constexpr int kRowsPerBlock = 16;  // 16 lanes per row, 256 threads
 constexpr int kLanesPerRow = 16;
@@ -278,130 +269,192 @@ __global__ void __launch_bounds__(256)
     O[blockIdx.x * RB + r] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
 }
 
-// Symmetric W4, group size 32, 2 <= M <= 16 x vectors, on fp32 MFMA
-// (v_mfma_f32_16x16x4_f32): C[m][n] = sum_g s[n][g] * sum_{k in g} x[m][k] q[n][k].
-//   * Block = 4 waves, one tile of 16 weight rows each (64 rows), and one part
-//     of at most kW4mMaxG groups of K (gridDim.y parts).  With more than one
-//     part each block writes its partial tile to P[part][M][N] and
-//     w4s_sum_parts adds the parts in order.
-//   * Every load of the block is issued up front: x of the part (staged in LDS
-//     as [k/4][m] float4, so a read of 16 rows x 16 B per lane group covers 256
-//     contiguous bytes), then each lane's weight chunks (lane (n = l%16, kq =
-//     l/16) takes groups 4s + kq of row n) and their scales.  Loads retire in
-//     issue order, so step s computes as soon as its own chunks are in.
-//   * Per step of 4 groups the wave moves its 16 rows x 64 B of chunks through
-//     a small LDS tile (row n's chunk kq in slot kq ^ (n/4), so the dword reads
-//     of one group hit 64 banks): lane (n, kq) then holds dword kq of every
-//     group, i.e. k = 8 kq + j of MFMA j, matching x[m][32g + 8kq + j].
-//   * Per group: eight MFMAs of K = 4 accumulate D = x q (exact nibble values,
-//     fp32 x and accumulation), then acc += s * D.
-constexpr int kW4mRows = 64;  // weight rows per block
-constexpr int kW4mMaxG = 12;  // K groups per block part at most (x of a part: 24 KB of LDS)
+// ------------------------------------------- 2 <= M <= 16: f16 MFMA path
+// Symmetric W4, groups of 32, on v_mfma_f32_16x16x32_f16 (D[16 x 16] +=
+// A[16 x 32] B[32 x 16]): B = 16 weight rows x one group, A = x rows.
+//   * Exact operands.  A nibble u = q + 8 enters as the f16 subnormal with bit
+//     pattern u (value u * 2^-24, exact; the MFMA keeps f16 subnormals), built
+//     by byte permutes of the nibble halves with zero high bytes.  x row m
+//     enters as two A rows, hi = f16(x * 2^-e_m) and lo = f16(x * 2^-e_m - hi),
+//     22 significant bits; e_m keeps the wave's largest |x| of row m below
+//     2^14, so f16 cannot overflow.  Products are exact in fp32, so the result
+//     differs from the fp32 VALU path only by accumulation order and the
+//     22-bit x.  Per group: acc += s * (2^(24 + e_m) * (D_hi + D_lo) - 8 * sum x).
+//   * Layout.  Lane (n = l%16, q = l/16) loads the 16 bytes of group g0 + q of
+//     weight row n (four lanes read 64 contiguous bytes of each of 16 rows);
+//     a 4 x 4 dword transpose across the lane groups (v_permlane32_swap then
+//     v_permlane16_swap) gives lane (n, q) dword q of each of the four groups,
+//     i.e. k = 8q..8q+7 of MFMA j, as the B layout wants.
+//   * Block = 4 waves on the same 16 rows, each a slice of GQ groups of K; x
+//     of the slice is staged per wave in LDS as f16 hi/lo (no block barrier
+//     before the MFMAs), the four slices are added through LDS at the end.
+//     Blocks of one row tile cover K in gridDim.y parts; with more than one
+//     part the partial tiles go through P[part][M][N] and w4s_sum_parts.
+//   * MT = 8-row tiles of x (1: M <= 8, 2: M <= 16), MS = steps of 4 groups
+//     per wave (GQ = 4 MS).
+typedef _Float16 w4h8 __attribute__((ext_vector_type(8)));
+typedef float w4f4 __attribute__((ext_vector_type(4)));
 
-// MS = steps of 4 groups per part (4 MS >= the part's groups); every step
-// runs, groups past the part multiply zero x.  Straight-line steps keep each
-// step's chunks in registers (two blocks per CU by LDS: up to 256 VGPRs).
-template <int MS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-    w4s_mfma(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
-             const float *__restrict__ X, int64_t ldx, float *__restrict__ O, int64_t ldo,
-             float *__restrict__ P, int M, int N, int K) {
-  typedef float v4f __attribute__((ext_vector_type(4)));
-  constexpr int XPT = MS * 4 * 8 * 16 / 256;  // x float4 per thread
-  __shared__ __align__(16) float4 xl[MS * 4 * 8][16];  // [k/4 within the part][m]
-  __shared__ __align__(16) uint32_t wt[4][2][16 * 16];   // [wave][buf][row*16 + slot*4 + dword]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ln = lane & 15, kq = lane >> 4;
-  const int ng = K >> 5;
-  const int part = blockIdx.y, nparts = gridDim.y;
-  const int g0 = part * ng / nparts, g1 = (part + 1) * ng / nparts;  // g1 - g0 <= 4 MS
-  const int nk4 = 8 * (g1 - g0);                                     // float4 of x per row
-  const int n = min((int)blockIdx.x * kW4mRows + 16 * wave + ln, N - 1);  // rows past N: never stored
-  // 1. x of the part: thread t -> (m = t % 16, k/4 = t / 16 + 16 i); rows m >= M stay zero
-  const int xm = tid & 15, xc = tid >> 4;
-  const float *xrow = X + (int64_t)min(xm, M - 1) * ldx + 32 * g0;
-  float4 xv[XPT];
+// Eight nibbles (element order, low nibble = even element) as eight f16
+// subnormals with the nibble as bit pattern.
+__device__ __forceinline__ w4h8 nib8_f16(uint32_t t) {
+  const uint32_t lo = t & 0x0F0F0F0Fu, hi = (t >> 4) & 0x0F0F0F0Fu;
+  uint32_t d[4];
+  d[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);
+  d[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);
+  d[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
+  d[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
+  w4h8 r;
+  __builtin_memcpy(&r, d, 16);
+  return r;
+}
+
+// Lane (n, q) holds w[0..3] = dwords of group q; afterwards w[j] = dword q of
+// group j (4 x 4 transpose across the lane groups q = lane / 16).
+__device__ __forceinline__ void xpose4x4(uint32_t (&w)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  w[0] = a[0];
+  w[2] = a[1];
+  w[1] = b[0];
+  w[3] = b[1];
+  const auto c = __builtin_amdgcn_permlane16_swap(w[0], w[1], false, false);
+  const auto e = __builtin_amdgcn_permlane16_swap(w[2], w[3], false, false);
+  w[0] = c[0];
+  w[1] = c[1];
+  w[2] = e[0];
+  w[3] = e[1];
+}
+
+template <int MT, int RT>
+__global__ void __launch_bounds__(256)
+    w4s_h16(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
+            const float *__restrict__ X, int64_t ldx, float *__restrict__ O, int64_t ldo,
+            float *__restrict__ P, int M, int N, int K, int chunks) {
+  constexpr int GQ = 8, MS = 2, XR = 8 * MT, KS = 32 * GQ;  // groups / k of a chunk, x rows
+  constexpr int XE = XR / 4;  // x float4 per thread: float4 i of thread t is row wave + 4 i
+  __shared__ __align__(16) _Float16 xh[XR][KS];
+  __shared__ __align__(16) _Float16 xl[XR][KS];
+  __shared__ float xs[XR][GQ];
+  __shared__ float fm[XR];
+  const int G = K >> 5;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, n16 = lane & 15, q = lane >> 4;
+  const int row0 = ((int)blockIdx.x * 4 + wave) * RT * 16;
+  const int ar = n16 >> 1;  // x row (within an 8-row tile) of this lane's A fragment
+  float acc[RT][MT][2];
 #pragma unroll
-  for (int i = 0; i < XPT; i++) {
-    const int c = xc + 16 * i;
-    xv[i] = (xm < M && c < nk4) ? *(const float4 *)(xrow + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  // 2. this lane's weight chunks and scales (clamped; groups past g1 are not used)
-  const uint8_t *wrow = W + (int64_t)n * ldw;
-  const float *srow = S + (int64_t)n * lds;
-  // (named registers, not arrays: an array here is moved to LDS by the
-  // compiler's alloca promotion, which serializes the loads)
-  static_assert(MS <= 6, "at most six steps per part");
-  uint4 wv0, wv1, wv2, wv3, wv4, wv5;
-  float sv0, sv1, sv2, sv3, sv4, sv5;
-  auto wv = [&](auto ST) -> uint4 & {
-    constexpr int i = decltype(ST)::value;
-    if constexpr (i == 0) return wv0; else if constexpr (i == 1) return wv1;
-    else if constexpr (i == 2) return wv2; else if constexpr (i == 3) return wv3;
-    else if constexpr (i == 4) return wv4; else return wv5;
-  };
-  auto sv = [&](auto ST) -> float & {
-    constexpr int i = decltype(ST)::value;
-    if constexpr (i == 0) return sv0; else if constexpr (i == 1) return sv1;
-    else if constexpr (i == 2) return sv2; else if constexpr (i == 3) return sv3;
-    else if constexpr (i == 4) return sv4; else return sv5;
-  };
-  static_for<0, MS>([&](auto ST) {
-    const int g = min(g0 + 4 * decltype(ST)::value + kq, ng - 1);
-    wv(ST) = *(const uint4 *)(wrow + 16 * g);
-    sv(ST) = srow[g];
-  });
-  __builtin_amdgcn_sched_barrier(0);  // all loads issued before the staging below waits
+  for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-  for (int i = 0; i < XPT; i++) xl[xc + 16 * i][xm] = xv[i];  // zero past the part
-  lds_barrier();
-  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-  const int swz = ln >> 2;
-  static_for<0, MS>([&](auto ST) {  // unrolled: each step's chunk stays in its register
-    constexpr int st = decltype(ST)::value;
-    *(uint4 *)&wt[wave][st & 1][ln * 16 + ((kq ^ swz) << 2)] = wv(ST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's tile is written
-    __builtin_amdgcn_wave_barrier();
-    // the step's four groups as four independent MFMA chains (a dependent
-    // 16x16x4 f32 MFMA waits ~40 cycles for its predecessor; four chains keep
-    // the pipe busy)
-    float xs[4][8];
-    uint32_t d[4];
+    for (int t = 0; t < MT; t++) acc[rt][t][0] = acc[rt][t][1] = 0.f;
+  for (int c = 0; c < chunks; c++) {
+    const int gbeg = ((int)blockIdx.y * chunks + c) * GQ, gend = min(G, gbeg + GQ);
+    if (gbeg >= G) break;  // uniform per block
+    // every load of the chunk first: weights and scales, then x
+    uint4 wv[RT][MS];
+    float sc[RT][MS][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int gl = 4 * st + j;  // group within the part
-      const float4 xa = xl[8 * gl + 2 * kq][ln], xb = xl[8 * gl + 2 * kq + 1][ln];
-      xs[j][0] = xa.x; xs[j][1] = xa.y; xs[j][2] = xa.z; xs[j][3] = xa.w;
-      xs[j][4] = xb.x; xs[j][5] = xb.y; xs[j][6] = xb.z; xs[j][7] = xb.w;
-      d[j] = wt[wave][st & 1][ln * 16 + ((j ^ swz) << 2) + kq];
+    for (int rt = 0; rt < RT; rt++) {
+      const int n = min(row0 + 16 * rt + n16, N - 1);
+      const uint8_t *wrow = W + (int64_t)n * ldw;
+      const float *srow = S + (int64_t)n * lds;
+#pragma unroll
+      for (int st = 0; st < MS; st++) {
+        wv[rt][st] = *(const uint4 *)(wrow + 16 * min(gbeg + 4 * st + q, G - 1));
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[rt][st][j] = srow[min(gbeg + 4 * st + j, G - 1)];
+      }
     }
-    v4f D[4];
+    float4 xr[XE];
 #pragma unroll
-    for (int j = 0; j < 4; j++) D[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < XE; i++) {
+      const int m = wave + 4 * i, k = 32 * gbeg + 4 * lane;
+      xr[i] = (m < M && k < K) ? *(const float4 *)(X + (int64_t)m * ldx + k)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (c > 0) lds_barrier();  // the previous chunk's x reads are done
+    // x of the chunk: each wave holds whole rows (64 lanes x 4 = KS values)
 #pragma unroll
-    for (int e = 0; e < 8; e++)
+    for (int i = 0; i < XE; i++) {
+      const int m = wave + 4 * i;
+      const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+      const float mx = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      int ex = 0;
+      if (mx > 16384.f) frexpf(mx * (1.f / 16384.f), &ex);  // mx / 2^ex < 16384
+      const float down = ldexpf(1.f, -ex);
+      _Float16 h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float y = v[e] * down;
+        h[e] = (_Float16)y;
+        l[e] = (_Float16)(y - (float)h[e]);
+      }
+      __builtin_memcpy(&xh[m][4 * lane], h, 8);
+      __builtin_memcpy(&xl[m][4 * lane], l, 8);
+      float t = (v[0] + v[1]) + (v[2] + v[3]);
+      t += __shfl_xor(t, 1);
+      t += __shfl_xor(t, 2);
+      t += __shfl_xor(t, 4);
+      if ((lane & 7) == 0) xs[m][lane >> 3] = t;
+      if (lane == 0) fm[m] = ldexpf(1.f, 24 + ex);
+    }
+    lds_barrier();
+#pragma unroll
+    for (int st = 0; st < MS; st++) {
+      if (gbeg + 4 * st >= gend) break;  // uniform per block
+      uint32_t t4[RT][4];
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++) {
+        t4[rt][0] = wv[rt][st].x ^ 0x88888888u;
+        t4[rt][1] = wv[rt][st].y ^ 0x88888888u;
+        t4[rt][2] = wv[rt][st].z ^ 0x88888888u;
+        t4[rt][3] = wv[rt][st].w ^ 0x88888888u;
+        xpose4x4(t4[rt]);
+      }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const float q = (float)(((int)(d[j] << (28 - 4 * e))) >> 28);  // signed nibble e
-        D[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[j][e], q, D[j], 0, 0, 0);
-      }
+        const int gl = 4 * st + j;
+        if (gbeg + gl >= gend) break;
+        w4h8 a[MT];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float sc = __shfl(sv(ST), ln + 16 * j);  // scale of (row ln, group g0 + 4 st + j)
-      acc = acc + sc * D[j];
-    }
-  });
-  // acc[r] = C[m = 4 kq + r][this wave's row ln] over this block's part of K
-  const int nn = (int)blockIdx.x * kW4mRows + 16 * wave + ln;
-  if (nn < N) {
+        for (int t = 0; t < MT; t++) {
+          const int m = 8 * t + ar;
+          a[t] = w4h8{0, 0, 0, 0, 0, 0, 0, 0};
+          if (m < M) a[t] = *(const w4h8 *)((n16 & 1 ? &xl[m][0] : &xh[m][0]) + 32 * gl + 8 * q);
+        }
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int m = 4 * kq + r;
-      if (m < M) {
-        if (nparts == 1) O[(int64_t)m * ldo + nn] = acc[r];
-        else P[((int64_t)part * M + m) * N + nn] = acc[r];
+        for (int rt = 0; rt < RT; rt++) {
+          const w4h8 b = nib8_f16(t4[rt][j]);
+          w4f4 d[MT];
+#pragma unroll
+          for (int t = 0; t < MT; t++)
+            d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, w4f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const float sv = sc[rt][st][j];
+#pragma unroll
+          for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+              const int m = 8 * t + 2 * q + e;  // D rows 4q + 2e (hi) and 4q + 2e + 1 (lo)
+              acc[rt][t][e] = fmaf(sv * fm[m], d[t][2 * e] + d[t][2 * e + 1],
+                                   fmaf(-8.f * sv, xs[m][gl], acc[rt][t][e]));
+            }
+        }
       }
     }
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+    const int nn = row0 + 16 * rt + n16;
+    if (nn >= N) continue;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int m = 8 * t + 2 * q + e;
+        if (m >= M) continue;
+        if (gridDim.y == 1) O[(int64_t)m * ldo + nn] = acc[rt][t][e];
+        else P[((int64_t)blockIdx.y * M + m) * N + nn] = acc[rt][t][e];
+      }
   }
 }
 
@@ -506,24 +559,27 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     hipLaunchKernelGGL(w4s_generic, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, W, ldw, S,
                        lds, X, ldx, O, ldo, M, N, K, gs);
   } else if (M >= 2 && gs == 32) {
-    // several x vectors, groups of 32: fp32 MFMA.  The K parts make about two
-    // blocks per CU; with more than one part the partial tiles go through a
-    // workspace and a second, ordered sum.
-    const int nb = (int)cdiv(N, kW4mRows), ng = K / 32;
-    const int occ = nb >= num_cus() ? 1 : (int)cdiv(2 * num_cus(), nb);
-    const int parts = (int)std::min<int64_t>(ng, std::max<int64_t>(cdiv(ng, kW4mMaxG), occ));
+    // several x vectors, groups of 32: f16 MFMA.  A block takes 4 waves x RT
+    // tiles of 16 weight rows and `chunks` chunks of 8 groups of K; the K parts
+    // (gridDim.y) make about two blocks per CU, and with more than one part the
+    // partial tiles go through a workspace and an ordered sum.
+    constexpr int RT = 2;
+    const int nb = (int)cdiv(N, 64 * RT), ng = K / 32, nck = (int)cdiv(ng, 8);
+    const int want = (int)std::max<int64_t>(1, cdiv(2 * num_cus(), nb));
+    const int chunks = (int)cdiv(nck, std::min(want, nck));
+    const int parts = (int)cdiv(nck, chunks);
     float *P = nullptr;
     if (parts > 1) {
       int rc = workspace(st, sizeof(float) * (size_t)parts * M * N, (void **)&P, 2);
       if (rc) return rc;
     }
-    const int ms = (int)cdiv(cdiv(ng, parts), 4);  // steps for the largest part
-    KernelTimer kt(st, "w4s_mfma");
-#define W4M(MSV) hipLaunchKernelGGL((w4s_mfma<MSV>), dim3((unsigned)nb, (unsigned)parts), dim3(256), 0, st, \
-                                    W, ldw, S, lds, X, ldx, O, ldo, P, M, N, K)
-    if (ms <= 2) W4M(2);
-    else W4M(3);
-#undef W4M
+    KernelTimer kt(st, "w4s_h16");
+    if (M <= 8)
+      hipLaunchKernelGGL((w4s_h16<1, RT>), dim3((unsigned)nb, (unsigned)parts), dim3(256), 0, st, W,
+                         ldw, S, lds, X, ldx, O, ldo, P, M, N, K, chunks);
+    else
+      hipLaunchKernelGGL((w4s_h16<2, RT>), dim3((unsigned)nb, (unsigned)parts), dim3(256), 0, st, W,
+                         ldw, S, lds, X, ldx, O, ldo, P, M, N, K, chunks);
     if (parts > 1)
       hipLaunchKernelGGL(w4s_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256)), dim3(256), 0, st, P,
                          parts, O, ldo, M, N);
