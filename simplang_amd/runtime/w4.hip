@@ -411,10 +411,12 @@ __global__ void __launch_bounds__(256)
         t4[rt][3] = wv[rt][st].w ^ 0x88888888u;
         xpose4x4(t4[rt]);
       }
+      // all MFMAs of the step first (independent accumulators), then the
+      // per-group scaling, so no MFMA result is waited for right after issue
+      w4f4 d[4][RT][MT];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int gl = 4 * st + j;
-        if (gbeg + gl >= gend) break;
+        const int gl = min(4 * st + j, GQ - 1);  // groups past the chunk: computed, not used
         w4h8 a[MT];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
@@ -425,20 +427,28 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
           const w4h8 b = nib8_f16(t4[rt][j]);
-          w4f4 d[MT];
 #pragma unroll
           for (int t = 0; t < MT; t++)
-            d[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, w4f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          const float sv = sc[rt][st][j];
-#pragma unroll
-          for (int t = 0; t < MT; t++)
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-              const int m = 8 * t + 2 * q + e;  // D rows 4q + 2e (hi) and 4q + 2e + 1 (lo)
-              acc[rt][t][e] = fmaf(sv * fm[m], d[t][2 * e] + d[t][2 * e + 1],
-                                   fmaf(-8.f * sv, xs[m][gl], acc[rt][t][e]));
-            }
+            d[j][rt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], b, w4f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int gl = 4 * st + j;
+        if (gbeg + gl >= gend) break;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            const int m = 8 * t + 2 * q + e;  // D rows 4q + 2e (hi) and 4q + 2e + 1 (lo)
+            const float f = fm[m], xsm = xs[m][gl];
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+              const float sv = sc[rt][st][j];
+              acc[rt][t][e] = fmaf(sv * f, d[j][rt][t][2 * e] + d[j][rt][t][2 * e + 1],
+                                   fmaf(-8.f * sv, xsm, acc[rt][t][e]));
+            }
+          }
       }
     }
   }
