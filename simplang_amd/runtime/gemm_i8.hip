@@ -1,4 +1,4 @@
-// gemm_i8.hip -- exact int8 GEMM on CDNA4 int8 MFMA (v_mfma_i32_32x32x32_i8).
+// gemm_i8.hip -- exact int8 GEMM on CDNA4 int8 MFMA.
 //
 // Semantics replaced (citations into the SimpLang tree):
 //   s8 x s8 -> i32  tensor_matmul i8 branch, ConvertSimpToMemRef.cpp:3136-3279
@@ -8,29 +8,31 @@
 //                   natively, so this path needs no correction at all.
 //   u8 x s8 -> i32  raw vpdpbusd (simptensor/tests/test_vnni_correctness.cpp:28-42).
 //                   MFMA has no u8 x s8 form: A is flipped to A^0x80 = A-128 as s8
-//                   and C = MFMA(A^0x80, B) + 128*colsum(B)[j].  The column sums come
-//                   from the B fragments already in registers (v_dot4 against
-//                   0x01010101), so no extra pass over B is made.
+//                   and C = MFMA(A^0x80, B) + 128*colsum(B)[j].
 // Integer sums are order independent, so every tiling / split-K choice is
 // bit-exact with the reference's sequential K loop.
 //
-// Kernel structure (one workgroup = BM x BN tile of C):
-//   * K is walked in BK-byte tiles, double-buffered in LDS: the global loads of
-//     tile t+1 are in flight while the MFMAs of tile t run, one barrier per tile.
-//   * LDS holds 16-byte K-chunks, chunk-major ([BK/16][rows][16 B]), the exact
-//     operand shape of one lane of v_mfma_i32_32x32x32_i8 (16 consecutive K of
-//     one row/column).  Row indices are XOR-swizzled so that both the 128-bit
-//     stores and the 128-bit MFMA-operand reads hit distinct banks.
-//   * B given as [K,N] (tensor_matmul's layout) is transposed on the way into LDS:
-//     each thread loads 16 K-rows x 4 columns as dwords (a wave reads 256
-//     contiguous bytes per row) and transposes 4x4 byte blocks with v_perm_b32.
-//     The reference materialises B_T with a separate 8x8-tiled pass
-//     (ConvertSimpToMemRef.cpp:3168-3216); here that pass is fused away.
-//   * Workgroup ids are remapped so that each of the 8 XCDs owns a contiguous
-//     range of tiles (blocks are dispatched round-robin over XCDs), and tiles are
-//     ordered in groups of 8 tile-rows so co-resident tiles share A and B in L2.
-//   * Skinny / small problems split K over gridDim.y and combine partial tiles
-//     with integer atomics into a zero-filled C (exact).
+// Kernels, by problem size (dispatch<> picks one):
+//   * gemm_i8_dma -- problems of at least one 256x256 tile per CU, K % 64 == 0:
+//     persistent, global -> LDS DMA ring, v_mfma_i32_16x16x64_i8, 16-byte
+//     nontemporal C stores.  B given as [K,N] is first transposed into a
+//     workspace B_T[N,K] (transpose_i8), as the reference materialises B_T
+//     (ConvertSimpToMemRef.cpp:3168-3216); the u8 column sums are formed in the
+//     same pass (or by colsum_nk_i8 when B_T is given).
+//   * gemm_i8_nt16 -- the same tile sizes for K % 64 != 0 (K % 16 == 0), LDS
+//     double-buffered through registers.
+//   * gemm_i8_mfma -- smaller problems and batches (grid z): BMxBN tiles on
+//     v_mfma_i32_32x32x32_i8, K walked in double-buffered LDS tiles; B given as
+//     [K,N] is transposed on the way into LDS (4x4 byte blocks with v_perm_b32);
+//     the u8 column sums come from the B fragments in registers (v_dot4
+//     against 0x01010101).  Skinny problems split K over grid y and combine
+//     partial tiles with integer atomics into a zero-filled C (exact).
+//   * gemm_i8_generic -- operands the MFMA kernels cannot load with aligned
+//     vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases): one
+//     output element per thread.
+// Workgroup ids are remapped so that each of the 8 XCDs owns a contiguous range
+// of tiles (blocks are dispatched round-robin over XCDs), and tiles are ordered
+// in groups of 8 tile-rows so co-resident tiles share A and B in L2.
 #include <algorithm>
 
 #include "rt_internal.h"
