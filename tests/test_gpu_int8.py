@@ -149,6 +149,28 @@ def test_int8_strided_views(dev, orc):
     assert (out[:, :20] == 0).all() and (out[:, 276:] == 0).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 128),     # K-steps < ring stages
+                                   (8192, 8192, 512),     # 4 tiles per workgroup
+                                   (8192, 4096, 1088),    # odd K-step count
+                                   (4100, 4112, 1024)])   # ragged last tiles
+@pytest.mark.parametrize("variant", ["u8s8", "s8s8"])
+def test_int8_persistent_kernel_exact(dev, orc, M, N, K, variant):
+    """Every element of the persistent LDS-DMA kernel's output, at sizes where
+    workgroups walk several tiles (tile transitions overlap one tile's stores
+    with the next tile's loads), against the oracle."""
+    import torch
+    print(f"[int8-persistent] {variant} M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K, seed=9)
+    if variant == "s8s8":
+        a = a.view(np.int8)
+    want, _ = orc.matmul_i8_vnni(a, b, a_unsigned=variant == "u8s8", nthreads=8)
+    fn = sa.matmul_u8s8_i32 if variant == "u8s8" else sa.tensor_matmul_i8
+    got = _run(dev, fn, a, b, M, N)
+    assert np.array_equal(got, want)
+    del got
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("variant", ["u8s8", "nt_s8s8"])
 def test_int8_large_tile_unaligned_c(dev, orc, variant):
     """Large-tile kernels with a C view that is only 4-byte aligned (scalar stores)."""
