@@ -12,9 +12,11 @@
 // 65536, final RMSNorm and an fp32 classifier.  The RoPE loop of the program
 // discards its results (:123-140) and is not run.
 //
-// Kernels per layer: norm+quantize, one int8 GEMV over Wq|Wk|Wv with the K/V
-// cache store fused, attention (one block per head), Wo GEMV adding into x,
-// norm+quantize, one paired W1|W3 GEMV writing ffn_hb, W2 GEMV adding into x.
+// Kernels per layer: one int8 GEMV over Wq|Wk|Wv with the attention RMSNorm
+// and quantization in its prologue and the K/V cache store in its epilogue,
+// attention (one block per head), Wo GEMV adding into x, one paired W1|W3 GEMV
+// (FFN RMSNorm + quantization in its prologue) writing ffn_hb, W2 GEMV adding
+// into x.
 // The int8 GEMVs are HBM-bound: each wave reads whole rows of W_t as 1 KB
 // coalesced lines, x sits in registers, v_dot4_i32_i8 accumulates exactly, so
 // every integer the program computes is reproduced bit for bit.
@@ -103,43 +105,97 @@ struct L32Segs {
   int rows[3];
 };
 
-template <int C, int R, int MODE>
+//   NORM      the block first forms xq itself from xn: the RMSNorm of xn with
+//             weight nw, quantized as l32_quant127 (the l32_norm_k arithmetic;
+//             xq is then unused).  The weight loads are issued before the norm,
+//             which waits only on xn; xq sits in K bytes of dynamic LDS.
+template <int C, int R, int MODE, bool NORM>
 __global__ void __launch_bounds__(256)
     l32_gemv_k(L32Segs sg, const int8_t *__restrict__ xq, int K, int32_t *__restrict__ q,
                int8_t *__restrict__ krow, int8_t *__restrict__ vrow, float *__restrict__ x,
-               int8_t *__restrict__ hb) {
+               int8_t *__restrict__ hb, const float *__restrict__ xn,
+               const float *__restrict__ nw, float eps) {
   constexpr int NM = MODE == kL32Pair ? 2 : 1;  // matrices read per row
+  extern __shared__ uint4 xs[];                 // NORM: xq, K bytes
+  __shared__ float scratch[16];
   const int lane = threadIdx.x & 63;
   const int total = MODE == kL32QKV ? sg.rows[0] + sg.rows[1] + sg.rows[2] : sg.rows[0];
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-  if (row0 >= total) return;  // uniform per wave
+  const bool active = row0 < total;  // uniform per wave
+  if (!NORM && !active) return;      // (NORM: every wave takes part in the norm)
   const int nch = K >> 4;
-  uint4 xv[C];
+  // NORM: element quads 4 (tid + 256 j) of xn and nw (K <= 1024 C)
+  float4 xf[NORM ? C : 1], wf[NORM ? C : 1];
+  if constexpr (NORM) {
 #pragma unroll
-  for (int j = 0; j < C; j++) {
-    const int c = lane + 64 * j;
-    xv[j] = c < nch ? *(const uint4 *)(xq + 16 * c) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < C; j++) {
+      const int i4 = threadIdx.x + 256 * j;
+      const bool in = 4 * i4 < K;
+      xf[j] = in ? *(const float4 *)(xn + 4 * i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      wf[j] = in ? *(const float4 *)(nw + 4 * i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  uint4 xv[C];
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const int c = lane + 64 * j;
+      xv[j] = c < nch ? *(const uint4 *)(xq + 16 * c) : make_uint4(0, 0, 0, 0);
+    }
   }
   uint4 wv[NM][R][C];
+  if (active) {
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int row = min(row0 + r, total - 1);
-    const int8_t *base[NM];
-    if constexpr (MODE == kL32QKV) {
-      const int s = row < sg.rows[0] ? 0 : (row < sg.rows[0] + sg.rows[1] ? 1 : 2);
-      const int rr = s == 0 ? row : (s == 1 ? row - sg.rows[0] : row - sg.rows[0] - sg.rows[1]);
-      base[0] = sg.w[s] + (int64_t)rr * K;
-    } else {
+    for (int r = 0; r < R; r++) {
+      const int row = min(row0 + r, total - 1);
+      const int8_t *base[NM];
+      if constexpr (MODE == kL32QKV) {
+        const int s = row < sg.rows[0] ? 0 : (row < sg.rows[0] + sg.rows[1] ? 1 : 2);
+        const int rr = s == 0 ? row : (s == 1 ? row - sg.rows[0] : row - sg.rows[0] - sg.rows[1]);
+        base[0] = sg.w[s] + (int64_t)rr * K;
+      } else {
 #pragma unroll
-      for (int mtx = 0; mtx < NM; mtx++) base[mtx] = sg.w[mtx] + (int64_t)row * K;
-    }
-#pragma unroll
-    for (int mtx = 0; mtx < NM; mtx++)
-#pragma unroll
-      for (int j = 0; j < C; j++) {
-        const int c = lane + 64 * j;
-        wv[mtx][r][j] = c < nch ? *(const uint4 *)(base[mtx] + 16 * c) : make_uint4(0, 0, 0, 0);
+        for (int mtx = 0; mtx < NM; mtx++) base[mtx] = sg.w[mtx] + (int64_t)row * K;
       }
+#pragma unroll
+      for (int mtx = 0; mtx < NM; mtx++)
+#pragma unroll
+        for (int j = 0; j < C; j++) {
+          const int c = lane + 64 * j;
+          wv[mtx][r][j] = c < nch ? *(const uint4 *)(base[mtx] + 16 * c) : make_uint4(0, 0, 0, 0);
+        }
+    }
+  }
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      ss = fmaf(xf[j].x, xf[j].x, ss);
+      ss = fmaf(xf[j].y, xf[j].y, ss);
+      ss = fmaf(xf[j].z, xf[j].z, ss);
+      ss = fmaf(xf[j].w, xf[j].w, ss);
+    }
+    ss = block_sum_lds(ss, scratch);
+    const float rms = sqrtf(ss / (float)K + eps);
+    uint32_t *xs32 = (uint32_t *)xs;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const int i4 = threadIdx.x + 256 * j;
+      if (4 * i4 < K) {
+        const uint32_t b0 = (uint8_t)l32_quant127((xf[j].x / rms) * wf[j].x);
+        const uint32_t b1 = (uint8_t)l32_quant127((xf[j].y / rms) * wf[j].y);
+        const uint32_t b2 = (uint8_t)l32_quant127((xf[j].z / rms) * wf[j].z);
+        const uint32_t b3 = (uint8_t)l32_quant127((xf[j].w / rms) * wf[j].w);
+        xs32[i4] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+    }
+    lds_barrier();
+    if (!active) return;
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const int c = lane + 64 * j;
+      xv[j] = c < nch ? xs[c] : make_uint4(0, 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -299,17 +355,24 @@ int l32_alloc(L32Model &m) {
   return SIMP_RT_OK;
 }
 
-// One int8 GEMV launch: C chunks per lane from K, R rows per wave.
+// One int8 GEMV launch: C chunks per lane from K, R rows per wave.  With xn
+// (and nw) given, the kernel forms xq as the RMSNorm of xn quantized.
 template <int MODE>
 int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, int8_t *krow,
-             int8_t *vrow, float *x, int8_t *hb, hipStream_t st) {
+             int8_t *vrow, float *x, int8_t *hb, hipStream_t st, const float *xn = nullptr,
+             const float *nw = nullptr, float eps = 0.f) {
   const int C = (int)cdiv(K / 16, 64);
-  const int R = MODE == kL32Pair ? 1 : 2;
+  constexpr int R = MODE == kL32Pair ? 1 : 2;
   const unsigned grid = (unsigned)cdiv(total, 4 * R);
+  const size_t lds = xn ? (size_t)K : 0;
 #define L32G(CC)                                                                              \
   case CC:                                                                                    \
-    hipLaunchKernelGGL((l32_gemv_k<CC, (MODE == kL32Pair ? 1 : 2), MODE>), dim3(grid),        \
-                       dim3(256), 0, st, sg, xq, K, q, krow, vrow, x, hb);                    \
+    if (xn)                                                                                   \
+      hipLaunchKernelGGL((l32_gemv_k<CC, R, MODE, true>), dim3(grid), dim3(256), lds, st, sg, \
+                         xq, K, q, krow, vrow, x, hb, xn, nw, eps);                           \
+    else                                                                                      \
+      hipLaunchKernelGGL((l32_gemv_k<CC, R, MODE, false>), dim3(grid), dim3(256), 0, st, sg,  \
+                         xq, K, q, krow, vrow, x, hb, xn, nw, eps);                           \
     break;
   switch (C) {
     L32G(1) L32G(2) L32G(4) L32G(8) L32G(16)
@@ -317,7 +380,6 @@ int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, 
       return set_error(SIMP_RT_EUNSUPPORTED, "llama32_forward: K=%d per matrix row", K);
   }
 #undef L32G
-  (void)R;
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
 }
@@ -331,8 +393,6 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
   const size_t attn_lds = sizeof(float) * (size_t)(m.hs + pos + 1);
   for (int64_t l = 0; l < m.L; l++) {
     int8_t *kc = m.kc + l * m.S * kv, *vc = m.vc + l * m.S * kv;
-    hipLaunchKernelGGL(l32_norm_k, dim3(1), dim3(1024), 0, st, (const float *)m.x,
-                       m.rms_att + l * dim, (float *)nullptr, m.xq, dim, eps);
     L32Segs s{};
     s.w[0] = m.wq + l * m.dim * m.dim;
     s.w[1] = m.wk + l * m.kv * m.dim;
@@ -340,8 +400,9 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
     s.rows[0] = dim;
     s.rows[1] = kv;
     s.rows[2] = kv;
-    if ((rc = l32_gemv<kL32QKV>(s, dim + 2 * kv, dim, m.xq, m.q, kc + pos * kv, vc + pos * kv,
-                                nullptr, nullptr, st)))
+    if ((rc = l32_gemv<kL32QKV>(s, dim + 2 * kv, dim, nullptr, m.q, kc + pos * kv,
+                                vc + pos * kv, nullptr, nullptr, st, m.x, m.rms_att + l * dim,
+                                eps)))
       return rc;
     hipLaunchKernelGGL(l32_attn_k, dim3((unsigned)m.nh), dim3(256), attn_lds, st,
                        (const int32_t *)m.q, (const int8_t *)kc, (const int8_t *)vc, m.attn, m.xq,
@@ -351,13 +412,12 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
     s.rows[0] = dim;
     if ((rc = l32_gemv<kL32Resid>(s, dim, dim, m.xq, nullptr, nullptr, nullptr, m.x, nullptr, st)))
       return rc;
-    hipLaunchKernelGGL(l32_norm_k, dim3(1), dim3(1024), 0, st, (const float *)m.x,
-                       m.rms_ffn + l * dim, (float *)nullptr, m.xq, dim, eps);
     s = L32Segs{};
     s.w[0] = m.w1 + l * m.hid * m.dim;
     s.w[1] = m.w3 + l * m.hid * m.dim;
     s.rows[0] = hid;
-    if ((rc = l32_gemv<kL32Pair>(s, hid, dim, m.xq, nullptr, nullptr, nullptr, nullptr, m.hq, st)))
+    if ((rc = l32_gemv<kL32Pair>(s, hid, dim, nullptr, nullptr, nullptr, nullptr, nullptr, m.hq,
+                                 st, m.x, m.rms_ffn + l * dim, eps)))
       return rc;
     s = L32Segs{};
     s.w[0] = m.w2 + l * m.dim * m.hid;
