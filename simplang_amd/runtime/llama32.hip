@@ -226,11 +226,13 @@ __global__ void __launch_bounds__(256)
 
 // Attention of one layer, one block per head (:161-216).  Scores: one thread
 // per position, the program's order and operations within a position (fp32
-// product then sum, no fused multiply-add), / 8; four positions per thread
-// are loaded before any is summed.  Softmax over pos + 1 scores.  V sum: a
-// thread takes 16 consecutive d of every P-th position (four rows in flight),
-// partitions added in order.  attn_out = (i32) sum; xq = its i8 quantization
-// (float)attn_out / 256, clamped.  Head size and kv_dim multiples of 16.
+// product then sum, no fused multiply-add), / 8; the 16-byte chunks of four
+// positions are loaded four chunks at a time before any is summed.  Softmax
+// over pos + 1 scores.  V sum: a thread takes 16 consecutive d of every P-th
+// position (four rows in flight), partitions added in order; the first four
+// rows of every thread are loaded at entry, so they arrive alongside the K
+// rows.  attn_out = (i32) sum; xq = its i8 quantization (float)attn_out / 256,
+// clamped.  Head size and kv_dim multiples of 16.
 // LDS: head_size + pos + 1 floats (dynamic, at most 47 KB) + 16 KB.
 __global__ void __launch_bounds__(256)
     l32_attn_k(const int32_t *__restrict__ Q, const int8_t *__restrict__ kc,
@@ -239,9 +241,19 @@ __global__ void __launch_bounds__(256)
   extern __shared__ float sm[];
   __shared__ float red[4096];
   __shared__ float scratch[16];
-  constexpr int U = 4;
+  constexpr int U = 4, CG = 4;
   const int h = blockIdx.x, kho = (h / n_rep) * hs, n = pos + 1;
   const int hc = hs >> 4;  // 16-byte chunks per row
+  const int P = 256 / hc;  // V position partitions (hs <= 256: P >= 16)
+  const int vcol = threadIdx.x % hc, vp = threadIdx.x / hc;
+  // this thread's first V rows (positions vp + P u), issued ahead of everything
+  uint4 v0[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int t = vp + P * u;
+    v0[u] = (vp < P && t < n) ? *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * vcol)
+                              : make_uint4(0, 0, 0, 0);
+  }
   float *qf = sm, *att = sm + hs;
   for (int d = threadIdx.x; d < hs; d += 256) qf[d] = (float)Q[h * hs + d];
   __syncthreads();
@@ -249,22 +261,28 @@ __global__ void __launch_bounds__(256)
     float score[U];
 #pragma unroll
     for (int u = 0; u < U; u++) score[u] = 0.f;
-    for (int c = 0; c < hc; c++) {
-      uint4 v[U];
+    for (int c0 = 0; c0 < hc; c0 += CG) {
+      uint4 kv4[U][CG];
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int t = min(t0 + 256 * u, n - 1);
-        v[u] = *(const uint4 *)(kc + (int64_t)t * kv + kho + 16 * c);
-      }
+      for (int u = 0; u < U; u++)
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float kf = (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)));
-          score[u] = __fadd_rn(score[u], __fmul_rn(qf[16 * c + e], kf));
+        for (int cc = 0; cc < CG; cc++) {
+          const int t = t0 + 256 * u, c = c0 + cc;
+          kv4[u][cc] = (t < n && c < hc) ? *(const uint4 *)(kc + (int64_t)t * kv + kho + 16 * c)
+                                         : make_uint4(0, 0, 0, 0);
         }
-      }
+#pragma unroll
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int cc = 0; cc < CG; cc++) {
+          if (c0 + cc >= hc) break;
+          const uint32_t wd[4] = {kv4[u][cc].x, kv4[u][cc].y, kv4[u][cc].z, kv4[u][cc].w};
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const float kf = (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)));
+            score[u] = __fadd_rn(score[u], __fmul_rn(qf[16 * (c0 + cc) + e], kf));
+          }
+        }
     }
 #pragma unroll
     for (int u = 0; u < U; u++)
@@ -283,18 +301,21 @@ __global__ void __launch_bounds__(256)
   l = block_sum(l, scratch);
   for (int t = threadIdx.x; t < n; t += 256) att[t] = att[t] / l;
   __syncthreads();
-  const int P = 256 / hc;  // position partitions (hs <= 256: P >= 16)
-  const int c = threadIdx.x % hc, p = threadIdx.x / hc;
-  if (p < P) {
+  if (vp < P) {
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[e] = 0.f;
-    for (int t0 = p; t0 < n; t0 += P * U) {
+    for (int t0 = vp; t0 < n; t0 += P * U) {
       uint4 v[U];
+      if (t0 == vp) {
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int t = min(t0 + P * u, n - 1);
-        v[u] = *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * c);
+        for (int u = 0; u < U; u++) v[u] = v0[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          const int t = min(t0 + P * u, n - 1);
+          v[u] = *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * vcol);
+        }
       }
 #pragma unroll
       for (int u = 0; u < U; u++) {
@@ -307,11 +328,13 @@ __global__ void __launch_bounds__(256)
       }
     }
 #pragma unroll
-    for (int e = 0; e < 16; e++) red[p * hs + 16 * c + e] = acc[e];
+    for (int e = 0; e < 16; e++) red[vp * hs + 16 * vcol + e] = acc[e];
   }
   __syncthreads();
   for (int dd = threadIdx.x; dd < hs; dd += 256) {
     float v = red[dd];
+    // in partition order; unrolled so that the LDS reads run ahead of the adds
+#pragma unroll 8
     for (int pp = 1; pp < P; pp++) v = __fadd_rn(v, red[pp * hs + dd]);
     const int32_t a = (int32_t)v;
     attn_out[h * hs + dd] = a;
