@@ -39,6 +39,7 @@ from .host import (  # noqa: F401
     stories110M_forward,
     llama2_quant_forward,
     llama32_forward,
+    Llama32Program,
     forward_cache_clear,
     W_F32,
     W_W4S,

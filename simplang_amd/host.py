@@ -282,6 +282,28 @@ def llama32_forward(arrays: dict, pos, dim, hidden_dim, n_layers, n_heads, n_kv_
     return r
 
 
+class Llama32Program:
+    """``llama32_forward`` bound to one set of arrays, as a C++ host binds it:
+    the 22 descriptors are built once, and each call passes only the position
+    (the arrays must stay alive and in place while the object is used)."""
+
+    def __init__(self, arrays: dict, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
+                 vocab_size, max_seq_len, head_dim):
+        args = []
+        for name in LLAMA32_ARRAYS:
+            args += desc1(arrays[name])
+        self._arrays = arrays
+        self._args = args
+        self._dims = (dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, max_seq_len,
+                      head_dim)
+
+    def __call__(self, pos) -> float:
+        r = lib.llama32_forward(*self._args, pos, *self._dims)
+        if r != r:
+            raise SimpRTError("llama32_forward", -1, lib.simp_rt_last_error().decode())
+        return r
+
+
 def forward_cache_clear() -> None:
     _check("simp_rt_forward_cache_clear", lib.simp_rt_forward_cache_clear())
 

@@ -72,6 +72,29 @@ def test_llama32_device_arrays_long_context(dev, orc):
     sa.forward_cache_clear()
 
 
+def test_llama32_bound_program_matches(dev, orc):
+    """Llama32Program (descriptors built once) against the oracle, device arrays."""
+    import torch
+    cfg = CFG_SMALL
+    arrays = make_arrays(cfg, seed=8, wide=True)
+    ref = {k: v.copy() for k, v in arrays.items()}
+    darr = {k: torch.from_numpy(v).to(dev) for k, v in arrays.items()}
+    dims = [cfg[k] for k in DIMS]
+    fwd = sa.Llama32Program(darr, *dims)
+    for pos in range(6):
+        r = fwd(pos)
+        want = orc.llama32_int8_forward(ref, pos, *dims)
+        logits = darr["logits"].cpu().numpy()
+        assert r == logits[0]
+        _close(logits, ref["logits"])
+        assert abs(want - r) <= TOL * max(np.abs(ref["logits"]).max(), 1e-30)
+        kv = cfg["n_kv_heads"] * cfg["head_dim"]
+        got = darr["k_cache"].cpu().numpy().reshape(cfg["n_layers"], cfg["max_seq_len"], kv)[:, pos]
+        exp = ref["k_cache"].reshape(cfg["n_layers"], cfg["max_seq_len"], kv)[:, pos]
+        assert np.array_equal(got, exp)
+    sa.forward_cache_clear()
+
+
 def test_llama32_rejects(dev):
     cfg = CFG_SMALL
     arrays = make_arrays(cfg, seed=1)
