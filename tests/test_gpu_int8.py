@@ -191,3 +191,26 @@ def test_int8_large_tile_unaligned_c(dev, orc, variant):
     out = c_full.cpu().numpy()
     assert np.array_equal(out[:, 1:N + 1], want)
     assert (out[:, 0] == -7).all() and (out[:, N + 1:] == -7).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(0, 64, 32), (48, 0, 32), (48, 64, 0), (0, 0, 0)])
+def test_empty_dimensions(dev, M, N, K):
+    """Empty operands: M or N = 0 is a no-op that leaves C alone, K = 0 writes
+    C = 0 (the empty sum), on the int8 (KN and NT) and fp32 / f64 entry points."""
+    import torch
+    print(f"[empty] M={M} N={N} K={K}", flush=True)
+    cases = [
+        (sa.tensor_matmul_i8, torch.int8, torch.int8, False, torch.int32),
+        (sa.matmul_u8s8_i32, torch.uint8, torch.int8, False, torch.int32),
+        (sa.tensor_matmul_nt_i8, torch.int8, torch.int8, True, torch.int32),
+        (sa.tensor_matmul_f32, torch.float32, torch.float32, False, torch.float32),
+        (sa.tensor_matmul_f64, torch.float64, torch.float64, False, torch.float64),
+    ]
+    for fn, ta_t, tb_t, nt, tc_t in cases:
+        a = torch.ones((M, K), dtype=ta_t, device=dev)
+        b = torch.ones((N, K) if nt else (K, N), dtype=tb_t, device=dev)
+        c = torch.full((M, N), 7, dtype=tc_t, device=dev)
+        fn(a, b, c)
+        torch.cuda.synchronize()
+        want = 0 if (K == 0 and M and N) else 7
+        assert (c == want).all().item(), (fn.__name__, M, N, K)
