@@ -183,24 +183,26 @@ __global__ void __launch_bounds__(256)
 }
 
 // Symmetric W4 with one x vector (the decode shape).  Same lane -> row mapping
-// as w4s_gemv (RB = 8 rows per block, chunk groups g = t / 8, chunks g + 32u),
+// as w4s_gemv (RB = 8 rows per block, chunk groups g = t / 8, chunks g + Gu),
 // but no block-wide barrier before the compute: a block barrier makes every
 // wave wait for all of its outstanding weight loads (the fence drains vmcnt),
 // which serialises the unpack/FMA work behind the last byte of the transfer.
 // Instead each wave stages into its own LDS region just the x chunks its lanes
 // use, with the x loads issued before the weight loads (loads retire in issue
 // order), and each chunk's work then waits only for that chunk's bytes.
-// Requires 32 * UB >= K / 32.
-template <int UB>
-__global__ void __launch_bounds__(256)
+// NWV waves per block (G = 8 NWV chunk groups): 8 for long rows over few
+// blocks, which halves each wave's serial unpack/FMA work.
+// Requires G * UB >= K / 32.
+template <int UB, int NWV>
+__global__ void __launch_bounds__(64 * NWV)
     w4s_gemv1(const uint8_t *__restrict__ W, int64_t ldw, const float *__restrict__ S, int64_t lds,
               const float *__restrict__ X, float *__restrict__ O, int N, int K, int gs) {
-  constexpr int RB = 8, G = 256 / RB, GW = 64 / RB;  // chunk groups per block / per wave
-  constexpr int CW = GW * UB;                         // x chunks staged per wave
-  constexpr int XPL = CW * 8 / 64;                    // x float4 per lane
-  __shared__ float red[4][RB];
-  __shared__ __align__(16) float xw[4][CW][32];
-  __shared__ float xsw[4][CW];
+  constexpr int RB = 8, G = 64 * NWV / RB, GW = 64 / RB;  // chunk groups per block / per wave
+  constexpr int CW = GW * UB;                              // x chunks staged per wave
+  constexpr int XPL = CW * 8 / 64;                         // x float4 per lane
+  __shared__ float red[NWV][RB];
+  __shared__ __align__(16) float xw[NWV][CW][32];
+  __shared__ float xsw[NWV][CW];
   const int nchunk = K >> 5, cpg = gs >> 5, cps = cpg_log2(cpg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
@@ -265,8 +267,14 @@ __global__ void __launch_bounds__(256)
   for (int d = RB; d < 64; d <<= 1) acc += __shfl_xor(acc, d);
   if (lane < RB) red[wave][r] = acc;
   __syncthreads();
-  if (threadIdx.x < RB && (int)blockIdx.x * RB + (int)threadIdx.x < N)
-    O[blockIdx.x * RB + r] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+  if (threadIdx.x < RB && (int)blockIdx.x * RB + (int)threadIdx.x < N) {
+    // the waves' partial sums in pairs, then the pairs in order
+    float t = 0.f;
+#pragma unroll
+    for (int v = 0; v < NWV; v += 4)
+      t += (red[v][r] + red[v + 1][r]) + (red[v + 2][r] + red[v + 3][r]);
+    O[blockIdx.x * RB + r] = t;
+  }
 }
 
 // ------------------------------------------- 2 <= M <= 16: f16 MFMA path
@@ -594,16 +602,23 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
       hipLaunchKernelGGL(w4s_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256)), dim3(256), 0, st, P,
                          parts, O, ldo, M, N);
   } else if (M == 1 && K / 32 <= 32 * 16) {
-    // one x vector: the barrier-free kernel, UB chunks per lane with 32*UB >= K/32
+    // one x vector: the barrier-free kernel, UB chunks per lane with G*UB >= K/32;
+    // 8 waves per block when there are fewer than two blocks of 8 rows per CU
     const int nchunk = K / 32;
     const dim3 grid((unsigned)cdiv(N, 8));
     KernelTimer kt(st, "w4s_gemv");
-#define W4S1(U) hipLaunchKernelGGL((w4s_gemv1<U>), grid, dim3(256), 0, st, W, ldw, S, lds, X, O, N, K, gs)
-    if (nchunk <= 64) W4S1(2);
-    else if (nchunk <= 128) W4S1(4);
-    else if (nchunk <= 256) W4S1(8);
-    else if (nchunk <= 384) W4S1(12);
-    else W4S1(16);
+#define W4S1(U, V) \
+  hipLaunchKernelGGL((w4s_gemv1<U, V>), grid, dim3(64 * V), 0, st, W, ldw, S, lds, X, O, N, K, gs)
+    if ((int64_t)grid.x < 2 * num_cus() && nchunk > 128) {
+      if (nchunk <= 384) W4S1(6, 8);
+      else W4S1(8, 8);
+    } else {
+      if (nchunk <= 64) W4S1(2, 4);
+      else if (nchunk <= 128) W4S1(4, 4);
+      else if (nchunk <= 256) W4S1(8, 4);
+      else if (nchunk <= 384) W4S1(12, 4);
+      else W4S1(16, 4);
+    }
 #undef W4S1
   } else {
     // 8 rows per block keeps >= 400 blocks at N = 3200; x in LDS when it fits.

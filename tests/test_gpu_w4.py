@@ -47,7 +47,10 @@ def test_w4s_baseline_shapes(dev, orc, M, N, K):
 @pytest.mark.parametrize("M,N,K,gs", [(3, 17, 96, 32), (2, 100, 256, 64), (5, 33, 512, 128),
                                       (1, 1, 32, 32), (16, 70, 640, 32),
                                       (2, 9, 40, 8),      # K % 32 != 0: generic kernel
-                                      (17, 12, 64, 32)])  # M > 16: generic kernel
+                                      (17, 12, 64, 32),   # M > 16: generic kernel
+                                      # M = 1, long rows over few blocks: 8-wave kernel
+                                      (1, 1003, 16384, 32), (1, 2000, 12320, 32),
+                                      (1, 100, 4128, 96)])
 def test_w4s_ragged_and_fallback(dev, orc, M, N, K, gs):
     import torch
     w, s, x = _w4s_inputs(M, N, K, gs, seed=N * 7 + K)
