@@ -203,9 +203,19 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Sum of NWV per-wave values: pairs of pairs, then the groups of four in order
+// (for NWV = 4: (v0 + v1) + (v2 + v3)).
+template <int NWV>
+__device__ __forceinline__ float sum_waves(const float *v) {
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NWV; i += 4) t += (v[i] + v[i + 1]) + (v[i + 2] + v[i + 3]);
+  return t;
+}
+
 // W4 (symmetric, group gs) multi-matrix GEMV: lane -> row (8 rows per block),
-// 32 chunk groups of 16-byte chunks per block, 8 per wave.  The four waves
-// partition a row's chunks (wave w takes the chunks c with c % 32 in
+// G = 8 NWV chunk groups of 16-byte chunks per block, 8 per wave.  The NWV
+// waves partition a row's chunks (wave w takes the chunks c with c % G in
 // [8w, 8w + 8)), so each wave stages only its own x chunks in LDS and no block
 // barrier precedes the compute: a chunk's work waits only for its own bytes
 // (x loads are issued first, then the weights; loads retire in issue order).
@@ -215,17 +225,17 @@ __global__ void __launch_bounds__(256)
 //     the 1/rms factor multiplies the finished row sums.
 //   OUT kPairSwiGLU: lanes r < 4 take row i of segment 0 (W1), lanes r >= 4
 //     the same row of segment 1 (W3); segment 0's output gets silu(h1) * h3.
-template <int PRO, int OUT, int UB>
-__global__ void __launch_bounds__(256)
+template <int PRO, int OUT, int UB, int NWV = 4>
+__global__ void __launch_bounds__(64 * NWV)
     dgemv_w4(Segs sg, int K, int gs, const float *__restrict__ x0, const float *__restrict__ nw,
              float eps) {
-  constexpr int RB = 8, G = 256 / RB, GW = 64 / RB;
+  constexpr int RB = 8, G = 64 * NWV / RB, GW = 64 / RB;
   constexpr int CW = GW * UB;         // x chunks staged per wave
   constexpr int XPL = CW * 8 / 64;    // x float4 per lane
-  __shared__ float red[4][RB];
-  __shared__ float ssq[4];
-  __shared__ __align__(16) float xw[4][CW][32];
-  __shared__ float xsw[4][CW];
+  __shared__ float red[NWV][RB];
+  __shared__ float ssq[NWV];
+  __shared__ __align__(16) float xw[NWV][CW][32];
+  __shared__ float xsw[NWV][CW];
   const int nchunk = K >> 5, cpg = gs >> 5, cps = cpg_log2(cpg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = threadIdx.x % RB, g = threadIdx.x / RB, gl = lane / RB;
@@ -317,9 +327,13 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   float scale = 1.f;
   if constexpr (PRO == kRmsNorm)
-    scale = 1.f / sqrtf(((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) / (float)K + eps);
+    scale = 1.f / sqrtf(sum_waves<NWV>(ssq) / (float)K + eps);
   auto row_sum = [&](int rr2) {
-    return ((red[0][rr2] + red[1][rr2]) + (red[2][rr2] + red[3][rr2])) * scale;
+    float t = 0.f;
+#pragma unroll
+    for (int v = 0; v < NWV; v += 4)
+      t += (red[v][rr2] + red[v + 1][rr2]) + (red[v + 2][rr2] + red[v + 3][rr2]);
+    return t * scale;
   };
   if constexpr (OUT == kPairSwiGLU) {
     if (threadIdx.x < RB / 2 && row0 + r < sgm.rows)  // r < 4: segment 0
@@ -839,10 +853,15 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
     }
     const int gs = m.cfg.group_size;
     const int nchunk = K / 32;
+    // 8 waves per block for long rows over fewer than two blocks per CU (the
+    // down projection): half the serial unpack/FMA work per wave
+    const bool wide = !pair && nchunk > 128 && tiles < 2 * num_cus();
 #define DWU(P, O, U) hipLaunchKernelGGL((dgemv_w4<P, O, U>), dim3(tiles), dim3(256), 0, st, sg, K, gs, x0, nw, eps)
+#define DWU8(P, O, U) hipLaunchKernelGGL((dgemv_w4<P, O, U, 8>), dim3(tiles), dim3(512), 0, st, sg, K, gs, x0, nw, eps)
 #define DW(P, O)                      \
   do {                                \
-    if (nchunk <= 32) DWU(P, O, 1);   \
+    if (wide) DWU8(P, O, 5);          \
+    else if (nchunk <= 32) DWU(P, O, 1);   \
     else if (nchunk <= 64) DWU(P, O, 2); \
     else if (nchunk <= 128) DWU(P, O, 4); \
     else if (nchunk <= 256) DWU(P, O, 8); \
@@ -852,6 +871,7 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
     else { if (out_mode == kAccum) DW(kPlain, kAccum); else DW(kPlain, kStore); }
 #undef DW
 #undef DWU
+#undef DWU8
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
