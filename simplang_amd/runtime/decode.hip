@@ -853,14 +853,15 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
     }
     const int gs = m.cfg.group_size;
     const int nchunk = K / 32;
-    // 8 waves per block for long rows over fewer than two blocks per CU (the
-    // down projection): half the serial unpack/FMA work per wave
-    const bool wide = !pair && nchunk > 128 && tiles < 2 * num_cus();
+    // 8 waves per block for rows of more than 64 chunks over fewer than 8
+    // blocks per CU: half the serial unpack/FMA work per wave
+    const bool wide = nchunk > 64 && tiles < 8 * num_cus();
 #define DWU(P, O, U) hipLaunchKernelGGL((dgemv_w4<P, O, U>), dim3(tiles), dim3(256), 0, st, sg, K, gs, x0, nw, eps)
 #define DWU8(P, O, U) hipLaunchKernelGGL((dgemv_w4<P, O, U, 8>), dim3(tiles), dim3(512), 0, st, sg, K, gs, x0, nw, eps)
 #define DW(P, O)                      \
   do {                                \
-    if (wide) DWU8(P, O, 5);          \
+    if (wide && nchunk <= 128) DWU8(P, O, 2); \
+    else if (wide) DWU8(P, O, 5);     \
     else if (nchunk <= 32) DWU(P, O, 1);   \
     else if (nchunk <= 64) DWU(P, O, 2); \
     else if (nchunk <= 128) DWU(P, O, 4); \

@@ -603,14 +603,17 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
                          parts, O, ldo, M, N);
   } else if (M == 1 && K / 32 <= 32 * 16) {
     // one x vector: the barrier-free kernel, UB chunks per lane with G*UB >= K/32;
-    // 8 waves per block when there are fewer than two blocks of 8 rows per CU
+    // 8 waves per block for rows of more than 64 chunks unless there are 8 or
+    // more blocks of 8 rows per CU (3200x8640: 7.45 -> 7.1 us, 8640x3200:
+    // 10.6 -> 8.8 us; 3200x32000 measured no better)
     const int nchunk = K / 32;
     const dim3 grid((unsigned)cdiv(N, 8));
     KernelTimer kt(st, "w4s_gemv");
 #define W4S1(U, V) \
   hipLaunchKernelGGL((w4s_gemv1<U, V>), grid, dim3(64 * V), 0, st, W, ldw, S, lds, X, O, N, K, gs)
-    if ((int64_t)grid.x < 2 * num_cus() && nchunk > 128) {
-      if (nchunk <= 384) W4S1(6, 8);
+    if (nchunk > 64 && (int64_t)grid.x < 8 * num_cus()) {
+      if (nchunk <= 128) W4S1(2, 8);
+      else if (nchunk <= 384) W4S1(6, 8);
       else W4S1(8, 8);
     } else {
       if (nchunk <= 64) W4S1(2, 4);
