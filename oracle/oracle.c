@@ -719,7 +719,7 @@ int64_t orc_argmax(const float *logits, int64_t n) {
 }
 
 
-/* ---- symmetric W4 quantization (BASELINE format) ---- */
+/* ---- symmetric W4 quantization (signed nibbles, one scale per group) ---- */
 void orc_quantize_w4s(const float *w, int64_t rows, int64_t cols, int64_t gs, uint8_t *qw,
                       float *scales) {
   const int64_t gpr = cols / gs;

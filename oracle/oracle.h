@@ -135,7 +135,7 @@ void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
 void orc_quantize_f5(const float *w, int64_t total, int64_t gs, uint8_t *qw,
                      float *scales, float *zeros);
 
-/* BASELINE W4 format (F6): signed nibbles in [-8,7] (sign-extended as in
+/* Symmetric W4 format (F6): signed nibbles in [-8,7] (sign-extended as in
  * ConvertSimpToMemRef.cpp:3016-3037, low nibble = even k), W[N,K] packed along
  * K (row = K/2 bytes), one fp32 scale per group of gs along K (scales[N, K/gs]),
  * no zero point.  out[m,n] = sum_k (q[n,k]*s[n,k/gs]) * x[m,k], accumulated in
@@ -229,7 +229,7 @@ float orc_llama32_int8_forward(const orc_llama_cfg *cfg, int64_t head_dim, const
 /* Strict-'>' argmax, first maximum wins (examples/llama2/generate_stories110M.cpp:73-83). */
 int64_t orc_argmax(const float *logits, int64_t n);
 
-/* Symmetric W4 quantization (the BASELINE format, no reference counterpart):
+/* Symmetric W4 quantization (the format above; no reference counterpart):
  * per row of cols, groups of gs: scale = max|w| / 7 (1 for an all-zero group),
  * q = clamp(round(w / scale), -8, 7), two's-complement nibbles, low = even k. */
 void orc_quantize_w4s(const float *w, int64_t rows, int64_t cols, int64_t gs, uint8_t *qw,

@@ -2,8 +2,8 @@
 exist offline; the reference's own hosts use random weights too:
 examples/llama2/test_stories110M.cpp:20-22,122-133, N(0, 0.02) for every array).
 
-fp32 models: every array N(0, 0.02).
-W4 models: norms and embedding N(0, 0.02) fp32; every linear
+fp32 models (the 110M benchmark configuration): every array N(0, 0.02).
+W4 models (the 3B W4-g32 configuration): norms and embedding N(0, 0.02) fp32; every linear
 weight (classifier included) symmetric int4 uniform in [-8, 7], packed two per
 byte along K (low nibble = even k), one fp32 scale |N(0, 0.02)|/7 per group of
 32 along K.  Generated on the device with torch (seeded) so that 3B-size models

@@ -26,7 +26,7 @@
 //               groups of `gs` over a tensor, scale = (max - min) / 15 (at
 //               least 1e-8), zero = min, q = clamp(round((w - min) / scale),
 //               0, 15), low nibble = even index.
-//   W4 (sym.)   the BASELINE format: per row, groups of gs along K, scale =
+//   W4 (sym.)   the benchmark W4 format: per row, groups of gs along K, scale =
 //               max|w| / 7 (1 for an all-zero group), q = clamp(round(w / s),
 //               -8, 7).
 #include <algorithm>

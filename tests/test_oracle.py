@@ -353,7 +353,7 @@ def test_rope_properties(orc):
 
 
 def test_quantize_w4s_properties(orc):
-    """Symmetric W4 (BASELINE format): every value within half a step of its
+    """Symmetric W4 (signed nibbles, one scale per group): every value within half a step of its
     dequantized value, the group maximum at +-7, an all-zero group at scale 1,
     two's-complement nibbles with the even index low."""
     rng = np.random.default_rng(11)
