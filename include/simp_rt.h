@@ -51,6 +51,11 @@ extern "C" {
 /* No reference counterpart: the reference runs in-process on the CPU.  The
  * loader it replaces is KernelRunner (runtime/include/kernel_runner.hpp:27-103). */
 const char *simp_rt_last_error(void);
+/* Number of errors raised on the calling thread so far.  The model-level exports
+ * return a float (NaN on error, as the compiled programs have no status); a
+ * caller compares this count before and after the call to tell an error from a
+ * NaN the arithmetic produced.  Those exports also clear the message on entry. */
+int64_t simp_rt_error_count(void);
 int32_t simp_rt_version(void);
 int32_t simp_rt_init(void);
 int32_t simp_rt_set_stream(void *hip_stream); /* per calling thread; NULL = null stream */
@@ -126,6 +131,46 @@ int32_t simp_rt_tensor_matmul_i4(
     const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
     const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
     int16_t *c_alloc, int16_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
+/* ------------------------------------------- int8 benchmark programs -- */
+
+/* The reference's compiled int8 benchmark programs, with their symbols and
+ * signatures, so its own hosts can dlopen this library.
+ *
+ * benchmark_int8_matmul_<N>() replaces fn benchmark_int8_matmul_<N>() -> i32 of
+ * simptensor/benchmarks/bench_int8_matmul.sl:11-335 (looked up by
+ * bench_int8_matmul_runner.cpp:24,247): it builds val = ((i*N + j) % 127) - 64,
+ * A[i,j] = B[j,i] = val, computes C = tensor_matmul(A, B) (s8 x s8 -> i32) and
+ * returns the i32 wraparound sum of C.  The program has no error path; here an
+ * error returns 0 and raises simp_rt_error_count(). */
+int32_t benchmark_int8_matmul_32(void);
+int32_t benchmark_int8_matmul_64(void);
+int32_t benchmark_int8_matmul_128(void);
+int32_t benchmark_int8_matmul_256(void);
+int32_t benchmark_int8_matmul_384(void);
+int32_t benchmark_int8_matmul_512(void);
+int32_t benchmark_int8_matmul_768(void);
+int32_t benchmark_int8_matmul_1024(void);
+int32_t benchmark_int8_matmul_2048(void);
+int32_t benchmark_int8_matmul_4096(void);
+
+/* int8_chunk_<N>(i8[] A, i8[] B, i32[] C, i64 row_start) replaces
+ * fn int8_chunk_<N> of simptensor/benchmarks/bench_int8_matmul_parallel.sl:5-73
+ * (typedef ChunkFunc, bench_int8_parallel_runner.cpp:13-16, looked up at :122):
+ * C rows [row_start, row_start + N/8) = A rows [row_start, row_start + N/8) x B,
+ * all N x N row-major in rank-1 arrays.  Returns 0, or a negative SIMP_RT_E*
+ * status (the program always returns 0).  Safe to call from several host
+ * threads on disjoint rows, as that runner does. */
+#define SIMP_RT_INT8_CHUNK(N)                                                                   \
+  int32_t int8_chunk_##N(int8_t *A_alloc, int8_t *A, int64_t A_off, int64_t A_size,             \
+                         int64_t A_stride, int8_t *B_alloc, int8_t *B, int64_t B_off,            \
+                         int64_t B_size, int64_t B_stride, int32_t *C_alloc, int32_t *C,         \
+                         int64_t C_off, int64_t C_size, int64_t C_stride, int64_t row_start)
+SIMP_RT_INT8_CHUNK(256);
+SIMP_RT_INT8_CHUNK(512);
+SIMP_RT_INT8_CHUNK(768);
+SIMP_RT_INT8_CHUNK(1024);
+SIMP_RT_INT8_CHUNK(2048);
 
 /* ----------------------------------------------------------------- W4 -- */
 

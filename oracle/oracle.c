@@ -359,6 +359,37 @@ void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
   }
 }
 
+void orc_matmul_quant_f5_refidx(const uint8_t *qw, const float *scales, const float *zeros,
+                                const float *in, float *out, int64_t rows, int64_t cols,
+                                int64_t gs, int64_t off) {
+  int64_t ngroups = cols / gs;                           /* :3929 numGroups = cols / gs */
+  for (int64_t i = 0; i < rows; i++) {
+    int64_t row_off = i * cols;                          /* :3919 rowOffset */
+    out[i] = 0.0f;                                       /* :3922 */
+    for (int64_t g = 0; g < ngroups; g++) {
+      int64_t gidx = row_off / gs + g;                   /* :3936-3937, offset not added */
+      float s = scales[gidx], z = zeros[gidx];
+      float acc = 0.0f;
+      for (int64_t t = 0; t < 8; t++) {                  /* :3942 numTiles = 8 */
+        float tile[16];
+        int64_t k0 = g * gs + t * 16;                    /* :3947-3949 kStart */
+        for (int j = 0; j < 16; j++) {                   /* :3953-3982, unmasked loads */
+          int64_t widx = off + row_off + k0 + j;
+          uint32_t q = 0;
+          if (k0 + j < cols) {  /* the reference loads past the row here; the value is unused */
+            uint8_t byte = qw[widx >> 1];
+            q = (widx & 1) ? (uint32_t)(byte >> 4) & 15u : (uint32_t)byte & 15u;
+          }
+          tile[j] = (float)q * s + z;
+        }
+        for (int j = 0; j < 16; j++)                     /* :3985-4003, k < cols */
+          if (k0 + j < cols) acc = acc + tile[j] * in[k0 + j];
+      }
+      out[i] = out[i] + acc;                             /* :4007-4010 */
+    }
+  }
+}
+
 void orc_quantize_f5(const float *w, int64_t total, int64_t gs, uint8_t *qw,
                      float *scales, float *zeros) {
   int64_t ng = (total + gs - 1) / gs;

@@ -129,6 +129,18 @@ void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
                          const float *zeros, const float *in, float *out,
                          int64_t rows, int64_t cols, int64_t gs, int64_t off);
 
+/* MatMulQuantOpLowering exactly as the reference emits it
+ * (src/mlir/lowering/ConvertSimpToMemRef.cpp:3906-4011), defects included:
+ * the scale/zero index is (i*cols)/gs + g without the weight offset, and every
+ * group runs a fixed 8 tiles of 16 weights from g*gs, so for gs < 128 the tiles
+ * of neighbouring groups overlap (weights k with k < cols only; each is
+ * dequantised with the scale of the group whose loop reads it).  Used by tests
+ * to show where orc_matmul_quant_f5 (and the GPU) differ from the reference:
+ * equal for off = 0 and gs = 128, otherwise not. */
+void orc_matmul_quant_f5_refidx(const uint8_t *qw, const float *scales, const float *zeros,
+                                const float *in, float *out, int64_t rows, int64_t cols,
+                                int64_t gs, int64_t off);
+
 /* Reference quantizer for F5 (examples/llama2/bench_llama_quant.cpp:51-93):
  * per flat group, scale = max((max-min)/15, 1e-8), zero = min,
  * q = clamp(round((w-min)/scale), 0, 15). */

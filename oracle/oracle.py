@@ -3,7 +3,10 @@
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker.  Nothing on the product path
 imports it.  The optional in-place reference build (oracle/_ref/libsimpref.so,
-only where the SimpLang sources are mounted) is exposed as ``ref`` (or None).
+only where the SimpLang sources are mounted in this container) is loaded only on
+request, by ``load_ref()`` (None when it is not built).  It is listed in
+.gpurunignore: it never travels to the GPU box, and no GPU test, smoke() or
+bench.py loads it.
 """
 from __future__ import annotations
 
@@ -20,7 +23,7 @@ REF_VNNI_TEST = os.path.join(HERE, "_ref", "test_vnni_correctness")
 if not os.path.exists(LIB):
     raise ImportError(f"{LIB} not built (make -C oracle)")
 _o = C.CDLL(LIB)
-ref = C.CDLL(REF_LIB) if os.path.exists(REF_LIB) else None
+_ref = None
 
 _P, _I, _F = C.c_void_p, C.c_int64, C.c_float
 
@@ -162,14 +165,21 @@ class LlamaQuantOracle:
         return logits
 
 
-if ref is not None:
-    for n in ("ref_scalar_vpdpbusd", "ref_hw_vpdpbusd"):
-        getattr(ref, n).argtypes = [_P, _P, _P, _P]
-    for n in (64, 128, 256, 512, 1024, 2048):
-        getattr(ref, f"ref_vnni_matmul_{n}").argtypes = [_P, _P, _P]
-    for n in (32, 64, 128):
-        getattr(ref, f"ref_scalar_int4_{n}").restype = C.c_int32
-        getattr(ref, f"ref_packed_int4_{n}").restype = C.c_int32
+def load_ref():
+    """The reference's own kernels compiled in place (oracle/Makefile target
+    ``ref``), or None where they are not built.  Loaded on first use only."""
+    global _ref
+    if _ref is None and os.path.exists(REF_LIB):
+        r = C.CDLL(REF_LIB)
+        for n in ("ref_scalar_vpdpbusd", "ref_hw_vpdpbusd"):
+            getattr(r, n).argtypes = [_P, _P, _P, _P]
+        for n in (64, 128, 256, 512, 1024, 2048):
+            getattr(r, f"ref_vnni_matmul_{n}").argtypes = [_P, _P, _P]
+        for n in (32, 64, 128):
+            getattr(r, f"ref_scalar_int4_{n}").restype = C.c_int32
+            getattr(r, f"ref_packed_int4_{n}").restype = C.c_int32
+        _ref = r
+    return _ref
 
 
 def _p(a: np.ndarray) -> int:

@@ -36,6 +36,8 @@ def _load():
 
 lib = _load()
 lib.simp_rt_last_error.restype = C.c_char_p
+lib.simp_rt_error_count.restype = C.c_int64
+lib.simp_rt_error_count.argtypes = []
 lib.simp_rt_get_stream.restype = C.c_void_p
 
 _P, _I = C.c_void_p, C.c_int64
@@ -97,12 +99,29 @@ def declared_symbols(header: str = HEADER) -> list[str]:
     names = set(re.findall(r"\b(simp_rt_\w+)\s*\(", text))
     # model-level exports keep the reference program's names
     names |= set(re.findall(r"^float\s+(\w+_forward)\s*\(", text, re.M))
+    # the int8 benchmark programs keep theirs too
+    names |= set(re.findall(r"^int32_t\s+(benchmark_int8_matmul_\d+)\s*\(", text, re.M))
+    names |= {f"int8_chunk_{n}" for n in re.findall(r"^SIMP_RT_INT8_CHUNK\((\d+)\);", text, re.M)}
     return sorted(names)
 
 
 def _check(fn: str, rc: int):
     if rc != 0:
         raise SimpRTError(fn, rc, lib.simp_rt_last_error().decode())
+
+
+def last_error() -> str:
+    """The calling thread's last error message ('' after a model-level export
+    that succeeded)."""
+    return lib.simp_rt_last_error().decode()
+
+
+def _check_float(fn: str, errors_before: int, r: float) -> float:
+    """Model-level exports return a float (NaN on error): an error is told from
+    a NaN of the arithmetic by the thread's error count."""
+    if lib.simp_rt_error_count() != errors_before:
+        raise SimpRTError(fn, -1, lib.simp_rt_last_error().decode())
+    return r
 
 
 # ------------------------------------------------------------------ operands
@@ -230,13 +249,10 @@ def stories110M_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_h
     args = []
     for name in STORIES_ARRAYS:
         args += desc1(arrays[name])
+    n0 = lib.simp_rt_error_count()
     r = lib.stories110M_forward(*args, token, pos, dim, hidden_dim, n_layers, n_heads,
                                 n_kv_heads, vocab_size, seq_len)
-    if r != r:
-        msg = lib.simp_rt_last_error().decode()
-        if msg:
-            raise SimpRTError("stories110M_forward", -1, msg)
-    return r
+    return _check_float("stories110M_forward", n0, r)
 
 
 QUANT_ARRAYS = ("token_emb", "rms_att_w", "rms_ffn_w", "rms_final_w", "wcls", "qweights",
@@ -252,13 +268,10 @@ def llama2_quant_forward(arrays: dict, token, pos, dim, hidden_dim, n_layers, n_
     args = []
     for name in QUANT_ARRAYS:
         args += desc1(arrays[name])
+    n0 = lib.simp_rt_error_count()
     r = lib.llama2_quant_forward(*args, token, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
                                  vocab_size, seq_len, group_size, *offsets)
-    if r != r:
-        msg = lib.simp_rt_last_error().decode()
-        if msg:
-            raise SimpRTError("llama2_quant_forward", -1, msg)
-    return r
+    return _check_float("llama2_quant_forward", n0, r)
 
 
 LLAMA32_ARRAYS = ("x_i8", "rms_att_w", "rms_ffn_w", "rms_final_w", "wq_t", "wk_t", "wv_t",
@@ -271,15 +284,14 @@ def llama32_forward(arrays: dict, pos, dim, hidden_dim, n_layers, n_heads, n_kv_
     """``llama32_forward`` of examples/llama2/llama32_1b_int8_tensor.sl, called as
     bench_llama32_1b_int8.cpp calls it: ``arrays`` maps the program's parameter
     names (LLAMA32_ARRAYS) to 1-D arrays (i8 / f32 / i32).  Returns logits[0]
-    (NaN on error, with the message in simp_rt_last_error)."""
+    (raises SimpRTError when the call reports an error)."""
     args = []
     for name in LLAMA32_ARRAYS:
         args += desc1(arrays[name])
+    n0 = lib.simp_rt_error_count()
     r = lib.llama32_forward(*args, pos, dim, hidden_dim, n_layers, n_heads, n_kv_heads,
                             vocab_size, max_seq_len, head_dim)
-    if r != r:
-        raise SimpRTError("llama32_forward", -1, lib.simp_rt_last_error().decode())
-    return r
+    return _check_float("llama32_forward", n0, r)
 
 
 class Llama32Program:
@@ -298,10 +310,35 @@ class Llama32Program:
                       head_dim)
 
     def __call__(self, pos) -> float:
+        n0 = lib.simp_rt_error_count()
         r = lib.llama32_forward(*self._args, pos, *self._dims)
-        if r != r:
-            raise SimpRTError("llama32_forward", -1, lib.simp_rt_last_error().decode())
-        return r
+        return _check_float("llama32_forward", n0, r)
+
+
+BENCH_INT8_SIZES = (32, 64, 128, 256, 384, 512, 768, 1024, 2048, 4096)
+CHUNK_INT8_SIZES = (256, 512, 768, 1024, 2048)
+for _n in BENCH_INT8_SIZES:
+    _sig(f"benchmark_int8_matmul_{_n}", [])
+for _n in CHUNK_INT8_SIZES:
+    _sig(f"int8_chunk_{_n}", [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64] * 3
+         + [C.c_int64])
+
+
+def benchmark_int8_matmul(n: int) -> int:
+    """``benchmark_int8_matmul_<n>()`` of bench_int8_matmul.sl: the recipe
+    inputs' s8 x s8 product, returned as the i32 wraparound checksum of C."""
+    n0 = lib.simp_rt_error_count()
+    r = getattr(lib, f"benchmark_int8_matmul_{n}")()
+    if lib.simp_rt_error_count() != n0:
+        raise SimpRTError(f"benchmark_int8_matmul_{n}", -1, last_error())
+    return r
+
+
+def int8_chunk(n: int, a, b, c, row_start: int) -> None:
+    """``int8_chunk_<n>(A, B, C, row_start)`` of bench_int8_matmul_parallel.sl:
+    rows [row_start, row_start + n/8) of C = A x B for flat n*n arrays."""
+    fn = f"int8_chunk_{n}"
+    _check(fn, getattr(lib, fn)(*desc1(a), *desc1(b), *desc1(c), row_start))
 
 
 def forward_cache_clear() -> None:

@@ -1194,26 +1194,41 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
 namespace simp {
 namespace {
 
-// One engine instance per (weights, config) seen by a model-level export.
-// Weights that are device memory are used in place; host weights are mirrored
-// once as immutable registered ranges (a reference host passes the same
-// std::vector buffers on every call and never writes them).
+// One engine instance per (weights, config) seen by a model-level export:
+// the engine, the device copies of host weights and the KV continuity state
+// (export_state.hip).  At most kMaxEntries engines are kept; the least recently
+// used one is freed to make room (a host that frees its model and loads
+// another at new addresses leaves an entry that is never called again).
 struct ForwardEntry {
   simp_rt_llama *model = nullptr;
-  std::vector<const void *> registered;
+  ExportWeights weights;
+  KvState kv;
+  uint64_t last_use = 0;
 };
+constexpr size_t kMaxEntries = 4;
 std::mutex g_fwd_mu;
 std::map<std::vector<int64_t>, ForwardEntry> g_fwd;
+uint64_t g_fwd_clock = 0;
+
+void forward_entry_free(ForwardEntry &e) {
+  if (e.model) simp_rt_llama_destroy(e.model);
+  e.model = nullptr;
+  e.weights.release();
+}
 
 }  // namespace
 
-int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *name,
-                  std::vector<const void *> &registered) {
-  if (device_view(p, bytes, dev, name) == SIMP_RT_OK) return SIMP_RT_OK;
-  int rc = simp_rt_register(p, (int64_t)bytes, SIMP_RT_REG_IMMUTABLE);
-  if (rc) return rc;
-  registered.push_back(p);
-  return device_view(p, bytes, dev, name);
+// Frees the least recently used entry of `map` while it holds `cap` or more.
+template <class Map, class Free>
+void evict_lru(Map &map, size_t cap, Free free_entry) {
+  while (map.size() >= cap) {
+    auto old = map.begin();
+    for (auto it = map.begin(); it != map.end(); ++it)
+      if (it->second.last_use < old->second.last_use) old = it;
+    (void)hipDeviceSynchronize();
+    free_entry(old->second);
+    map.erase(old);
+  }
 }
 
 }  // namespace simp
@@ -1232,6 +1247,7 @@ float stories110M_forward(
     SIMP_DESC_F32(value_cache), int64_t token, int64_t pos, int64_t dim, int64_t hidden_dim,
     int64_t n_layers, int64_t n_heads, int64_t n_kv_heads, int64_t vocab_size, int64_t seq_len) {
   const float nan = std::numeric_limits<float>::quiet_NaN();
+  clear_error();
   // the scratch activations of the program (x ... att_soft) are not used: the
   // engine keeps its own device buffers and leaves the caller's unchanged
   (void)x; (void)xb; (void)xb2; (void)hb; (void)hb_silu; (void)q; (void)k; (void)v; (void)att;
@@ -1287,42 +1303,57 @@ float stories110M_forward(
   for (int i = 0; i < 12; i++) wp[i] = ins[i].p + ins[i].off;
   std::vector<int64_t> key = {dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len};
   for (int i = 0; i < 12; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
-  simp_rt_llama *model = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(g_fwd_mu);
-    ForwardEntry &e = g_fwd[key];
-    if (!e.model) {
-      const void *d[12];
-      for (int i = 0; i < 12; i++)
-        if (dev_or_mirror(wp[i], 4 * (size_t)ins[i].need, &d[i], ins[i].name, e.registered))
-          return nan;
-      simp_rt_llama_weights w{};
-      w.token_embedding = (const float *)d[0];
-      w.rms_att = (const float *)d[1];
-      w.wq = (const float *)d[2];
-      w.wk = (const float *)d[3];
-      w.wv = (const float *)d[4];
-      w.wo = (const float *)d[5];
-      w.rms_ffn = (const float *)d[6];
-      w.w1 = (const float *)d[7];
-      w.w2 = (const float *)d[8];
-      w.w3 = (const float *)d[9];
-      w.rms_final = (const float *)d[10];
-      w.wcls = (const float *)d[11];
-      if (simp_rt_llama_create(&cfg, &w, &e.model)) {
-        e.model = nullptr;
+  // One caller at a time per process: the entry's engine, copies and KV state
+  // are shared by every thread that passes these arrays.
+  std::lock_guard<std::mutex> lk(g_fwd_mu);
+  auto it = g_fwd.find(key);
+  if (it == g_fwd.end()) {
+    evict_lru(g_fwd, kMaxEntries, forward_entry_free);
+    it = g_fwd.emplace(key, ForwardEntry{}).first;
+    ForwardEntry &e = it->second;
+    const void *d[12];
+    for (int i = 0; i < 12; i++)
+      if (e.weights.bind(wp[i], 4 * (size_t)ins[i].need, &d[i], ins[i].name)) {
+        forward_entry_free(e);
+        g_fwd.erase(it);
         return nan;
       }
+    simp_rt_llama_weights w{};
+    w.token_embedding = (const float *)d[0];
+    w.rms_att = (const float *)d[1];
+    w.wq = (const float *)d[2];
+    w.wk = (const float *)d[3];
+    w.wv = (const float *)d[4];
+    w.wo = (const float *)d[5];
+    w.rms_ffn = (const float *)d[6];
+    w.w1 = (const float *)d[7];
+    w.w2 = (const float *)d[8];
+    w.w3 = (const float *)d[9];
+    w.rms_final = (const float *)d[10];
+    w.wcls = (const float *)d[11];
+    if (simp_rt_llama_create(&cfg, &w, &e.model)) {
+      e.model = nullptr;
+      forward_entry_free(e);
+      g_fwd.erase(it);
+      return nan;
     }
-    model = e.model;
   }
-  float *lg = logits + logits_off;
-  if (simp_rt_llama_forward(model, token, pos, lg)) return nan;
-  // the step's K and V rows at pos go back into the caller's caches
-  // ([n_layers, seq_len, kv_dim], stories110M.sl:115-121)
-  auto *m = (LlamaModel *)model;
+  ForwardEntry &ent = it->second;
+  ent.last_use = ++g_fwd_clock;
+  auto *m = (LlamaModel *)ent.model;
+  m->stream = cur_stream();
   const size_t pitch = 4 * (size_t)(seq_len * kvd), row = 4 * (size_t)kvd;
   const size_t at = (size_t)(pos * kvd);
+  // the program reads the caches' rows [0, pos) and every weight on each call
+  bool restart = false;
+  if (ent.kv.prepare(pos, key_cache + key_cache_off, value_cache + value_cache_off, m->kcache,
+                     m->vcache, row, pitch, L, m->stream, &restart) ||
+      ent.weights.verify(restart))
+    return nan;
+  float *lg = logits + logits_off;
+  if (simp_rt_llama_forward(ent.model, token, pos, lg)) return nan;
+  // the step's K and V rows at pos go back into the caller's caches
+  // ([n_layers, seq_len, kv_dim], stories110M.sl:115-121)
   hipError_t e1 = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kcache + at, pitch, row,
                                    (size_t)L, hipMemcpyDefault, m->stream);
   hipError_t e2 = e1 == hipSuccess
@@ -1334,6 +1365,7 @@ float stories110M_forward(
     hip_fail(e2, "stories110M_forward: KV row copy");
     return nan;
   }
+  ent.kv.done(pos);
   // logits are on the host now (simp_rt_llama_forward synchronised)
   float l0 = nan;
   if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
@@ -1377,7 +1409,9 @@ struct QuantModel {
   float *x = nullptr, *xb = nullptr, *xb2 = nullptr, *qkv = nullptr, *hb = nullptr, *hb2 = nullptr,
         *logits = nullptr, *kc = nullptr, *vc = nullptr, *attn_ws = nullptr;
   StepState *state = nullptr;
-  std::vector<const void *> registered;
+  ExportWeights weights;
+  KvState kv;
+  uint64_t last_use = 0;
 };
 
 void quant_free(QuantModel &m) {
@@ -1385,7 +1419,9 @@ void quant_free(QuantModel &m) {
                   (void *)m.hb2, (void *)m.logits, (void *)m.kc, (void *)m.vc, (void *)m.attn_ws,
                   (void *)m.state})
     if (p) (void)hipFree(p);
-  for (const void *p : m.registered) (void)simp_rt_unregister(p);
+  m.x = m.xb = m.xb2 = m.qkv = m.hb = m.hb2 = m.logits = m.kc = m.vc = m.attn_ws = nullptr;
+  m.state = nullptr;
+  m.weights.release();
 }
 
 int quant_alloc(QuantModel &m) {
@@ -1462,6 +1498,7 @@ float llama2_quant_forward(
     int64_t vocab_size, int64_t seq_len, int64_t group_size, int64_t wq_off, int64_t wk_off,
     int64_t wv_off, int64_t wo_off, int64_t w1_off, int64_t w2_off, int64_t w3_off) {
   const float nan = std::numeric_limits<float>::quiet_NaN();
+  clear_error();
   (void)x; (void)xb; (void)xb2; (void)q; (void)k; (void)v; (void)att; (void)att_soft; (void)hb;
   (void)hb_silu; (void)hb2;
   auto fail = [&](const char *msg) {
@@ -1515,38 +1552,44 @@ float llama2_quant_forward(
   for (int i = 0; i < 7; i++) key.push_back(offs[i]);
   for (int i = 0; i < 8; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
   hipStream_t st = cur_stream();
-  QuantModel *m = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(g_fwd_mu);
-    auto it = g_qfwd.find(key);
-    if (it == g_qfwd.end()) {
-      QuantModel nm;
-      nm.dim = dim; nm.hid = hidden_dim; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
-      nm.V = vocab_size; nm.seq = seq_len; nm.gs = group_size;
-      for (int i = 0; i < 7; i++) nm.off[i] = offs[i];
-      nm.kv_dim = (int)kvd;
-      nm.hs = (int)hs;
-      const void *d[8];
-      for (int i = 0; i < 8; i++)
-        if (dev_or_mirror(wp[i], esz[i] * (size_t)ins[i].need, &d[i], ins[i].name, nm.registered)) {
-          quant_free(nm);
-          return nan;
-        }
+  std::lock_guard<std::mutex> lk(g_fwd_mu);
+  auto it = g_qfwd.find(key);
+  if (it == g_qfwd.end()) {
+    evict_lru(g_qfwd, kMaxEntries, quant_free);
+    it = g_qfwd.emplace(key, QuantModel{}).first;
+    QuantModel &nm = it->second;
+    nm.dim = dim; nm.hid = hidden_dim; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
+    nm.V = vocab_size; nm.seq = seq_len; nm.gs = group_size;
+    for (int i = 0; i < 7; i++) nm.off[i] = offs[i];
+    nm.kv_dim = (int)kvd;
+    nm.hs = (int)hs;
+    const void *d[8];
+    bool ok = true;
+    for (int i = 0; i < 8 && ok; i++)
+      ok = nm.weights.bind(wp[i], esz[i] * (size_t)ins[i].need, &d[i], ins[i].name) == SIMP_RT_OK;
+    if (ok) {
       nm.emb = (const float *)d[0]; nm.rms_att = (const float *)d[1]; nm.rms_ffn = (const float *)d[2];
       nm.rms_final = (const float *)d[3]; nm.wcls = (const float *)d[4];
       nm.qw = (const uint8_t *)d[5]; nm.scales = (const float *)d[6]; nm.zeros = (const float *)d[7];
-      if (quant_alloc(nm)) {
-        quant_free(nm);
-        return nan;
-      }
-      it = g_qfwd.emplace(key, std::move(nm)).first;
+      ok = quant_alloc(nm) == SIMP_RT_OK;
     }
-    m = &it->second;
+    if (!ok) {
+      quant_free(nm);
+      g_qfwd.erase(it);
+      return nan;
+    }
   }
-  if (quant_step(*m, token, pos, st)) return nan;
-  float *lg = logits + logits_off;
+  QuantModel *m = &it->second;
+  m->last_use = ++g_fwd_clock;
   const size_t pitch = 4 * (size_t)(seq_len * kvd), row = 4 * (size_t)kvd;
   const size_t at = (size_t)(pos * kvd);
+  bool restart = false;
+  if (m->kv.prepare(pos, key_cache + key_cache_off, value_cache + value_cache_off, m->kc, m->vc,
+                    row, pitch, L, st, &restart) ||
+      m->weights.verify(restart))
+    return nan;
+  if (quant_step(*m, token, pos, st)) return nan;
+  float *lg = logits + logits_off;
   hipError_t e = hipMemcpyAsync(lg, m->logits, 4 * (size_t)vocab_size, hipMemcpyDefault, st);
   if (e == hipSuccess)
     e = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kc + at, pitch, row, (size_t)L,
@@ -1559,6 +1602,7 @@ float llama2_quant_forward(
     hip_fail(e, "llama2_quant_forward: result copies");
     return nan;
   }
+  m->kv.done(pos);
   float l0 = nan;
   if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
   return l0;
@@ -1573,10 +1617,7 @@ extern "C" {
 
 int32_t simp_rt_forward_cache_clear(void) {
   std::lock_guard<std::mutex> lk(g_fwd_mu);
-  for (auto &kv : g_fwd) {
-    if (kv.second.model) simp_rt_llama_destroy(kv.second.model);
-    for (const void *p : kv.second.registered) (void)simp_rt_unregister(p);
-  }
+  for (auto &kv : g_fwd) forward_entry_free(kv.second);
   g_fwd.clear();
   for (auto &kv : g_qfwd) {
     (void)hipDeviceSynchronize();

@@ -352,14 +352,19 @@ struct L32Model {
   float *x = nullptr, *xb = nullptr, *logits = nullptr;
   int8_t *xi = nullptr, *xq = nullptr, *hq = nullptr, *kc = nullptr, *vc = nullptr;
   int32_t *q = nullptr, *attn = nullptr;
-  std::vector<const void *> registered;
+  ExportWeights weights;
+  KvState kvs;
+  uint64_t last_use = 0;
 };
 
 void l32_free(L32Model &m) {
   for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.logits, (void *)m.xi, (void *)m.xq,
                   (void *)m.hq, (void *)m.kc, (void *)m.vc, (void *)m.q, (void *)m.attn})
     if (p) (void)hipFree(p);
-  for (const void *p : m.registered) (void)simp_rt_unregister(p);
+  m.x = m.xb = m.logits = nullptr;
+  m.xi = m.xq = m.hq = m.kc = m.vc = nullptr;
+  m.q = m.attn = nullptr;
+  m.weights.release();
 }
 
 int l32_alloc(L32Model &m) {
@@ -456,6 +461,8 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
 
 std::mutex g_l32_mu;
 std::map<std::vector<int64_t>, L32Model> g_l32;
+uint64_t g_l32_clock = 0;
+constexpr size_t kMaxL32Entries = 4;
 
 }  // namespace
 
@@ -486,6 +493,7 @@ float llama32_forward(
     int64_t dim, int64_t hidden_dim, int64_t n_layers, int64_t n_heads, int64_t n_kv_heads,
     int64_t vocab_size, int64_t max_seq_len, int64_t head_dim) {
   const float nan = std::numeric_limits<float>::quiet_NaN();
+  clear_error();
   (void)xb_i8; (void)att_scores; (void)att_probs; (void)attn_out; (void)ffn_hb;
   (void)xb_i8_alloc; (void)att_scores_alloc; (void)att_probs_alloc; (void)attn_out_alloc;
   (void)ffn_hb_alloc;
@@ -538,46 +546,62 @@ float llama32_forward(
                               max_seq_len, head_dim};
   for (int i = 0; i < NW; i++) key.push_back((int64_t)(uintptr_t)wp[i]);
   hipStream_t st = cur_stream();
-  L32Model *m = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(g_l32_mu);
-    auto it = g_l32.find(key);
-    if (it == g_l32.end()) {
-      L32Model nm;
-      nm.dim = D; nm.hid = H; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
-      nm.V = vocab_size; nm.S = max_seq_len; nm.hs = head_dim; nm.kv = kv;
-      const void *d[NW];
-      for (int i = 0; i < NW; i++)
-        if (dev_or_mirror(wp[i], ins[i].esz * (size_t)ins[i].need, &d[i], ins[i].name,
-                          nm.registered)) {
-          l32_free(nm);
-          return nan;
-        }
+  // one caller at a time: the engine, its copies and its KV state are shared
+  std::lock_guard<std::mutex> lk(g_l32_mu);
+  auto it = g_l32.find(key);
+  if (it == g_l32.end()) {
+    while (g_l32.size() >= kMaxL32Entries) {  // free the least recently used engine
+      auto old = g_l32.begin();
+      for (auto j = g_l32.begin(); j != g_l32.end(); ++j)
+        if (j->second.last_use < old->second.last_use) old = j;
+      (void)hipDeviceSynchronize();
+      l32_free(old->second);
+      g_l32.erase(old);
+    }
+    it = g_l32.emplace(key, L32Model{}).first;
+    L32Model &nm = it->second;
+    nm.dim = D; nm.hid = H; nm.L = L; nm.nh = n_heads; nm.nkv = n_kv_heads;
+    nm.V = vocab_size; nm.S = max_seq_len; nm.hs = head_dim; nm.kv = kv;
+    const void *d[NW];
+    const char *err = nullptr;
+    bool ok = true;
+    for (int i = 0; i < NW && ok; i++)
+      ok = nm.weights.bind(wp[i], ins[i].esz * (size_t)ins[i].need, &d[i], ins[i].name) ==
+           SIMP_RT_OK;
+    if (ok) {
       nm.rms_att = (const float *)d[0]; nm.rms_ffn = (const float *)d[1];
       nm.rms_final = (const float *)d[2]; nm.wcls = (const float *)d[3];
       nm.wq = (const int8_t *)d[4]; nm.wk = (const int8_t *)d[5]; nm.wv = (const int8_t *)d[6];
       nm.wo = (const int8_t *)d[7]; nm.w1 = (const int8_t *)d[8]; nm.w2 = (const int8_t *)d[9];
       nm.w3 = (const int8_t *)d[10];
-      for (int i = 4; i < NW; i++)
+      for (int i = 4; i < NW && ok; i++)
         if ((uintptr_t)d[i] & 15) {
-          l32_free(nm);
-          return fail("int8 weight arrays must start 16-byte aligned (offset included)");
+          ok = false;
+          err = "int8 weight arrays must start 16-byte aligned (offset included)";
         }
-      if (l32_alloc(nm)) {
-        l32_free(nm);
-        return nan;
-      }
-      it = g_l32.emplace(key, std::move(nm)).first;
     }
-    m = &it->second;
+    if (ok) ok = l32_alloc(nm) == SIMP_RT_OK;
+    if (!ok) {
+      l32_free(nm);
+      g_l32.erase(it);
+      return err ? fail(err) : nan;
+    }
   }
+  L32Model *m = &it->second;
+  m->last_use = ++g_l32_clock;
+  const size_t pitch = (size_t)(max_seq_len * kv), row = (size_t)kv, at = (size_t)(pos * kv);
+  // the program reads the caches' rows [0, pos) and every weight on each call
+  bool restart = false;
+  if (m->kvs.prepare(pos, k_cache + k_cache_off, v_cache + v_cache_off, m->kc, m->vc, row, pitch,
+                     L, st, &restart) ||
+      m->weights.verify(restart))
+    return nan;
   hipError_t e = hipMemcpyAsync(m->xi, x_i8 + x_i8_off, (size_t)D, hipMemcpyDefault, st);
   if (e != hipSuccess) {
     hip_fail(e, "llama32_forward: input copy");
     return nan;
   }
   if (l32_step(*m, pos, st)) return nan;
-  const size_t pitch = (size_t)(max_seq_len * kv), row = (size_t)kv, at = (size_t)(pos * kv);
   e = hipMemcpyAsync(logits + logits_off, m->logits, 4 * (size_t)vocab_size, hipMemcpyDefault, st);
   if (e == hipSuccess)
     e = hipMemcpyAsync(x_fp32 + x_fp32_off, m->x, 4 * (size_t)D, hipMemcpyDefault, st);
@@ -594,6 +618,7 @@ float llama32_forward(
     hip_fail(e, "llama32_forward: result copies");
     return nan;
   }
+  m->kvs.done(pos);
   float l0 = nan;
   if (hipMemcpy(&l0, logits + logits_off, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
   return l0;

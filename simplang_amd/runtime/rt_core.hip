@@ -21,6 +21,7 @@
 namespace simp {
 
 static thread_local std::string t_err;
+static thread_local int64_t t_err_count = 0;
 static thread_local hipStream_t t_stream = nullptr;
 
 int set_error(int code, const char *fmt, ...) {
@@ -30,8 +31,11 @@ int set_error(int code, const char *fmt, ...) {
   vsnprintf(buf, sizeof buf, fmt, ap);
   va_end(ap);
   t_err = buf;
+  t_err_count++;
   return code;
 }
+
+void clear_error() { t_err.clear(); }
 
 int hip_fail(hipError_t e, const char *what) {
   return set_error(SIMP_RT_EHIP, "%s failed: %s", what, hipGetErrorString(e));
@@ -142,16 +146,22 @@ static bool is_device_memory(const void *p) {
   return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-int device_view(const void *p, size_t bytes, const void **dev, const char *name) {
-  if (!p) return set_error(SIMP_RT_EINVAL, "%s: null pointer", name);
+bool try_device_view(const void *p, size_t bytes, const void **dev) {
+  if (!p) return false;
   if (is_device_memory(p)) {
     *dev = p;
-    return SIMP_RT_OK;
+    return true;
   }
   if (void *m = find_mirror(p, bytes, nullptr)) {
     *dev = m;
-    return SIMP_RT_OK;
+    return true;
   }
+  return false;
+}
+
+int device_view(const void *p, size_t bytes, const void **dev, const char *name) {
+  if (!p) return set_error(SIMP_RT_EINVAL, "%s: null pointer", name);
+  if (try_device_view(p, bytes, dev)) return SIMP_RT_OK;
   return set_error(SIMP_RT_EINVAL,
                    "%s: must be device memory or inside a simp_rt_register'd range", name);
 }
@@ -188,7 +198,10 @@ int Operand::bind(const void *p, size_t bytes, Dir dir, const char *name) {
                      hipGetErrorString(e));
   }
   staged_ = true;
-  if (dir & kIn) {
+  // Outputs are staged in too: a strided view's span holds bytes between its
+  // rows (or batches) that the kernels never write, and commit() copies the
+  // whole span back, so those bytes must return to the host as they were.
+  if (dir & (kIn | kOut)) {
     e = hipMemcpyAsync(dev_, p, bytes, hipMemcpyHostToDevice, cur_stream());
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(stage in)");
   }
@@ -345,6 +358,8 @@ int32_t simp_rt_timing_query(const char *kernel, double *total_ms, int64_t *laun
 }
 
 const char *simp_rt_last_error(void) { return t_err.c_str(); }
+
+int64_t simp_rt_error_count(void) { return t_err_count; }
 
 int32_t simp_rt_version(void) { return SIMP_RT_ABI_VERSION; }
 

@@ -14,6 +14,9 @@ namespace simp {
 
 // Thread-local error text behind simp_rt_last_error().
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Empties the message (the model-level exports call it first: their NaN return
+// cannot carry a status, so an old message must not be read as theirs).
+void clear_error();
 int hip_fail(hipError_t e, const char *what);
 
 #define SIMP_HIP(call)                                         \
@@ -58,12 +61,51 @@ class Operand {
 // Device address of a caller range that must already be device-resident
 // (device memory, or inside a simp_rt_register'd range); no staging.
 int device_view(const void *p, size_t bytes, const void **dev, const char *name);
+// The same lookup without an error: false when p is plain host memory.
+bool try_device_view(const void *p, size_t bytes, const void **dev);
 
-// Device address of a model-level export's weight array: device memory is used
-// in place; host memory is registered once as an immutable mirror (appended
-// to `registered`, for simp_rt_unregister when the export's engine is freed).
-int dev_or_mirror(const void *p, size_t bytes, const void **dev, const char *name,
-                  std::vector<const void *> &registered);
+// Weight arrays of one model-level export entry (export_state.hip).  Device
+// memory and simp_rt_register'd ranges are used in place; any other host array
+// gets a private device copy with a fingerprint per 64 KiB chunk, re-checked by
+// verify(): every chunk when `full` (a call that starts a sequence), else the
+// next chunk of each array in rotation (a mismatch re-checks that whole
+// array); changed chunks are uploaded again.  The caller must not have kernels
+// reading the copies in flight (the exports synchronise before returning).
+class ExportWeights {
+ public:
+  int bind(const void *p, size_t bytes, const void **dev, const char *name);
+  int verify(bool full);
+  void release();
+  int64_t refreshed_chunks() const { return refreshed_; }
+
+ private:
+  struct Range {
+    const char *host = nullptr;
+    size_t bytes = 0;
+    char *dev = nullptr;
+    std::vector<uint64_t> hash;
+    size_t cursor = 0;
+  };
+  int refresh(Range &r, bool all, size_t first);
+  std::vector<Range> ranges_;
+  bool fresh_ = true;
+  int64_t refreshed_ = 0;
+};
+
+// Position continuity of a model-level export's KV cache.  prepare() is called
+// before a step at `pos`: unless the call continues the previous one (pos is
+// the previous pos + 1 with the same caller cache arrays) it copies the
+// caller's rows [0, pos) of every layer into the engine's cache (layout
+// [layers, seq_len, kv_dim], `pitch_bytes` per layer) and reports a restart.
+// done() records a completed step.
+struct KvState {
+  int64_t next_pos = -1;
+  const void *k = nullptr, *v = nullptr;
+  int prepare(int64_t pos, const void *caller_k, const void *caller_v, void *dev_k, void *dev_v,
+              size_t row_bytes, size_t pitch_bytes, int64_t layers, hipStream_t st,
+              bool *restart);
+  void done(int64_t pos) { next_pos = pos + 1; }
+};
 
 // Frees the engines of llama32_forward (part of simp_rt_forward_cache_clear).
 void l32_cache_clear();

@@ -3,11 +3,13 @@ reference benchmark's deterministic inputs
     val = ((i*N + j) % 127) - 64;  A[i,j] = B[j,i] = val
 (simptensor/benchmarks/bench_int8_matmul_runner.cpp:33-64).
 
-Sizes up to 2048 come from the reference's own vnni_matmul_single_thread<N>
-(simptensor/benchmarks/bench_int8_matmul_multicore.cpp:39-89), compiled in
-place by `make -C oracle ref`.  4096 (the largest size bench_int8_matmul.sl
-defines) comes from the oracle's VNNI restatement, which equals the reference
-kernel bit for bit at every size both cover.  Run here, where the reference
+Sizes 64..2048 that the reference's own vnni_matmul_single_thread<N>
+(simptensor/benchmarks/bench_int8_matmul_multicore.cpp:39-89) is instantiated
+for come from it, compiled in place by `make -C oracle ref`.  The other sizes
+benchmark_int8_matmul_<N> defines (32, 384, 768, 4096:
+simptensor/benchmarks/bench_int8_matmul.sl:11-335) come from the oracle's VNNI
+restatement, which equals the reference kernel bit for bit at every size both
+cover.  Run here, where the reference
 is mounted:  python tests/golden/make_int8_recipe_checksums.py
 """
 import json
@@ -22,12 +24,13 @@ import oracle  # noqa: E402
 
 out = {"recipe": "val=((i*N+j)%127)-64; A[i,j]=B[j,i]=val; checksum = i32 wraparound sum of C",
        "checksums": {}, "source": {}}
-for n in (64, 128, 256, 512, 1024, 2048, 4096):
+ref = oracle.load_ref()
+for n in (32, 64, 128, 256, 384, 512, 768, 1024, 2048, 4096):
     a, b = oracle.recipe_inputs(n)
-    if oracle.ref is not None and n <= 2048:
+    if ref is not None and n in (64, 128, 256, 512, 1024, 2048):
         bt = np.ascontiguousarray(b.T)
         c = np.zeros((n, n), np.int32)
-        getattr(oracle.ref, f"ref_vnni_matmul_{n}")(a.ctypes.data, bt.ctypes.data, c.ctypes.data)
+        getattr(ref, f"ref_vnni_matmul_{n}")(a.ctypes.data, bt.ctypes.data, c.ctypes.data)
         src = "reference vnni_matmul_single_thread"
         c2, _ = oracle.matmul_i8_vnni(a, b, nthreads=8)
         assert (c2 == c).all(), n

@@ -218,3 +218,21 @@ def test_rejects(dev):
         sa.tensor_batch_matmul(torch.empty(2, 2, 2, dtype=torch.int32, device=dev),
                                torch.empty(2, 2, 2, dtype=torch.int32, device=dev),
                                torch.empty(2, 2, 2, dtype=torch.int32, device=dev))
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.int8])
+def test_batch_strided_views_host_arrays(dev, orc, dt):
+    """Padded rows and batch gaps with numpy host operands (staged): the bytes
+    of the output buffer outside the view keep their values."""
+    rng = np.random.default_rng(8)
+    bt, m, k, n = 3, 33, 80, 48
+    A = _rand(rng, (bt, m + 5, k + 16), dt)
+    B = _rand(rng, (bt + 1, k + 3, n + 16), dt)
+    odt = np.float32 if dt == np.float32 else np.int32
+    C = np.full((bt, m + 2, n + 32), 77, dtype=odt)
+    a, b, c = A[:, 2:2 + m, 16:16 + k], B[1:, :k, :n], C[:, 1:1 + m, 16:16 + n]
+    sa.tensor_batch_matmul(a, b, c)
+    want = orc.batch_matmul(np.ascontiguousarray(a), np.ascontiguousarray(b))
+    _check(np.ascontiguousarray(c), want, dt)
+    assert (C[:, 0] == 77).all() and (C[:, 1 + m:] == 77).all()
+    assert (C[:, :, :16] == 77).all() and (C[:, :, 16 + n:] == 77).all()

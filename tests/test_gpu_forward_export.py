@@ -172,3 +172,121 @@ def test_llama2_quant_forward_long_context(dev, orc, heads):
             got = arrays["logits"].astype(np.float64)
             assert np.abs(got - want).max() <= TOL * np.abs(want).max(), pos
     sa.forward_cache_clear()
+
+
+# ---------------------------------------------------------- caller state --
+# The compiled programs read every weight and the caches' rows [0, pos] from the
+# caller's arrays on every call.  The exports keep device copies, so they must
+# follow changes the caller makes between calls.
+
+def _stories_oracle(orc, w, arrays=None, upto=0):
+    o = orc.LlamaOracle(dict(CFG, eps=1e-5, rope_theta=10000.0, weight_format=0), w)
+    if arrays is not None:      # start from the caller's cache rows [0, upto)
+        kv = CFG["dim"] * CFG["n_kv_heads"] // CFG["n_heads"]
+        for name, dst in (("key_cache", o.kc), ("value_cache", o.vc)):
+            src = arrays[name].reshape(CFG["n_layers"], CFG["seq_len"], kv)
+            dst.reshape(CFG["n_layers"], CFG["seq_len"], kv)[:, :upto] = src[:, :upto]
+    return o
+
+
+def _same(got, want):
+    got, want = got.astype(np.float64), want.astype(np.float64)
+    assert np.abs(got - want).max() <= TOL * np.abs(want).max()
+
+
+def test_stories110M_forward_weights_rewritten_in_place(dev, orc):
+    """Weights rewritten in place between calls (what a host that frees its
+    model and loads another into the same addresses does): the very next call,
+    mid-sequence, and a restart at pos 0 use the new values."""
+    sa.forward_cache_clear()
+    wa, arrays = _host_model(31)
+    wb, arrays_b = _host_model(32)
+    for pos, t in enumerate([4, 9, 16]):
+        sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+    for k in ("token_embedding_table", "rms_att_w", "rms_ffn_w", "rms_final_w", "wq", "wk",
+              "wv", "wo", "w1", "w2", "w3", "wcls"):
+        np.copyto(arrays[k], arrays_b[k])            # same addresses, new contents
+    o = _stories_oracle(orc, wb, arrays, upto=3)
+    print("[forward-export] rewritten weights, pos=3", flush=True)
+    sa.stories110M_forward(arrays, 25, 3, *_cfg_args())
+    _same(arrays["logits"], o.forward(25, 3))
+    o = _stories_oracle(orc, wb)
+    for pos, t in enumerate([7, 3]):
+        sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+        _same(arrays["logits"], o.forward(t, pos))
+    # one edited row of the classifier, then a new sequence (pos 0 re-checks
+    # every chunk of every array)
+    arrays["wcls"][:CFG["dim"]] *= 3.0
+    o = _stories_oracle(orc, {**wb, "wcls": arrays["wcls"].reshape(wb["wcls"].shape)})
+    for pos, t in enumerate([7, 3, 8]):
+        sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+        _same(arrays["logits"], o.forward(t, pos))
+    sa.forward_cache_clear()
+
+
+def test_stories110M_forward_jumps_and_host_filled_caches(dev, orc):
+    """A first call at pos 6 on caches the host filled, a jump back to pos 2,
+    and a jump forward: each reads the caller's cache rows [0, pos)."""
+    sa.forward_cache_clear()
+    w, arrays = _host_model(33)
+    toks = [11, 22, 33, 44, 55, 66, 77, 88, 99, 101]
+    full = _stories_oracle(orc, w)
+    for pos in range(6):
+        full.forward(toks[pos], pos)
+    arrays["key_cache"][:] = full.kc
+    arrays["value_cache"][:] = full.vc
+    for pos in (6, 2, 7, 9):
+        print(f"[forward-export] jump to pos={pos}", flush=True)
+        o = _stories_oracle(orc, w, arrays, upto=pos)
+        sa.stories110M_forward(arrays, toks[pos], pos, *_cfg_args())
+        _same(arrays["logits"], o.forward(toks[pos], pos))
+    sa.forward_cache_clear()
+
+
+def test_stories110M_forward_nan_is_not_an_error(dev, orc):
+    """A NaN the arithmetic produces comes back as NaN without an exception,
+    even after an earlier failed call left a message behind."""
+    sa.forward_cache_clear()
+    w, arrays = _host_model(34)
+    with pytest.raises(sa.SimpRTError):
+        sa.stories110M_forward(arrays, 0, CFG["seq_len"], *_cfg_args())   # pos out of range
+    arrays["token_embedding_table"][:CFG["dim"]] = np.nan                # token 0 embeds NaN
+    r = sa.stories110M_forward(arrays, 0, 0, *_cfg_args())
+    assert r != r and np.isnan(arrays["logits"]).all()
+    assert sa.last_error() == ""
+    sa.forward_cache_clear()
+
+
+def test_llama2_quant_forward_caller_state(dev, orc):
+    """llama2_quant_forward: rewritten weights and jumps with host-filled caches."""
+    sa.forward_cache_clear()
+    gs = 128
+    arrays, offs = _quant_model(orc, 41, gs)
+    arrays_b, _ = _quant_model(orc, 42, gs)
+    dims = tuple(QCFG[k] for k in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
+                                   "vocab_size", "seq_len"))
+    names = ("token_emb", "rms_att_w", "rms_ffn_w", "rms_final_w", "wcls", "scales", "zeros")
+    kv = QCFG["dim"] * QCFG["n_kv_heads"] // QCFG["n_heads"]
+
+    def oracle(arr, upto=0):
+        o = orc.LlamaQuantOracle(QCFG, {k: arr[k] for k in names} |
+                                 {"qweights": arr["qweights"].view(np.uint8)}, gs, offs)
+        for name, dst in (("key_cache", o.kc), ("value_cache", o.vc)):
+            src = arrays[name].reshape(QCFG["n_layers"], QCFG["seq_len"], kv)
+            dst.reshape(QCFG["n_layers"], QCFG["seq_len"], kv)[:, :upto] = src[:, :upto]
+        return o
+
+    for pos, t in enumerate([50, 60, 70]):
+        sa.llama2_quant_forward(arrays, t, pos, *dims, gs, offs)
+    for k in names + ("qweights",):
+        np.copyto(arrays[k], arrays_b[k])
+    print("[quant-export] rewritten weights, pos=3", flush=True)
+    o = oracle(arrays, upto=3)
+    sa.llama2_quant_forward(arrays, 80, 3, *dims, gs, offs)
+    _same(arrays["logits"], o.forward(80, 3))
+    for pos in (1, 5):                                   # jumps: rows [0, pos) from the host
+        print(f"[quant-export] jump to pos={pos}", flush=True)
+        o = oracle(arrays, upto=pos)
+        sa.llama2_quant_forward(arrays, 90 + pos, pos, *dims, gs, offs)
+        _same(arrays["logits"], o.forward(90 + pos, pos))
+    sa.forward_cache_clear()

@@ -214,3 +214,57 @@ def test_empty_dimensions(dev, M, N, K):
         torch.cuda.synchronize()
         want = 0 if (K == 0 and M and N) else 7
         assert (c == want).all().item(), (fn.__name__, M, N, K)
+
+
+def test_int8_strided_views_host_arrays(dev, orc):
+    """The same views as numpy host arrays (staged through device memory): the
+    result lands in the view, and the bytes between the output rows, which lie
+    inside the staged span but outside the view, come back unchanged."""
+    a, b = _inputs(128, 256, 512, seed=5)
+    c_full = np.full((128, 300), -7, dtype=np.int32)
+    c_full[:, 276:] = 12345
+    c = c_full[:, 20:276]
+    sa.matmul_u8s8_i32(a[:, 64:320], b[128:384, :], c)
+    want = orc.matmul_i8(np.ascontiguousarray(a[:, 64:320]), np.ascontiguousarray(b[128:384]),
+                         a_unsigned=True)
+    assert np.array_equal(c_full[:, 20:276], want)
+    assert (c_full[:, :20] == -7).all() and (c_full[:, 276:] == 12345).all()
+
+
+def _gold_checksums():
+    import json
+    import os
+    return json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "int8_recipe_checksums.json")))["checksums"]
+
+
+def test_benchmark_int8_programs(dev):
+    """benchmark_int8_matmul_<N>() (bench_int8_matmul.sl:11-335) returns the
+    checksum of the reference's own kernel (golden fixture) at every size the
+    program defines, twice (the second call reuses the inputs' workspace)."""
+    gold = _gold_checksums()
+    for n in sa.host.BENCH_INT8_SIZES:
+        print(f"[bench-program] N={n}", flush=True)
+        assert sa.benchmark_int8_matmul(n) == gold[str(n)], n
+        assert sa.benchmark_int8_matmul(n) == gold[str(n)], n
+
+
+@pytest.mark.parametrize("n", [256, 512, 768, 1024, 2048])
+def test_int8_chunk_programs(dev, orc, n):
+    """int8_chunk_<N> called the way bench_int8_parallel_runner.cpp:38-89 calls
+    it: host arrays of the recipe inputs, eight row chunks issued from eight
+    host threads at once; C equals the oracle's product bit for bit."""
+    from concurrent.futures import ThreadPoolExecutor
+    print(f"[chunk-program] N={n}", flush=True)
+    a, b = orc.recipe_inputs(n)
+    fa, fb = a.reshape(-1).copy(), b.reshape(-1).copy()
+    c = np.zeros(n * n, np.int32)
+    rows = n // 8
+    with ThreadPoolExecutor(8) as ex:
+        list(ex.map(lambda i: sa.int8_chunk(n, fa, fb, c, i * rows), range(8)))
+    want = orc.matmul_i8(a, b)
+    assert np.array_equal(c.reshape(n, n), want)
+    if str(n) in _gold_checksums():
+        assert orc.checksum_i32(c) == _gold_checksums()[str(n)]
+    with pytest.raises(sa.SimpRTError):
+        sa.int8_chunk(n, fa, fb, c, n - rows + 1)           # rows past the end

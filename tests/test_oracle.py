@@ -55,9 +55,9 @@ def test_vpdpbusd_random_vs_reference(orc):
         got = orc.vpdpbusd16(a, b, acc)
         exp = (acc.astype(np.int64) + (a.astype(np.int64) * b).reshape(16, 4).sum(1))
         assert (got == exp.astype(np.int32)).all()
-        if orc.ref is not None:
+        if orc.load_ref() is not None:
             ref = np.empty(16, np.int32)
-            orc.ref.ref_scalar_vpdpbusd(a.ctypes.data, b.ctypes.data, acc.ctypes.data,
+            orc.load_ref().ref_scalar_vpdpbusd(a.ctypes.data, b.ctypes.data, acc.ctypes.data,
                                         ref.ctypes.data)
             assert (got == ref).all()
 
@@ -118,7 +118,7 @@ def test_vnni_algorithm_equals_textbook(orc, M, N, K, a_unsigned, b_nk):
 @pytest.mark.parametrize("n", [64, 128, 256, 512])
 def test_vnni_vs_reference_kernel(orc, n):
     """Oracle == the reference's vnni_matmul_single_thread<N>, compiled in place."""
-    if orc.ref is None:
+    if orc.load_ref() is None:
         pytest.skip("reference not built here")
     if "avx512_vnni" not in open("/proc/cpuinfo").read():
         pytest.skip("host lacks AVX-512 VNNI")
@@ -127,7 +127,7 @@ def test_vnni_vs_reference_kernel(orc, n):
                   RNG.integers(-128, 128, (n, n)).astype(np.int8))):
         bt = np.ascontiguousarray(b.T)
         ref = np.zeros((n, n), np.int32)
-        getattr(orc.ref, f"ref_vnni_matmul_{n}")(a.ctypes.data, bt.ctypes.data, ref.ctypes.data)
+        getattr(orc.load_ref(), f"ref_vnni_matmul_{n}")(a.ctypes.data, bt.ctypes.data, ref.ctypes.data)
         assert (orc.matmul_i8(a, b) == ref).all()
         c, _ = orc.matmul_i8_vnni(a, b, nthreads=4)
         assert (c == ref).all()
@@ -151,7 +151,7 @@ def test_checksum_recipe_fixture(orc):
 def test_int4_nibble_convention_vs_reference(orc):
     """F6 nibble unpack (low = even k, sign-extend >= 8) reproduces the
     reference's packed int4 GEMM checksum (bench_int4_matmul_runner.cpp:74-150)."""
-    if orc.ref is None:
+    if orc.load_ref() is None:
         pytest.skip("reference not built here")
     for n in (32, 64, 128):
         idx = np.arange(n * n).reshape(n, n)
@@ -163,8 +163,8 @@ def test_int4_nibble_convention_vs_reference(orc):
                            a, gs=32)
         c16 = np.rint(c).astype(np.int64).astype(np.int16)      # i16 result type
         chk = np.int64(c16.astype(np.int64).sum()).astype(np.int32)
-        assert int(chk) == int(getattr(orc.ref, f"ref_packed_int4_{n}")())
-        assert int(chk) == int(getattr(orc.ref, f"ref_scalar_int4_{n}")())
+        assert int(chk) == int(getattr(orc.load_ref(), f"ref_packed_int4_{n}")())
+        assert int(chk) == int(getattr(orc.load_ref(), f"ref_scalar_int4_{n}")())
 
 
 def test_matmul_i4_recipe_fixture(orc):
@@ -180,9 +180,9 @@ def test_matmul_i4_recipe_fixture(orc):
             continue
         ap, bp = orc.int4_recipe_inputs(n)
         assert orc.checksum_i16(orc.matmul_i4(ap, bp, n, n, n)) == want, n
-    if orc.ref is not None:
+    if orc.load_ref() is not None:
         for n in (32, 64, 128):
-            assert gold["checksums"][str(n)] == int(getattr(orc.ref, f"ref_packed_int4_{n}")())
+            assert gold["checksums"][str(n)] == int(getattr(orc.load_ref(), f"ref_packed_int4_{n}")())
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 7, 9), (16, 33, 64), (33, 18, 101), (1, 1, 1)])
