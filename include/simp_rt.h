@@ -112,6 +112,25 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
     const int8_t *bt_alloc, const int8_t *bt, int64_t bt_off, int64_t bt_s0, int64_t bt_s1, int64_t bt_st0, int64_t bt_st1,
     int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
 
+/* No counterpart in the reference: an allocation-free variant of
+ * simp_rt_matmul_u8s8_i32 (same operands, same result bits) for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  It calls no hipMalloc / hipFree:
+ * A, B and C must already be device memory (or inside simp_rt_register'd
+ * ranges); host pointers are rejected (SIMP_RT_EINVAL).  Its kernels use a
+ * static device array of 64 MiB + 64 KiB per GPU (held until the process ends)
+ * for the column sums of B and B transposed, so shapes that take the large-tile
+ * path need 4*N (rounded up to 256) + K*N bytes there: larger requests (e.g.
+ * K*N above 64 MiB, such as N = K = 16384) are rejected with SIMP_RT_EINVAL.
+ * All calls on one GPU share that array: calls that overlap on one GPU (other
+ * streams or threads) race and must be ordered by the caller.  The device
+ * address of each GPU's copy is looked up by simp_rt_init() or by the first
+ * call on that device. */
+int32_t simp_rt_matmul_u8s8_i32_noalloc(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1);
+
 /* tensor_matvecmul on i8 tensors: the same s8 x s8 -> i32 product as
  * simp_rt_tensor_matmul_i8 (A[M,K] x B[K,N], C overwritten).  Replaces
  * TensorMatVecMulOpLowering's int8 branch (ConvertSimpToMemRef.cpp:3632-3762),

@@ -54,7 +54,7 @@ def _sig(name, argtypes):
 
 for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
            "simp_rt_matmul_u8s8_i32", "simp_rt_matmul_nt_u8s8_i32", "simp_rt_tensor_matmul_i4",
-           "simp_rt_tensor_matvecmul_i8"):
+           "simp_rt_tensor_matvecmul_i8", "simp_rt_matmul_u8s8_i32_noalloc"):
     _sig(_n, _D2 * 3)
 _sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
 _sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
@@ -360,6 +360,12 @@ def tensor_matmul_i4(a_packed, b_packed, c):
 def matmul_u8s8_i32(a, b, c):
     """C = A(u8) x B(s8) -> i32, vpdpbusd semantics, B as [K,N]."""
     return _gemm("simp_rt_matmul_u8s8_i32", a, b, c)
+
+
+def matmul_u8s8_i32_noalloc(a, b, c):
+    """simp_rt_matmul_u8s8_i32_noalloc: the u8 x s8 -> i32 product with no
+    device allocation (operands must be device-resident)."""
+    return _gemm("simp_rt_matmul_u8s8_i32_noalloc", a, b, c)
 
 
 def matmul_nt_u8s8_i32(a, bt, c):

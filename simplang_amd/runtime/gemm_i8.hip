@@ -34,6 +34,8 @@
 // of tiles (blocks are dispatched round-robin over XCDs), and tiles are ordered
 // in groups of 8 tile-rows so co-resident tiles share A and B in L2.
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "rt_internal.h"
 
@@ -718,6 +720,10 @@ struct GemmArgs {
   int M, N, K;
   int batch = 1;                   // products on grid z (at most 65535)
   int64_t sa = 0, sb = 0, sc = 0;  // element distance between consecutive products
+  // Caller-provided device scratch for the column sums and B_T of the large
+  // path (the allocation-free entry point); null: the stream's workspace.
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8>
@@ -789,8 +795,18 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     GemmArgs h = g;
     const size_t cs_bytes = AU8 ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
     void *ws = nullptr;
-    int rc = workspace(st, cs_bytes + (BNK ? 0 : (size_t)g.K * g.N), &ws);
-    if (rc) return rc;
+    const size_t need = cs_bytes + (BNK ? 0 : (size_t)g.K * g.N);
+    if (g.scratch) {
+      if (need > g.scratch_bytes)
+        return set_error(SIMP_RT_EINVAL,
+                         "scratch of %zu bytes needed for M=%d N=%d K=%d, above the "
+                         "allocation-free maximum of %zu bytes", need, g.M, g.N, g.K,
+                         g.scratch_bytes);
+      ws = g.scratch;
+    } else {
+      int rc = workspace(st, need, &ws);
+      if (rc) return rc;
+    }
     int32_t *colsum = AU8 ? (int32_t *)ws : nullptr;
     if (!BNK) {  // B[K,N] -> B_T[N,K], column sums on the way
       constexpr int KT = 256;
@@ -985,11 +1001,80 @@ int batch_i8_entry(const int8_t *a, int64_t a_off, const int64_t *as, const int6
 }
 
 }  // namespace
+
+// ------------------------------------------------ allocation-free variant --
+// Scratch of simp_rt_matmul_u8s8_i32_noalloc: the column sums of B (N i32,
+// rounded up to 256 bytes) followed by B_T[N,K], as the stream workspace holds
+// them.  One copy per GPU, for the life of the process.
+constexpr size_t kNoAllocScratchBytes = (size_t(64) << 20) + (size_t(64) << 10);
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void *> g_scratch_addr;  // device address of `scratch`, per device
+}  // namespace
+
+// The host-side name `scratch` is not a device address: the device address of
+// each GPU's copy is looked up once, with that device current, and kept.
+int noalloc_scratch(void **ptr) {
+  const int dev = ensure_device();
+  if (dev < 0) return dev;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if ((int)g_scratch_addr.size() <= dev) g_scratch_addr.resize(dev + 1, nullptr);
+  if (!g_scratch_addr[dev]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_error(SIMP_RT_EHIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_addr[dev] = p;
+  }
+  *ptr = g_scratch_addr[dev];
+  return SIMP_RT_OK;
+}
+
 }  // namespace simp
 
 using namespace simp;
 
 extern "C" {
+
+int32_t simp_rt_matmul_u8s8_i32_noalloc(
+    const uint8_t *a_alloc, const uint8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,
+    const int8_t *b_alloc, const int8_t *b, int64_t b_off, int64_t b_s0, int64_t b_s1, int64_t b_st0, int64_t b_st1,
+    int32_t *c_alloc, int32_t *c, int64_t c_off, int64_t c_s0, int64_t c_s1, int64_t c_st0, int64_t c_st1) {
+  (void)a_alloc; (void)b_alloc; (void)c_alloc;
+  const char *name = "matmul_u8s8_i32_noalloc";
+  int rc;
+  if ((rc = check_desc2("A", a, a_off, a_s0, a_s1, a_st0, a_st1))) return rc;
+  if ((rc = check_desc2("B", b, b_off, b_s0, b_s1, b_st0, b_st1))) return rc;
+  if ((rc = check_desc2("C", c, c_off, c_s0, c_s1, c_st0, c_st1))) return rc;
+  const int64_t M = a_s0, K = a_s1, N = b_s1;
+  if (b_s0 != K || c_s0 != M || c_s1 != N)
+    return set_error(SIMP_RT_EINVAL, "%s: shape mismatch A[%lld,%lld] B[%lld,%lld] C[%lld,%lld]",
+                     name, (long long)a_s0, (long long)a_s1, (long long)b_s0, (long long)b_s1,
+                     (long long)c_s0, (long long)c_s1);
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "%s: dimension above 2^31-1", name);
+  if (M == 0 || N == 0) return SIMP_RT_OK;
+  // operands must already be on the device: staging host memory would allocate
+  const void *da = nullptr, *db = nullptr, *dc = nullptr;
+  const size_t a_bytes = K ? (size_t)((M - 1) * a_st0 + K) : 0;
+  const size_t b_bytes = K ? (size_t)((K - 1) * b_st0 + N) : 0;
+  const size_t c_bytes = (size_t)((M - 1) * c_st0 + N) * 4;
+  if (K && ((rc = device_view(a + a_off, a_bytes, &da, "A")) ||
+            (rc = device_view(b + b_off, b_bytes, &db, "B"))))
+    return rc;
+  if ((rc = device_view(c + c_off, c_bytes, &dc, "C"))) return rc;
+  void *ws = nullptr;
+  if ((rc = noalloc_scratch(&ws))) return rc;
+  GemmArgs g{(const int8_t *)da, a_st0, (const int8_t *)db, b_st0, (int32_t *)dc, c_st0,
+             (int)M, (int)N, (int)K};
+  g.scratch = ws;
+  g.scratch_bytes = kNoAllocScratchBytes;
+  if ((rc = dispatch<false, true>(g, cur_stream()))) return rc;
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
 
 int32_t simp_rt_tensor_matmul_i8(
     const int8_t *a_alloc, const int8_t *a, int64_t a_off, int64_t a_s0, int64_t a_s1, int64_t a_st0, int64_t a_st1,

@@ -369,7 +369,9 @@ int32_t simp_rt_init(void) {
   if (n <= 0) return set_error(SIMP_RT_ENODEV, "no HIP device visible");
   int dev = ensure_device();
   if (dev < 0) return dev;
-  return num_cus() > 0 ? SIMP_RT_OK : SIMP_RT_ENODEV;
+  if (num_cus() <= 0) return SIMP_RT_ENODEV;
+  void *scratch = nullptr;  // set-up of simp_rt_matmul_u8s8_i32_noalloc on this device
+  return noalloc_scratch(&scratch);
 }
 
 int32_t simp_rt_set_stream(void *stream) {

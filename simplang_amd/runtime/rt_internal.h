@@ -107,6 +107,10 @@ struct KvState {
   void done(int64_t pos) { next_pos = pos + 1; }
 };
 
+// Device address of the allocation-free int8 entry point's static scratch on
+// the current device (looked up on first use per device, then cached).
+int noalloc_scratch(void **ptr);
+
 // Frees the engines of llama32_forward (part of simp_rt_forward_cache_clear).
 void l32_cache_clear();
 

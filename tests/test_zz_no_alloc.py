@@ -1,0 +1,50 @@
+"""simp_rt_matmul_u8s8_i32_noalloc (the allocation-free variant of
+simp_rt_matmul_u8s8_i32, whose large-shape scratch lives in a static device
+array) against simp_rt_matmul_u8s8_i32 itself, bit for bit, through the C ABI:
+two calls in a row that both take the large-tile path (column sums and B_T in
+the static scratch), the second smaller, so the second must clear and refill
+what the first left there; a small shape (no scratch); and the documented
+rejections (host operands, a scratch need above the maximum)."""
+import numpy as np
+import pytest
+
+import simplang_amd as sa
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(dev, M, N, K, seed):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    a = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (K, N), dtype=torch.int8, device=dev, generator=g)
+    return a, b
+
+
+def test_noalloc_matches_allocating_entry_point(dev):
+    import torch
+    for (M, N, K, seed) in ((4096, 4096, 4096, 1), (4096, 4096, 1024, 2), (256, 320, 192, 3)):
+        print(f"[noalloc] M={M} N={N} K={K}", flush=True)
+        a, b = _pair(dev, M, N, K, seed)
+        want = torch.empty((M, N), dtype=torch.int32, device=dev)
+        got = torch.full((M, N), -1, dtype=torch.int32, device=dev)
+        sa.matmul_u8s8_i32(a, b, want)
+        sa.matmul_u8s8_i32_noalloc(a, b, got)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (M, N, K)
+
+
+def test_noalloc_rejections(dev):
+    import torch
+    a = np.zeros((64, 64), np.uint8)                       # host memory: would need staging
+    b = np.zeros((64, 64), np.int8)
+    c = np.zeros((64, 64), np.int32)
+    with pytest.raises(sa.SimpRTError):
+        sa.matmul_u8s8_i32_noalloc(a, b, c)
+    M, N, K = 2048, 16384, 8192                            # B_T of 128 MiB > the maximum
+    print(f"[noalloc] rejection M={M} N={N} K={K}", flush=True)
+    da = torch.zeros((M, K), dtype=torch.uint8, device=dev)
+    db = torch.zeros((K, N), dtype=torch.int8, device=dev)
+    dc = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    with pytest.raises(sa.SimpRTError, match="allocation-free maximum"):
+        sa.matmul_u8s8_i32_noalloc(da, db, dc)
