@@ -193,7 +193,13 @@ typedef struct {
  * of llama2_quant.sl:98 and score scale 1/sqrt(hs) (F11).  key_cache and
  * value_cache are [L, seq_len, kv_dim]; logits[vocab] is written.  Matrix-vector
  * products accumulate in double (exact reference for the tolerance check);
- * everything else is fp32 as in the program. */
+ * everything else is fp32 as in the program.  Pinned (tests/test_oracle_decode.py)
+ * by a float64 brute force in another formulation (whole sequence with a causal
+ * mask, RoPE as complex rotation) for MHA / GQA / MQA, closed forms (zero
+ * projections, pos-0 independence of wq / wk / theta, wq = 0 gives the mean of
+ * V), GQA = MHA with duplicated K/V heads, and W4 = fp32 on dequantized
+ * matrices; planted mistakes (no RoPE, reversed RoPE, wrong head map, no score
+ * scale) fail those pins. */
 void orc_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
                        float *key_cache, float *value_cache, int64_t token,
                        int64_t pos, float *logits);
@@ -204,7 +210,10 @@ void orc_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
  * wq_off.. advanced per layer by rows*cols as in :77-79,136,156-158), no RoPE,
  * score scale 1/sqrt(head_size), fp32 classifier wcls[vocab, dim].  Dims are
  * taken from cfg (the program hard-codes 1536/6144/128, deviation D4).
- * cfg->w4 / gs / theta are ignored; group size is `gs`. */
+ * cfg->w4 / gs / theta are ignored; group size is `gs`.  Pinned
+ * (tests/test_oracle_decode.py) by the float64 brute force without RoPE on the
+ * matrices dequantized from the flat array at the per-layer offsets (gs 32 and
+ * 128), and at pos 0 by orc_llama_forward on the same dequantized matrices. */
 void orc_llama_quant_forward(const orc_llama_cfg *cfg, const float *emb, const float *rms_att,
                              const float *rms_ffn, const float *rms_final, const float *wcls,
                              const uint8_t *qw, const float *scales, const float *zeros,
