@@ -26,9 +26,17 @@
  *   orc_rope                  -- pos 0 identity, rotation preserves pair norms,
  *                                closed-form angle for pair 0
  *   orc_llama_forward,
- *   orc_llama_quant_forward,
- *   orc_llama32_int8_forward  -- parity unpinned beyond its parts: the reference
- *                                holds no golden logits (docs/benchmark/llama_results.md:81-95)
+ *   orc_llama_quant_forward   -- the reference holds no golden logits
+ *                                (docs/benchmark/llama_results.md:81-95): float64
+ *                                brute force in another formulation, closed forms
+ *                                and invariances (tests/test_oracle_decode.py)
+ *   orc_matmul_quant_f5_refidx -- equals orc_matmul_quant_f5 at offset 0, gs 128;
+ *                                rotated scales at offset > 0; overlapping-tile
+ *                                closed form at gs 32
+ *   orc_llama32_int8_forward  -- closed forms: zero weights, layer-0 cache rows,
+ *                                one layer's FFN and final norm in int64 / float64,
+ *                                inert attention, x86 wrap of ffn_hb, layer
+ *                                offsets (tests/test_oracle.py)
  *   orc_quantize_w4s          -- properties: |dequant - w| <= scale/2 inside the
  *                                range, the group maximum maps to +-7 exactly,
  *                                all-zero groups; brute force in numpy

@@ -509,3 +509,71 @@ def test_llama32_fptosi_wraps_like_x86(orc):
     hb = a["ffn_hb"].astype(np.int64)
     assert np.unique(hb).size > 100                       # wrapped values cover the byte range
     assert np.isin(hb, (-128, 127)).mean() < 0.05         # a clamp would pile them up at the ends
+
+
+def test_llama32_ffn_composition_closed_form(orc):
+    """One layer with the attention matrices zero (Wo sees zeros): the FFN and
+    the final norm in float64 / int64 with the program's integer steps
+    (llama32_1b_int8_tensor.sl:232-280): xq = trunc(clamp(rmsnorm(x) * 127)),
+    G = W1 xq and U = W3 xq exact (i32), ffn_hb = low byte of
+    trunc(silu(G / 65536) * (U / 65536) * 127), x += (W2 ffn_hb) / 65536,
+    logits = wcls . rmsnorm(x).  ffn_hb is compared except where fp32 and
+    float64 may round across an integer (within 1e-3 of one); x and the logits
+    are then recomputed from the oracle's own ffn_hb."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg = dict(CFG_SMALL, n_layers=1)
+    a = make_arrays(cfg, seed=14, wide=True)
+    for k in ("wq_t", "wk_t", "wv_t", "wo_t"):
+        a[k][:] = 0
+    x0 = a["x_i8"].astype(np.float64)
+    orc.llama32_int8_forward(a, 2, *_l32_dims(cfg))
+    D, H = cfg["dim"], cfg["hidden_dim"]
+    v = x0 / np.sqrt((x0 * x0).mean() + 1e-5) * a["rms_ffn_w"][:D] * 127.0
+    assert not ((np.abs(v - np.round(v)) < 1e-4) & (v != np.round(v))).any()
+    xq = np.trunc(np.clip(v, -128, 127)).astype(np.int64)
+    G = a["w1_t"].reshape(H, D).astype(np.int64) @ xq
+    U = a["w3_t"].reshape(H, D).astype(np.int64) @ xq
+    g = G / 65536.0
+    val = g / (1 + np.exp(-g)) * (U / 65536.0) * 127.0
+    want_hb = (np.trunc(val).astype(np.int64) & 0xFF).astype(np.uint8).view(np.int8)
+    tie = np.abs(val - np.round(val)) < 1e-3
+    assert tie.mean() < 0.05
+    assert np.array_equal(a["ffn_hb"][~tie], want_hb[~tie])
+    x1 = x0 + (a["w2_t"].reshape(D, H).astype(np.int64) @ a["ffn_hb"].astype(np.int64)) / 65536.0
+    np.testing.assert_allclose(a["x_fp32"], x1, rtol=1e-6, atol=1e-6 * np.abs(x1).max())
+    xb = x1 / np.sqrt((x1 * x1).mean() + 1e-5) * a["rms_final_w"]
+    lg = a["wcls"].reshape(cfg["vocab_size"], D).astype(np.float64) @ xb
+    np.testing.assert_allclose(a["logits"], lg, rtol=1e-4, atol=1e-4 * np.abs(lg).max())
+    assert not np.array_equal(a["x_fp32"], a["x_i8"].astype(np.float32))  # the FFN acted
+
+
+def test_llama32_layer_offsets(orc):
+    """Per-layer slices (l * dim, l * kv * dim, ... and the cache rows of layer
+    l): a two-layer model whose first layer has all-zero int8 weights equals the
+    one-layer model made of its second layer (weights and both norms), logits
+    and the second layer's cache rows alike."""
+    from _llama32 import CFG_SMALL, make_arrays
+    cfg2 = dict(CFG_SMALL, n_layers=2)
+    cfg1 = dict(CFG_SMALL, n_layers=1)
+    a = make_arrays(cfg2, seed=15, wide=True)
+    D, H = cfg2["dim"], cfg2["hidden_dim"]
+    kv = cfg2["n_kv_heads"] * cfg2["head_dim"]
+    per = {"wq_t": D * D, "wk_t": kv * D, "wv_t": kv * D, "wo_t": D * D, "w1_t": H * D,
+           "w2_t": D * H, "w3_t": H * D}
+    for k, n in per.items():
+        a[k][:n] = 0                                        # layer 0 does nothing
+    b = make_arrays(cfg1, seed=16, wide=True)
+    for k, n in per.items():
+        b[k][:] = a[k][n:]
+    for k in ("rms_att_w", "rms_ffn_w"):
+        b[k][:] = a[k][D:]
+    for k in ("x_i8", "rms_final_w", "wcls"):
+        b[k][:] = a[k]
+    for pos in range(3):
+        orc.llama32_int8_forward(a, pos, *_l32_dims(cfg2))
+        orc.llama32_int8_forward(b, pos, *_l32_dims(cfg1))
+        assert np.array_equal(a["logits"], b["logits"]), pos
+    S = cfg2["max_seq_len"]
+    for c in ("k_cache", "v_cache"):
+        assert np.array_equal(a[c].reshape(2, S, kv)[1], b[c].reshape(1, S, kv)[0])
+        assert not a[c].reshape(2, S, kv)[0].any()
