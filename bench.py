@@ -12,12 +12,14 @@ with HIP events on the stream they run on (simp_rt_timing), so ``achieved`` is
 2*M*N*K over that kernel's average launch time.
 
 Also reported on the same line: the configs[1] sweep (TOPS per shape), the W4
-GEMV, fp32 GEMM and decode sections, and the CPU baseline -- the oracle's restatement of
-the reference's VNNI kernel timed on this host's cores on a bounded row-block
-sample of the same 8192^3 problem.
+GEMV (with its CPU baseline per shape), rmsnorm / softmax / silu, fp32 GEMM and
+decode sections, and the CPU baseline -- the oracle's restatement of the
+reference's VNNI kernel timed on the host cores one GPU gets (and on one core)
+on a bounded row-block sample of the same 8192^3 problem, with the host's CPU
+model, nproc and AVX-512 VNNI flag.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-sweep] [--no-cpu]
-                    [--only gemm|w4|f32|decode|copy]
+                    [--only gemm|w4|f32|decode|norm|copy]
 
 ``--only copy`` times a plain 256 MiB device copy (the calibration run for the
 rocprofv3 FETCH_SIZE / WRITE_SIZE counters) and prints its own JSON line.
@@ -63,34 +65,66 @@ def make_inputs(M, N, K, dev, seed=42):
     return a, b, c
 
 
-def cpu_baseline(n, budget_s=10.0):
-    """Oracle VNNI restatement on host cores, row blocks of the n^3 problem,
-    repeated until about budget_s of CPU work (the whole problem takes well
-    under a second on 16 AVX-512 VNNI cores, so a single pass is too short to
-    time steadily)."""
+# One MI355X's share of its box's host CPUs: the GPU boxes give each GPU 16
+# cores whatever nproc reports, so "all cores" means at most 16 there.
+CPU_SHARE = 16
+
+
+def host_info():
+    """nproc, the CPU model (as lscpu prints it) and the AVX-512 VNNI flag."""
+    info = {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "model": None, "avx512_vnni": False}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and info["model"] is None:
+                    info["model"] = line.split(":", 1)[1].strip()
+                elif line.startswith("flags"):
+                    info["avx512_vnni"] = "avx512_vnni" in line.split()
+                    break
+    except OSError:
+        pass
+    info["cores_used"] = min(info["affinity"], CPU_SHARE)
+    return info
+
+
+def cpu_baseline(n, threads, budget_s):
+    """Oracle VNNI restatement on `threads` host cores, 64-row blocks of the n^3
+    problem, repeated until about budget_s of CPU work."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    cores = min(os.cpu_count() or 1, 16)
     rng = np.random.default_rng(42)
     rows = 64
     a = rng.integers(0, 256, (rows, n)).astype(np.uint8)
     b = rng.integers(-128, 128, (n, n)).astype(np.int8)
     bt = np.ascontiguousarray(b.T)
-    oracle.matmul_i8_vnni(a[:8], bt, a_unsigned=True, b_nk=True, nthreads=cores)  # warm
+    oracle.matmul_i8_vnni(a[:8], bt, a_unsigned=True, b_nk=True, nthreads=threads)  # warm
     done, t0, hw = 0, time.perf_counter(), False
     while True:
-        _, hw = oracle.matmul_i8_vnni(a, bt, a_unsigned=True, b_nk=True, nthreads=cores)
+        _, hw = oracle.matmul_i8_vnni(a, bt, a_unsigned=True, b_nk=True, nthreads=threads)
         done += 1
         el = time.perf_counter() - t0
-        if el >= budget_s and done * rows >= n:
+        if el >= budget_s:
             break
     tops = 2.0 * done * rows * n * n / el / 1e12
-    return {"value": round(tops, 4), "unit": "TOPS", "cores": cores, "kind": "port",
-            "sample": (f"{done} blocks of {rows} rows x {n} x {n} ({done * rows / n:.1f} passes "
+    return {"value": round(tops, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": (f"{done} blocks of {rows} rows x {n} x {n} ({done * rows / n:.2f} passes "
                        f"over the {n}^3 problem; u8xs8->i32, B pre-transposed as the "
-                       f"reference's B_T) in {el:.1f}s; "
+                       f"reference's B_T) in {el:.1f}s on {threads} thread(s); "
                        f"{'AVX-512 VNNI' if hw else 'scalar (host lacks AVX-512 VNNI)'}")}
+
+
+def cpu_baselines(n):
+    """The headline's CPU baseline on all the cores one GPU gets (value) and on
+    one core, with the host's identity."""
+    host = host_info()
+    line = cpu_baseline(n, host["cores_used"], 10.0)
+    one = cpu_baseline(n, 1, 5.0)
+    line["single_thread"] = {"value": one["value"], "unit": "TOPS", "cores": 1,
+                             "sample": one["sample"]}
+    line["host"] = host
+    return line
 
 
 def graph_time_ms(calls, stream, replays=5):
@@ -125,14 +159,30 @@ def graph_time_ms(calls, stream, replays=5):
     return t0.elapsed_time(t1) / (replays * len(calls))
 
 
-def w4_bench(dev, stream):
+def w4_cpu_us(w, s, x, threads, budget_s=0.4):
+    """The W4 product through the reference lowering's loop structure
+    (oracle orc_matmul_w4s_lowering, ConvertSimpToMemRef.cpp:3906-4011) on the
+    host: microseconds per call."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    oracle.matmul_w4s_lowering(w, s, x, 32, threads)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        oracle.matmul_w4s_lowering(w, s, x, 32, threads)
+        n += 1
+    return (time.perf_counter() - t0) / n * 1e6
+
+
+def w4_bench(dev, stream, with_cpu=True):
     """W4 GEMV/skinny GEMM, BASELINE configs[2].  Weight copies are rotated so
     that more than 512 MB is touched per pass: every launch streams its weights
     from HBM (the 256 MB Infinity Cache cannot hold them), as in a decode step.
-    Timed by HIP-graph replay of one launch per copy."""
+    Timed by HIP-graph replay of one launch per copy.  Each row also carries the
+    CPU baseline on the cores one GPU gets."""
     import torch
     import simplang_amd as sa
     out = []
+    threads = host_info()["cores_used"]
     g = torch.Generator(device=dev)
     g.manual_seed(42)
     for (K, N) in ((3200, 8640), (8640, 3200), (3200, 32000)):
@@ -141,17 +191,68 @@ def w4_bench(dev, stream):
         ws = [torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g)
               for _ in range(copies)]
         ss = [(torch.rand((N, K // 32), device=dev, generator=g) * 0.02 / 7) for _ in range(copies)]
+        wh, sh = (ws[0].cpu().numpy(), ss[0].cpu().numpy()) if with_cpu else (None, None)
         for M in (1, 4, 16):
             x = torch.randn((M, K), device=dev, generator=g)
             o = torch.empty((M, N), device=dev)
             calls = [(lambda i=i: sa.matmul_w4s(ws[i], ss[i], x, o, 32)) for i in range(copies)]
             ms = graph_time_ms(calls, stream)
             byts = N * K / 2 + 4 * N * K / 32 + 4 * M * K + 4 * M * N
-            out.append({"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
-                        "GBs": round(byts / (ms * 1e-3) / 1e9, 1),
-                        "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)})
+            row = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+                   "GBs": round(byts / (ms * 1e-3) / 1e9, 1),
+                   "frac_hbm": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            if with_cpu:
+                cus = w4_cpu_us(wh, sh, x.cpu().numpy(), threads)
+                row["cpu_baseline"] = {"us": round(cus, 1), "GBs": round(byts / cus / 1e3, 2),
+                                       "cores": threads, "kind": "port"}
+            out.append(row)
         del ws, ss
         torch.cuda.empty_cache()
+    return out
+
+
+def norm_bench(dev, stream, with_cpu=True):
+    """rmsnorm / softmax / silu (rows a9-a11) as standalone launches at the model
+    sizes (768 and 3200 dims, 2048 and 8640 FFN widths, 288 and 512 attention
+    rows): GPU time by HIP-graph replay of back-to-back launches, GB/s over the
+    algorithmic bytes (12n, 16n, 8n), and the oracle's restatement of the
+    reference loop on one host core."""
+    import numpy as np
+    import torch
+    import simplang_amd as sa
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    out = []
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    cases = [("rmsnorm", n) for n in (768, 3200, 8640)] + \
+            [("softmax", n) for n in (288, 512, 768, 3200, 8640)] + \
+            [("silu", n) for n in (768, 2048, 3200, 8640)]
+    for op, n in cases:
+        x = torch.randn(n, device=dev, generator=g)
+        w = torch.randn(n, device=dev, generator=g)
+        o = torch.empty(n, device=dev)
+        if op == "rmsnorm":
+            call, byts = (lambda: sa.rmsnorm(x, w, o, n)), 12 * n
+            cpu = lambda xh=x.cpu().numpy(), wh=w.cpu().numpy(): oracle.rmsnorm(xh, wh)
+        elif op == "softmax":
+            call, byts = (lambda: sa.softmax(x, o, n)), 16 * n
+            cpu = lambda xh=x.cpu().numpy(): oracle.softmax(xh)
+        else:
+            call, byts = (lambda: sa.silu(x, o, n)), 8 * n
+            cpu = lambda xh=x.cpu().numpy(): oracle.silu(xh)
+        ms = graph_time_ms([call] * 50, stream)
+        row = {"op": op, "n": n, "us": round(ms * 1e3, 2),
+               "GBs": round(byts / (ms * 1e-3) / 1e9, 2)}
+        if with_cpu:
+            cpu()
+            k, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 0.1:
+                cpu()
+                k += 1
+            row["cpu_baseline"] = {"us": round((time.perf_counter() - t0) / k * 1e6, 2),
+                                   "cores": 1, "kind": "port"}
+        out.append(row)
     return out
 
 
@@ -316,7 +417,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "w4", "f32", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemm", "w4", "f32", "decode", "norm", "copy"], default=None,
                     help="run one section (for profiling); the JSON line is still printed")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -394,13 +495,16 @@ def main():
             del a, b, c
         torch.cuda.empty_cache()
 
-    w4 = w4_bench(dev, stream) if args.only == "w4" or (args.only is None and not args.no_sweep) else []
+    w4 = (w4_bench(dev, stream, with_cpu=not args.no_cpu)
+          if args.only == "w4" or (args.only is None and not args.no_sweep) else [])
+    norms = (norm_bench(dev, stream, with_cpu=not args.no_cpu)
+             if args.only == "norm" or (args.only is None and not args.no_sweep) else [])
     f32 = f32_bench(dev, stream) if args.only == "f32" or (args.only is None and not args.no_sweep) else []
     decode = [] if args.no_decode else decode_bench(dev, stream, with_cpu=not args.no_cpu)
     if not args.no_decode:
         decode.append(llama32_bench(dev, with_cpu=not args.no_cpu))
 
-    cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baseline(n)
+    cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baselines(n)
 
     ktops = 2.0 * n * n * n / (kern_ms * 1e-3) / 1e12 if kern_ms > 0 else 0.0
     line = {
@@ -420,11 +524,16 @@ def main():
                    "M": n, "N": n, "K": n, "layout": "A[M,K], B[K,N] row-major, C[M,N] i32"},
         "roofline": {"bound": "mfma", "achieved": round(ktops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(ktops / INT8_PEAK_TOPS, 4),
-                     "traffic": load_traffic(f"{kern}_{n}"), "kernel": kern,
+                     "traffic": load_traffic(f"{kern}_{n}"),
+                     "traffic_source": "profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and "
+                                       "WRITE_SIZE of this kernel at this size, copy-calibrated "
+                                       "(a committed measurement, not this run's counters)",
+                     "kernel": kern,
                      "launch_us": round(kern_ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "sweep": sweep,
         "w4_gemv": w4,
+        "norms": norms,
         "f32_gemm": f32,
         "decode": decode,
     }

@@ -464,6 +464,35 @@ void orc_matmul_w4s_f32(const uint8_t *qw, const float *scales, const float *x,
   }
 }
 
+void orc_matmul_w4s_lowering(const uint8_t *qw, const float *scales, const float *x,
+                             float *out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                             int nthreads) {
+  const int64_t ng = K / gs, ntiles = gs / 16;
+  if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+  for (int64_t i = 0; i < N; i++) {                       /* row loop, :3916 */
+    const uint8_t *row = qw + i * (K / 2);
+    for (int64_t m = 0; m < M; m++) {
+      const float *in = x + m * K;
+      float o = 0.0f;                                      /* :3922 */
+      for (int64_t g = 0; g < ng; g++) {                   /* group loop, :3929-3932 */
+        const float scale = scales[i * ng + g];            /* :3938, no zero point */
+        float acc = 0.0f;
+        for (int64_t t = 0; t < ntiles; t++) {             /* tile loop, :3942-4005 */
+          float tile[16];
+          const int64_t k0 = g * gs + t * 16;
+          for (int j = 0; j < 16; j++)                      /* dequantise 16, :3953-3982 */
+            tile[j] = (float)s4_at(row, k0 + j) * scale;
+          for (int j = 0; j < 16; j++)                      /* dot, :3985-4003 */
+            if (k0 + j < K) acc = acc + tile[j] * in[k0 + j];
+        }
+        o = o + acc;                                       /* :4007-4010 */
+      }
+      out[m * N + i] = o;
+    }
+  }
+}
+
 /* -------------------------------------------------------------- decode -- */
 
 void orc_rope(float *q, float *k, int64_t dim, int64_t kv_dim, int64_t hs,

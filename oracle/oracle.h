@@ -161,6 +161,17 @@ void orc_matmul_w4s_f32(const uint8_t *qw, const float *scales, const float *x,
                         float *out, int64_t M, int64_t N, int64_t K, int64_t gs,
                         int nthreads);
 
+/* The symmetric format through the loop structure MatMulQuantOpLowering emits
+ * (ConvertSimpToMemRef.cpp:3906-4011): per output row, per group an fp32
+ * partial over gs/16 tiles of 16 weights, each tile dequantised into a buffer
+ * (q * scale; this format has no zero point) and then dotted with x in order,
+ * the partial added to the row's sum.  One x row after another (the reference
+ * op takes one); OpenMP over output rows.  The CPU baseline of the W4 GEMV
+ * (bench.py); agrees with orc_matmul_w4s to fp32 rounding. */
+void orc_matmul_w4s_lowering(const uint8_t *qw, const float *scales, const float *x,
+                             float *out, int64_t M, int64_t N, int64_t K, int64_t gs,
+                             int nthreads);
+
 /* -------------------------------------------------------------- decode -- */
 
 /* RoPE of the LLaMA programs (examples/llama2/stories110M.sl:86-112):

@@ -55,6 +55,7 @@ _s("orc_matmul_quant_f5_refidx", [_P, _P, _P, _P, _P, _I, _I, _I, _I])
 _s("orc_quantize_f5", [_P, _I, _I, _P, _P, _P])
 _s("orc_matmul_w4s", [_P, _P, _P, _P, _I, _I, _I, _I])
 _s("orc_matmul_w4s_f32", [_P, _P, _P, _P, _I, _I, _I, _I, C.c_int])
+_s("orc_matmul_w4s_lowering", [_P, _P, _P, _P, _I, _I, _I, _I, C.c_int])
 _s("orc_rope", [_P, _P, _I, _I, _I, _I, _F])
 _s("orc_argmax", [_P, _I], C.c_int64)
 _s("orc_quantize_w4s", [_P, _I, _I, _I, _P, _P])
@@ -404,6 +405,17 @@ def matmul_w4s_f32(qw, scales, x, gs=32, nthreads=1):
     N = qw.shape[0]
     out = np.empty((M, N), np.float32)
     _o.orc_matmul_w4s_f32(_p(qw), _p(scales), _p(x), _p(out), M, N, K, gs, nthreads)
+    return out
+
+
+def matmul_w4s_lowering(qw, scales, x, gs=32, nthreads=1):
+    """The symmetric W4 product through MatMulQuantOpLowering's loop structure
+    (the W4 GEMV CPU baseline)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    N = qw.shape[0]
+    out = np.empty((M, N), np.float32)
+    _o.orc_matmul_w4s_lowering(_p(qw), _p(scales), _p(x), _p(out), M, N, K, gs, nthreads)
     return out
 
 

@@ -330,6 +330,8 @@ def test_w4s_vs_dequant_and_f5_equivalence(orc):
     np.testing.assert_allclose(f5_out, out[0], rtol=1e-4, atol=1e-5)
     f32 = orc.matmul_w4s_f32(packed, sc, x, gs, nthreads=2)
     np.testing.assert_allclose(f32, out, rtol=1e-4, atol=1e-5)
+    low = orc.matmul_w4s_lowering(packed, sc, x, gs, nthreads=2)   # the CPU baseline
+    np.testing.assert_allclose(low, out, rtol=1e-4, atol=1e-5)
 
 
 # ------------------------------------------------------------------- RoPE --
