@@ -841,6 +841,20 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
     else { if (out_mode == kAccum) DG(kPlain, kAccum); else DG(kPlain, kStore); }
 #undef DG
 #undef DGJ
+  } else if (w4d8_supported(K, m.cfg.group_size, x0, pro == kRmsNorm ? nw : nullptr)) {
+    // exact integer chunk products on v_dot8_i32_i4 (w4d8.hip)
+    W4D8Args a{};
+    for (int i = 0; i < sg.n; i++)
+      a.s[i] = W4D8Seg{(const uint8_t *)sg.s[i].W, sg.s[i].S, sg.s[i].out, K / 2,
+                       K / m.cfg.group_size, sg.s[i].rows};
+    a.n = sg.n;
+    a.K = K;
+    a.gs = m.cfg.group_size;
+    a.x0 = x0;
+    a.nw = pro == kRmsNorm ? nw : nullptr;
+    a.eps = eps;
+    a.out_mode = out_mode;
+    return launch_w4d8(a, st);
   } else {
     int tiles = 0;
     if (pair) {

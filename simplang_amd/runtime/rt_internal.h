@@ -165,6 +165,31 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
 int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X, float *O, int rows,
                int cols, int gs, int64_t off, hipStream_t st);
 int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, hipStream_t st);
+
+// Symmetric W4 GEMV with one x vector on v_dot8_i32_i4 (w4d8.hip).  Up to three
+// row segments, each with its own weights [rows, ldw bytes], scales
+// [rows, lds floats] and output; x = x0, or rmsnorm(x0) * nw when nw is set;
+// out_mode 0 stores, 1 adds to the output, 2 pairs row i of segment 0 (W1)
+// with row i of segment 1 (W3) and stores silu(h1) * h3 into segment 0's output.
+struct W4D8Seg {
+  const uint8_t *W;
+  const float *S;
+  float *out;
+  int64_t ldw, lds;
+  int rows;
+};
+struct W4D8Args {
+  W4D8Seg s[3];
+  int n;
+  int K, gs;
+  const float *x0, *nw;
+  float eps;
+  int out_mode;
+  int bstart[3];  // first block of each segment (set by launch_w4d8)
+};
+// K a multiple of 32 and of gs (a multiple of 32), K <= 20480, x0 and nw 16-byte aligned.
+bool w4d8_supported(int K, int gs, const void *x0, const void *nw);
+int launch_w4d8(const W4D8Args &a, hipStream_t st);
 // C = beta*C + A*B (beta 0 or 1), row-major with leading dimensions in elements.
 int launch_matmul_f32(const float *A, int64_t lda, const float *B, int64_t ldb, float *C,
                       int64_t ldc, int M, int N, int K, float beta, hipStream_t st);

@@ -601,6 +601,18 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     if (parts > 1)
       hipLaunchKernelGGL(w4s_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256)), dim3(256), 0, st, P,
                          parts, O, ldo, M, N);
+  } else if (M == 1 && w4d8_supported(K, gs, X, nullptr)) {
+    // one x vector: exact integer chunk products on v_dot8_i32_i4 (w4d8.hip)
+    W4D8Args a{};
+    a.s[0] = W4D8Seg{W, S, O, ldw, lds, N};
+    a.n = 1;
+    a.K = K;
+    a.gs = gs;
+    a.x0 = X;
+    a.nw = nullptr;
+    a.eps = 0.f;
+    a.out_mode = 0;
+    return launch_w4d8(a, st);
   } else if (M == 1 && K / 32 <= 32 * 16) {
     // one x vector: the barrier-free kernel, UB chunks per lane with G*UB >= K/32;
     // 8 waves per block for rows of more than 64 chunks unless there are 8 or

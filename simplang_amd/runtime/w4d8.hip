@@ -1,0 +1,418 @@
+// w4d8.hip -- symmetric W4 GEMV with one x vector on v_dot8_i32_i4.
+//
+// The product out[n] = sum_k q[n,k] * s[n, k/gs] * x[k] of
+// MatMulQuantOpLowering (ConvertSimpToMemRef.cpp:3906-4005) for the signed
+// nibble format (q in [-8,7], two per byte, low nibble = even k), computed as
+// exact integer dot products per 32-weight chunk:
+//   * x is converted once per block into six signed 4-bit limbs per element:
+//     with e the exponent of the chunk's largest |x| (|x| < 2^e),
+//     I = round(x * 2^(22-e)) is a 23-bit integer, written in balanced base 16
+//     as I = sum_j d_j 16^j with d_j in [-8,7].  Limb j of eight consecutive
+//     elements forms one dword whose nibble i is d_j of element i -- the same
+//     nibble order as the weight dword, so v_dot8_i32_i4(w, L_j) is
+//     sum_i q_i d_{j,i} exactly.
+//   * Per chunk (4 weight dwords) T = sum_j 16^j sum_d dot8(w_d, L_{j,d}) is
+//     evaluated Horner-style in one int32 chain (|T| < 32 * 8 * 2^22 = 2^30,
+//     so it is exact), then out += (s * 2^(e-22)) * float(T).  The only
+//     departure from exact products of the fp32 inputs is x rounded to 23
+//     significant bits relative to its chunk's maximum, and the order of the
+//     fp32 sums over chunks and lanes.
+// Layout: lane -> K.  A wave's lanes own fixed chunks of K (C per lane, KT
+// waves cover a row), so the limbs live in registers for the whole kernel and
+// a wave load covers a contiguous run of one row.  Rows of a block are split
+// over its teams of KT waves; each team streams its rows through a window of
+// D rows in flight (row i + D is requested right after row i is consumed),
+// which keeps the memory queues short enough for x (requested first) to
+// arrive early, and keeps arrival order close to consumption order.
+// Segments: up to three matrices with their own weights, scales and outputs
+// (Wq | Wk | Wv as one launch), or, in the paired mode, rows i of W1 and W3
+// computed by the same wave and combined as silu(h1) * h3.
+#include <algorithm>
+
+#include "rt_device.h"
+#include "rt_internal.h"
+
+namespace simp {
+namespace {
+
+// u[i]: 24-bit offset-binary values I_i + 0x888888 (six nibbles each).  L[j]
+// nibble i = nibble j of u[i] xor 8 (= the balanced digit d_j of I_i in
+// two's complement).  Byte permutes gather 16-bit halves, then bytes, then a
+// bitfield insert interleaves the nibbles of even and odd elements.
+__device__ __forceinline__ void limbs8(const uint32_t (&u)[8], uint32_t (&L)[6]) {
+  uint32_t a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    a[i] = __builtin_amdgcn_perm(u[i + 4], u[i], 0x05040100u);  // bytes 0,1 of u_i, u_i+4
+    b[i] = __builtin_amdgcn_perm(u[i + 4], u[i], 0x0C060C02u);  // byte 2 of u_i, u_i+4
+  }
+  uint32_t c[2], d[2], e[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    c[i] = __builtin_amdgcn_perm(a[i + 2], a[i], 0x06020400u);  // byte 0 of u_i, i+2, i+4, i+6
+    d[i] = __builtin_amdgcn_perm(a[i + 2], a[i], 0x07030501u);  // byte 1
+    e[i] = __builtin_amdgcn_perm(b[i + 2], b[i], 0x06020400u);  // byte 2
+  }
+  const uint32_t m = 0x0F0F0F0Fu;
+  L[0] = (c[0] & m) | ((c[1] << 4) & ~m);
+  L[1] = ((c[0] >> 4) & m) | (c[1] & ~m);
+  L[2] = (d[0] & m) | ((d[1] << 4) & ~m);
+  L[3] = ((d[0] >> 4) & m) | (d[1] & ~m);
+  L[4] = (e[0] & m) | ((e[1] << 4) & ~m);
+  L[5] = ((e[0] >> 4) & m) | (e[1] & ~m);
+#pragma unroll
+  for (int j = 0; j < 6; j++) L[j] ^= 0x88888888u;
+}
+
+// Sums each of the RM per-lane values over the 64 lanes of the wave.  After
+// the call, lane l holds the total of row l >> (6 - log2 RM) in p[0]
+// (transposed butterfly: each exchange step halves the values per lane).
+template <int RM>
+__device__ __forceinline__ void rows_reduce(float (&p)[RM], int lane) {
+  int cnt = RM;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    if (cnt > 1) {
+      const bool h = (lane & m) != 0;
+#pragma unroll
+      for (int i = 0; i < RM / 2; i++) {
+        if (i < cnt / 2) {
+          const float a = p[i], b = p[i + cnt / 2];
+          const float send = h ? a : b, keep = h ? b : a;
+          p[i] = keep + __shfl_xor(send, m);
+        }
+      }
+      cnt >>= 1;
+    } else {
+      p[0] += __shfl_xor(p[0], m);
+    }
+  }
+}
+
+__device__ __forceinline__ float silu_mul(float h1, float h3) {
+  return (h1 / (1.f + expf(-h1))) * h3;
+}
+
+// C chunks per lane, KT waves per row, NW waves per block (NW / KT teams),
+// D rows in flight per team, MULTI: more than one segment (a single segment
+// reads every argument at a fixed offset, one round of scalar loads),
+// NORM: x = x0 * nw / rms, OUT: 0 store,
+// 1 accumulate, 2 pairs (W1 row i, W3 row i) -> silu(h1) * h3 into seg 0.
+// Units are rows (pairs of rows in mode 2); the blocks of a segment split its
+// units evenly, team t of a block takes the block's units t, t + teams, ...
+template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI>
+__global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
+  constexpr int NT = 64 * NW, NTM = NW / KT, UPR = OUT == 2 ? 2 : 1;
+  static_assert(RM % UPR == 0 && RM >= D, "rows");
+  extern __shared__ __align__(16) uint32_t sm[];
+  const int K = a.K, nchunk = K >> 5, ngrp8 = K >> 3;
+  const int cpg = a.gs >> 5, cps = cpg_log2(cpg);
+  uint32_t *xl = sm;                            // [nchunk][6 limbs][4 dwords]
+  float *xf = (float *)(sm + 24 * nchunk);      // [nchunk] 2^(e-22)
+  float *ssq = xf + nchunk;                     // [NW]
+  float *red = ssq + NW;                        // [NW][RM] row totals per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int team = wave / KT, kw = wave - team * KT;
+  // x first, before anything else reads the arguments (the weight requests of
+  // every wave queue behind it otherwise):
+  // one k-group of 8 elements per thread per pass; a config covers at most
+  // 64*C*KT chunks, so XP passes cover K, all requested before any weight
+  constexpr int XP = (4 * C * KT + NW - 1) / NW;
+  float4 xa[XP], xb[XP], na[XP], nb[XP];
+#pragma unroll
+  for (int ps = 0; ps < XP; ps++) {
+    const int g8 = min((int)threadIdx.x + NT * ps, ngrp8 - 1);
+    xa[ps] = *(const float4 *)(a.x0 + 8 * g8);
+    xb[ps] = *(const float4 *)(a.x0 + 8 * g8 + 4);
+    if constexpr (NORM) {
+      na[ps] = *(const float4 *)(a.nw + 8 * g8);
+      nb[ps] = *(const float4 *)(a.nw + 8 * g8 + 4);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int lpw = (nchunk + KT * C - 1) / (KT * C);  // lanes per wave that own chunks
+  int cj[C];
+  bool aj[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    const int cc = j * KT * lpw + kw * lpw + lane;
+    cj[j] = min(cc, nchunk - 1);
+    aj[j] = lane < lpw && cc < nchunk;
+  }
+  int sgo[C];  // scale index of the lane's chunks
+#pragma unroll
+  for (int j = 0; j < C; j++) sgo[j] = chunk_group(cj[j], cpg, cps);
+  // the block's segment (blocks [bstart[s], bstart[s+1]) take segment s; in
+  // the paired mode all blocks take the pairs of segments 0 and 1) and its units
+  const int bx = (int)blockIdx.x;
+  const int sg = (OUT == 2 || !MULTI) ? 0 : (bx >= a.bstart[1]) + (bx >= a.bstart[2]);
+  const int bs0 = !MULTI ? 0 : (sg == 0 ? 0 : (sg == 1 ? a.bstart[1] : a.bstart[2]));
+  const int bs1 = !MULTI ? (int)gridDim.x
+                         : (sg == 0 ? min(a.bstart[1], (int)gridDim.x)
+                                    : (sg == 1 ? min(a.bstart[2], (int)gridDim.x) : (int)gridDim.x));
+  const int seg_units = sg == 0 ? a.s[0].rows : (sg == 1 ? a.s[1].rows : a.s[2].rows);
+  const int ub = (int)((int64_t)(bx - bs0) * seg_units / (bs1 - bs0));
+  const int ue = (int)((int64_t)(bx - bs0 + 1) * seg_units / (bs1 - bs0));
+  const int cnt = max(ue - ub - team + NTM - 1, 0) / NTM * UPR;  // rows of this team
+
+  uint4 w[D][C];
+  float s[D][C];
+  // Row pointers of the team, stepped row by row (the team's rows are units
+  // ub + team, + NTM, ... of one segment): a 64-bit add per row and matrix.
+  // Past its last row a team repeats the last row's requests (cache hits), so
+  // every load is unconditional and the compiler's wait counts stay exact.
+  const int unit0 = min(ub + team, seg_units - 1);
+  const int64_t ldw = sg == 0 ? a.s[0].ldw : (sg == 1 ? a.s[1].ldw : a.s[2].ldw);
+  const int64_t lds = sg == 0 ? a.s[0].lds : (sg == 1 ? a.s[1].lds : a.s[2].lds);
+  const uint8_t *wp = (sg == 0 ? a.s[0].W : (sg == 1 ? a.s[1].W : a.s[2].W)) + (int64_t)unit0 * ldw;
+  const float *sp = (sg == 0 ? a.s[0].S : (sg == 1 ? a.s[1].S : a.s[2].S)) + (int64_t)unit0 * lds;
+  // paired mode: the W3 row of the same unit
+  const uint8_t *wp3 = OUT == 2 ? a.s[1].W + (int64_t)unit0 * a.s[1].ldw : nullptr;
+  const float *sp3 = OUT == 2 ? a.s[1].S + (int64_t)unit0 * a.s[1].lds : nullptr;
+  auto advance = [&]() {  // to the team's next unit
+    wp += NTM * ldw;
+    sp += NTM * lds;
+    if constexpr (OUT == 2) {
+      wp3 += NTM * a.s[1].ldw;
+      sp3 += NTM * a.s[1].lds;
+    }
+  };
+  // row i of the team into a window slot; rows are requested in order
+  auto issue = [&](int slot, int i) {
+    const bool odd = OUT == 2 && (i & 1);
+    const float *srow = odd ? sp3 : sp;
+    const uint8_t *wrow = odd ? wp3 : wp;
+#pragma unroll
+    for (int j = 0; j < C; j++) s[slot][j] = *(const float *)((const char *)srow + (uint32_t)(4u * (uint32_t)sgo[j]));
+#pragma unroll
+    for (int j = 0; j < C; j++) w[slot][j] = *(const uint4 *)(wrow + (uint32_t)(16u * (uint32_t)cj[j]));
+    if (i + 1 < cnt && (OUT != 2 || odd)) advance();
+  };
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    issue(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // x -> limbs in LDS, one k-group of 8 elements per thread per pass
+  float ss = 0.f;
+#pragma unroll
+  for (int pass = 0; pass < XP; pass++) {
+    const int g8 = (int)threadIdx.x + NT * pass;
+    const float4 ya = xa[pass], yb = xb[pass];
+    float4 ma = make_float4(0.f, 0.f, 0.f, 0.f), mb = ma;
+    if constexpr (NORM) {
+      ma = na[pass];
+      mb = nb[pass];
+    }
+    float v[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+    if constexpr (NORM) {
+      if (g8 < ngrp8) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) ss = fmaf(v[k], v[k], ss);
+      }
+      const float nv[8] = {ma.x, ma.y, ma.z, ma.w, mb.x, mb.y, mb.z, mb.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] *= nv[k];
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+    // the 4 k-groups of a chunk are lanes 4c..4c+3 of one wave
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    int e;
+    frexpf(m, &e);       // m < 2^e (e = 0 for m = 0)
+    e = max(e, -100);    // chunks below 2^-101 keep fewer bits; 2^(e-22) stays normal
+    const float sc = ldexpf(1.f, 22 - e);
+    uint32_t u[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)  // fp32 bits of v*2^(22-e) + 1.5*2^23 hold round(v*2^(22-e)) + 2^22
+      u[k] = __float_as_uint(fmaf(v[k], sc, 12582912.f)) - 0x4AB77778u;
+    uint32_t L[6];
+    limbs8(u, L);
+    if (g8 < ngrp8) {
+      const int ch = g8 >> 2, dd = g8 & 3;
+#pragma unroll
+      for (int j = 0; j < 6; j++) xl[ch * 24 + 4 * j + dd] = L[j];
+      if (dd == 0) xf[ch] = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
+    }
+  }
+  if constexpr (NORM) {
+    ss = wave_sum(ss);
+    if (lane == 0) ssq[wave] = ss;
+  }
+  lds_barrier();
+  float rs = 1.f;
+  if constexpr (NORM) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; i++) t += ssq[i];
+    rs = 1.f / sqrtf(t / (float)K + a.eps);
+  }
+  uint32_t L[C][6][4];
+  float f[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+      const uint4 t = *(const uint4 *)&xl[cj[j] * 24 + 4 * q];
+      L[j][q][0] = t.x;
+      L[j][q][1] = t.y;
+      L[j][q][2] = t.z;
+      L[j][q][3] = t.w;
+    }
+    f[j] = xf[cj[j]];
+  }
+
+  // rows 0 .. RM-1 unrolled (cnt <= RM); row i + D is requested right after
+  // row i is consumed; requests past cnt repeat the last row (cache hits)
+  float p[RM];
+#pragma unroll
+  for (int i = 0; i < RM; i++) {
+    const int slot = i % D;
+    float acc = 0.f;
+    if (i < cnt) {
+#pragma unroll
+      for (int j = 0; j < C; j++) {
+        // Horner over the limbs, most significant first
+        int T = 0;
+#pragma unroll
+        for (int q = 5; q >= 0; q--) {
+          if (q < 5) T = (int)((uint32_t)T << 4);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].x, (int)L[j][q][0], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].y, (int)L[j][q][1], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].z, (int)L[j][q][2], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].w, (int)L[j][q][3], T, false);
+        }
+        acc = fmaf(aj[j] ? s[slot][j] * f[j] : 0.f, (float)T, acc);
+      }
+    }
+    p[i] = acc;
+    if (i + D < RM) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(slot, i + D);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  rows_reduce<RM>(p, lane);
+  // lanes (64/RM)*i .. hold the wave's total of row i of the team
+  constexpr int LB = RM >= 64 ? 6 : RM >= 32 ? 5 : RM >= 16 ? 4 : RM >= 8 ? 3 : RM >= 4 ? 2 : 1;
+  constexpr int GL = 1 << (6 - LB);  // lanes per row after the reduction
+  const int ir = lane >> (6 - LB);
+  if constexpr (KT == 1) {
+    // one wave per row: the writer lanes store the outputs directly (stored
+    // after the loop, so no store waits on a weight load in flight)
+    const float v = p[0] * rs;
+    if constexpr (OUT == 2) {
+      const float h3 = __shfl_down(v, GL);  // row ir + 1: the W3 half of the pair
+      if ((lane & (2 * GL - 1)) == 0 && ir < cnt)
+        a.s[0].out[ub + team + NTM * (ir >> 1)] = silu_mul(v, h3);
+    } else if ((lane & (GL - 1)) == 0 && ir < cnt) {
+      float *o = (sg == 0 ? a.s[0].out : (sg == 1 ? a.s[1].out : a.s[2].out)) + ub + team + NTM * ir;
+      *o = OUT == 1 ? *o + v : v;
+    }
+    return;
+  }
+  // KT waves per row: the wave totals meet in LDS, summed in wave order
+  if ((lane & (GL - 1)) == 0 && ir < cnt) red[wave * RM + ir] = p[0];
+  lds_barrier();
+  const int nu = ue - ub;
+  for (int q = threadIdx.x; q < nu; q += NT) {
+    const int t = q % NTM, iu = q / NTM, unit = ub + q;
+    float h[UPR];
+#pragma unroll
+    for (int sub = 0; sub < UPR; sub++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KT; k++) acc += red[(t * KT + k) * RM + iu * UPR + sub];
+      h[sub] = acc * rs;
+    }
+    if constexpr (OUT == 2) {
+      a.s[0].out[unit] = silu_mul(h[0], h[UPR - 1]);
+    } else {
+      float *o = (sg == 0 ? a.s[0].out : (sg == 1 ? a.s[1].out : a.s[2].out)) + unit;
+      *o = OUT == 1 ? *o + h[0] : h[0];
+    }
+  }
+}
+
+template <int C, int KT, int NW, int D, int RM>
+int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
+  const int nchunk = a.K / 32;
+  const size_t shm = sizeof(float) * ((size_t)25 * nchunk + NW + (size_t)NW * RM);
+  if (shm > 64 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
+  KernelTimer kt(st, "w4s_gemv_d8");
+  const bool norm = a.nw != nullptr;
+#define L8(NORMV, OUTV, MV)                                                                       \
+  hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV>), dim3((unsigned)G), dim3(64 * NW), \
+                     shm, st, a)
+  const bool multi = a.out_mode != 2 && a.n > 1;
+  if (norm) {
+    if (a.out_mode == 2) L8(true, 2, false);
+    else if (multi) L8(true, 0, true);
+    else L8(true, 0, false);
+  } else {
+    if (a.out_mode == 1) L8(false, 1, false);
+    else if (multi) L8(false, 0, true);
+    else L8(false, 0, false);
+  }
+#undef L8
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+// Blocks: at least one per CU, and enough that a team has at most 16 rows
+// (about 16 rows per team streams best); the segments' blocks are
+// proportional to their rows.
+template <int C, int KT, int NW, int D>
+int launch_cfg(W4D8Args a, hipStream_t st) {
+  constexpr int teams = NW / KT;
+  const int upr = a.out_mode == 2 ? 2 : 1;
+  const int nseg = a.out_mode == 2 ? 1 : a.n;
+  int64_t total = 0;
+  for (int i = 0; i < nseg; i++) total += a.s[i].rows;
+  const int64_t G0 = std::max<int64_t>(num_cus(), cdiv(total * upr, (int64_t)teams * 16));
+  int nb[3] = {0, 0, 0}, G = 0;
+  int64_t rows = 0;  // rows per team at most
+  for (int i = 0; i < nseg; i++) {
+    const int64_t u = a.s[i].rows;
+    int64_t b = std::max<int64_t>(cdiv(G0 * u, total), cdiv(u * upr, (int64_t)teams * 16));
+    b = std::max<int64_t>(1, std::min<int64_t>(b, u));
+    nb[i] = (int)b;
+    G += nb[i];
+    rows = std::max<int64_t>(rows, cdiv(cdiv(u, b), teams) * upr);
+  }
+  a.bstart[0] = 0;
+  a.bstart[1] = nseg > 1 ? nb[0] : INT32_MAX;
+  a.bstart[2] = nseg > 2 ? nb[0] + nb[1] : INT32_MAX;
+  if (rows <= 8) return launch_rm<C, KT, NW, D, 8>(a, G, st);
+  if (rows <= 16) return launch_rm<C, KT, NW, D, 16>(a, G, st);
+  return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: %lld rows per team", (long long)rows);
+}
+
+}  // namespace
+
+bool w4d8_supported(int K, int gs, const void *x0, const void *nw) {
+  return K > 0 && K % 32 == 0 && gs > 0 && gs % 32 == 0 && K % gs == 0 && K / 32 <= 640 &&
+         ((uintptr_t)x0 & 15) == 0 && ((uintptr_t)nw & 15) == 0;
+}
+
+int launch_w4d8(const W4D8Args &a, hipStream_t st) {
+  if (!w4d8_supported(a.K, a.gs, a.x0, a.nw) || a.n < 1 || a.n > 3 ||
+      (a.out_mode == 2 && a.n != 2))
+    return set_error(SIMP_RT_EINVAL, "w4d8: unsupported arguments (K=%d gs=%d)", a.K, a.gs);
+  for (int i = 0; i < (a.out_mode == 2 ? 1 : a.n); i++)
+    if (a.s[i].rows <= 0) return set_error(SIMP_RT_EINVAL, "w4d8: empty segment");
+  const int nchunk = a.K / 32;
+  if (nchunk <= 64) return launch_cfg<1, 1, 4, 4>(a, st);
+  if (nchunk <= 128) return launch_cfg<2, 1, 4, 4>(a, st);
+  if (nchunk <= 192) return launch_cfg<1, 3, 6, 4>(a, st);
+  if (nchunk <= 320) return launch_cfg<1, 5, 10, 4>(a, st);
+  return launch_cfg<2, 5, 10, 4>(a, st);
+}
+
+}  // namespace simp
