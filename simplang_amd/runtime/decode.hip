@@ -502,7 +502,8 @@ __global__ void __launch_bounds__(256)
     attn_split_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
                  float *__restrict__ out, float *__restrict__ ws,
                  const StepState *__restrict__ st, int dim, int kv_dim, int n_heads,
-                 int n_kv_heads, int hs, const float2 *__restrict__ rope, int max_splits) {
+                 int n_kv_heads, int hs, const float2 *__restrict__ rope, int max_splits,
+                 int nsplit, int seq_len) {
   constexpr int TP = kAttnTP, LPP = 256 / TP, KF = 32 / LPP;  // lanes per position, K float4 per lane
   __shared__ __align__(16) float qs[128];
   __shared__ __align__(16) float kn[128];
@@ -511,35 +512,31 @@ __global__ void __launch_bounds__(256)
   __shared__ __align__(16) float4 red[256];
   __shared__ float ml[2];
   const int h = blockIdx.x, s = blockIdx.y;
-  const int pos = st->pos;
   const int t0 = s * TP;
-  if (t0 > pos) return;  // uniform per block
-  const int nloc = min(TP, pos + 1 - t0);
-  const int nsplit = pos / TP + 1;
   const int kvh = h * n_kv_heads / n_heads;
   const float *kbase = kc + kvh * hs, *vbase = vc + kvh * hs;
   const int hs4 = hs >> 2;
-  // 1. cache loads of the chunk (rows t < pos only)
+  // 1. cache loads of the whole chunk, issued before pos is known (the grid has
+  // exactly the chunks of the step's position range, so no block is idle);
+  // rows at or past pos are loaded (clamped to the cache) and never used
   const int lt = threadIdx.x / LPP, sub = threadIdx.x % LPP;
   float4 kr[KF];
   {
-    const int t = t0 + lt;
+    const int t = min(t0 + lt, seq_len - 1);
     const float4 *krow = (const float4 *)(kbase + (int64_t)t * kv_dim);
 #pragma unroll
-    for (int i = 0; i < KF; i++) {
-      const int j = sub + LPP * i;
-      kr[i] = (j < hs4 && t < pos) ? krow[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int i = 0; i < KF; i++) kr[i] = krow[min(sub + LPP * i, hs4 - 1)];
   }
   const int P = 256 / hs4;  // position groups of the V sum (8 * P >= TP)
   const int d4 = threadIdx.x % hs4, pg = threadIdx.x / hs4;
   float4 vv[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) {
-    const int tl = pg + e * P, t = t0 + tl;
-    vv[e] = (pg < P && tl < TP && t < pos) ? ((const float4 *)(vbase + (int64_t)t * kv_dim))[d4]
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    const int t = min(t0 + min(pg + e * P, TP - 1), seq_len - 1);
+    vv[e] = ((const float4 *)(vbase + (int64_t)t * kv_dim))[d4];
   }
+  const int pos = st->pos;
+  const int nloc = min(TP, pos + 1 - t0);  // >= 1: chunk s starts at or before pos
   // 2. q (and, in the chunk holding pos, the new k and v) with RoPE
   const float *q = qkv + h * hs, *k = qkv + dim + kvh * hs, *v = qkv + dim + kv_dim + kvh * hs;
   const bool has_pos = pos < t0 + TP;
@@ -651,12 +648,11 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Combines the chunks of attn_split_k (nothing to do when pos < 64).
+// Combines the nsplit (> 1) chunks of attn_split_k.
 __global__ void __launch_bounds__(128)
-    attn_combine_k(const float *__restrict__ ws, float *__restrict__ out,
-                   const StepState *__restrict__ st, int hs, int max_splits) {
-  const int h = blockIdx.x, nsplit = st->pos / kAttnTP + 1;
-  if (nsplit == 1) return;
+    attn_combine_k(const float *__restrict__ ws, float *__restrict__ out, int hs, int max_splits,
+                   int nsplit) {
+  const int h = blockIdx.x;
   const float *w = ws + (int64_t)h * max_splits * (hs + 4);
   float M = -INFINITY;
   for (int s = 0; s < nsplit; s++) M = fmaxf(M, w[s * (hs + 4) + hs]);
@@ -670,49 +666,49 @@ __global__ void __launch_bounds__(128)
   }
 }
 
-// How a step computes attention, chosen on the host from pos (the graph of a
-// step is captured once per mode):
-//   kAttnOne    one 1024-thread block per head
-//   kAttnChunk  attn_split_k alone: pos < 64, one chunk per head, written directly
-//   kAttnSplit  attn_split_k over all chunks + attn_combine_k
-enum AttnMode { kAttnOne = 0, kAttnChunk = 1, kAttnSplit = 2 };
-
+// How a step computes attention, chosen on the host from pos; the graph of a
+// step is captured once per key:
+//   key 0      one 1024-thread block per head (attn_k)
+//   key n > 0  attn_split_k over the n chunks of 64 positions that cover
+//              [0, pos] (the same n for every pos in [64(n-1), 64n)), then,
+//              for n > 1, attn_combine_k
 // Workspace floats of the split attention (0: the split kernel is not used).
 int64_t attn_ws_floats(int64_t n_heads, int64_t seq_len, int hs) {
   if (hs % 4 != 0 || hs > 128) return 0;
   return n_heads * cdiv(seq_len, kAttnTP) * (hs + 4);
 }
 
-// The mode for a step at pos: the split kernel alone while one chunk covers the
+// The key for a step at pos: the split kernel alone while one chunk covers the
 // context, then the one-block kernel up to `split_from`, then split + combine.
 // split_from is where split + combine measured faster on MI355X (26/12 layers,
 // cold caches): for 32 heads of 100 from pos 64 on (pos 160: 7.8 vs 8.5 us,
 // pos 511: 11.5 vs 27.5 us per layer), for 12 heads of 64 from about 480 (pos
 // 300: 9.3 vs 8.6, pos 700: 13.1 vs 16.5).  Fewer heads leave the one-block
 // kernel more CUs per head, so it keeps up longer.
-int attn_mode(int64_t pos, bool have_ws, int64_t n_heads) {
-  if (!have_ws) return kAttnOne;
-  if (pos < kAttnTP) return kAttnChunk;
+int attn_key(int64_t pos, bool have_ws, int64_t n_heads) {
+  if (!have_ws) return 0;
+  if (pos < kAttnTP) return 1;
   const int64_t split_from = n_heads >= 32 ? kAttnTP : 480;
-  return pos >= split_from ? kAttnSplit : kAttnOne;
+  return pos >= split_from ? (int)(pos / kAttnTP + 1) : 0;
 }
 
 // One decode step's attention for one layer (cache rows [seq_len, kv_dim]).
-int launch_attention(int mode, const float *qkv, float *kc, float *vc, float *out, float *ws,
+int launch_attention(int key, const float *qkv, float *kc, float *vc, float *out, float *ws,
                      const StepState *state, int dim, int kv_dim, int n_heads, int n_kv_heads,
                      int hs, const float2 *rope, int64_t seq_len, hipStream_t st) {
-  if (mode == kAttnOne) {
+  if (key == 0) {
     hipLaunchKernelGGL(attn_k, dim3((unsigned)n_heads), dim3(kAttnThreads),
                        sizeof(float) * (size_t)seq_len, st, qkv, kc, vc, out, state, dim, kv_dim,
                        n_heads, n_kv_heads, hs, rope);
   } else {
     const int splits = (int)cdiv(seq_len, kAttnTP);
-    hipLaunchKernelGGL(attn_split_k, dim3((unsigned)n_heads, (unsigned)(mode == kAttnChunk ? 1 : splits)),
-                       dim3(256), 0, st, qkv, kc, vc, out, ws, state, dim, kv_dim, n_heads,
-                       n_kv_heads, hs, rope, splits);
-    if (mode == kAttnSplit)
+    if (key > splits) return set_error(SIMP_RT_EINVAL, "attention: %d chunks of %d", key, splits);
+    hipLaunchKernelGGL(attn_split_k, dim3((unsigned)n_heads, (unsigned)key), dim3(256), 0, st, qkv,
+                       kc, vc, out, ws, state, dim, kv_dim, n_heads, n_kv_heads, hs, rope, splits,
+                       key, (int)seq_len);
+    if (key > 1)
       hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128), 0, st,
-                         (const float *)ws, out, state, hs, splits);
+                         (const float *)ws, out, hs, splits, key);
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
@@ -808,8 +804,8 @@ struct LlamaModel {
   float *attn_ws = nullptr;  // split-attention partials; null: one block per head
   StepState *state = nullptr;
   int *prompt = nullptr, *tokens = nullptr;
-  hipGraph_t graph[3] = {};  // one step, per attention mode (AttnMode)
-  hipGraphExec_t exec[3] = {};
+  // one captured step per attention key (attn_key)
+  std::map<int, std::pair<hipGraph_t, hipGraphExec_t>> graphs;
 };
 
 namespace {
@@ -896,7 +892,7 @@ Seg seg_f32(const float *W, float *out, int rows) { return Seg{W, nullptr, out, 
 Seg seg_w4(const uint8_t *W, const float *S, float *out, int rows) { return Seg{W, S, out, rows, 0}; }
 
 // Enqueues one decode step (token and pos read from the device state).
-// attn: the AttnMode of the step's position.
+// attn: the attention key of the step's position (attn_key).
 int enqueue_step(LlamaModel &m, int attn) {
   const auto &c = m.cfg;
   const int dim = (int)c.dim, hid = (int)c.hidden_dim, kv = m.kv_dim, hs = m.hs;
@@ -1109,9 +1105,9 @@ int32_t simp_rt_llama_destroy(simp_rt_llama *h) {
   auto *m = (LlamaModel *)h;
   if (!m) return SIMP_RT_OK;
   (void)hipStreamSynchronize(m->stream);
-  for (int i = 0; i < 3; i++) {
-    if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
-    if (m->graph[i]) (void)hipGraphDestroy(m->graph[i]);
+  for (auto &kv : m->graphs) {
+    if (kv.second.second) (void)hipGraphExecDestroy(kv.second.second);
+    if (kv.second.first) (void)hipGraphDestroy(kv.second.first);
   }
   for (void *p : {(void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->h13, (void *)m->logits,
                   (void *)m->kcache, (void *)m->vcache, (void *)m->rope, (void *)m->attn_ws,
@@ -1131,7 +1127,7 @@ int32_t simp_rt_llama_forward(simp_rt_llama *h, int64_t token, int64_t pos, floa
   m->stream = cur_stream();
   StepState s{(int)token, (int)pos, 0, 0};
   SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->stream));
-  int rc = enqueue_step(*m, attn_mode(pos, m->attn_ws != nullptr, m->cfg.n_heads));
+  int rc = enqueue_step(*m, attn_key(pos, m->attn_ws != nullptr, m->cfg.n_heads));
   if (rc) return rc;
   if (logits) {
     Operand ol;
@@ -1165,10 +1161,10 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
   int rc;
   const int64_t steps = total - 1;  // the last sampled token needs no forward pass
   // step i runs at pos i
-  auto mode_of = [&](int64_t i) { return attn_mode(i, m->attn_ws != nullptr, m->cfg.n_heads); };
+  auto mode_of = [&](int64_t i) { return attn_key(i, m->attn_ws != nullptr, m->cfg.n_heads); };
   if (use_graph) {
     auto capture = [&](int mode) -> int {
-      if (m->exec[mode]) return SIMP_RT_OK;
+      if (m->graphs.count(mode)) return SIMP_RT_OK;
       SIMP_HIP(hipStreamSynchronize(st));
       hipStream_t cap;
       SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
@@ -1182,13 +1178,19 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
       (void)hipStreamDestroy(cap);
       if (rc2) return rc2;
       if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-      m->graph[mode] = g;
-      SIMP_HIP(hipGraphInstantiate(&m->exec[mode], g, nullptr, nullptr, 0));
+      hipGraphExec_t ge = nullptr;
+      const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      if (ie != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(ie, "hipGraphInstantiate");
+      }
+      m->graphs[mode] = {g, ge};
       return SIMP_RT_OK;
     };
-    for (int64_t i = 0; i < steps; i++)  // capture every mode the run needs up front
+    for (int64_t i = 0; i < steps; i++)  // capture every key the run needs up front
       if ((rc = capture(mode_of(i)))) return rc;
-    for (int64_t i = 0; i < steps; i++) SIMP_HIP(hipGraphLaunch(m->exec[mode_of(i)], st));
+    for (int64_t i = 0; i < steps; i++)
+      SIMP_HIP(hipGraphLaunch(m->graphs[mode_of(i)].second, st));
   } else {
     for (int64_t i = 0; i < steps; i++)
       if ((rc = enqueue_step(*m, mode_of(i)))) return rc;
@@ -1473,7 +1475,7 @@ int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim, kvd, dim, gs, m.off[1] + l * m.dim * kvd, st))) return rc;
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv + dim + kvd, kvd, dim, gs, m.off[2] + l * m.dim * kvd, st))) return rc;
     float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
-    if ((rc = launch_attention(attn_mode(pos, m.attn_ws != nullptr, m.nh), m.qkv, kc, vc, m.xb2,
+    if ((rc = launch_attention(attn_key(pos, m.attn_ws != nullptr, m.nh), m.qkv, kc, vc, m.xb2,
                                m.attn_ws, m.state, dim, kvd, (int)m.nh,
                                (int)m.nkv, m.hs, nullptr, m.seq, st)))  // llama2_quant.sl: no RoPE
       return rc;

@@ -18,6 +18,58 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Cross-lane moves that stay in the VALU (no LDS round trip, unlike
+// __shfl_xor's ds_bpermute): DPP quad permutes and row mirrors/rotations, and
+// gfx950's v_permlane{16,32}_swap.  Lane layouts were checked on the device.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141; // within 8 lanes: i <-> 7 - i (= lane ^ 7)
+constexpr int kDppMirror = 0x140;     // within 16 lanes: i <-> 15 - i
+constexpr int kDppRor8 = 0x128;       // within 16 lanes: i <- i + 8 (= lane ^ 8)
+// a' = rows (a0, b0, a2, b2), b' = rows (a1, b1, a3, b3) of 16 lanes
+__device__ __forceinline__ void permlane16_swap(float &a, float &b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// a' = halves (a_lo, b_lo), b' = halves (a_hi, b_hi) of 32 lanes
+__device__ __forceinline__ void permlane32_swap(float &a, float &b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+// Sum / max over the 64 lanes, every lane gets the result (VALU only).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_mov<kDppXor1>(v);
+  v += dpp_mov<kDppXor2>(v);
+  v += dpp_mov<kDppHalfMirror>(v);
+  v += dpp_mov<kDppMirror>(v);
+  float a = v, b = v;
+  permlane16_swap(a, b);
+  v = a + b;
+  a = v;
+  b = v;
+  permlane32_swap(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_mov<kDppXor1>(v));
+  v = fmaxf(v, dpp_mov<kDppXor2>(v));
+  v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_mov<kDppMirror>(v));
+  float a = v, b = v;
+  permlane16_swap(a, b);
+  v = fmaxf(a, b);
+  a = v;
+  b = v;
+  permlane32_swap(a, b);
+  return fmaxf(a, b);
+}
+
 // Workgroup barrier for LDS traffic only: this wave's LDS operations complete
 // (lgkmcnt(0)), then s_barrier.  __syncthreads() also waits for every
 // outstanding global load of the wave (its fence drains vmcnt), which would

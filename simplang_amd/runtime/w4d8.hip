@@ -66,12 +66,45 @@ __device__ __forceinline__ void limbs8(const uint32_t (&u)[8], uint32_t (&L)[6])
 
 // Sums each of the RM per-lane values over the 64 lanes of the wave.  After
 // the call, lane l holds the total of row l >> (6 - log2 RM) in p[0]
-// (transposed butterfly: each exchange step halves the values per lane).
+// (transposed butterfly: each exchange step halves the values per lane).  The
+// exchanges across 32 and 16 lanes are v_permlane{32,16}_swap (a' + b' pairs
+// each value with the other half's), the ones inside a row DPP moves with a
+// select; every step stays in the VALU.
 template <int RM>
 __device__ __forceinline__ void rows_reduce(float (&p)[RM], int lane) {
   int cnt = RM;
+  // masks 32 and 16
+  if (cnt > 1) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
+    for (int i = 0; i < RM / 2; i++) {
+      float a = p[i], b = p[i + RM / 2];
+      permlane32_swap(a, b);
+      p[i] = a + b;
+    }
+    cnt >>= 1;
+  } else {
+    float a = p[0], b = p[0];
+    permlane32_swap(a, b);
+    p[0] = a + b;
+  }
+  if (cnt > 1) {
+#pragma unroll
+    for (int i = 0; i < RM / 4; i++) {
+      if (i < cnt / 2) {
+        float a = p[i], b = p[i + cnt / 2];
+        permlane16_swap(a, b);
+        p[i] = a + b;
+      }
+    }
+    cnt >>= 1;
+  } else {
+    float a = p[0], b = p[0];
+    permlane16_swap(a, b);
+    p[0] = a + b;
+  }
+  // mask 8 (row_ror:8 is lane ^ 8), then 4 (half mirror flips bit 2; the
+  // quad steps after it cover the partner's quad), 2, 1
+  auto step = [&](auto dppfn, int m) {
     if (cnt > 1) {
       const bool h = (lane & m) != 0;
 #pragma unroll
@@ -79,14 +112,18 @@ __device__ __forceinline__ void rows_reduce(float (&p)[RM], int lane) {
         if (i < cnt / 2) {
           const float a = p[i], b = p[i + cnt / 2];
           const float send = h ? a : b, keep = h ? b : a;
-          p[i] = keep + __shfl_xor(send, m);
+          p[i] = keep + dppfn(send);
         }
       }
       cnt >>= 1;
     } else {
-      p[0] += __shfl_xor(p[0], m);
+      p[0] += dppfn(p[0]);
     }
-  }
+  };
+  step([](float v) { return dpp_mov<kDppRor8>(v); }, 8);
+  step([](float v) { return dpp_mov<kDppHalfMirror>(v); }, 4);
+  step([](float v) { return dpp_mov<kDppXor2>(v); }, 2);
+  step([](float v) { return dpp_mov<kDppXor1>(v); }, 1);
 }
 
 __device__ __forceinline__ float silu_mul(float h1, float h3) {
@@ -222,8 +259,8 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
 #pragma unroll
     for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
     // the 4 k-groups of a chunk are lanes 4c..4c+3 of one wave
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, dpp_mov<kDppXor1>(m));
+    m = fmaxf(m, dpp_mov<kDppXor2>(m));
     int e;
     frexpf(m, &e);       // m < 2^e (e = 0 for m = 0)
     e = max(e, -100);    // chunks below 2^-101 keep fewer bits; 2^(e-22) stays normal
@@ -242,7 +279,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     }
   }
   if constexpr (NORM) {
-    ss = wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     if (lane == 0) ssq[wave] = ss;
   }
   lds_barrier();
