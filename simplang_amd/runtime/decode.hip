@@ -483,166 +483,161 @@ __global__ void __launch_bounds__(kAttnThreads)
 }
 
 // Attention split over positions (head_size % 4 == 0, head_size <= 128):
-// block (h, s) of 256 threads takes positions [64 s, 64 s + 64) of head h, so
-// a long context spreads over up to seq_len / 64 CUs per head instead of one.
-// Each block issues its chunk's K rows (4 lanes per position, float4) and V
-// rows (thread (d4, pg) holds float4 d4 of positions pg, pg + P, ...) before
-// anything else, then applies RoPE to q (and to the new k for the chunk that
-// holds pos; the first head of each kv head stores k, v at pos), takes the
-// chunk's scores, a chunk-local softmax (max m_s, sum l_s) and the V sum o_s.
-// A single chunk (pos < 64) writes out = o / l directly; otherwise (o_s, m_s,
-// l_s) go to ws[h][s] and attn_combine_k forms
+// block (h, s) of NWV waves takes positions [TP s, TP s + TP) of head h,
+// TP = 16 NWV, so a long context spreads over up to seq_len / TP CUs per head
+// (4 waves and 64 positions: 8 waves and 128 positions measured 8.4 against
+// 6.4 us per launch at pos 150, one CU moving twice the rows); the grid has
+// exactly the chunks of the step's position range.  Latency is what costs
+// here, so:
+//   * every load is issued first, before pos is known: wave w's 16 positions
+//     t (4 lanes per position, float4 j = sub + 4 i of the head dimension),
+//     q and this token's k, v, and for the V sum V[t][d4] of the wave's 16
+//     positions (lane d4 < head_size / 4); then pos and the RoPE row of pos;
+//   * rows at or past pos are loaded (clamped to the cache) and never used:
+//     position pos takes this token's k, v, which the first head of each kv
+//     head stores into the cache at pos;
+//   * each wave takes the scores of its positions (4-lane DPP sums), a softmax
+//     over them (m_w, l_w) and the V sum o_w with the probabilities broadcast
+//     from their lanes (v_readlane), all in the VALU;
+//   * one barrier, then the NWV (m_w, l_w, o_w) are combined into the
+//     chunk's (m, l, o).
+// A single chunk (pos < TP) writes out = o / l directly; otherwise (o, m, l)
+// go to ws[h][s] and attn_combine_k forms
 //   out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s,  M = max_s m_s,
 // which equals the one-pass softmax-weighted sum up to rounding.  (Combining in
 // the last chunk's block instead, after a count of the others in a global
 // counter, measured ~4 us slower than the separate kernel: the agent-scope
 // round trips cost more than a launch.)
-constexpr int kAttnTP = 64;
-__global__ void __launch_bounds__(256)
+constexpr int kAttnNWV = 4, kAttnTP = 16 * kAttnNWV;
+template <int NWV>
+__global__ void __launch_bounds__(64 * NWV)
     attn_split_k(const float *__restrict__ qkv, float *__restrict__ kc, float *__restrict__ vc,
                  float *__restrict__ out, float *__restrict__ ws,
                  const StepState *__restrict__ st, int dim, int kv_dim, int n_heads,
                  int n_kv_heads, int hs, const float2 *__restrict__ rope, int max_splits,
                  int nsplit, int seq_len) {
-  constexpr int TP = kAttnTP, LPP = 256 / TP, KF = 32 / LPP;  // lanes per position, K float4 per lane
-  __shared__ __align__(16) float qs[128];
-  __shared__ __align__(16) float kn[128];
-  __shared__ __align__(16) float vn[128];
-  __shared__ float att[TP];
-  __shared__ __align__(16) float4 red[256];
-  __shared__ float ml[2];
+  constexpr int KF = 8;   // float4 per lane and position: head_size <= 128
+  constexpr int WP = 16;  // positions per wave
+  constexpr int TP = WP * NWV;
+  __shared__ __align__(16) float4 wo[NWV][32];
+  __shared__ float wml[NWV][2];
   const int h = blockIdx.x, s = blockIdx.y;
-  const int t0 = s * TP;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = s * TP, tw = t0 + WP * wave;  // first position of the wave
   const int kvh = h * n_kv_heads / n_heads;
-  const float *kbase = kc + kvh * hs, *vbase = vc + kvh * hs;
   const int hs4 = hs >> 2;
-  // 1. cache loads of the whole chunk, issued before pos is known (the grid has
-  // exactly the chunks of the step's position range, so no block is idle);
-  // rows at or past pos are loaded (clamped to the cache) and never used
-  const int lt = threadIdx.x / LPP, sub = threadIdx.x % LPP;
-  float4 kr[KF];
+  const int lp = lane >> 2, sub = lane & 3;  // position (of the wave) and quarter of this lane
+  const float4 *kbase = (const float4 *)(kc + kvh * hs), *vbase = (const float4 *)(vc + kvh * hs);
+  const int kv4 = kv_dim >> 2;
+  // 1. loads, all before pos
+  float4 kr[KF], qv[KF], kn[KF];
   {
-    const int t = min(t0 + lt, seq_len - 1);
-    const float4 *krow = (const float4 *)(kbase + (int64_t)t * kv_dim);
+    const int t = min(tw + lp, seq_len - 1);
+    const float4 *q4 = (const float4 *)(qkv + h * hs), *k4 = (const float4 *)(qkv + dim + kvh * hs);
 #pragma unroll
-    for (int i = 0; i < KF; i++) kr[i] = krow[min(sub + LPP * i, hs4 - 1)];
+    for (int i = 0; i < KF; i++) {
+      const int j = min(sub + 4 * i, hs4 - 1);
+      kr[i] = kbase[(int64_t)t * kv4 + j];
+      qv[i] = q4[j];
+      kn[i] = k4[j];
+    }
   }
-  const int P = 256 / hs4;  // position groups of the V sum (8 * P >= TP)
-  const int d4 = threadIdx.x % hs4, pg = threadIdx.x / hs4;
-  float4 vv[8];
+  const int d4 = min(lane, hs4 - 1);
+  float4 vv[WP];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const int t = min(t0 + min(pg + e * P, TP - 1), seq_len - 1);
-    vv[e] = ((const float4 *)(vbase + (int64_t)t * kv_dim))[d4];
-  }
+  for (int e = 0; e < WP; e++) vv[e] = vbase[(int64_t)min(tw + e, seq_len - 1) * kv4 + d4];
+  const float4 vn = ((const float4 *)(qkv + dim + kv_dim + kvh * hs))[d4];
   const int pos = st->pos;
-  const int nloc = min(TP, pos + 1 - t0);  // >= 1: chunk s starts at or before pos
-  // 2. q (and, in the chunk holding pos, the new k and v) with RoPE
-  const float *q = qkv + h * hs, *k = qkv + dim + kvh * hs, *v = qkv + dim + kv_dim + kvh * hs;
-  const bool has_pos = pos < t0 + TP;
-  for (int j = 2 * threadIdx.x; j < hs; j += 512) {
-    const float2 f = rope ? rope[(int64_t)pos * (hs >> 1) + (j >> 1)] : make_float2(1.f, 0.f);
-    qs[j] = q[j] * f.x - q[j + 1] * f.y;
-    qs[j + 1] = q[j] * f.y + q[j + 1] * f.x;
-    if (has_pos) {
-      kn[j] = k[j] * f.x - k[j + 1] * f.y;
-      kn[j + 1] = k[j] * f.y + k[j + 1] * f.x;
-      vn[j] = v[j];
-      vn[j + 1] = v[j + 1];
-    }
-  }
-  __syncthreads();
-  const bool writer = h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh;
-  if (has_pos && writer)
-    for (int j = threadIdx.x; j < hs; j += 256) {
-      kc[(int64_t)pos * kv_dim + kvh * hs + j] = kn[j];
-      vc[(int64_t)pos * kv_dim + kvh * hs + j] = vn[j];
-    }
-  // 3. scores of the chunk
-  const float inv_scale = 1.f / sqrtf((float)hs);
-  const float4 *q4 = (const float4 *)qs;
-  {
-    float sacc = 0.f;
-    const int t = t0 + lt;
-    if (lt < nloc) {
-      if (t < pos) {
+  float4 rf[KF];  // (cos, sin) of the two pairs of float4 j at pos
 #pragma unroll
-        for (int i = 0; i < KF; i++) {
-          const int j = sub + LPP * i;
-          if (j < hs4) {
-            const float4 a = kr[i], b = q4[j];
-            sacc = fmaf(a.x, b.x, sacc);
-            sacc = fmaf(a.y, b.y, sacc);
-            sacc = fmaf(a.z, b.z, sacc);
-            sacc = fmaf(a.w, b.w, sacc);
-          }
-        }
-      } else {
-        const float4 *kn4 = (const float4 *)kn;
-        for (int j = sub; j < hs4; j += LPP) {
-          const float4 a = kn4[j], b = q4[j];
-          sacc = fmaf(a.x, b.x, sacc);
-          sacc = fmaf(a.y, b.y, sacc);
-          sacc = fmaf(a.z, b.z, sacc);
-          sacc = fmaf(a.w, b.w, sacc);
-        }
-      }
-    }
+  for (int i = 0; i < KF; i++) {
+    const int j = min(sub + 4 * i, hs4 - 1);
+    rf[i] = rope ? ((const float4 *)(rope + (int64_t)pos * (hs >> 1)))[j] : make_float4(1.f, 0.f, 1.f, 0.f);
+  }
+  // 2. RoPE of q and of this token's k (pairs (x, y) and (z, w) of a float4)
+  auto rot = [](float4 a, float4 f) {
+    return make_float4(a.x * f.x - a.y * f.y, a.x * f.y + a.y * f.x, a.z * f.z - a.w * f.w,
+                       a.z * f.w + a.w * f.z);
+  };
 #pragma unroll
-    for (int o = 1; o < LPP; o <<= 1) sacc += __shfl_xor(sacc, o);
-    if (sub == 0) att[lt] = lt < nloc ? sacc * inv_scale : -INFINITY;
+  for (int i = 0; i < KF; i++) {
+    qv[i] = rot(qv[i], rf[i]);
+    kn[i] = rot(kn[i], rf[i]);
   }
-  __syncthreads();
-  // 4. chunk softmax (one wave: TP == 64 lanes)
-  if (threadIdx.x < 64) {
-    const float a = att[threadIdx.x];
-    const float m = wave_max(a);
-    const float e = (int)threadIdx.x < nloc ? expf(a - m) : 0.f;
-    const float l = wave_sum(e);
-    att[threadIdx.x] = e;
-    if (threadIdx.x == 0) {
-      ml[0] = m;
-      ml[1] = l;
-    }
-  }
-  __syncthreads();
-  // 5. V sum of the chunk; the P partitions added through LDS
-  if (pg < P) {
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  // the first head of each kv head stores k, v at pos (chunk holding pos)
+  const bool writer = (h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh) && pos >= t0 &&
+                      pos < t0 + TP && wave == 0;
+  if (writer) {
+    float4 *krow = (float4 *)(kc + (int64_t)pos * kv_dim + kvh * hs);
+    if (lane < 4)
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const int tl = pg + e * P;
-      if (tl < nloc) {
-        const float4 x = t0 + tl == pos ? ((const float4 *)vn)[d4] : vv[e];
-        const float a = att[tl];
-        o.x = fmaf(a, x.x, o.x);
-        o.y = fmaf(a, x.y, o.y);
-        o.z = fmaf(a, x.z, o.z);
-        o.w = fmaf(a, x.w, o.w);
-      }
+      for (int i = 0; i < KF; i++)
+        if (sub + 4 * i < hs4) krow[sub + 4 * i] = kn[i];
+    if (lane < hs4) ((float4 *)(vc + (int64_t)pos * kv_dim + kvh * hs))[lane] = vn;
+  }
+  // 3. scores of the wave's positions
+  const int t = tw + lp;
+  float sc = 0.f;
+#pragma unroll
+  for (int i = 0; i < KF; i++) {
+    if (sub + 4 * i < hs4) {
+      const float4 a = t == pos ? kn[i] : kr[i], b = qv[i];
+      sc = fmaf(a.x, b.x, sc);
+      sc = fmaf(a.y, b.y, sc);
+      sc = fmaf(a.z, b.z, sc);
+      sc = fmaf(a.w, b.w, sc);
     }
-    red[pg * hs4 + d4] = o;
+  }
+  sc += dpp_mov<kDppXor1>(sc);
+  sc += dpp_mov<kDppXor2>(sc);
+  sc = t <= pos ? sc * (1.f / sqrtf((float)hs)) : -INFINITY;
+  // 4. softmax over the wave's positions (each replicated in 4 lanes)
+  const float m = wave_max_dpp(sc);
+  const float pe = t <= pos ? expf(sc - m) : 0.f;  // t <= pos: m is finite
+  const float l = wave_sum_dpp(sub == 0 ? pe : 0.f);
+  // 5. V sum: lane d4 over the wave's positions, probabilities from lanes 4e
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int e = 0; e < WP; e++) {
+    const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 4 * e));
+    const float4 x = tw + e == pos ? vn : vv[e];
+    o.x = fmaf(pt, x.x, o.x);
+    o.y = fmaf(pt, x.y, o.y);
+    o.z = fmaf(pt, x.z, o.z);
+    o.w = fmaf(pt, x.w, o.w);
+  }
+  if (lane < hs4) wo[wave][lane] = o;
+  if (lane == 0) {
+    wml[wave][0] = m;
+    wml[wave][1] = l;
   }
   __syncthreads();
+  // 6. the NWV waves of the chunk (a wave wholly past pos has m = -inf, l = 0)
   if ((int)threadIdx.x < hs4) {
-    float4 sum = red[threadIdx.x];
-    for (int pp = 1; pp < P; pp++) {
-      const float4 x = red[pp * hs4 + threadIdx.x];
-      sum.x += x.x;
-      sum.y += x.y;
-      sum.z += x.z;
-      sum.w += x.w;
+    float M = wml[0][0];
+#pragma unroll
+    for (int w = 1; w < NWV; w++) M = fmaxf(M, wml[w][0]);
+    float L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NWV; w++) {
+      const float f = wml[w][1] > 0.f ? expf(wml[w][0] - M) : 0.f;
+      L = fmaf(f, wml[w][1], L);
+      const float4 x = wo[w][threadIdx.x];
+      O.x = fmaf(f, x.x, O.x);
+      O.y = fmaf(f, x.y, O.y);
+      O.z = fmaf(f, x.z, O.z);
+      O.w = fmaf(f, x.w, O.w);
     }
     if (nsplit == 1) {
-      const float il = 1.f / ml[1];
-      ((float4 *)(out + h * hs))[threadIdx.x] =
-          make_float4(sum.x * il, sum.y * il, sum.z * il, sum.w * il);
+      const float il = 1.f / L;
+      ((float4 *)(out + h * hs))[threadIdx.x] = make_float4(O.x * il, O.y * il, O.z * il, O.w * il);
     } else {
       float *w = ws + ((int64_t)h * max_splits + s) * (hs + 4);
-      ((float4 *)w)[threadIdx.x] = sum;
+      ((float4 *)w)[threadIdx.x] = O;
       if (threadIdx.x == 0) {
-        w[hs] = ml[0];
-        w[hs + 1] = ml[1];
+        w[hs] = M;
+        w[hs + 1] = L;
       }
     }
   }
@@ -679,12 +674,11 @@ int64_t attn_ws_floats(int64_t n_heads, int64_t seq_len, int hs) {
 }
 
 // The key for a step at pos: the split kernel alone while one chunk covers the
-// context, then the one-block kernel up to `split_from`, then split + combine.
-// split_from is where split + combine measured faster on MI355X (26/12 layers,
-// cold caches): for 32 heads of 100 from pos 64 on (pos 160: 7.8 vs 8.5 us,
-// pos 511: 11.5 vs 27.5 us per layer), for 12 heads of 64 from about 480 (pos
-// 300: 9.3 vs 8.6, pos 700: 13.1 vs 16.5).  Fewer heads leave the one-block
-// kernel more CUs per head, so it keeps up longer.
+// context, then the one-block kernel up to `split_from`, then split + combine
+// (the split kernel needs head_size % 4 == 0 and <= 128).  split_from is where
+// split + combine measured faster on MI355X (26/12 layers, cold caches): for
+// 32 heads of 100 from pos 64 on, for 12 heads of 64 from about 480.  Fewer
+// heads leave the one-block kernel more CUs per head, so it keeps up longer.
 int attn_key(int64_t pos, bool have_ws, int64_t n_heads) {
   if (!have_ws) return 0;
   if (pos < kAttnTP) return 1;
@@ -703,9 +697,9 @@ int launch_attention(int key, const float *qkv, float *kc, float *vc, float *out
   } else {
     const int splits = (int)cdiv(seq_len, kAttnTP);
     if (key > splits) return set_error(SIMP_RT_EINVAL, "attention: %d chunks of %d", key, splits);
-    hipLaunchKernelGGL(attn_split_k, dim3((unsigned)n_heads, (unsigned)key), dim3(256), 0, st, qkv,
-                       kc, vc, out, ws, state, dim, kv_dim, n_heads, n_kv_heads, hs, rope, splits,
-                       key, (int)seq_len);
+    hipLaunchKernelGGL(attn_split_k<kAttnNWV>, dim3((unsigned)n_heads, (unsigned)key),
+                       dim3(64 * kAttnNWV), 0, st, qkv, kc, vc, out, ws, state, dim, kv_dim,
+                       n_heads, n_kv_heads, hs, rope, splits, key, (int)seq_len);
     if (key > 1)
       hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128), 0, st,
                          (const float *)ws, out, hs, splits, key);
