@@ -15,12 +15,15 @@
 // Kernels, by problem size (dispatch<> picks one):
 //   * gemm_i8_dma -- problems of at least one 256x256 tile per CU, K % 64 == 0:
 //     persistent, global -> LDS DMA ring, v_mfma_i32_16x16x64_i8, 16-byte
-//     nontemporal C stores.  B given as [K,N] is first transposed into a
-//     workspace B_T[N,K] (transpose_i8), as the reference materialises B_T
-//     (ConvertSimpToMemRef.cpp:3168-3216); the u8 column sums are formed in the
-//     same pass (or by colsum_nk_i8 when B_T is given).
+//     nontemporal C stores.  B given as [K,N] with 16-byte aligned rows is
+//     read in place and transposed by the LDS reads (ds_read_b64_tr_b8); the
+//     u8 column sums come from colsum_kn_i8.  B_T[N,K] inputs are read as
+//     rows (column sums by colsum_nk_i8), and a [K,N] B the in-place read
+//     cannot serve is first transposed into a workspace B_T (transpose_i8, which
+//     forms the column sums on the way), as the reference materialises B_T
+//     (ConvertSimpToMemRef.cpp:3168-3216).
 //   * gemm_i8_nt16 -- the same tile sizes for K % 64 != 0 (K % 16 == 0), LDS
-//     double-buffered through registers.
+//     double-buffered through registers, on B_T.
 //   * gemm_i8_mfma -- smaller problems and batches (grid z): BMxBN tiles on
 //     v_mfma_i32_32x32x32_i8, K walked in double-buffered LDS tiles; B given as
 //     [K,N] is transposed on the way into LDS (4x4 byte blocks with v_perm_b32);
@@ -42,6 +45,7 @@
 namespace simp {
 namespace {
 
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
@@ -434,6 +438,13 @@ __device__ __forceinline__ uint32_t lds_offset(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
 
+// ds_read_b64_tr_b8 at byte offset `off` of the shared array `lds`.
+__device__ __forceinline__ v2i lds_read_tr8(const void *lds, uint32_t off) {
+  auto *p = (__attribute__((address_space(3))) v2i *)((__attribute__((address_space(3))) char *)(
+                (const __attribute__((address_space(3))) char *)lds) + off);
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32(p);
+}
+
 __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -462,7 +473,15 @@ __device__ __forceinline__ void block_barrier() {
 //   * The MFMA computes C^T tiles (B fragment as the first operand), so a lane
 //     ends with 4 consecutive columns of one row of C: 16-byte nontemporal
 //     stores.
-template <int STAGES, bool AU8>
+//   * B given as [K,N] (BNK false) is read as it lies, with no transpose pass:
+//     a stage's B part is 64 k-rows x 256 columns, one DMA instruction = 4
+//     k-rows (16 lanes read one row's 256 bytes), and the MFMA's K-contiguous
+//     B fragments come from ds_read_b64_tr_b8, which gives lane p of a 16-lane
+//     group byte p of the 8 rows of 16 bytes that lanes 2j, 2j+1 address.
+//     Column block cb of k-row k sits at block cb ^ (k & 7) ^ 8 ((k >> 4) & 1),
+//     so the 32 lanes of a half-wave read 32 distinct 8-byte bank pairs.
+//     Columns past N read a clamped in-bounds block; they are never stored.
+template <int STAGES, bool AU8, bool BNK>
 __global__ void __launch_bounds__(512)
     gemm_i8_dma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
@@ -479,6 +498,9 @@ __global__ void __launch_bounds__(512)
   const int drow = lane >> 2, dkc = (lane & 3) ^ ((drow >> 1) & 3);  // DMA lane -> row, chunk
   const int rslot = lrow * 4 + (lkc ^ ((lrow >> 1) & 3));          // operand lane -> slot
   const uint32_t lds_wave = lds_offset(lds) + 2048 * wave;  // wave w fills blocks 2w, 2w+1
+  // [K,N] B: lane l reads k-row 16 (l/16) + (l%16)/2 (+8), swizzle of that row
+  const uint32_t boff = (16 * lkc + (lrow >> 1)) * 256 + 8 * (lrow & 1);
+  const int bsw = (lrow >> 1) ^ ((lkc & 1) << 3);
 
   for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
     int tm, tn;
@@ -486,15 +508,26 @@ __global__ void __launch_bounds__(512)
     const int m0 = tm * BM, n0 = tn * BN;
     const int8_t *srcA0 = A + (int64_t)min(m0 + 32 * wave + drow, M - 1) * lda + 16 * dkc;
     const int8_t *srcA1 = A + (int64_t)min(m0 + 32 * wave + 16 + drow, M - 1) * lda + 16 * dkc;
-    const int8_t *srcB0 = B + (int64_t)min(n0 + 32 * wave + drow, N - 1) * ldb + 16 * dkc;
-    const int8_t *srcB1 = B + (int64_t)min(n0 + 32 * wave + 16 + drow, N - 1) * ldb + 16 * dkc;
+    const int8_t *srcB0, *srcB1;
+    if constexpr (BNK) {
+      srcB0 = B + (int64_t)min(n0 + 32 * wave + drow, N - 1) * ldb + 16 * dkc;
+      srcB1 = B + (int64_t)min(n0 + 32 * wave + 16 + drow, N - 1) * ldb + 16 * dkc;
+    } else {
+      // k-rows 8w + 4d + lane/16 (d = 0, 1) of the stage; lane l fills column
+      // block slot l%16 with block (l%16) ^ (k & 7) ^ 8 ((k >> 4) & 1)
+      const int kr = lane >> 4, sw8 = ((wave >> 1) & 1) << 3;
+      const int cb0 = (lane & 15) ^ kr ^ sw8, cb1 = (lane & 15) ^ (4 + kr) ^ sw8;
+      srcB0 = B + (int64_t)(8 * wave + kr) * ldb + min(n0 + 16 * cb0, N - 16);
+      srcB1 = B + (int64_t)(8 * wave + 4 + kr) * ldb + min(n0 + 16 * cb1, N - 16);
+    }
     auto issue = [&](int kt) {
       const uint32_t st = lds_wave + (kt % STAGES) * STAGE;
       const int64_t k0 = (int64_t)kt * BK;
       dma16(srcA0 + k0, st);
       dma16(srcA1 + k0, st + 1024);
-      dma16(srcB0 + k0, st + BM * BK);
-      dma16(srcB1 + k0, st + BM * BK + 1024);
+      const int64_t kb = BNK ? k0 : k0 * ldb;
+      dma16(srcB0 + kb, st + BM * BK);
+      dma16(srcB1 + kb, st + BM * BK + 1024);
     };
     v4i acc[FM][FN];
 #pragma unroll
@@ -509,6 +542,19 @@ __global__ void __launch_bounds__(512)
       return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
     };
     constexpr int BOFF = BM * BK / 1024;  // first B block of a stage
+    // B fragment j of stage kt: B_T rows (BNK) or two transposing reads of the
+    // [k][n] tile, k = 16 (l/16) + 8 t + (l%16)/2, bytes 8 (l & 1) of its block
+    auto bfrag = [&](int kt, int j) {
+      if constexpr (BNK) {
+        return frag(kt, BOFF + wn0 / 16 + j);
+      } else {
+        const int cb = ((wn0 >> 4) + j) ^ bsw;
+        const uint32_t base = (kt % STAGES) * STAGE + BM * BK + (cb << 4) + boff;
+        const v2i lo = lds_read_tr8(lds, base);
+        const v2i hi = lds_read_tr8(lds, base + 8 * 256);
+        return v4i{lo.x, lo.y, hi.x, hi.y};
+      }
+    };
     // The previous tile's stores (also counted by vmcnt) drain before this tile's
     // load accounting starts; every wave finished reading LDS at that tile's last
     // barrier, so its stages may be overwritten.
@@ -521,7 +567,7 @@ __global__ void __launch_bounds__(512)
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     block_barrier();  // ... and on every wave
 #pragma unroll
-    for (int j = 0; j < FN; j++) fb[0][j] = frag(0, BOFF + wn0 / 16 + j);
+    for (int j = 0; j < FN; j++) fb[0][j] = bfrag(0, j);
 #pragma unroll
     for (int i = 0; i < FM; i++) fa[i] = frag(0, wm0 / 16 + i);
     // K-step kt: certify stage kt+1, refill the buffer of stage kt (its fragments
@@ -539,7 +585,7 @@ __global__ void __launch_bounds__(512)
       if (kt + STAGES < nk) issue(kt + STAGES);
       if (more) {
 #pragma unroll
-        for (int j = 0; j < FN; j++) fb[cb ^ 1][j] = frag(kt + 1, BOFF + wn0 / 16 + j);
+        for (int j = 0; j < FN; j++) fb[cb ^ 1][j] = bfrag(kt + 1, j);
       }
 #pragma unroll
       for (int i = 0; i < FM; i++) {
@@ -674,6 +720,55 @@ __global__ void __launch_bounds__(256)
   if (lane == 0) colsum[n] = acc;
 }
 
+// colsum[n] += sum of B[k][n] over the rows k of blockIdx.y's KT-row band, as
+// signed bytes; B as [K,N] with 16-byte aligned rows, N % 16 == 0.  A lane
+// takes 16 columns (one 16-byte load per row, eight rows in flight), a wave
+// 1024 columns, the 8 waves of a workgroup every 8th row of the band; the
+// waves' sums meet in LDS and one atomic per column and workgroup adds them
+// (exact: integer sums).
+template <int KT>
+__global__ void __launch_bounds__(512)
+    colsum_kn_i8(const int8_t *__restrict__ B, int64_t ldb, int32_t *__restrict__ colsum, int K,
+                 int N) {
+  constexpr int NW = 8, U = 8;
+  __shared__ int part[NW][1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = blockIdx.x * 1024 + 16 * lane;
+  const int kb = blockIdx.y * KT, ke = min(K, kb + KT);
+  int sum[16];
+#pragma unroll
+  for (int c = 0; c < 16; c++) sum[c] = 0;
+  auto add = [&](const uint4 &v) {
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int c = 0; c < 16; c++)
+      sum[c] = __builtin_amdgcn_sdot4((int)d[c >> 2], 1 << (8 * (c & 3)), sum[c], false);
+  };
+  if (c0 < N) {
+    const int8_t *p = B + c0;
+    int k = kb + wave;
+    for (; k + NW * (U - 1) < ke; k += NW * U) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) v[u] = *(const uint4 *)(p + (int64_t)(k + NW * u) * ldb);
+#pragma unroll
+      for (int u = 0; u < U; u++) add(v[u]);
+    }
+    for (; k < ke; k += NW) add(*(const uint4 *)(p + (int64_t)k * ldb));
+  }
+#pragma unroll
+  for (int c = 0; c < 16; c++) part[wave][16 * lane + c] = sum[c];
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int col = 2 * threadIdx.x + q, n = blockIdx.x * 1024 + col;
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) t += part[w][col];
+    if (n < N) atomicAdd(colsum + n, t);
+  }
+}
+
 // Correctness fallback for shapes the MFMA path cannot load with aligned
 // vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).  Rows
 // stride over grid y; z is the batch.
@@ -791,11 +886,18 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     return SIMP_RT_OK;
   }
   if (g.batch == 1 && tiles(256, 256) >= cus && g.N % 16 == 0) {
-    // Workspace: [colsum: N int32, 256-byte aligned][B_T: N x K bytes when B is [K,N]]
+    const int tm = (int)cdiv(g.M, 256), tn = (int)cdiv(g.N, 256);
+    const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
+    // persistent grid: one workgroup per CU, a multiple of 8 (XCD round-robin)
+    const int grid = (int)std::max<int64_t>(8, std::min<int64_t>(cus, (int64_t)tm * tn) / 8 * 8);
+    // B[K,N] with 16-byte aligned rows is read in place by gemm_i8_dma
+    const bool direct = !BNK && g.K % 64 == 0 && g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0;
+    // Workspace: [colsum: N int32, 256-byte aligned][B_T: N x K bytes when B is [K,N]
+    // and not read in place]
     GemmArgs h = g;
     const size_t cs_bytes = AU8 ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
     void *ws = nullptr;
-    const size_t need = cs_bytes + (BNK ? 0 : (size_t)g.K * g.N);
+    const size_t need = cs_bytes + (BNK || direct ? 0 : (size_t)g.K * g.N);
     if (g.scratch) {
       if (need > g.scratch_bytes)
         return set_error(SIMP_RT_EINVAL,
@@ -808,6 +910,22 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       if (rc) return rc;
     }
     int32_t *colsum = AU8 ? (int32_t *)ws : nullptr;
+    if (direct) {
+      if (AU8) {
+        constexpr int KT = 64;
+        hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
+                           (int64_t)g.N, 1, g.N, (int64_t)0);
+        KernelTimer kt(st, "colsum_kn_i8");
+        hipLaunchKernelGGL(colsum_kn_i8<KT>, dim3((unsigned)cdiv(g.N, 1024), (unsigned)cdiv(g.K, KT)),
+                           dim3(512), 0, st, g.B, g.ldb, colsum, g.K, g.N);
+      }
+      KernelTimer kt(st, "gemm_i8_dma");
+      hipLaunchKernelGGL((gemm_i8_dma<4, AU8, false>), dim3(grid), dim3(512), 0, st, g.A, g.lda,
+                         g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, (const int32_t *)colsum,
+                         vec);
+      SIMP_HIP(hipGetLastError());
+      return SIMP_RT_OK;
+    }
     if (!BNK) {  // B[K,N] -> B_T[N,K], column sums on the way
       constexpr int KT = 256;
       int8_t *bt = (int8_t *)ws + cs_bytes;
@@ -823,14 +941,11 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       hipLaunchKernelGGL(colsum_nk_i8, dim3((unsigned)cdiv(g.N, 4)), dim3(256), 0, st, g.B, g.ldb,
                          colsum, g.N, g.K);
     }
-    const int tm = (int)cdiv(g.M, 256), tn = (int)cdiv(g.N, 256);
     if (g.K % 64 == 0) {
-      const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
-      // persistent grid: one workgroup per CU, a multiple of 8 (XCD round-robin)
-      const int grid = (int)std::max<int64_t>(8, std::min<int64_t>(cus, (int64_t)tm * tn) / 8 * 8);
       KernelTimer kt(st, "gemm_i8_dma");
-      hipLaunchKernelGGL((gemm_i8_dma<4, AU8>), dim3(grid), dim3(512), 0, st, h.A, h.lda, h.B,
-                         h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn, (const int32_t *)colsum, vec);
+      hipLaunchKernelGGL((gemm_i8_dma<4, AU8, true>), dim3(grid), dim3(512), 0, st, h.A, h.lda,
+                         h.B, h.ldb, h.C, h.ldc, h.M, h.N, h.K, tm, tn, (const int32_t *)colsum,
+                         vec);
     } else {
       KernelTimer kt(st, "gemm_i8_nt16");
       hipLaunchKernelGGL((gemm_i8_nt16<256, 256, 128, 2, 4, AU8>), dim3(tm * tn), dim3(512), 0,
@@ -1004,8 +1119,9 @@ int batch_i8_entry(const int8_t *a, int64_t a_off, const int64_t *as, const int6
 
 // ------------------------------------------------ allocation-free variant --
 // Scratch of simp_rt_matmul_u8s8_i32_noalloc: the column sums of B (N i32,
-// rounded up to 256 bytes) followed by B_T[N,K], as the stream workspace holds
-// them.  One copy per GPU, for the life of the process.
+// rounded up to 256 bytes) followed, when B is not read in place, by B_T[N,K],
+// as the stream workspace holds them.  One copy per GPU, for the life of the
+// process.
 constexpr size_t kNoAllocScratchBytes = (size_t(64) << 20) + (size_t(64) << 10);
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 

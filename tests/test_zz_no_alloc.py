@@ -1,9 +1,10 @@
 """simp_rt_matmul_u8s8_i32_noalloc (the allocation-free variant of
 simp_rt_matmul_u8s8_i32, whose large-shape scratch lives in a static device
 array) against simp_rt_matmul_u8s8_i32 itself, bit for bit, through the C ABI:
-two calls in a row that both take the large-tile path (column sums and B_T in
-the static scratch), the second smaller, so the second must clear and refill
-what the first left there; a small shape (no scratch); and the documented
+two calls in a row that take the large-tile path with B read in place (column
+sums in the static scratch), two that transpose B there (K % 64 != 0: column
+sums and B_T in the scratch), each second call smaller, so it must clear and
+refill what the first left; a small shape (no scratch); and the documented
 rejections (host operands, a scratch need above the maximum)."""
 import numpy as np
 import pytest
@@ -23,7 +24,8 @@ def _pair(dev, M, N, K, seed):
 
 def test_noalloc_matches_allocating_entry_point(dev):
     import torch
-    for (M, N, K, seed) in ((4096, 4096, 4096, 1), (4096, 4096, 1024, 2), (256, 320, 192, 3)):
+    for (M, N, K, seed) in ((4096, 4096, 4096, 1), (4096, 4096, 1024, 2),
+                            (4096, 4096, 2064, 4), (4096, 4096, 1040, 5), (256, 320, 192, 3)):
         print(f"[noalloc] M={M} N={N} K={K}", flush=True)
         a, b = _pair(dev, M, N, K, seed)
         want = torch.empty((M, N), dtype=torch.int32, device=dev)
@@ -41,7 +43,7 @@ def test_noalloc_rejections(dev):
     c = np.zeros((64, 64), np.int32)
     with pytest.raises(sa.SimpRTError):
         sa.matmul_u8s8_i32_noalloc(a, b, c)
-    M, N, K = 2048, 16384, 8192                            # B_T of 128 MiB > the maximum
+    M, N, K = 2048, 16384, 8208                            # K % 64 != 0: B_T of 128 MiB > the maximum
     print(f"[noalloc] rejection M={M} N={N} K={K}", flush=True)
     da = torch.zeros((M, K), dtype=torch.uint8, device=dev)
     db = torch.zeros((K, N), dtype=torch.int8, device=dev)
