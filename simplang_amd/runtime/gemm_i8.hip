@@ -37,6 +37,7 @@
 // of tiles (blocks are dispatched round-robin over XCDs), and tiles are ordered
 // in groups of 8 tile-rows so co-resident tiles share A and B in L2.
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -769,6 +770,96 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+// Skinny product, M <= MR <= 2 rows of A, B as [K,N] (K % 16 == 0, N % 8 == 0,
+// 8-byte aligned rows): a v_dot4_i32_i8 GEMV instead of MFMA tiles.
+//   * Workgroup (g, s) takes columns 512 g .. 512 g + 511 and the K band
+//     s*k_span .. +k_span; lane l the 8 columns 512 g + 8 l, wave w every 4th
+//     quad of k-rows of the band, U quads (4U 8-byte row loads) in flight.  A
+//     quad's row pieces are transposed in registers (two 4x4 byte blocks,
+//     v_perm) so each column's 4 k-values form one dword: one v_dot4 per column
+//     and row of A.  A's 4 bytes of a quad are uniform (scalar loads).
+//   * u8 x s8 flips A to A^0x80 = A-128 and adds 128 * colsum(B) over the
+//     band, summed here from the same dwords (v_dot4 against 0x01010101).
+//   * The 4 waves meet in LDS; with one K band the workgroup stores C, with
+//     more it adds its band's sums into a zero-filled C with integer atomics
+//     (exact in any order).
+// With more rows of A the dot4 work per byte of B grows and the MFMA tiles
+// (16 times the MACs per instruction) are faster from M = 3 on (measured).
+template <int MR, bool AU8, bool ATOMIC>
+__global__ void __launch_bounds__(256)
+    gemv_i8_kn(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+               int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+               int k_span) {
+  constexpr int NR = MR + (AU8 ? 1 : 0);  // sums per column: MR products (+ column sum)
+  constexpr int U = 8;                    // quads in flight per wave
+  constexpr int CW = 512;                 // columns per workgroup
+  __shared__ int red[4][NR][CW];
+  // wave index made visibly uniform, so A's bytes come through scalar loads
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x, s = blockIdx.y;
+  const int c0 = g * CW + 8 * lane;
+  const int kb = s * k_span, ke = min(K, kb + k_span);
+  int acc[NR][8];
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[r][j] = 0;
+  const int8_t *bp = B + min(c0, N - 8);  // lanes past N read in-bounds bytes, never stored
+  auto quad = [&](int k, const uint2 (&d)[4]) {
+    uint32_t o[8];
+    transpose4x4(d[0].x, d[1].x, d[2].x, d[3].x, o[0], o[1], o[2], o[3]);
+    transpose4x4(d[0].y, d[1].y, d[2].y, d[3].y, o[4], o[5], o[6], o[7]);
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      int a4 = 0;
+      if (m < M) a4 = *(const int *)(A + (int64_t)m * lda + k);
+      if constexpr (AU8) a4 ^= (int)0x80808080;
+#pragma unroll
+      for (int j = 0; j < 8; j++) acc[m][j] = __builtin_amdgcn_sdot4((int)o[j], a4, acc[m][j], false);
+    }
+    if constexpr (AU8) {
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        acc[MR][j] = __builtin_amdgcn_sdot4((int)o[j], 0x01010101, acc[MR][j], false);
+    }
+  };
+  // U quads per round trip; a band's last batch loads clamped rows for the
+  // quads past its end and skips them (bands and K are multiples of 16, so a
+  // quad is wholly inside or outside)
+  for (int k = kb + 4 * wave; k < ke; k += 16 * U) {
+    uint2 d[U][4];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        d[u][r] = *(const uint2 *)(bp + (int64_t)min(k + 16 * u + r, K - 1) * ldb);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (k + 16 * u < ke) quad(k + 16 * u, d[u]);
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) red[wave][r][8 * lane + j] = acc[r][j];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int col = threadIdx.x + 256 * h, n = g * CW + col;
+    if (n >= N) break;
+    int t[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+      t[r] = red[0][r][col] + red[1][r][col] + red[2][r][col] + red[3][r][col];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      if (m >= M) break;
+      const int v = AU8 ? t[m] + 128 * t[MR] : t[m];
+      if constexpr (ATOMIC) atomicAdd(C + (int64_t)m * ldc + n, v);
+      else C[(int64_t)m * ldc + n] = v;
+    }
+  }
+}
+
 // Correctness fallback for shapes the MFMA path cannot load with aligned
 // vector loads (K % 16 != 0, N % 4 != 0 for B[K,N], misaligned bases).  Rows
 // stride over grid y; z is the batch.
@@ -954,6 +1045,41 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     }
     SIMP_HIP(hipGetLastError());
     return SIMP_RT_OK;
+  }
+  if constexpr (!BNK) {
+    // M = 1 with B of 4 MB or more, M = 2 with 8 MB or more (smaller B is
+    // launch-bound either way): the dot4 GEMV, K split into bands for about
+    // 2048 waves (bands of at least 64 rows; more waves measured slower, the
+    // atomics growing with them), summed into a zero-filled C when there is
+    // more than one
+    const int64_t kn = (int64_t)g.K * g.N;
+    const bool gemv = (g.M == 1 && kn >= (int64_t(4) << 20)) || (g.M == 2 && kn >= (int64_t(8) << 20));
+    if (g.batch == 1 && gemv && g.N % 8 == 0 && g.ldb % 8 == 0 && ((uintptr_t)g.B & 7) == 0) {
+      const int G = (int)cdiv(g.N, 512);
+      int S = (int)std::max<int64_t>(1, std::min<int64_t>(g.K / 64, cdiv(2048, 4 * (int64_t)G)));
+      const int k_span = (int)cdiv(cdiv(g.K, S), 16) * 16;
+      S = (int)cdiv(g.K, k_span);
+      if (S > 1) {
+        const int64_t tot = (int64_t)g.M * g.N;
+        hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, g.C,
+                           g.ldc, g.M, g.N, (int64_t)0);
+      }
+      dim3 grid(G, S);
+      KernelTimer kt(st, "gemv_i8_kn");
+      auto go = [&](auto mr) {
+        constexpr int MR = decltype(mr)::value;
+        if (S > 1)
+          hipLaunchKernelGGL((gemv_i8_kn<MR, AU8, true>), grid, dim3(256), 0, st, g.A, g.lda, g.B,
+                             g.ldb, g.C, g.ldc, g.M, g.N, g.K, k_span);
+        else
+          hipLaunchKernelGGL((gemv_i8_kn<MR, AU8, false>), grid, dim3(256), 0, st, g.A, g.lda,
+                             g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, k_span);
+      };
+      if (g.M == 1) go(std::integral_constant<int, 1>{});
+      else go(std::integral_constant<int, 2>{});
+      SIMP_HIP(hipGetLastError());
+      return SIMP_RT_OK;
+    }
   }
   if (tiles(128, 128) * g.batch >= cus) return launch_mfma<128, 128, 128, 2, 2, BNK, AU8>(g, 1, st);
   if (g.M > 32) {

@@ -67,6 +67,63 @@ def test_int8_nt_variants_bit_exact(dev, orc, M, N, K):
     assert np.array_equal(_run(dev, sa.tensor_matmul_nt_i8, a.view(np.int8), bt, M, N), want_s8)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("N,K", [(264, 80), (4104, 1040), (4100, 1040), (65536, 64),
+                                 (8640, 3200), (2056, 4096)])
+def test_int8_skinny_gemv_bit_exact(dev, orc, M, N, K):
+    """M = 1 with B of 4 MB or more (M = 2: 8 MB) and B as [K,N] runs the dot4
+    GEMV, in one K band (stores, K = 64) or several (atomic sums); N % 8 != 0,
+    small B and M = 3 take the MFMA tiles."""
+    print(f"[int8-gemv] M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K, seed=11)
+    want_u8, _ = orc.matmul_i8_vnni(a, b, a_unsigned=True, nthreads=8)
+    assert np.array_equal(_run(dev, sa.matmul_u8s8_i32, a, b, M, N), want_u8)
+    want_s8, _ = orc.matmul_i8_vnni(a.view(np.int8), b, nthreads=8)
+    assert np.array_equal(_run(dev, sa.tensor_matmul_i8, a.view(np.int8), b, M, N), want_s8)
+
+
+def test_int8_skinny_gemv_call_sequence(dev, orc):
+    """Consecutive GEMV calls of other widths and depths on one stream (one K
+    band and several, so plain stores and atomic sums into the filled C), with
+    A, B and C as windows of wider arrays: the columns beside C stay intact."""
+    import torch
+    for i, (M, N, K) in enumerate([(1, 8640, 3200), (8, 264, 80), (1, 65536, 64),
+                                   (1, 264, 80), (2, 8640, 1040), (7, 8640, 3200)]):
+        print(f"[int8-gemv-seq] M={M} N={N} K={K}", flush=True)
+        a, b = _inputs(M, N, K, seed=20 + i)
+        want, _ = orc.matmul_i8_vnni(a, b, a_unsigned=True, nthreads=8)
+        ta = torch.zeros((M, K + 48), dtype=torch.uint8, device=dev)
+        ta[:, 16:16 + K] = torch.from_numpy(a).to(dev)
+        tb = torch.zeros((K, N + 16), dtype=torch.int8, device=dev)
+        tb[:, 8:8 + N] = torch.from_numpy(b).to(dev)
+        tc = torch.full((M, N + 12), -5, dtype=torch.int32, device=dev)
+        sa.matmul_u8s8_i32(ta[:, 16:16 + K], tb[:, 8:8 + N], tc[:, 8:8 + N])
+        torch.cuda.synchronize()
+        out = tc.cpu().numpy()
+        assert np.array_equal(out[:, 8:8 + N], want), (M, N, K)
+        assert (out[:, :8] == -5).all() and (out[:, 8 + N:] == -5).all()
+
+
+@pytest.mark.parametrize("pad", [64, 4])
+def test_int8_large_b_window(dev, orc, pad):
+    """Large-tile path with B as a column window of a wider [K, N + pad] array:
+    16-byte aligned rows (pad 64) are read in place, others (pad 4) are
+    transposed first; rows of C are checked in full against the oracle."""
+    import torch
+    M, N, K = 4096, 4096, 1024
+    print(f"[int8-bwin] pad={pad}", flush=True)
+    a, b = _inputs(M, N, K, seed=31)
+    tb = torch.zeros((K, N + pad), dtype=torch.int8, device=dev)
+    tb[:, pad // 2:pad // 2 + N] = torch.from_numpy(b).to(dev)
+    ta = torch.from_numpy(a).to(dev)
+    tc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    sa.matmul_u8s8_i32(ta, tb[:, pad // 2:pad // 2 + N], tc)
+    torch.cuda.synchronize()
+    rows = np.r_[0:8, 1000:1004, M - 8:M]
+    want, _ = orc.matmul_i8_vnni(np.ascontiguousarray(a[rows]), b, a_unsigned=True, nthreads=8)
+    assert np.array_equal(tc.cpu().numpy()[rows], want)
+
+
 @pytest.mark.parametrize("M,N,K", [(5, 9, 13), (3, 130, 100), (17, 6, 24)])
 def test_int8_unaligned_shapes_fallback(dev, orc, M, N, K):
     """K % 16 != 0 or N % 4 != 0 take the generic kernel; still bit-exact."""
