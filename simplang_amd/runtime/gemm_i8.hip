@@ -635,6 +635,245 @@ __global__ void __launch_bounds__(512)
   }
 }
 
+// Mid-size kernel (K % 128 == 0): BMxBN tiles (128x128 or 64x64, one per CU at
+// 2048^2 / 1024^2 outputs), 4 waves of (BM/2)x(BN/2), v_mfma_i32_16x16x64_i8,
+// K-stages of 128 through a ring of SLOTS stages filled by LDS DMA.
+//   * A and B_T rows contribute 128 bytes (a whole line) per stage: a DMA
+//     instruction is 8 rows x 128 B, lane l row l/8, 16-byte chunk
+//     (l%8) ^ ((row >> 1) & 7), which keeps the 16 lanes of an operand read
+//     (rows R0..R0+15, one chunk) on 16 distinct 4-bank groups.
+//   * B as [K,N] is read in place: a stage's B part is 128 k-rows of BN bytes,
+//     turned into K-contiguous fragments by ds_read_b64_tr_b8 (as in
+//     gemm_i8_dma), with column block cb of k-row k at cb ^ fB(k), fB chosen
+//     per row width so that each half-wave's 32 reads cover the 64 banks.
+//   * A stage is two K-steps of 64; fragments are double-buffered in registers
+//     and the stage's one barrier sits between its two K-steps (as in the
+//     whole-line variant of gemm_i8_dma): this wave's DMAs of stage s+1 are
+//     waited for, every wave has read stage s, and stage s+SLOTS is issued into
+//     its slot.  With K / 128 <= SLOTS the whole of K is in flight at once.
+//   * u8 x s8: the waves of the first wave row also sum their B fragments
+//     (v_dot4 against 0x01010101) into the column sums, which meet in LDS.
+// s_waitcnt vmcnt(D * n) for a run-time n in 0..Q (the immediate must be a constant)
+template <int D, int Q>
+__device__ __forceinline__ void wait_vm_le(int n) {
+  if constexpr (Q >= 0) {
+    if (n == Q) __builtin_amdgcn_s_waitcnt(waitcnt_vm(D * Q));
+    else wait_vm_le<D, Q - 1>(n);
+  }
+}
+
+template <int BN>
+__device__ __forceinline__ int ring_fb(int lrow, int lkc) {
+  if constexpr (BN == 256) return (lrow >> 1) ^ ((lkc & 1) << 3);
+  else if constexpr (BN == 128) return ((lrow >> 2) & 3) | ((lkc & 1) << 2);
+  else return ((lrow >> 3) & 1) | ((lkc & 1) << 1);
+}
+template <int BN>
+__device__ __forceinline__ int ring_fb_row(int k) {  // the same swizzle by k-row
+  if constexpr (BN == 256) return (k & 7) ^ (((k >> 4) & 1) << 3);
+  else if constexpr (BN == 128) return ((k >> 1) & 3) | (((k >> 4) & 1) << 2);
+  else return ((k >> 2) & 1) | (((k >> 4) & 1) << 1);
+}
+
+// v_mfma_i32_16x16x64_i8 with the accumulator held in the same VGPRs across
+// the K loop (inline asm: the compiler's own allocation renames the
+// accumulators between unrolled K-steps, copying them through AGPRs and
+// chaining MFMAs through the copies).  The compiler does not insert the wait
+// states such an MFMA needs after VALU writes of its sources or before VALU
+// reads of its result; the caller places them.
+__device__ __forceinline__ void mfma_v(v4i &acc, const v4i &a, const v4i &b) {
+  asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+
+template <int BM, int BN, int WGM, int WGN, int SLOTS, bool AU8, bool BNK>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+    gemm_i8_ring(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
+                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
+                 int tiles_m, int tiles_n, int vec_store) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+  constexpr int BK = 128;
+  constexpr int SA = BM * BK, SB = BN * BK, STAGE = SA + SB;  // bytes
+  constexpr int DA = SA / 1024 / NW, DB = SB / 1024 / NW;    // DMA instructions per wave
+  constexpr int DPW = DA + DB;
+  static_assert(DA >= 1 && DB >= 1 && DPW * (SLOTS - 1) <= 63, "ring shape");
+  __shared__ uint4 lds[SLOTS * STAGE / 16];
+  __shared__ int cs_lds[AU8 ? BN : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wy = wave / WGN, wx = wave % WGN;
+  const int wm0 = wy * WM, wn0 = wx * WN;
+  const int ns = K / BK;
+  const int ntiles = tiles_m * tiles_n;
+  const int lrow = lane & 15, lkc = lane >> 4;
+  const uint32_t lds_base = lds_offset(lds);
+  const int fa = (lrow >> 1) & 7;   // A / B_T chunk swizzle of this lane's operand rows
+  const int fb = ring_fb<BN>(lrow, lkc);
+  constexpr int RPI = 1024 / BN, LPR = BN / 16;  // [K,N] B: k-rows per DMA, lanes per k-row
+
+  for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
+    int tm, tn;
+    tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int8_t *srcA[DA], *srcB[DB];
+#pragma unroll
+    for (int i = 0; i < DA; i++) {
+      const int r = 8 * (wave * DA + i) + (lane >> 3);  // row within the tile
+      srcA[i] = A + (int64_t)min(m0 + r, M - 1) * lda + 16 * ((lane & 7) ^ ((r >> 1) & 7));
+    }
+#pragma unroll
+    for (int i = 0; i < DB; i++) {
+      if constexpr (BNK) {
+        const int r = 8 * (wave * DB + i) + (lane >> 3);
+        srcB[i] = B + (int64_t)min(n0 + r, N - 1) * ldb + 16 * ((lane & 7) ^ ((r >> 1) & 7));
+      } else {
+        const int kr = RPI * (wave * DB + i) + lane / LPR;  // k-row within the stage
+        const int cb = (lane % LPR) ^ ring_fb_row<BN>(kr);
+        srcB[i] = B + (int64_t)kr * ldb + min(n0 + 16 * cb, N - 16);
+      }
+    }
+    auto issue = [&](int st) {
+      const uint32_t dst = lds_base + (uint32_t)(st % SLOTS) * STAGE;
+      const int64_t ka = (int64_t)st * BK;
+#pragma unroll
+      for (int i = 0; i < DA; i++) dma16(srcA[i] + ka, dst + 1024 * (wave * DA + i));
+      const int64_t kb = BNK ? ka : ka * ldb;
+#pragma unroll
+      for (int i = 0; i < DB; i++) dma16(srcB[i] + kb, dst + SA + 1024 * (wave * DB + i));
+    };
+    auto afrag = [&](int st, int r0, int h) {
+      const uint32_t off = (uint32_t)(st % SLOTS) * STAGE + (r0 + lrow) * 128 +
+                           (((4 * h + lkc) ^ fa) << 4);
+      const uint4 v = lds[off >> 4];
+      return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+    };
+    auto bfrag = [&](int st, int c0, int h) {
+      if constexpr (BNK) {
+        const uint32_t off = (uint32_t)(st % SLOTS) * STAGE + SA + (c0 + lrow) * 128 +
+                             (((4 * h + lkc) ^ fa) << 4);
+        const uint4 v = lds[off >> 4];
+        return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+      } else {
+        const uint32_t off = (uint32_t)(st % SLOTS) * STAGE + SA +
+                             (64 * h + 16 * lkc + (lrow >> 1)) * BN +
+                             ((((c0 >> 4) ^ fb)) << 4) + 8 * (lrow & 1);
+        const v2i lo = lds_read_tr8(lds, off);
+        const v2i hi = lds_read_tr8(lds, off + 8 * BN);
+        return v4i{lo.x, lo.y, hi.x, hi.y};
+      }
+    };
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    int csum[FN];
+#pragma unroll
+    for (int j = 0; j < FN; j++) csum[j] = 0;
+    v4i fra[2][FM], frb[2][FN];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7");  // VALU writes of the accumulators -> MFMA reads
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // previous tile's stores
+    const int first = min(SLOTS, ns);
+    for (int st = 0; st < first; st++) issue(st);
+    // stage 0 done on this wave (the later stages may be outstanding) ...
+    auto wait_after = [&](int n_after) { wait_vm_le<DPW, SLOTS - 1>(n_after); };
+    wait_after(first - 1);
+    block_barrier();  // ... and on every wave
+#pragma unroll
+    for (int j = 0; j < FN; j++) frb[0][j] = bfrag(0, wn0 + 16 * j, 0);
+#pragma unroll
+    for (int i = 0; i < FM; i++) fra[0][i] = afrag(0, wm0 + 16 * i, 0);
+    auto mfmas = [&](int cb) {
+      if constexpr (AU8) {
+        if (wy == 0) {
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              csum[j] = __builtin_amdgcn_sdot4(frb[cb][j][q], 0x01010101, csum[j], false);
+        }
+      }
+      v4i a[FM];
+#pragma unroll
+      for (int i = 0; i < FM; i++) a[i] = AU8 ? (fra[cb][i] ^ (int)0x80808080) : fra[cb][i];
+      if constexpr (AU8) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7");  // VALU writes (a ^ 0x80) -> MFMA reads
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) mfma_v(acc[i][j], frb[cb][j], a[i]);
+    };
+    for (int s = 0; s < ns; s++) {
+      // K-step (s,0): read (s,1)'s fragments, run (s,0)
+#pragma unroll
+      for (int j = 0; j < FN; j++) frb[1][j] = bfrag(s, wn0 + 16 * j, 1);
+#pragma unroll
+      for (int i = 0; i < FM; i++) fra[1][i] = afrag(s, wm0 + 16 * i, 1);
+      mfmas(0);
+      const bool more = s + 1 < ns;
+      // stages issued so far: 0 .. min(s + SLOTS - 1, ns - 1); stage s+1 must be done
+      if (more) wait_after(min(SLOTS - 2, ns - 2 - s));
+      __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0);  // this wave's reads of stage s landed
+      block_barrier();
+      if (s + SLOTS < ns) issue(s + SLOTS);
+      // K-step (s,1): read (s+1,0)'s fragments, run (s,1)
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) frb[0][j] = bfrag(s + 1, wn0 + 16 * j, 0);
+#pragma unroll
+        for (int i = 0; i < FM; i++) fra[0][i] = afrag(s + 1, wm0 + 16 * i, 0);
+      }
+      mfmas(1);
+    }
+    // MFMA results -> VALU reads of the same registers
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // u8 x s8: column sums of this tile's columns, from the first wave row
+    if constexpr (AU8) {
+      if (wy == 0) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          int t = csum[j];
+          t += __shfl_xor(t, 16);
+          t += __shfl_xor(t, 32);
+          if (lkc == 0) cs_lds[wn0 + 16 * j + lrow] = t;
+        }
+      }
+      __syncthreads();
+    }
+    // acc[i][j][r] = C[m0 + wm0 + 16 i + l%16][n0 + wn0 + 16 j + 4 (l/16) + r]
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int cl = wn0 + 16 * j + 4 * lkc, col = n0 + cl;
+      v4i bias = v4i{0, 0, 0, 0};
+      if constexpr (AU8) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) bias[r] = cs_lds[cl + r] * 128;
+      }
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int row = m0 + wm0 + 16 * i + lrow;
+        if (row >= M || col >= N) continue;
+        const v4i v = acc[i][j] + bias;
+        int32_t *dst = C + (int64_t)row * ldc + col;
+        if (vec_store) {
+          *(v4i *)dst = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            if (col + r < N) dst[r] = v[r];
+        }
+      }
+    }
+    if constexpr (AU8) __syncthreads();  // cs_lds is rewritten by the next tile
+  }
+}
+
 // B[K,N] -> B_T[N,K] (K % 16 == 0, N % 16 == 0): a workgroup takes 128
 // columns and KT rows of B, through 128x128 LDS tiles.  Reads: 8 lanes per row,
 // 16 bytes each, so a wave reads whole 128-byte lines.  Writes: a thread
@@ -1045,6 +1284,31 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     }
     SIMP_HIP(hipGetLastError());
     return SIMP_RT_OK;
+  }
+  {
+    // mid sizes (K % 128 == 0): the ring kernel, 128x128 tiles from about half
+    // a tile per CU on, else 64x64 tiles; 8 waves (2 per SIMD) either way
+    const bool ok = g.batch == 1 && g.K % 128 == 0 && g.N % 16 == 0 && g.ldb % 16 == 0 &&
+                    ((uintptr_t)g.B & 15) == 0;
+    const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
+    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) {
+      const int tm = (int)cdiv(g.M, 128), tn = (int)cdiv(g.N, 128);
+      const int grid = (int)std::min<int64_t>((int64_t)tm * tn, cus);
+      KernelTimer kt(st, "gemm_i8_ring");
+      hipLaunchKernelGGL((gemm_i8_ring<128, 128, 4, 2, 4, AU8, BNK>), dim3(grid), dim3(512), 0,
+                         st, g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, vec);
+      SIMP_HIP(hipGetLastError());
+      return SIMP_RT_OK;
+    }
+    if (ok && tiles(64, 64) >= cus / 2 && g.M > 32) {
+      const int tm = (int)cdiv(g.M, 64), tn = (int)cdiv(g.N, 64);
+      const int grid = (int)std::min<int64_t>((int64_t)tm * tn, cus);
+      KernelTimer kt(st, "gemm_i8_ring");
+      hipLaunchKernelGGL((gemm_i8_ring<64, 64, 4, 2, 8, AU8, BNK>), dim3(grid), dim3(512), 0, st,
+                         g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, vec);
+      SIMP_HIP(hipGetLastError());
+      return SIMP_RT_OK;
+    }
   }
   if constexpr (!BNK) {
     // M = 1 with B of 4 MB or more, M = 2 with 8 MB or more (smaller B is

@@ -67,6 +67,24 @@ def test_int8_nt_variants_bit_exact(dev, orc, M, N, K):
     assert np.array_equal(_run(dev, sa.tensor_matmul_nt_i8, a.view(np.int8), bt, M, N), want_s8)
 
 
+@pytest.mark.parametrize("M,N,K", [(1024, 1024, 128), (1024, 1024, 256), (1000, 1040, 1024),
+                                   (768, 768, 768), (2048, 2048, 384), (2000, 2064, 1152),
+                                   (1536, 1024, 2048)])
+def test_int8_ring_kernel_bit_exact(dev, orc, M, N, K):
+    """Mid sizes with K % 128 == 0 run the ring kernel (64x64 or 128x128 tiles,
+    K-stages of 128, whole K in flight when it fits): one stage, fewer stages
+    than slots, ragged M and N, B as [K,N] and as B_T, u8 and s8 A."""
+    print(f"[int8-ring] M={M} N={N} K={K}", flush=True)
+    a, b = _inputs(M, N, K, seed=13)
+    bt = np.ascontiguousarray(b.T)
+    want_u8, _ = orc.matmul_i8_vnni(a, b, a_unsigned=True, nthreads=8)
+    assert np.array_equal(_run(dev, sa.matmul_u8s8_i32, a, b, M, N), want_u8)
+    assert np.array_equal(_run(dev, sa.matmul_nt_u8s8_i32, a, bt, M, N), want_u8)
+    want_s8, _ = orc.matmul_i8_vnni(a.view(np.int8), b, nthreads=8)
+    assert np.array_equal(_run(dev, sa.tensor_matmul_i8, a.view(np.int8), b, M, N), want_s8)
+    assert np.array_equal(_run(dev, sa.tensor_matmul_nt_i8, a.view(np.int8), bt, M, N), want_s8)
+
+
 @pytest.mark.parametrize("M", [1, 2, 3])
 @pytest.mark.parametrize("N,K", [(264, 80), (4104, 1040), (4100, 1040), (65536, 64),
                                  (8640, 3200), (2056, 4096)])
