@@ -112,18 +112,20 @@ def test_110m_f32_greedy_256(dev, orc):
 
 
 def test_3b_w4_logits_and_greedy(dev, orc):
-    """BASELINE configs[4] at full size: logits at 3 positions and 4 greedy steps
-    (the oracle needs ~1 s per 3B step on the host)."""
+    """BASELINE configs[4] at full size: logits at 3 positions and 16 greedy
+    steps through the captured step graphs (the oracle needs ~1 s per 3B step
+    on the host)."""
     import torch
     cfg = CFG_3B_W4
     w = make_model(cfg, dev, seed=3)
     prompt = np.random.default_rng(3).integers(0, cfg["vocab_size"], 3).astype(np.int32)
     print("[decode] 3B W4 logits", flush=True)
     _check_logits(dev, orc, cfg, w, prompt)
+    print("[decode] 3B W4 greedy 16", flush=True)
     m = sa.Llama(cfg, w)
-    got = m.generate(prompt, 4, use_graph=True)
+    got = m.generate(prompt, 16, use_graph=True)
     m.close()
-    want, margins = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 4)
+    want, margins = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 16)
     assert np.array_equal(got, want), (got, want, margins)
     del w
     torch.cuda.empty_cache()
