@@ -186,6 +186,10 @@ struct W4D8Args {
   float eps;
   int out_mode;
   int bstart[3];  // first block of each segment (set by launch_w4d8)
+  // mx > 1 (at most 4) x vectors, rows ldx floats apart, outputs rows ldo apart
+  // (one segment, out_mode 0, no norm)
+  int mx = 1;
+  int64_t ldx = 0, ldo = 0;
 };
 // K a multiple of 32 and of gs (a multiple of 32), K <= 20480, x0 and nw 16-byte aligned.
 bool w4d8_supported(int K, int gs, const void *x0, const void *nw);

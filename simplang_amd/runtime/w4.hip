@@ -576,6 +576,24 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     const int64_t tot = (int64_t)M * N;
     hipLaunchKernelGGL(w4s_generic, dim3((unsigned)cdiv(tot, 256)), dim3(256), 0, st, W, ldw, S,
                        lds, X, ldx, O, ldo, M, N, K, gs);
+  } else if (M >= 2 && M <= 4 && w4d8_supported(K, gs, X, nullptr) &&
+             (size_t)100 * (M <= 2 ? 2 : 4) * (K / 32) + 4096 <= 160 * 1024) {
+    // up to four x vectors: the dot8 kernel with the limbs of every vector in
+    // registers, the weights read once (w4d8.hip); their limb tables (100
+    // bytes per vector and chunk) must fit the 160 KB of LDS
+    W4D8Args a{};
+    a.s[0] = W4D8Seg{W, S, O, ldw, lds, N};
+    a.n = 1;
+    a.K = K;
+    a.gs = gs;
+    a.x0 = X;
+    a.nw = nullptr;
+    a.eps = 0.f;
+    a.out_mode = 0;
+    a.mx = M;
+    a.ldx = ldx;
+    a.ldo = ldo;
+    return launch_w4d8(a, st);
   } else if (M >= 2 && gs == 32) {
     // several x vectors, groups of 32: f16 MFMA.  A block takes 4 waves x RT
     // tiles of 16 weight rows and `chunks` chunks of 8 groups of K; the K parts

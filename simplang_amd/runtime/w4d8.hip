@@ -1,4 +1,4 @@
-// w4d8.hip -- symmetric W4 GEMV with one x vector on v_dot8_i32_i4.
+// w4d8.hip -- symmetric W4 GEMV with one to four x vectors on v_dot8_i32_i4.
 //
 // The product out[n] = sum_k q[n,k] * s[n, k/gs] * x[k] of
 // MatMulQuantOpLowering (ConvertSimpToMemRef.cpp:3906-4005) for the signed
@@ -135,19 +135,23 @@ __device__ __forceinline__ float silu_mul(float h1, float h3) {
 // reads every argument at a fixed offset, one round of scalar loads),
 // NORM: x = x0 * nw / rms, OUT: 0 store,
 // 1 accumulate, 2 pairs (W1 row i, W3 row i) -> silu(h1) * h3 into seg 0.
+// MX x vectors (rows of x ldx apart, of out ldo apart; a.mx of them are real):
+// each weight dword meets the limbs of every vector, so the weights are read
+// once for all of them.
 // Units are rows (pairs of rows in mode 2); the blocks of a segment split its
 // units evenly, team t of a block takes the block's units t, t + teams, ...
-template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI>
+template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI, int MX>
 __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   constexpr int NT = 64 * NW, NTM = NW / KT, UPR = OUT == 2 ? 2 : 1;
   static_assert(RM % UPR == 0 && RM >= D, "rows");
+  static_assert(MX == 1 || (OUT == 0 && !NORM && !MULTI), "several x vectors: plain stores");
   extern __shared__ __align__(16) uint32_t sm[];
   const int K = a.K, nchunk = K >> 5, ngrp8 = K >> 3;
   const int cpg = a.gs >> 5, cps = cpg_log2(cpg);
-  uint32_t *xl = sm;                            // [nchunk][6 limbs][4 dwords]
-  float *xf = (float *)(sm + 24 * nchunk);      // [nchunk] 2^(e-22)
-  float *ssq = xf + nchunk;                     // [NW]
-  float *red = ssq + NW;                        // [NW][RM] row totals per wave
+  uint32_t *xl = sm;                            // [MX][nchunk][6 limbs][4 dwords]
+  float *xf = (float *)(sm + MX * 24 * nchunk); // [MX][nchunk] 2^(e-22)
+  float *ssq = xf + MX * nchunk;                // [NW]
+  float *red = ssq + NW;                        // [NW][MX][RM] row totals per wave
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int team = wave / KT, kw = wave - team * KT;
@@ -156,12 +160,16 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   // one k-group of 8 elements per thread per pass; a config covers at most
   // 64*C*KT chunks, so XP passes cover K, all requested before any weight
   constexpr int XP = (4 * C * KT + NW - 1) / NW;
-  float4 xa[XP], xb[XP], na[XP], nb[XP];
+  float4 xa[MX][XP], xb[MX][XP], na[XP], nb[XP];
 #pragma unroll
   for (int ps = 0; ps < XP; ps++) {
     const int g8 = min((int)threadIdx.x + NT * ps, ngrp8 - 1);
-    xa[ps] = *(const float4 *)(a.x0 + 8 * g8);
-    xb[ps] = *(const float4 *)(a.x0 + 8 * g8 + 4);
+#pragma unroll
+    for (int m = 0; m < MX; m++) {
+      const float *xr = a.x0 + (int64_t)min(m, a.mx - 1) * a.ldx;  // vectors past mx repeat the last
+      xa[m][ps] = *(const float4 *)(xr + 8 * g8);
+      xb[m][ps] = *(const float4 *)(xr + 8 * g8 + 4);
+    }
     if constexpr (NORM) {
       na[ps] = *(const float4 *)(a.nw + 8 * g8);
       nb[ps] = *(const float4 *)(a.nw + 8 * g8 + 4);
@@ -237,9 +245,11 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   // x -> limbs in LDS, one k-group of 8 elements per thread per pass
   float ss = 0.f;
 #pragma unroll
-  for (int pass = 0; pass < XP; pass++) {
+  for (int pass = 0; pass < XP; pass++)
+#pragma unroll
+  for (int mv = 0; mv < MX; mv++) {
     const int g8 = (int)threadIdx.x + NT * pass;
-    const float4 ya = xa[pass], yb = xb[pass];
+    const float4 ya = xa[mv][pass], yb = xb[mv][pass];
     float4 ma = make_float4(0.f, 0.f, 0.f, 0.f), mb = ma;
     if constexpr (NORM) {
       ma = na[pass];
@@ -274,8 +284,9 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     if (g8 < ngrp8) {
       const int ch = g8 >> 2, dd = g8 & 3;
 #pragma unroll
-      for (int j = 0; j < 6; j++) xl[ch * 24 + 4 * j + dd] = L[j];
-      if (dd == 0) xf[ch] = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
+      for (int j = 0; j < 6; j++) xl[(mv * nchunk + ch) * 24 + 4 * j + dd] = L[j];
+      if (dd == 0)
+        xf[mv * nchunk + ch] = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
     }
   }
   if constexpr (NORM) {
@@ -290,60 +301,75 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     for (int i = 0; i < NW; i++) t += ssq[i];
     rs = 1.f / sqrtf(t / (float)K + a.eps);
   }
-  uint32_t L[C][6][4];
-  float f[C];
+  uint32_t L[MX][C][6][4];
+  float f[MX][C];
+#pragma unroll
+  for (int mv = 0; mv < MX; mv++)
 #pragma unroll
   for (int j = 0; j < C; j++) {
 #pragma unroll
     for (int q = 0; q < 6; q++) {
-      const uint4 t = *(const uint4 *)&xl[cj[j] * 24 + 4 * q];
-      L[j][q][0] = t.x;
-      L[j][q][1] = t.y;
-      L[j][q][2] = t.z;
-      L[j][q][3] = t.w;
+      const uint4 t = *(const uint4 *)&xl[(mv * nchunk + cj[j]) * 24 + 4 * q];
+      L[mv][j][q][0] = t.x;
+      L[mv][j][q][1] = t.y;
+      L[mv][j][q][2] = t.z;
+      L[mv][j][q][3] = t.w;
     }
-    f[j] = xf[cj[j]];
+    f[mv][j] = xf[mv * nchunk + cj[j]];
   }
 
   // rows 0 .. RM-1 unrolled (cnt <= RM); row i + D is requested right after
   // row i is consumed; requests past cnt repeat the last row (cache hits)
-  float p[RM];
+  float p[MX][RM];
 #pragma unroll
   for (int i = 0; i < RM; i++) {
     const int slot = i % D;
-    float acc = 0.f;
+    float acc[MX];
+#pragma unroll
+    for (int mv = 0; mv < MX; mv++) acc[mv] = 0.f;
     if (i < cnt) {
 #pragma unroll
-      for (int j = 0; j < C; j++) {
+      for (int j = 0; j < C; j++)
+#pragma unroll
+      for (int mv = 0; mv < MX; mv++) {
         // Horner over the limbs, most significant first
         int T = 0;
 #pragma unroll
         for (int q = 5; q >= 0; q--) {
           if (q < 5) T = (int)((uint32_t)T << 4);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].x, (int)L[j][q][0], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].y, (int)L[j][q][1], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].z, (int)L[j][q][2], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].w, (int)L[j][q][3], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].x, (int)L[mv][j][q][0], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].y, (int)L[mv][j][q][1], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].z, (int)L[mv][j][q][2], T, false);
+          T = __builtin_amdgcn_sdot8((int)w[slot][j].w, (int)L[mv][j][q][3], T, false);
         }
-        acc = fmaf(aj[j] ? s[slot][j] * f[j] : 0.f, (float)T, acc);
+        acc[mv] = fmaf(aj[j] ? s[slot][j] * f[mv][j] : 0.f, (float)T, acc[mv]);
       }
     }
-    p[i] = acc;
+#pragma unroll
+    for (int mv = 0; mv < MX; mv++) p[mv][i] = acc[mv];
     if (i + D < RM) {
       __builtin_amdgcn_sched_barrier(0);
       issue(slot, i + D);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  rows_reduce<RM>(p, lane);
+#pragma unroll
+  for (int mv = 0; mv < MX; mv++) rows_reduce<RM>(p[mv], lane);
   // lanes (64/RM)*i .. hold the wave's total of row i of the team
   constexpr int LB = RM >= 64 ? 6 : RM >= 32 ? 5 : RM >= 16 ? 4 : RM >= 8 ? 3 : RM >= 4 ? 2 : 1;
   constexpr int GL = 1 << (6 - LB);  // lanes per row after the reduction
   const int ir = lane >> (6 - LB);
-  if constexpr (KT == 1) {
+  if constexpr (MX > 1 && KT == 1) {
+    if ((lane & (GL - 1)) == 0 && ir < cnt) {
+#pragma unroll
+      for (int mv = 0; mv < MX; mv++)
+        if (mv < a.mx) a.s[0].out[mv * a.ldo + ub + team + NTM * ir] = p[mv][0];
+    }
+    return;
+  } else if constexpr (KT == 1) {
     // one wave per row: the writer lanes store the outputs directly (stored
     // after the loop, so no store waits on a weight load in flight)
-    const float v = p[0] * rs;
+    const float v = p[0][0] * rs;
     if constexpr (OUT == 2) {
       const float h3 = __shfl_down(v, GL);  // row ir + 1: the W3 half of the pair
       if ((lane & (2 * GL - 1)) == 0 && ir < cnt)
@@ -355,9 +381,23 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     return;
   }
   // KT waves per row: the wave totals meet in LDS, summed in wave order
-  if ((lane & (GL - 1)) == 0 && ir < cnt) red[wave * RM + ir] = p[0];
+  if ((lane & (GL - 1)) == 0 && ir < cnt) {
+#pragma unroll
+    for (int mv = 0; mv < MX; mv++) red[(wave * MX + mv) * RM + ir] = p[mv][0];
+  }
   lds_barrier();
   const int nu = ue - ub;
+  if constexpr (MX > 1) {
+    for (int q = threadIdx.x; q < nu * MX; q += NT) {
+      const int mv = q / nu, qq = q - mv * nu;
+      const int t = qq % NTM, iu = qq / NTM, unit = ub + qq;
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KT; k++) acc += red[((t * KT + k) * MX + mv) * RM + iu];
+      if (mv < a.mx) a.s[0].out[mv * a.ldo + unit] = acc;
+    }
+    return;
+  }
   for (int q = threadIdx.x; q < nu; q += NT) {
     const int t = q % NTM, iu = q / NTM, unit = ub + q;
     float h[UPR];
@@ -365,7 +405,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     for (int sub = 0; sub < UPR; sub++) {
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < KT; k++) acc += red[(t * KT + k) * RM + iu * UPR + sub];
+      for (int k = 0; k < KT; k++) acc += red[(t * KT + k) * MX * RM + iu * UPR + sub];
       h[sub] = acc * rs;
     }
     if constexpr (OUT == 2) {
@@ -377,15 +417,21 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   }
 }
 
-template <int C, int KT, int NW, int D, int RM>
+template <int C, int KT, int NW, int D, int RM, int MX = 1>
 int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
   const int nchunk = a.K / 32;
-  const size_t shm = sizeof(float) * ((size_t)25 * nchunk + NW + (size_t)NW * RM);
-  if (shm > 64 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
+  const size_t shm = sizeof(float) * ((size_t)25 * MX * nchunk + NW + (size_t)NW * MX * RM);
+  if (shm > 160 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
   KernelTimer kt(st, "w4s_gemv_d8");
+  if constexpr (MX > 1) {
+    hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, false, 0, false, MX>), dim3((unsigned)G),
+                       dim3(64 * NW), shm, st, a);
+    SIMP_HIP(hipGetLastError());
+    return SIMP_RT_OK;
+  }
   const bool norm = a.nw != nullptr;
 #define L8(NORMV, OUTV, MV)                                                                       \
-  hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV>), dim3((unsigned)G), dim3(64 * NW), \
+  hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV, 1>), dim3((unsigned)G), dim3(64 * NW), \
                      shm, st, a)
   const bool multi = a.out_mode != 2 && a.n > 1;
   if (norm) {
@@ -405,7 +451,7 @@ int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
 // Blocks: at least one per CU, and enough that a team has at most 16 rows
 // (about 16 rows per team streams best); the segments' blocks are
 // proportional to their rows.
-template <int C, int KT, int NW, int D>
+template <int C, int KT, int NW, int D, int MX = 1>
 int launch_cfg(W4D8Args a, hipStream_t st) {
   constexpr int teams = NW / KT;
   const int upr = a.out_mode == 2 ? 2 : 1;
@@ -426,8 +472,8 @@ int launch_cfg(W4D8Args a, hipStream_t st) {
   a.bstart[0] = 0;
   a.bstart[1] = nseg > 1 ? nb[0] : INT32_MAX;
   a.bstart[2] = nseg > 2 ? nb[0] + nb[1] : INT32_MAX;
-  if (rows <= 8) return launch_rm<C, KT, NW, D, 8>(a, G, st);
-  if (rows <= 16) return launch_rm<C, KT, NW, D, 16>(a, G, st);
+  if (rows <= 8) return launch_rm<C, KT, NW, D, 8, MX>(a, G, st);
+  if (rows <= 16) return launch_rm<C, KT, NW, D, 16, MX>(a, G, st);
   return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: %lld rows per team", (long long)rows);
 }
 
@@ -445,6 +491,25 @@ int launch_w4d8(const W4D8Args &a, hipStream_t st) {
   for (int i = 0; i < (a.out_mode == 2 ? 1 : a.n); i++)
     if (a.s[i].rows <= 0) return set_error(SIMP_RT_EINVAL, "w4d8: empty segment");
   const int nchunk = a.K / 32;
+  if (a.mx > 1) {
+    // several x vectors: one chunk per lane (the limbs of every vector stay in
+    // registers), more waves per row instead
+    if (a.n != 1 || a.out_mode != 0 || a.nw || a.mx > 4 || (a.ldx & 3) != 0)
+      return set_error(SIMP_RT_EINVAL, "w4d8: several x vectors need one plain segment");
+    // (8 rows in flight per team measured slower at every shape)
+    if (a.mx == 2) {
+      if (nchunk <= 64) return launch_cfg<1, 1, 4, 4, 2>(a, st);
+      if (nchunk <= 128) return launch_cfg<1, 2, 8, 4, 2>(a, st);
+      if (nchunk <= 192) return launch_cfg<1, 3, 6, 4, 2>(a, st);
+      if (nchunk <= 320) return launch_cfg<1, 5, 10, 4, 2>(a, st);
+      return launch_cfg<1, 10, 10, 4, 2>(a, st);
+    }
+    if (nchunk <= 64) return launch_cfg<1, 1, 4, 4, 4>(a, st);
+    if (nchunk <= 128) return launch_cfg<1, 2, 8, 4, 4>(a, st);
+    if (nchunk <= 192) return launch_cfg<1, 3, 6, 4, 4>(a, st);
+    if (nchunk <= 320) return launch_cfg<1, 5, 10, 4, 4>(a, st);
+    return launch_cfg<1, 10, 10, 4, 4>(a, st);
+  }
   if (nchunk <= 64) return launch_cfg<1, 1, 4, 4>(a, st);
   if (nchunk <= 128) return launch_cfg<2, 1, 4, 4>(a, st);
   if (nchunk <= 192) return launch_cfg<1, 3, 6, 4>(a, st);

@@ -60,6 +60,27 @@ def test_w4s_ragged_and_fallback(dev, orc, M, N, K, gs):
     _close(out.cpu().numpy(), orc.matmul_w4s(w, s, x, gs).astype(np.float64))
 
 
+@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("N,K,gs", [(100, 2048, 32), (300, 4096, 64), (257, 6144, 32),
+                                    (640, 8640, 32), (96, 16384, 128)])
+def test_w4s_few_vectors_views(dev, orc, M, N, K, gs):
+    """2 <= M <= 4 runs the dot8 kernel with every vector's limbs in registers;
+    x and out as row windows of wider arrays (ldx = K + 4, ldo = N + 3), every
+    chunks-per-row configuration, group sizes 32 / 64 / 128."""
+    import torch
+    print(f"[w4s-mx] M={M} N={N} K={K} gs={gs}", flush=True)
+    w, s, x = _w4s_inputs(M, N, K, gs, seed=M * 7 + N + K)
+    tx = torch.zeros((M, K + 4), device=dev)
+    tx[:, :K] = torch.from_numpy(x).to(dev)
+    out = torch.full((M, N + 3), -3.0, device=dev)
+    sa.matmul_w4s(torch.from_numpy(w).to(dev), torch.from_numpy(s).to(dev), tx[:, :K],
+                  out[:, :N], gs)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    _close(o[:, :N], orc.matmul_w4s(w, s, x, gs).astype(np.float64))
+    assert (o[:, N:] == -3.0).all()
+
+
 def _f5_model(layers, rows, cols, gs, seed):
     """A concatenated reference-format weight buffer (examples/llama2/llama2_quant.sl
     layout) quantised with the reference's quantizer."""
