@@ -383,6 +383,99 @@ def llama32_bench(dev, with_cpu=True):
     return rec
 
 
+def llama2_quant_bench(dev, with_cpu=True):
+    """llama2_quant_forward (examples/llama2/llama2_quant.sl) at the "LLaMA 1B"
+    shape of bench_llama_quant.cpp:324 (dim 1536, 24 layers, 16 heads, hidden
+    6144, vocab 32000, seq_len 512, groups of 128): every array uniform +-0.01
+    (bench_llama_quant.cpp:42-47, drawn on the GPU), the seven matrices quantized
+    one after another into one flat array with the reference quantizer
+    (simp_rt_quantize_w4u, bit-identical to bench_llama_quant.cpp:51-93), then
+    the reference's loop: two warm-up calls, caches zeroed, 10 calls at pos
+    0..9 with token 50 + 10 pos (bench_llama_quant.cpp:232-292), timed three
+    times (median).  Once with host arrays as the reference host passes them
+    (per call: one fingerprint chunk per weight array checked, logits and the
+    new K/V rows copied back) and once with device-resident arrays."""
+    import numpy as np
+    import torch
+    import simplang_amd as sa
+    D, H, L, NH, NKV, V, S, GS = 1536, 6144, 24, 16, 16, 32000, 512, 128
+    kv = D * NKV // NH
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    u = lambda n: torch.rand((n,), device=dev, generator=g) * 0.02 - 0.01
+    per = [D * D, D * kv, D * kv, D * D, H * D, D * H, H * D]
+    total = L * sum(per)
+    q = torch.empty(total // 2, dtype=torch.uint8, device=dev)
+    sc = torch.empty(total // GS, device=dev)
+    ze = torch.empty(total // GS, device=dev)
+    offs, at = [], 0
+    for p in per:
+        w = u(L * p)
+        sa.quantize_w4u(w, GS, q[at // 2:], sc[at // GS:], ze[at // GS:])
+        offs.append(at)
+        at += L * p
+        del w
+    dv = {"token_emb": u(V * D), "rms_att_w": u(L * D), "rms_ffn_w": u(L * D), "rms_final_w": u(D),
+          "wcls": u(V * D), "qweights": q.view(torch.int8), "scales": sc, "zeros": ze}
+    for k, n in (("x", D), ("xb", D), ("xb2", D), ("q", D), ("k", kv), ("v", kv), ("att", NH * S),
+                 ("att_soft", NH * S), ("hb", H), ("hb_silu", H), ("hb2", H), ("logits", V),
+                 ("key_cache", L * S * kv), ("value_cache", L * S * kv)):
+        dv[k] = torch.zeros(n, device=dev)
+    torch.cuda.synchronize()
+    dims = (D, H, L, NH, NKV, V, S, GS)
+    wbytes = total // 2 + 8 * (total // GS) + 4 * V * D
+    out = {"model": "llama2_quant_forward LLaMA-1B W4 g128 (bench_llama_quant.cpp config 1)",
+           "weight_bytes": wbytes}
+
+    def run(arrays, label, zero):
+        for _ in range(2):
+            sa.llama2_quant_forward(arrays, 100, 0, *dims[:-1], GS, offs)
+        times = []
+        for _ in range(3):
+            zero(arrays)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for pos in range(10):
+                r = sa.llama2_quant_forward(arrays, 50 + pos * 10, pos, *dims[:-1], GS, offs)
+            times.append(time.perf_counter() - t0)
+            if not np.isfinite(r):
+                raise RuntimeError("llama2_quant_forward: non-finite logits[0]")
+        ms = float(np.median(times)) / 10 * 1e3
+        out[label] = {"ms_per_token": round(ms, 3), "tok_s": round(1e3 / ms, 1),
+                      "GBs": round(wbytes / ms / 1e6, 1)}
+
+    def zero_dev(a):
+        a["key_cache"].zero_()
+        a["value_cache"].zero_()
+
+    def zero_host(a):
+        a["key_cache"][:] = 0
+        a["value_cache"][:] = 0
+
+    run(dv, "device_arrays", zero_dev)
+    host = {k: v.cpu().numpy() for k, v in dv.items()}
+    sa.forward_cache_clear()
+    run(host, "host_arrays", zero_host)
+    sa.forward_cache_clear()
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        cfg = dict(dim=D, hidden_dim=H, n_layers=L, n_heads=NH, n_kv_heads=NKV, vocab_size=V,
+                   seq_len=S)
+        o = oracle.LlamaQuantOracle(cfg, {k: host[k] for k in ("token_emb", "rms_att_w", "rms_ffn_w",
+                                                              "rms_final_w", "wcls", "scales",
+                                                              "zeros")} |
+                                    {"qweights": host["qweights"].view(np.uint8)}, GS, offs)
+        t0 = time.perf_counter()
+        o.forward(50, 0)
+        out["cpu_baseline"] = {"tok_s": round(1 / (time.perf_counter() - t0), 3),
+                               "cores": host_info()["cores_used"], "kind": "port",
+                               "sample": "one token (pos 0) of the oracle's llama2_quant_forward"}
+    del dv, host
+    torch.cuda.empty_cache()
+    return out
+
+
 def decode_cpu(cfg, w, prompt, steps):
     """The oracle's restatement of the decode step on the host cores (OpenMP
     GEMVs, double accumulation), timed over a few steps."""
@@ -503,6 +596,7 @@ def main():
     decode = [] if args.no_decode else decode_bench(dev, stream, with_cpu=not args.no_cpu)
     if not args.no_decode:
         decode.append(llama32_bench(dev, with_cpu=not args.no_cpu))
+        decode.append(llama2_quant_bench(dev, with_cpu=not args.no_cpu))
 
     cpu = None if (args.no_cpu or args.only not in (None, "gemm")) else cpu_baselines(n)
 

@@ -23,6 +23,7 @@
 // replayed for every token with no host round trip.
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <map>
 #include <mutex>
@@ -48,6 +49,7 @@ struct Seg {
   float *out;       // [rows]
   int rows;
   int tile0;        // first row tile of this segment (W4 kernel)
+  const float *Z = nullptr;  // zeros [rows, K/gs] of the unsigned W4 format
 };
 struct Segs {
   Seg s[kMaxSeg];
@@ -804,13 +806,24 @@ struct LlamaModel {
 
 namespace {
 
+// Weight format and launch context of a step's GEMVs.  kFmtW4U: the
+// reference W4 format (unsigned nibbles, scale and zero per group), on the
+// dot8 kernel only.
+constexpr int kFmtW4U = 100;
+struct GemvCtx {
+  int fmt;  // SIMP_RT_W_F32, SIMP_RT_W_W4S or kFmtW4U
+  int gs;
+  float eps;
+  hipStream_t st;
+};
+
 // out_mode kPairSwiGLU: segments 0 and 1 are W1 and W3 (same rows), the
 // output is segment 0's.
-int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
-  const float eps = m.cfg.eps;
-  hipStream_t st = m.stream;
+int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
+  const float eps = c.eps;
+  hipStream_t st = c.st;
   const bool pair = out_mode == kPairSwiGLU;
-  if (m.cfg.weight_format == SIMP_RT_W_F32) {
+  if (c.fmt == SIMP_RT_W_F32) {
     int total = 0;
     if (pair) total = sg.s[0].rows;
     else for (int i = 0; i < sg.n; i++) total += sg.s[i].rows;
@@ -831,20 +844,22 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
     else { if (out_mode == kAccum) DG(kPlain, kAccum); else DG(kPlain, kStore); }
 #undef DG
 #undef DGJ
-  } else if (w4d8_supported(K, m.cfg.group_size, x0, pro == kRmsNorm ? nw : nullptr)) {
+  } else if (w4d8_supported(K, c.gs, x0, pro == kRmsNorm ? nw : nullptr)) {
     // exact integer chunk products on v_dot8_i32_i4 (w4d8.hip)
     W4D8Args a{};
     for (int i = 0; i < sg.n; i++)
-      a.s[i] = W4D8Seg{(const uint8_t *)sg.s[i].W, sg.s[i].S, sg.s[i].out, K / 2,
-                       K / m.cfg.group_size, sg.s[i].rows};
+      a.s[i] = W4D8Seg{(const uint8_t *)sg.s[i].W, sg.s[i].S, sg.s[i].out, K / 2, K / c.gs,
+                       sg.s[i].rows, c.fmt == kFmtW4U ? sg.s[i].Z : nullptr};
     a.n = sg.n;
     a.K = K;
-    a.gs = m.cfg.group_size;
+    a.gs = c.gs;
     a.x0 = x0;
     a.nw = pro == kRmsNorm ? nw : nullptr;
     a.eps = eps;
     a.out_mode = out_mode;
     return launch_w4d8(a, st);
+  } else if (c.fmt == kFmtW4U) {
+    return set_error(SIMP_RT_EUNSUPPORTED, "step GEMV: reference W4 format needs the dot8 kernel (K=%d)", K);
   } else {
     int tiles = 0;
     if (pair) {
@@ -855,7 +870,7 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
         tiles += (int)cdiv(sg.s[i].rows, 8);
       }
     }
-    const int gs = m.cfg.group_size;
+    const int gs = c.gs;
     const int nchunk = K / 32;
     // 8 waves per block for rows of more than 64 chunks over fewer than 8
     // blocks per CU: half the serial unpack/FMA work per wave
@@ -880,6 +895,11 @@ int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, 
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
+}
+
+int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
+  return gemv(GemvCtx{m.cfg.weight_format, m.cfg.group_size, m.cfg.eps, m.stream}, sg, K, pro,
+              out_mode, x0, nw);
 }
 
 Seg seg_f32(const float *W, float *out, int rows) { return Seg{W, nullptr, out, rows, 0}; }
@@ -952,6 +972,36 @@ int enqueue_step(LlamaModel &m, int attn) {
   hipLaunchKernelGGL(argmax_advance_k, dim3(1), dim3(1024), 0, st, m.logits, (int)c.vocab_size,
                      m.state, m.prompt, m.tokens);
   SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
+// Captures the step graph of attention key `mode` (once per key) on a
+// capture stream; the engine's stream is synchronised first.
+int capture_step(LlamaModel &m, int mode) {
+  if (m.graphs.count(mode)) return SIMP_RT_OK;
+  SIMP_HIP(hipStreamSynchronize(m.stream));
+  hipStream_t cap;
+  SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+  hipStream_t saved = m.stream;
+  m.stream = cap;
+  SIMP_HIP(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_step(m, mode);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(cap, &g);
+  m.stream = saved;
+  (void)hipStreamDestroy(cap);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  hipGraphExec_t ge = nullptr;
+  const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  if (ie != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_fail(ie, "hipGraphInstantiate");
+  }
+  m.graphs[mode] = {g, ge};
   return SIMP_RT_OK;
 }
 
@@ -1157,32 +1207,8 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
   // step i runs at pos i
   auto mode_of = [&](int64_t i) { return attn_key(i, m->attn_ws != nullptr, m->cfg.n_heads); };
   if (use_graph) {
-    auto capture = [&](int mode) -> int {
-      if (m->graphs.count(mode)) return SIMP_RT_OK;
-      SIMP_HIP(hipStreamSynchronize(st));
-      hipStream_t cap;
-      SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
-      hipStream_t saved = m->stream;
-      m->stream = cap;
-      SIMP_HIP(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal));
-      int rc2 = enqueue_step(*m, mode);
-      hipGraph_t g = nullptr;
-      hipError_t e = hipStreamEndCapture(cap, &g);
-      m->stream = saved;
-      (void)hipStreamDestroy(cap);
-      if (rc2) return rc2;
-      if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
-      hipGraphExec_t ge = nullptr;
-      const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-      if (ie != hipSuccess) {
-        (void)hipGraphDestroy(g);
-        return hip_fail(ie, "hipGraphInstantiate");
-      }
-      m->graphs[mode] = {g, ge};
-      return SIMP_RT_OK;
-    };
     for (int64_t i = 0; i < steps; i++)  // capture every key the run needs up front
-      if ((rc = capture(mode_of(i)))) return rc;
+      if ((rc = capture_step(*m, mode_of(i)))) return rc;
     for (int64_t i = 0; i < steps; i++)
       SIMP_HIP(hipGraphLaunch(m->graphs[mode_of(i)].second, st));
   } else {
@@ -1209,10 +1235,83 @@ namespace {
 // (export_state.hip).  At most kMaxEntries engines are kept; the least recently
 // used one is freed to make room (a host that frees its model and loads
 // another at new addresses leaves an entry that is never called again).
+// What a model-level export hands back per call: logits and the K/V rows of
+// the step's position in every layer.  Destinations in host memory are filled
+// through one pinned buffer -- device -> pinned copies on the stream, host
+// memcpy once it has synchronised -- since a 2-D copy into pageable memory is
+// staged row by row.  The same buffer holds the step state the call uploads.
+class StepIO {
+ public:
+  void release() {
+    if (buf_) (void)hipHostFree(buf_);
+    buf_ = nullptr;
+    cap_ = 0;
+  }
+  // token and pos into the device state, asynchronously on st
+  int upload_state(int64_t token, int64_t pos, StepState *dev, hipStream_t st) {
+    int rc;
+    if ((rc = reserve(0))) return rc;
+    auto *hs = (StepState *)buf_;
+    *hs = StepState{(int)token, (int)pos, 0, 0};
+    SIMP_HIP(hipMemcpyAsync(dev, hs, sizeof(StepState), hipMemcpyHostToDevice, st));
+    return SIMP_RT_OK;
+  }
+  // Copies lg_bytes of logits and L rows of `row` bytes (`pitch` apart) of K
+  // and V to the caller's arrays, then synchronises st.
+  int copy_back(void *lg_dst, const void *lg_src, size_t lg_bytes, char *k_dst, char *v_dst,
+                const char *k_src, const char *v_src, size_t row, size_t pitch, int64_t L,
+                hipStream_t st) {
+    const void *dv;
+    const size_t span = (size_t)(L - 1) * pitch + row;
+    const bool lg_host = !try_device_view(lg_dst, lg_bytes, &dv);
+    const bool kv_host = !try_device_view(k_dst, span, &dv) || !try_device_view(v_dst, span, &dv);
+    const size_t o_lg = kHead, o_k = o_lg + (lg_host ? align(lg_bytes) : 0);
+    const size_t o_v = o_k + (kv_host ? align((size_t)L * row) : 0);
+    const size_t need = o_v + (kv_host ? (size_t)L * row : 0);
+    int rc;
+    if ((rc = reserve(need))) return rc;
+    if (lg_host) SIMP_HIP(hipMemcpyAsync(buf_ + o_lg, lg_src, lg_bytes, hipMemcpyDeviceToHost, st));
+    else SIMP_HIP(hipMemcpyAsync(lg_dst, lg_src, lg_bytes, hipMemcpyDefault, st));
+    if (kv_host) {
+      SIMP_HIP(hipMemcpy2DAsync(buf_ + o_k, row, k_src, pitch, row, (size_t)L, hipMemcpyDeviceToHost, st));
+      SIMP_HIP(hipMemcpy2DAsync(buf_ + o_v, row, v_src, pitch, row, (size_t)L, hipMemcpyDeviceToHost, st));
+    } else {
+      SIMP_HIP(hipMemcpy2DAsync(k_dst, pitch, k_src, pitch, row, (size_t)L, hipMemcpyDefault, st));
+      SIMP_HIP(hipMemcpy2DAsync(v_dst, pitch, v_src, pitch, row, (size_t)L, hipMemcpyDefault, st));
+    }
+    SIMP_HIP(hipStreamSynchronize(st));
+    if (lg_host) std::memcpy(lg_dst, buf_ + o_lg, lg_bytes);
+    if (kv_host)
+      for (int64_t l = 0; l < L; l++) {
+        std::memcpy(k_dst + l * pitch, buf_ + o_k + l * row, row);
+        std::memcpy(v_dst + l * pitch, buf_ + o_v + l * row, row);
+      }
+    return SIMP_RT_OK;
+  }
+
+ private:
+  static constexpr size_t kHead = 256;  // the state slot
+  static size_t align(size_t n) { return (n + 255) & ~(size_t)255; }
+  int reserve(size_t n) {
+    n = std::max(n, kHead);
+    if (n <= cap_) return SIMP_RT_OK;
+    release();
+    if (hipHostMalloc((void **)&buf_, n, hipHostMallocDefault) != hipSuccess) {
+      buf_ = nullptr;
+      return set_error(SIMP_RT_ENOMEM, "model export: %zu bytes of pinned staging", n);
+    }
+    cap_ = n;
+    return SIMP_RT_OK;
+  }
+  char *buf_ = nullptr;
+  size_t cap_ = 0;
+};
+
 struct ForwardEntry {
   simp_rt_llama *model = nullptr;
   ExportWeights weights;
   KvState kv;
+  StepIO io;
   uint64_t last_use = 0;
 };
 constexpr size_t kMaxEntries = 4;
@@ -1224,6 +1323,7 @@ void forward_entry_free(ForwardEntry &e) {
   if (e.model) simp_rt_llama_destroy(e.model);
   e.model = nullptr;
   e.weights.release();
+  e.io.release();
 }
 
 }  // namespace
@@ -1361,22 +1461,20 @@ float stories110M_forward(
       ent.weights.verify(restart))
     return nan;
   float *lg = logits + logits_off;
-  if (simp_rt_llama_forward(ent.model, token, pos, lg)) return nan;
-  // the step's K and V rows at pos go back into the caller's caches
-  // ([n_layers, seq_len, kv_dim], stories110M.sl:115-121)
-  hipError_t e1 = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kcache + at, pitch, row,
-                                   (size_t)L, hipMemcpyDefault, m->stream);
-  hipError_t e2 = e1 == hipSuccess
-                      ? hipMemcpy2DAsync(value_cache + value_cache_off + at, pitch, m->vcache + at,
-                                         pitch, row, (size_t)L, hipMemcpyDefault, m->stream)
-                      : e1;
-  if (e2 == hipSuccess) e2 = hipStreamSynchronize(m->stream);
-  if (e2 != hipSuccess) {
-    hip_fail(e2, "stories110M_forward: KV row copy");
+  // the step as its captured graph (token and pos through the device state),
+  // then the logits and the step's K and V rows at pos back into the caller's
+  // arrays ([n_layers, seq_len, kv_dim], stories110M.sl:115-121)
+  const int mode = attn_key(pos, m->attn_ws != nullptr, m->cfg.n_heads);
+  if (capture_step(*m, mode) || ent.io.upload_state(token, pos, m->state, m->stream)) return nan;
+  if (hipGraphLaunch(m->graphs[mode].second, m->stream) != hipSuccess) {
+    hip_fail(hipGetLastError(), "stories110M_forward: hipGraphLaunch");
     return nan;
   }
+  if (ent.io.copy_back(lg, m->logits, 4 * (size_t)vocab_size, (char *)(key_cache + key_cache_off + at),
+                       (char *)(value_cache + value_cache_off + at), (const char *)(m->kcache + at),
+                       (const char *)(m->vcache + at), row, pitch, L, m->stream))
+    return nan;
   ent.kv.done(pos);
-  // logits are on the host now (simp_rt_llama_forward synchronised)
   float l0 = nan;
   if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
   return l0;
@@ -1392,8 +1490,13 @@ float stories110M_forward(
 // Its seven layer matrices are in the reference format (one flat nibble array,
 // u4 with a scale and zero per flat group of group_size, per-matrix element
 // offsets advanced per layer), the classifier is fp32 and there is no RoPE.
-// Dims come from the arguments (the program hard-codes 1536/6144/128).  The
-// step runs as a sequence of the library's kernels.
+// Dims come from the arguments (the program hard-codes 1536/6144/128).
+// Where the offsets, group size and dims allow (quant_fusable), the step is
+// the engine's fused form -- RMSNorm in the QKV and W1|W3 GEMV prologues, Wq|Wk|Wv
+// and W1|W3 as one launch each, residual adds and SwiGLU in the epilogues --
+// on the dot8 GEMV with the format's unsigned nibbles and zeros, captured
+// once per attention key as a graph and replayed per call; otherwise it runs
+// as a sequence of the library's kernels (quant_step).
 namespace simp {
 namespace {
 
@@ -1422,9 +1525,17 @@ struct QuantModel {
   ExportWeights weights;
   KvState kv;
   uint64_t last_use = 0;
+  bool fused = false;
+  std::map<int, std::pair<hipGraph_t, hipGraphExec_t>> graphs;  // per attention key
+  StepIO io;
 };
 
 void quant_free(QuantModel &m) {
+  for (auto &g : m.graphs) {
+    if (g.second.second) (void)hipGraphExecDestroy(g.second.second);
+    if (g.second.first) (void)hipGraphDestroy(g.second.first);
+  }
+  m.graphs.clear();
   for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.xb2, (void *)m.qkv, (void *)m.hb,
                   (void *)m.hb2, (void *)m.logits, (void *)m.kc, (void *)m.vc, (void *)m.attn_ws,
                   (void *)m.state})
@@ -1432,6 +1543,7 @@ void quant_free(QuantModel &m) {
   m.x = m.xb = m.xb2 = m.qkv = m.hb = m.hb2 = m.logits = m.kc = m.vc = m.attn_ws = nullptr;
   m.state = nullptr;
   m.weights.release();
+  m.io.release();
 }
 
 int quant_alloc(QuantModel &m) {
@@ -1485,6 +1597,105 @@ int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
   }
   if ((rc = launch_rmsnorm(m.x, m.rms_final, m.xb, dim, eps, st))) return rc;
   return launch_matmul_f32(m.wcls, dim, m.xb, 1, m.logits, 1, (int)m.V, 1, dim, 0.f, st);
+}
+
+// Whether the fused step applies: groups that start at row starts (offsets
+// and dims multiples of gs, gs a multiple of 32), rows the dot8 kernel takes
+// (K / 32 <= 640), 16-byte aligned operands, a classifier row the fp32 GEMV
+// holds in LDS.
+bool quant_fusable(const QuantModel &m) {
+  const int64_t gs = m.gs;
+  if (gs % 32 || m.dim % gs || m.hid % gs || m.dim > 9216 || m.hid / 32 > 640) return false;
+  for (int i = 0; i < 7; i++)
+    if (m.off[i] % gs || m.off[i] % 32) return false;
+  for (const void *p : {(const void *)m.qw, (const void *)m.rms_att, (const void *)m.rms_ffn,
+                        (const void *)m.rms_final, (const void *)m.wcls})
+    if ((uintptr_t)p & 15) return false;
+  return true;
+}
+
+// One fused step on st (token and pos read from the device state): the
+// kernels of enqueue_step on the reference W4 format, no RoPE, fp32
+// classifier, logits left in m.logits.
+int quant_enqueue_fused(QuantModel &m, int attn, hipStream_t st) {
+  const int dim = (int)m.dim, hid = (int)m.hid, kvd = m.kv_dim, gs = (int)m.gs;
+  const float eps = 1e-5f;  // llama2_quant.sl:73,146,184
+  const GemvCtx cq{kFmtW4U, gs, eps, st};
+  hipLaunchKernelGGL(embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st, m.emb, m.x, m.state, dim);
+  SIMP_HIP(hipGetLastError());
+  // matrix i of layer l: element offset off[i] + l * per (a multiple of gs)
+  auto seg = [&](int i, int64_t l, int64_t per, float *out, int rows) {
+    const int64_t e = m.off[i] + l * per;
+    Seg s{m.qw + e / 2, m.scales + e / gs, out, rows, 0};
+    s.Z = m.zeros + e / gs;
+    return s;
+  };
+  const int64_t D = m.dim, H = m.hid, KV = kvd;
+  float *q = m.qkv, *k = m.qkv + dim, *v = m.qkv + dim + kvd;
+  int rc;
+  for (int64_t l = 0; l < m.L; l++) {
+    Segs s{};
+    s.s[0] = seg(0, l, D * D, q, dim);
+    s.s[1] = seg(1, l, D * KV, k, kvd);
+    s.s[2] = seg(2, l, D * KV, v, kvd);
+    s.n = 3;
+    if ((rc = gemv(cq, s, dim, kRmsNorm, kStore, m.x, m.rms_att + l * dim))) return rc;
+    float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
+    if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb2, m.attn_ws, m.state, dim, kvd, (int)m.nh,
+                               (int)m.nkv, m.hs, nullptr, m.seq, st)))  // llama2_quant.sl: no RoPE
+      return rc;
+    s = Segs{};
+    s.s[0] = seg(3, l, D * D, m.x, dim);  // x += Wo xb2
+    s.n = 1;
+    if ((rc = gemv(cq, s, dim, kPlain, kAccum, m.xb2, nullptr))) return rc;
+    s = Segs{};
+    s.s[0] = seg(4, l, H * D, m.hb, hid);  // hb = silu(W1 xb) * (W3 xb)
+    s.s[1] = seg(6, l, H * D, nullptr, hid);
+    s.n = 2;
+    if ((rc = gemv(cq, s, dim, kRmsNorm, kPairSwiGLU, m.x, m.rms_ffn + l * dim))) return rc;
+    s = Segs{};
+    s.s[0] = seg(5, l, D * H, m.x, dim);  // x += W2 hb
+    s.n = 1;
+    if ((rc = gemv(cq, s, hid, kPlain, kAccum, m.hb, nullptr))) return rc;
+  }
+  Segs s{};
+  s.s[0] = seg_f32(m.wcls, m.logits, (int)m.V);
+  s.n = 1;
+  return gemv(GemvCtx{SIMP_RT_W_F32, gs, eps, st}, s, dim, kRmsNorm, kStore, m.x, m.rms_final);
+}
+
+// One token: the fused step as a captured graph (once per attention key),
+// else the kernel sequence.
+int quant_forward_device(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
+  if (!m.fused) return quant_step(m, token, pos, st);
+  int rc;
+  if ((rc = m.io.upload_state(token, pos, m.state, st))) return rc;
+  const int key = attn_key(pos, m.attn_ws != nullptr, m.nh);
+  auto it = m.graphs.find(key);
+  if (it == m.graphs.end()) {
+    SIMP_HIP(hipStreamSynchronize(st));
+    hipStream_t cap;
+    SIMP_HIP(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+    SIMP_HIP(hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal));
+    rc = quant_enqueue_fused(m, key, cap);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(cap, &g);
+    (void)hipStreamDestroy(cap);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "llama2_quant_forward: hipStreamEndCapture");
+    hipGraphExec_t ge = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      (void)hipGraphDestroy(g);
+      return hip_fail(ie, "llama2_quant_forward: hipGraphInstantiate");
+    }
+    it = m.graphs.emplace(key, std::make_pair(g, ge)).first;
+  }
+  SIMP_HIP(hipGraphLaunch(it->second.second, st));
+  return SIMP_RT_OK;
 }
 
 std::map<std::vector<int64_t>, QuantModel> g_qfwd;
@@ -1582,6 +1793,7 @@ float llama2_quant_forward(
       nm.rms_final = (const float *)d[3]; nm.wcls = (const float *)d[4];
       nm.qw = (const uint8_t *)d[5]; nm.scales = (const float *)d[6]; nm.zeros = (const float *)d[7];
       ok = quant_alloc(nm) == SIMP_RT_OK;
+      nm.fused = quant_fusable(nm);
     }
     if (!ok) {
       quant_free(nm);
@@ -1598,20 +1810,12 @@ float llama2_quant_forward(
                     row, pitch, L, st, &restart) ||
       m->weights.verify(restart))
     return nan;
-  if (quant_step(*m, token, pos, st)) return nan;
+  if (quant_forward_device(*m, token, pos, st)) return nan;
   float *lg = logits + logits_off;
-  hipError_t e = hipMemcpyAsync(lg, m->logits, 4 * (size_t)vocab_size, hipMemcpyDefault, st);
-  if (e == hipSuccess)
-    e = hipMemcpy2DAsync(key_cache + key_cache_off + at, pitch, m->kc + at, pitch, row, (size_t)L,
-                         hipMemcpyDefault, st);
-  if (e == hipSuccess)
-    e = hipMemcpy2DAsync(value_cache + value_cache_off + at, pitch, m->vc + at, pitch, row,
-                         (size_t)L, hipMemcpyDefault, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  if (e != hipSuccess) {
-    hip_fail(e, "llama2_quant_forward: result copies");
+  if (m->io.copy_back(lg, m->logits, 4 * (size_t)vocab_size, (char *)(key_cache + key_cache_off + at),
+                      (char *)(value_cache + value_cache_off + at), (const char *)(m->kc + at),
+                      (const char *)(m->vc + at), row, pitch, L, st))
     return nan;
-  }
   m->kv.done(pos);
   float l0 = nan;
   if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;

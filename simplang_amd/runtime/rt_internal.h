@@ -171,12 +171,15 @@ int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps,
 // [rows, lds floats] and output; x = x0, or rmsnorm(x0) * nw when nw is set;
 // out_mode 0 stores, 1 adds to the output, 2 pairs row i of segment 0 (W1)
 // with row i of segment 1 (W3) and stores silu(h1) * h3 into segment 0's output.
+// With zeros Z (laid out like S; every segment or none, one x vector) the
+// nibbles are unsigned and a weight is q * s + z (the reference W4 format).
 struct W4D8Seg {
   const uint8_t *W;
   const float *S;
   float *out;
   int64_t ldw, lds;
   int rows;
+  const float *Z = nullptr;
 };
 struct W4D8Args {
   W4D8Seg s[3];

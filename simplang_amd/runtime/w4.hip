@@ -693,6 +693,20 @@ int launch_w4u(const uint8_t *Q, const float *S, const float *Z, const float *X,
   if (!fast) {
     hipLaunchKernelGGL(w4u_generic, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, Q, S, Z, X, O,
                        rows, cols, gs, off);
+  } else if (w4d8_supported(cols, gs, X, nullptr)) {
+    // exact integer chunk products on v_dot8_i32_i4 (w4d8.hip): groups start
+    // at row starts (off and cols are multiples of gs), so row n's scales
+    // and zeros are at (off + n cols) / gs
+    W4D8Args a{};
+    a.s[0] = W4D8Seg{Q + off / 2, S + off / gs, O, cols / 2, cols / gs, rows, Z + off / gs};
+    a.n = 1;
+    a.K = cols;
+    a.gs = gs;
+    a.x0 = X;
+    a.nw = nullptr;
+    a.eps = 0.f;
+    a.out_mode = 0;
+    return launch_w4d8(a, st);
   } else {
     KernelTimer kt(st, "w4u_gemv");
     hipLaunchKernelGGL(w4u_gemv, dim3((unsigned)cdiv(rows, kRowsPerBlock)), dim3(256),

@@ -1,4 +1,4 @@
-// w4d8.hip -- symmetric W4 GEMV with one to four x vectors on v_dot8_i32_i4.
+// w4d8.hip -- W4 GEMV (symmetric nibbles, or unsigned with zeros) with one to four x vectors on v_dot8_i32_i4.
 //
 // The product out[n] = sum_k q[n,k] * s[n, k/gs] * x[k] of
 // MatMulQuantOpLowering (ConvertSimpToMemRef.cpp:3906-4005) for the signed
@@ -27,6 +27,10 @@
 // Segments: up to three matrices with their own weights, scales and outputs
 // (Wq | Wk | Wv as one launch), or, in the paired mode, rows i of W1 and W3
 // computed by the same wave and combined as silu(h1) * h3.
+// Unsigned nibbles with a zero per group (weight = u * s + z, the format of
+// MatMulQuantOpLowering): u - 8 is the signed nibble u ^ 8, so a chunk is
+// s * sum (u - 8) x + (8 s + z) * sum x; the chunk's sum of x is kept per
+// chunk from the same 23-bit integers, sum_i I_i exact in int32.
 #include <algorithm>
 
 #include "rt_device.h"
@@ -140,17 +144,20 @@ __device__ __forceinline__ float silu_mul(float h1, float h3) {
 // once for all of them.
 // Units are rows (pairs of rows in mode 2); the blocks of a segment split its
 // units evenly, team t of a block takes the block's units t, t + teams, ...
-template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI, int MX>
+// UZ: unsigned nibbles with zeros (every segment's Z set).
+template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI, int MX, bool UZ>
 __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   constexpr int NT = 64 * NW, NTM = NW / KT, UPR = OUT == 2 ? 2 : 1;
   static_assert(RM % UPR == 0 && RM >= D, "rows");
   static_assert(MX == 1 || (OUT == 0 && !NORM && !MULTI), "several x vectors: plain stores");
+  static_assert(MX == 1 || !UZ, "zeros: one x vector");
   extern __shared__ __align__(16) uint32_t sm[];
   const int K = a.K, nchunk = K >> 5, ngrp8 = K >> 3;
   const int cpg = a.gs >> 5, cps = cpg_log2(cpg);
   uint32_t *xl = sm;                            // [MX][nchunk][6 limbs][4 dwords]
   float *xf = (float *)(sm + MX * 24 * nchunk); // [MX][nchunk] 2^(e-22)
-  float *ssq = xf + MX * nchunk;                // [NW]
+  float *xs = xf + MX * nchunk;                 // [MX][nchunk] sum of the chunk's x (UZ)
+  float *ssq = xs + (UZ ? MX * nchunk : 0);     // [NW]
   float *red = ssq + NW;                        // [NW][MX][RM] row totals per wave
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -204,6 +211,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
 
   uint4 w[D][C];
   float s[D][C];
+  float z[UZ ? D : 1][UZ ? C : 1];
   // Row pointers of the team, stepped row by row (the team's rows are units
   // ub + team, + NTM, ... of one segment): a 64-bit add per row and matrix.
   // Past its last row a team repeats the last row's requests (cache hits), so
@@ -213,15 +221,20 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   const int64_t lds = sg == 0 ? a.s[0].lds : (sg == 1 ? a.s[1].lds : a.s[2].lds);
   const uint8_t *wp = (sg == 0 ? a.s[0].W : (sg == 1 ? a.s[1].W : a.s[2].W)) + (int64_t)unit0 * ldw;
   const float *sp = (sg == 0 ? a.s[0].S : (sg == 1 ? a.s[1].S : a.s[2].S)) + (int64_t)unit0 * lds;
+  const float *zp = UZ ? (sg == 0 ? a.s[0].Z : (sg == 1 ? a.s[1].Z : a.s[2].Z)) + (int64_t)unit0 * lds
+                       : nullptr;
   // paired mode: the W3 row of the same unit
   const uint8_t *wp3 = OUT == 2 ? a.s[1].W + (int64_t)unit0 * a.s[1].ldw : nullptr;
   const float *sp3 = OUT == 2 ? a.s[1].S + (int64_t)unit0 * a.s[1].lds : nullptr;
+  const float *zp3 = OUT == 2 && UZ ? a.s[1].Z + (int64_t)unit0 * a.s[1].lds : nullptr;
   auto advance = [&]() {  // to the team's next unit
     wp += NTM * ldw;
     sp += NTM * lds;
+    if constexpr (UZ) zp += NTM * lds;
     if constexpr (OUT == 2) {
       wp3 += NTM * a.s[1].ldw;
       sp3 += NTM * a.s[1].lds;
+      if constexpr (UZ) zp3 += NTM * a.s[1].lds;
     }
   };
   // row i of the team into a window slot; rows are requested in order
@@ -231,6 +244,11 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
     const uint8_t *wrow = odd ? wp3 : wp;
 #pragma unroll
     for (int j = 0; j < C; j++) s[slot][j] = *(const float *)((const char *)srow + (uint32_t)(4u * (uint32_t)sgo[j]));
+    if constexpr (UZ) {
+      const float *zrow = odd ? zp3 : zp;
+#pragma unroll
+      for (int j = 0; j < C; j++) z[slot][j] = *(const float *)((const char *)zrow + (uint32_t)(4u * (uint32_t)sgo[j]));
+    }
 #pragma unroll
     for (int j = 0; j < C; j++) w[slot][j] = *(const uint4 *)(wrow + (uint32_t)(16u * (uint32_t)cj[j]));
     if (i + 1 < cnt && (OUT != 2 || odd)) advance();
@@ -281,12 +299,23 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
       u[k] = __float_as_uint(fmaf(v[k], sc, 12582912.f)) - 0x4AB77778u;
     uint32_t L[6];
     limbs8(u, L);
+    int si = 0;  // sum of the chunk's integers I (UZ): u = I + 0x888888
+    if constexpr (UZ) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) si += (int)u[k];
+      si -= 8 * 0x888888;
+      si += __builtin_amdgcn_mov_dpp(si, kDppXor1, 0xF, 0xF, false);
+      si += __builtin_amdgcn_mov_dpp(si, kDppXor2, 0xF, 0xF, false);
+    }
     if (g8 < ngrp8) {
       const int ch = g8 >> 2, dd = g8 & 3;
 #pragma unroll
       for (int j = 0; j < 6; j++) xl[(mv * nchunk + ch) * 24 + 4 * j + dd] = L[j];
-      if (dd == 0)
-        xf[mv * nchunk + ch] = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
+      if (dd == 0) {
+        const float fe = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
+        xf[mv * nchunk + ch] = fe;
+        if constexpr (UZ) xs[mv * nchunk + ch] = (float)si * fe;
+      }
     }
   }
   if constexpr (NORM) {
@@ -303,6 +332,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   }
   uint32_t L[MX][C][6][4];
   float f[MX][C];
+  float fs[UZ ? MX : 1][UZ ? C : 1];
 #pragma unroll
   for (int mv = 0; mv < MX; mv++)
 #pragma unroll
@@ -316,6 +346,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
       L[mv][j][q][3] = t.w;
     }
     f[mv][j] = xf[mv * nchunk + cj[j]];
+    if constexpr (UZ) fs[mv][j] = xs[mv * nchunk + cj[j]];
   }
 
   // rows 0 .. RM-1 unrolled (cnt <= RM); row i + D is requested right after
@@ -332,17 +363,26 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
       for (int j = 0; j < C; j++)
 #pragma unroll
       for (int mv = 0; mv < MX; mv++) {
+        uint4 wd = w[slot][j];
+        if constexpr (UZ) {  // unsigned u -> signed u - 8
+          wd.x ^= 0x88888888u;
+          wd.y ^= 0x88888888u;
+          wd.z ^= 0x88888888u;
+          wd.w ^= 0x88888888u;
+        }
         // Horner over the limbs, most significant first
         int T = 0;
 #pragma unroll
         for (int q = 5; q >= 0; q--) {
           if (q < 5) T = (int)((uint32_t)T << 4);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].x, (int)L[mv][j][q][0], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].y, (int)L[mv][j][q][1], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].z, (int)L[mv][j][q][2], T, false);
-          T = __builtin_amdgcn_sdot8((int)w[slot][j].w, (int)L[mv][j][q][3], T, false);
+          T = __builtin_amdgcn_sdot8((int)wd.x, (int)L[mv][j][q][0], T, false);
+          T = __builtin_amdgcn_sdot8((int)wd.y, (int)L[mv][j][q][1], T, false);
+          T = __builtin_amdgcn_sdot8((int)wd.z, (int)L[mv][j][q][2], T, false);
+          T = __builtin_amdgcn_sdot8((int)wd.w, (int)L[mv][j][q][3], T, false);
         }
         acc[mv] = fmaf(aj[j] ? s[slot][j] * f[mv][j] : 0.f, (float)T, acc[mv]);
+        if constexpr (UZ)
+          acc[mv] = fmaf(aj[j] ? fmaf(8.f, s[slot][j], z[slot][j]) : 0.f, fs[mv][j], acc[mv]);
       }
     }
 #pragma unroll
@@ -417,21 +457,11 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   }
 }
 
-template <int C, int KT, int NW, int D, int RM, int MX = 1>
-int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
-  const int nchunk = a.K / 32;
-  const size_t shm = sizeof(float) * ((size_t)25 * MX * nchunk + NW + (size_t)NW * MX * RM);
-  if (shm > 160 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
-  KernelTimer kt(st, "w4s_gemv_d8");
-  if constexpr (MX > 1) {
-    hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, false, 0, false, MX>), dim3((unsigned)G),
-                       dim3(64 * NW), shm, st, a);
-    SIMP_HIP(hipGetLastError());
-    return SIMP_RT_OK;
-  }
+template <int C, int KT, int NW, int D, int RM, bool UZ>
+void launch_modes(const W4D8Args &a, int G, size_t shm, hipStream_t st) {
   const bool norm = a.nw != nullptr;
 #define L8(NORMV, OUTV, MV)                                                                       \
-  hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV, 1>), dim3((unsigned)G), dim3(64 * NW), \
+  hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV, 1, UZ>), dim3((unsigned)G), dim3(64 * NW), \
                      shm, st, a)
   const bool multi = a.out_mode != 2 && a.n > 1;
   if (norm) {
@@ -444,6 +474,23 @@ int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
     else L8(false, 0, false);
   }
 #undef L8
+}
+
+template <int C, int KT, int NW, int D, int RM, int MX = 1>
+int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
+  const int nchunk = a.K / 32;
+  const bool uz = a.s[0].Z != nullptr;
+  const size_t shm = sizeof(float) * ((size_t)(uz ? 26 : 25) * MX * nchunk + NW + (size_t)NW * MX * RM);
+  if (shm > 160 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
+  KernelTimer kt(st, "w4s_gemv_d8");
+  if constexpr (MX > 1) {
+    hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, false, 0, false, MX, false>), dim3((unsigned)G),
+                       dim3(64 * NW), shm, st, a);
+  } else if (uz) {
+    launch_modes<C, KT, NW, D, RM, true>(a, G, shm, st);
+  } else {
+    launch_modes<C, KT, NW, D, RM, false>(a, G, shm, st);
+  }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
 }
@@ -490,6 +537,10 @@ int launch_w4d8(const W4D8Args &a, hipStream_t st) {
     return set_error(SIMP_RT_EINVAL, "w4d8: unsupported arguments (K=%d gs=%d)", a.K, a.gs);
   for (int i = 0; i < (a.out_mode == 2 ? 1 : a.n); i++)
     if (a.s[i].rows <= 0) return set_error(SIMP_RT_EINVAL, "w4d8: empty segment");
+  for (int i = 1; i < a.n; i++)
+    if ((a.s[i].Z != nullptr) != (a.s[0].Z != nullptr))
+      return set_error(SIMP_RT_EINVAL, "w4d8: zeros on some segments only");
+  if (a.s[0].Z && a.mx > 1) return set_error(SIMP_RT_EINVAL, "w4d8: zeros with several x vectors");
   const int nchunk = a.K / 32;
   if (a.mx > 1) {
     // several x vectors: one chunk per lane (the limbs of every vector stay in

@@ -121,8 +121,10 @@ def _quant_model(orc, seed, gs=128, cfg=None):
     return arrays, offs
 
 
-def test_llama2_quant_forward_host_arrays(dev, orc):
-    gs = 128
+@pytest.mark.parametrize("gs", [128, 32, 16])
+def test_llama2_quant_forward_host_arrays(dev, orc, gs):
+    """gs 128 and 32: the fused step (dot8 GEMVs on the unsigned format, graph
+    replay); gs 16: the kernel sequence (groups shorter than a 32-weight chunk)."""
     arrays, offs = _quant_model(orc, 21, gs)
     o = orc.LlamaQuantOracle(QCFG, {k: arrays[k] for k in ("token_emb", "rms_att_w", "rms_ffn_w",
                                                            "rms_final_w", "wcls", "scales",
@@ -131,7 +133,7 @@ def test_llama2_quant_forward_host_arrays(dev, orc):
     dims = tuple(QCFG[k] for k in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
                                    "vocab_size", "seq_len"))
     for pos, t in enumerate([50, 60, 70, 80, 90]):     # bench_llama_quant.cpp:258 tokens
-        print(f"[quant-export] pos={pos}", flush=True)
+        print(f"[quant-export] gs={gs} pos={pos}", flush=True)
         r = sa.llama2_quant_forward(arrays, t, pos, *dims, gs, offs)
         want = o.forward(t, pos).astype(np.float64)
         got = arrays["logits"].astype(np.float64)
