@@ -14,7 +14,9 @@ import os
 import re
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-lib_path = os.path.join(_HERE, "libsimp_hip.so")
+# SIMP_HIP_LIB selects another build of the library (the host-sanitized
+# libsimp_hip_san.so, loaded with the compiler's ASan runtime preloaded)
+lib_path = os.environ.get("SIMP_HIP_LIB") or os.path.join(_HERE, "libsimp_hip.so")
 HEADER = os.path.join(os.path.dirname(_HERE), "include", "simp_rt.h")
 
 
