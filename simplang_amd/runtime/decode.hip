@@ -689,9 +689,12 @@ int attn_key(int64_t pos, bool have_ws, int64_t n_heads) {
 }
 
 // One decode step's attention for one layer (cache rows [seq_len, kv_dim]).
+// combine false: with more than one chunk the partials stay in ws for the
+// consumer (the Wo GEMV) to combine; out is not written.
 int launch_attention(int key, const float *qkv, float *kc, float *vc, float *out, float *ws,
                      const StepState *state, int dim, int kv_dim, int n_heads, int n_kv_heads,
-                     int hs, const float2 *rope, int64_t seq_len, hipStream_t st) {
+                     int hs, const float2 *rope, int64_t seq_len, hipStream_t st,
+                     bool combine = true) {
   if (key == 0) {
     hipLaunchKernelGGL(attn_k, dim3((unsigned)n_heads), dim3(kAttnThreads),
                        sizeof(float) * (size_t)seq_len, st, qkv, kc, vc, out, state, dim, kv_dim,
@@ -702,7 +705,7 @@ int launch_attention(int key, const float *qkv, float *kc, float *vc, float *out
     hipLaunchKernelGGL(attn_split_k<kAttnNWV>, dim3((unsigned)n_heads, (unsigned)key),
                        dim3(64 * kAttnNWV), 0, st, qkv, kc, vc, out, ws, state, dim, kv_dim,
                        n_heads, n_kv_heads, hs, rope, splits, key, (int)seq_len);
-    if (key > 1)
+    if (key > 1 && combine)
       hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128), 0, st,
                          (const float *)ws, out, hs, splits, key);
   }
@@ -817,9 +820,29 @@ struct GemvCtx {
   hipStream_t st;
 };
 
+// Split-attention partials that a GEMV combines into its x (launch_attention
+// with combine false): n chunks of max_splits per head of hs.
+struct Partials {
+  const float *ws;
+  int hs, max_splits, n;
+};
+
+// Whether the Wo GEMV of a step with attention key `attn` takes the partials
+// (the dot8 kernel; the other GEMVs read the combine kernel's output).  Every
+// Wo block reads all chunks of every head, so the fold stops paying past four
+// chunks (positions >= 256): measured on the 3B W4 decode at three chunks,
+// Wo 5.0 -> 6.9 us against the 4.0 us combine kernel it replaces.
+bool fold_combine(int fmt, int gs, int attn, int K, const float *x0) {
+  return attn > 1 && attn <= 4 && fmt != SIMP_RT_W_F32 && w4d8_supported(K, gs, x0, nullptr);
+}
+
 // out_mode kPairSwiGLU: segments 0 and 1 are W1 and W3 (same rows), the
-// output is segment 0's.
-int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
+// output is segment 0's.  cp: x combined from attention partials (only where
+// fold_combine holds).
+int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw,
+         const Partials *cp = nullptr) {
+  if (cp && (c.fmt == SIMP_RT_W_F32 || !w4d8_supported(K, c.gs, x0, nullptr)))
+    return set_error(SIMP_RT_EINVAL, "step GEMV: attention partials need the dot8 kernel");
   const float eps = c.eps;
   hipStream_t st = c.st;
   const bool pair = out_mode == kPairSwiGLU;
@@ -857,6 +880,12 @@ int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x
     a.nw = pro == kRmsNorm ? nw : nullptr;
     a.eps = eps;
     a.out_mode = out_mode;
+    if (cp) {
+      a.cws = cp->ws;
+      a.chs = cp->hs;
+      a.cmax = cp->max_splits;
+      a.cn = cp->n;
+    }
     return launch_w4d8(a, st);
   } else if (c.fmt == kFmtW4U) {
     return set_error(SIMP_RT_EUNSUPPORTED, "step GEMV: reference W4 format needs the dot8 kernel (K=%d)", K);
@@ -897,9 +926,10 @@ int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x
   return SIMP_RT_OK;
 }
 
-int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw) {
+int gemv(LlamaModel &m, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw,
+         const Partials *cp = nullptr) {
   return gemv(GemvCtx{m.cfg.weight_format, m.cfg.group_size, m.cfg.eps, m.stream}, sg, K, pro,
-              out_mode, x0, nw);
+              out_mode, x0, nw, cp);
 }
 
 Seg seg_f32(const float *W, float *out, int rows) { return Seg{W, nullptr, out, rows, 0}; }
@@ -935,17 +965,21 @@ int enqueue_step(LlamaModel &m, int attn) {
     }
     s.n = 3;
     if ((rc = gemv(m, s, dim, kRmsNorm, kStore, m.x, m.w.rms_att + (int64_t)l * dim))) return rc;
-    // 2. attention (RoPE, cache store at pos, softmax, V sum), one block per head
+    // 2. attention (RoPE, cache store at pos, softmax, V sum), one block per
+    // head or per chunk of positions; with chunks, the Wo GEMV on the dot8
+    // kernel combines them in its prologue
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
+    const bool fold = fold_combine(c.weight_format, gs, attn, dim, m.xb);
     if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb, m.attn_ws, m.state, dim, kv,
-                               (int)c.n_heads,
-                               (int)c.n_kv_heads, hs, (const float2 *)m.rope, c.seq_len, st)))
+                               (int)c.n_heads, (int)c.n_kv_heads, hs, (const float2 *)m.rope,
+                               c.seq_len, st, !fold)))
       return rc;
+    const Partials parts{m.attn_ws, hs, (int)cdiv(c.seq_len, kAttnTP), attn};
     // 3. Wo, accumulated into x (residual)
     s = Segs{};
     s.s[0] = w4 ? seg_w4(m.w.q_wo + lq / 2, m.w.s_wo + lq / gs, m.x, dim) : seg_f32(m.w.wo + lq, m.x, dim);
     s.n = 1;
-    if ((rc = gemv(m, s, dim, kPlain, kAccum, m.xb, nullptr))) return rc;
+    if ((rc = gemv(m, s, dim, kPlain, kAccum, m.xb, nullptr, fold ? &parts : nullptr))) return rc;
     // 4. W1 | W3 with the FFN RMSNorm, rows paired: g = silu(h1) * h3
     s = Segs{};
     if (w4) {
@@ -1641,13 +1675,15 @@ int quant_enqueue_fused(QuantModel &m, int attn, hipStream_t st) {
     s.n = 3;
     if ((rc = gemv(cq, s, dim, kRmsNorm, kStore, m.x, m.rms_att + l * dim))) return rc;
     float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
+    const bool fold = fold_combine(kFmtW4U, gs, attn, dim, m.xb2);
     if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb2, m.attn_ws, m.state, dim, kvd, (int)m.nh,
-                               (int)m.nkv, m.hs, nullptr, m.seq, st)))  // llama2_quant.sl: no RoPE
+                               (int)m.nkv, m.hs, nullptr, m.seq, st, !fold)))  // llama2_quant.sl: no RoPE
       return rc;
+    const Partials parts{m.attn_ws, m.hs, (int)cdiv(m.seq, kAttnTP), attn};
     s = Segs{};
     s.s[0] = seg(3, l, D * D, m.x, dim);  // x += Wo xb2
     s.n = 1;
-    if ((rc = gemv(cq, s, dim, kPlain, kAccum, m.xb2, nullptr))) return rc;
+    if ((rc = gemv(cq, s, dim, kPlain, kAccum, m.xb2, nullptr, fold ? &parts : nullptr))) return rc;
     s = Segs{};
     s.s[0] = seg(4, l, H * D, m.hb, hid);  // hb = silu(W1 xb) * (W3 xb)
     s.s[1] = seg(6, l, H * D, nullptr, hid);

@@ -193,6 +193,13 @@ struct W4D8Args {
   // (one segment, out_mode 0, no norm)
   int mx = 1;
   int64_t ldx = 0, ldo = 0;
+  // cws set: x is the combination of split-attention partials instead of x0
+  // (one segment, out_mode 1, no norm).  Chunk s of head h sits at
+  // cws + (h * cmax + s) * (chs + 4): the unnormalised o[chs], then m and l;
+  // x[h * chs + d] = sum_s e^(m_s - M) o_s[d] / sum_s e^(m_s - M) l_s over the
+  // cn chunks, M = max_s m_s.
+  const float *cws = nullptr;
+  int chs = 0, cmax = 0, cn = 0;
 };
 // K a multiple of 32 and of gs (a multiple of 32), K <= 20480, x0 and nw 16-byte aligned.
 bool w4d8_supported(int K, int gs, const void *x0, const void *nw);

@@ -134,6 +134,13 @@ __device__ __forceinline__ float silu_mul(float h1, float h3) {
   return (h1 / (1.f + expf(-h1))) * h3;
 }
 
+// Split-attention partials as x (CMB), in the arithmetic of the decode's
+// combine kernel: per head, M = max_s m_s, e_s = e^(m_s - M), 1/L with
+// L = sum_s e_s l_s; x = (sum_s e_s o_s) * (1/L).  The first kCmbRegs chunks
+// of the thread's elements are requested at kernel start with the heads'
+// statistics (one round trip); further chunks (contexts past 4 * 64) are
+// read when combined.
+constexpr int kCmbRegs = 4;
 // C chunks per lane, KT waves per row, NW waves per block (NW / KT teams),
 // D rows in flight per team, MULTI: more than one segment (a single segment
 // reads every argument at a fixed offset, one round of scalar loads),
@@ -144,13 +151,17 @@ __device__ __forceinline__ float silu_mul(float h1, float h3) {
 // once for all of them.
 // Units are rows (pairs of rows in mode 2); the blocks of a segment split its
 // units evenly, team t of a block takes the block's units t, t + teams, ...
-// UZ: unsigned nibbles with zeros (every segment's Z set).
-template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI, int MX, bool UZ>
+// UZ: unsigned nibbles with zeros (every segment's Z set).  CMB: x from
+// split-attention partials (a.cws), combined after the first weight rows are
+// requested.
+template <int C, int KT, int NW, int D, int RM, bool NORM, int OUT, bool MULTI, int MX, bool UZ,
+          bool CMB = false>
 __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   constexpr int NT = 64 * NW, NTM = NW / KT, UPR = OUT == 2 ? 2 : 1;
   static_assert(RM % UPR == 0 && RM >= D, "rows");
   static_assert(MX == 1 || (OUT == 0 && !NORM && !MULTI), "several x vectors: plain stores");
   static_assert(MX == 1 || !UZ, "zeros: one x vector");
+  static_assert(!CMB || (MX == 1 && !NORM && !MULTI && OUT == 1), "partials: plain accumulate");
   extern __shared__ __align__(16) uint32_t sm[];
   const int K = a.K, nchunk = K >> 5, ngrp8 = K >> 3;
   const int cpg = a.gs >> 5, cps = cpg_log2(cpg);
@@ -159,6 +170,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   float *xs = xf + MX * nchunk;                 // [MX][nchunk] sum of the chunk's x (UZ)
   float *ssq = xs + (UZ ? MX * nchunk : 0);     // [NW]
   float *red = ssq + NW;                        // [NW][MX][RM] row totals per wave
+  float *cef = red + NW * MX * RM;              // CMB: [heads][cmax] e_s, then [heads] 1/L
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int team = wave / KT, kw = wave - team * KT;
@@ -168,8 +180,31 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   // 64*C*KT chunks, so XP passes cover K, all requested before any weight
   constexpr int XP = (4 * C * KT + NW - 1) / NW;
   float4 xa[MX][XP], xb[MX][XP], na[XP], nb[XP];
+  // CMB: chunks 0 .. kCmbRegs-1 of the thread's 2 x XP groups of 4 elements
+  float4 cov[CMB ? XP : 1][2][CMB ? kCmbRegs : 1];
+  float2 cml[CMB ? kCmbRegs : 1];
+  if constexpr (CMB) {
+    const int st = a.chs + 4;
 #pragma unroll
-  for (int ps = 0; ps < XP; ps++) {
+    for (int ps = 0; ps < XP; ps++)
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int e0 = 8 * min((int)threadIdx.x + NT * ps, ngrp8 - 1) + 4 * hf;
+        const int h = e0 / a.chs;
+        const float *w = a.cws + (int64_t)h * a.cmax * st + (e0 - h * a.chs);
+#pragma unroll
+        for (int s = 0; s < kCmbRegs; s++)
+          cov[ps][hf][s] = s < a.cn ? *(const float4 *)(w + s * st) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    // the heads' statistics (m, l) of chunks 0 .. kCmbRegs-1: thread h < heads
+    const int h = min((int)threadIdx.x, K / a.chs - 1);
+    const float *w = a.cws + (int64_t)h * a.cmax * st + a.chs;
+#pragma unroll
+    for (int s = 0; s < kCmbRegs; s++)
+      cml[s] = s < a.cn ? *(const float2 *)(w + s * st) : make_float2(-INFINITY, 0.f);
+  }
+#pragma unroll
+  for (int ps = 0; ps < XP && !CMB; ps++) {
     const int g8 = min((int)threadIdx.x + NT * ps, ngrp8 - 1);
 #pragma unroll
     for (int m = 0; m < MX; m++) {
@@ -258,6 +293,57 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   for (int d = 0; d < D; d++) {
     issue(d, d);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (CMB) {
+    const int st = a.chs + 4, heads = K / a.chs;
+    if ((int)threadIdx.x < heads) {  // e_s and 1/L of head threadIdx.x
+      const int h = threadIdx.x;
+      const float *w = a.cws + (int64_t)h * a.cmax * st + a.chs;
+      float M = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < kCmbRegs; s++)
+        if (s < a.cn) M = fmaxf(M, cml[s].x);
+      for (int s = kCmbRegs; s < a.cn; s++) M = fmaxf(M, w[s * st]);
+      float L = 0.f;
+#pragma unroll
+      for (int s = 0; s < kCmbRegs; s++)
+        if (s < a.cn) {
+          const float e = expf(cml[s].x - M);
+          L += e * cml[s].y;
+          cef[h * a.cmax + s] = e;
+        }
+      for (int s = kCmbRegs; s < a.cn; s++) {
+        const float e = expf(w[s * st] - M);
+        L += e * w[s * st + 1];
+        cef[h * a.cmax + s] = e;
+      }
+      cef[heads * a.cmax + h] = 1.f / L;
+    }
+    lds_barrier();
+#pragma unroll
+    for (int ps = 0; ps < XP; ps++)
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int e0 = 8 * min((int)threadIdx.x + NT * ps, ngrp8 - 1) + 4 * hf;
+        const int h = e0 / a.chs;
+        const float *ef = cef + h * a.cmax;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto acc4 = [&](float e, float4 v) {
+          o.x = fmaf(e, v.x, o.x);
+          o.y = fmaf(e, v.y, o.y);
+          o.z = fmaf(e, v.z, o.z);
+          o.w = fmaf(e, v.w, o.w);
+        };
+#pragma unroll
+        for (int s = 0; s < kCmbRegs; s++)
+          if (s < a.cn) acc4(ef[s], cov[ps][hf][s]);
+        const float *w = a.cws + (int64_t)h * a.cmax * st + (e0 - h * a.chs);
+        for (int s = kCmbRegs; s < a.cn; s++) acc4(ef[s], *(const float4 *)(w + s * st));
+        const float il = cef[heads * a.cmax + h];
+        const float4 x = make_float4(o.x * il, o.y * il, o.z * il, o.w * il);
+        if (hf == 0) xa[0][ps] = x;
+        else xb[0][ps] = x;
+      }
   }
 
   // x -> limbs in LDS, one k-group of 8 elements per thread per pass
@@ -459,6 +545,11 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
 
 template <int C, int KT, int NW, int D, int RM, bool UZ>
 void launch_modes(const W4D8Args &a, int G, size_t shm, hipStream_t st) {
+  if (a.cws) {  // x from attention partials (checked by launch_w4d8: plain accumulate)
+    hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, false, 1, false, 1, UZ, true>), dim3((unsigned)G),
+                       dim3(64 * NW), shm, st, a);
+    return;
+  }
   const bool norm = a.nw != nullptr;
 #define L8(NORMV, OUTV, MV)                                                                       \
   hipLaunchKernelGGL((w4d8_gemv<C, KT, NW, D, RM, NORMV, OUTV, MV, 1, UZ>), dim3((unsigned)G), dim3(64 * NW), \
@@ -480,7 +571,8 @@ template <int C, int KT, int NW, int D, int RM, int MX = 1>
 int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
   const int nchunk = a.K / 32;
   const bool uz = a.s[0].Z != nullptr;
-  const size_t shm = sizeof(float) * ((size_t)(uz ? 26 : 25) * MX * nchunk + NW + (size_t)NW * MX * RM);
+  const size_t cmb = a.cws ? (size_t)(a.K / a.chs) * (a.cmax + 1) : 0;  // e_s and 1/L per head
+  const size_t shm = sizeof(float) * ((size_t)(uz ? 26 : 25) * MX * nchunk + NW + (size_t)NW * MX * RM + cmb);
   if (shm > 160 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
   KernelTimer kt(st, "w4s_gemv_d8");
   if constexpr (MX > 1) {
@@ -541,6 +633,9 @@ int launch_w4d8(const W4D8Args &a, hipStream_t st) {
     if ((a.s[i].Z != nullptr) != (a.s[0].Z != nullptr))
       return set_error(SIMP_RT_EINVAL, "w4d8: zeros on some segments only");
   if (a.s[0].Z && a.mx > 1) return set_error(SIMP_RT_EINVAL, "w4d8: zeros with several x vectors");
+  if (a.cws && (a.n != 1 || a.out_mode != 1 || a.nw || a.mx > 1 || a.chs <= 0 || a.chs % 4 ||
+                a.K % a.chs || a.K / a.chs > 256 || a.cn < 1 || a.cn > a.cmax))
+    return set_error(SIMP_RT_EINVAL, "w4d8: attention partials need one accumulating segment");
   const int nchunk = a.K / 32;
   if (a.mx > 1) {
     // several x vectors: one chunk per lane (the limbs of every vector stay in
