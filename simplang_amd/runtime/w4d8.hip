@@ -588,8 +588,8 @@ int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
 }
 
 // Blocks: at least one per CU, and enough that a team has at most 16 rows
-// (about 16 rows per team streams best); the segments' blocks are
-// proportional to their rows.
+// (about 16 rows per team streams best; caps of 24 and 32 with fewer blocks
+// measured 2-3% slower on the 3B W4 decode).
 template <int C, int KT, int NW, int D, int MX = 1>
 int launch_cfg(W4D8Args a, hipStream_t st) {
   constexpr int teams = NW / KT;
@@ -597,16 +597,37 @@ int launch_cfg(W4D8Args a, hipStream_t st) {
   const int nseg = a.out_mode == 2 ? 1 : a.n;
   int64_t total = 0;
   for (int i = 0; i < nseg; i++) total += a.s[i].rows;
-  const int64_t G0 = std::max<int64_t>(num_cus(), cdiv(total * upr, (int64_t)teams * 16));
+  // Whole rounds of blocks: a count just past a multiple of the CU count
+  // leaves a few CUs with one block more than the rest, and the launch lasts
+  // as long as they do (3B W4 decode: W1|W3 at 270 and QKV at 258 blocks;
+  // 966 -> 1047 tok/s with 512 and 256; at least two rounds measured slower).
+  // Segments take blocks in proportion to their rows, at least enough for 16
+  // rows per team; the remainder goes one by one to the segments in order.
+  const int64_t cus = num_cus();
+  int64_t G0 = std::max<int64_t>(cus, cdiv(total * upr, (int64_t)teams * 16));
+  G0 = cdiv(G0, cus) * cus;
   int nb[3] = {0, 0, 0}, G = 0;
   int64_t rows = 0;  // rows per team at most
+  int64_t rem = G0;
   for (int i = 0; i < nseg; i++) {
     const int64_t u = a.s[i].rows;
-    int64_t b = std::max<int64_t>(cdiv(G0 * u, total), cdiv(u * upr, (int64_t)teams * 16));
+    int64_t b = std::max<int64_t>(G0 * u / total, cdiv(u * upr, (int64_t)teams * 16));
     b = std::max<int64_t>(1, std::min<int64_t>(b, u));
     nb[i] = (int)b;
+    rem -= b;
+  }
+  for (bool more = true; rem > 0 && more;) {
+    more = false;
+    for (int i = 0; i < nseg && rem > 0; i++)
+      if (nb[i] < a.s[i].rows) {
+        nb[i]++;
+        rem--;
+        more = true;
+      }
+  }
+  for (int i = 0; i < nseg; i++) {
     G += nb[i];
-    rows = std::max<int64_t>(rows, cdiv(cdiv(u, b), teams) * upr);
+    rows = std::max<int64_t>(rows, cdiv(cdiv((int64_t)a.s[i].rows, nb[i]), teams) * upr);
   }
   a.bstart[0] = 0;
   a.bstart[1] = nseg > 1 ? nb[0] : INT32_MAX;
