@@ -385,12 +385,11 @@ int l32_alloc(L32Model &m) {
 
 // One int8 GEMV launch: C chunks per lane from K, R rows per wave.  With xn
 // (and nw) given, the kernel forms xq as the RMSNorm of xn quantized.
-template <int MODE>
-int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, int8_t *krow,
-             int8_t *vrow, float *x, int8_t *hb, hipStream_t st, const float *xn = nullptr,
-             const float *nw = nullptr, float eps = 0.f) {
+template <int MODE, int R>
+int l32_gemv_r(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, int8_t *krow,
+               int8_t *vrow, float *x, int8_t *hb, hipStream_t st, const float *xn,
+               const float *nw, float eps) {
   const int C = (int)cdiv(K / 16, 64);
-  constexpr int R = MODE == kL32Pair ? 1 : 2;
   const unsigned grid = (unsigned)cdiv(total, 4 * R);
   const size_t lds = xn ? (size_t)K : 0;
 #define L32G(CC)                                                                              \
@@ -410,6 +409,20 @@ int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, 
 #undef L32G
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
+}
+
+// Two rows per wave where that gives whole rounds of blocks (a multiple of
+// the CU count, or many rounds), else one: a count just past a round leaves
+// some CUs a second block (the 1B QKV: 384 blocks of two rows, 768 of one).
+template <int MODE>
+int l32_gemv(const L32Segs &sg, int total, int K, const int8_t *xq, int32_t *q, int8_t *krow,
+             int8_t *vrow, float *x, int8_t *hb, hipStream_t st, const float *xn = nullptr,
+             const float *nw = nullptr, float eps = 0.f) {
+  const int64_t cus = num_cus(), g2 = cdiv(total, 8);
+  if (MODE != kL32Pair && (g2 % cus == 0 || g2 >= 8 * cus))
+    return l32_gemv_r<MODE, MODE == kL32Pair ? 1 : 2>(sg, total, K, xq, q, krow, vrow, x, hb, st,
+                                                      xn, nw, eps);
+  return l32_gemv_r<MODE, 1>(sg, total, K, xq, q, krow, vrow, x, hb, st, xn, nw, eps);
 }
 
 int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
