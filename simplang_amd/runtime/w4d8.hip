@@ -677,6 +677,11 @@ int launch_w4d8(const W4D8Args &a, hipStream_t st) {
     if (nchunk <= 320) return launch_cfg<1, 5, 10, 4, 4>(a, st);
     return launch_cfg<1, 10, 10, 4, 4>(a, st);
   }
+  // x from attention partials: twice the waves per block, so each thread
+  // combines half as many x elements in the prologue (3B W4 decode Wo:
+  // 1068 -> 1087 tok/s; the same form for the other K = 3200 GEMVs measured
+  // equal or slower, and 2-6 rows in flight or 16 waves slower here)
+  if (a.cws && nchunk > 64 && nchunk <= 128) return launch_cfg<1, 2, 8, 4>(a, st);
   if (nchunk <= 64) return launch_cfg<1, 1, 4, 4>(a, st);
   if (nchunk <= 128) return launch_cfg<2, 1, 4, 4>(a, st);
   if (nchunk <= 192) return launch_cfg<1, 3, 6, 4>(a, st);
