@@ -602,7 +602,9 @@ __global__ void __launch_bounds__(64 * NWV)
 #pragma unroll
   for (int e = 0; e < WP; e++) {
     const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 4 * e));
-    const float4 x = tw + e == pos ? vn : vv[e];
+    // rows past pos are selected out, not weighted by 0: the cache beyond
+    // the written positions holds whatever the memory held (0 * NaN = NaN)
+    const float4 x = tw + e == pos ? vn : tw + e < pos ? vv[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     o.x = fmaf(pt, x.x, o.x);
     o.y = fmaf(pt, x.y, o.y);
     o.z = fmaf(pt, x.z, o.z);

@@ -245,6 +245,32 @@ def test_stories110M_forward_jumps_and_host_filled_caches(dev, orc):
     sa.forward_cache_clear()
 
 
+def test_stories110M_forward_nan_rows_past_pos_are_not_read(dev, orc):
+    """Cache rows past pos never reach the result, whatever they hold: a call
+    at pos 8 loads NaN rows [0, 8) into the engine's cache, and a jump back to
+    pos 1 (row 0 reloaded) must not see the NaN rows 2..7 that stay behind.
+    The split attention loads every row of its chunk before pos is known; a
+    row past pos weighted by probability 0 instead of dropped gives 0*NaN."""
+    sa.forward_cache_clear()
+    w, arrays = _host_model(35)
+    toks = [7, 70, 170]
+    arrays["key_cache"][:] = np.nan
+    arrays["value_cache"][:] = np.nan
+    sa.stories110M_forward(arrays, toks[2], 8, *_cfg_args())   # NaN attention: NaN result
+    ref = _stories_oracle(orc, w)
+    ref.forward(toks[0], 0)
+    arrays["key_cache"][:] = ref.kc
+    arrays["value_cache"][:] = ref.vc
+    kv =CFG["dim"] * CFG["n_kv_heads"] // CFG["n_heads"]
+    for name in ("key_cache", "value_cache"):
+        arrays[name].reshape(CFG["n_layers"], CFG["seq_len"], kv)[:, 1:] = np.nan
+    print("[forward-export] NaN rows past pos 1", flush=True)
+    r = sa.stories110M_forward(arrays, toks[1], 1, *_cfg_args())
+    assert np.isfinite(arrays["logits"]).all() and r == r
+    _same(arrays["logits"], ref.forward(toks[1], 1))
+    sa.forward_cache_clear()
+
+
 def test_stories110M_forward_nan_is_not_an_error(dev, orc):
     """A NaN the arithmetic produces comes back as NaN without an exception,
     even after an earlier failed call left a message behind."""
