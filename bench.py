@@ -6,10 +6,17 @@ Headline (the JSON line's ``value``): exact int8 GEMM throughput, u8 x s8 -> i32
 (8192^3), inputs resident in HBM.  One step = one C = A x B over the
 synthetic batch (A u8 uniform [0,255], B s8 uniform [-128,127], seed 42).
 
-``value`` and ``ms_per_step`` cover the whole call (B transpose + column sums +
-GEMM).  ``roofline`` is the dominant kernel alone: its launches are bracketed
-with HIP events on the stream they run on (simp_rt_timing), so ``achieved`` is
-2*M*N*K over that kernel's average launch time.
+``value`` and ``ms_per_step`` cover the whole call (column sums + GEMM).
+``roofline`` is the dominant kernel alone: its launches are bracketed with HIP
+events on the stream they run on (simp_rt_timing), so ``achieved`` is 2*M*N*K
+over that kernel's average launch time.
+
+Clock settling: under this kernel's sustained load the chip's clocks dip and
+recover over its first ~60 calls (per-call times on one box: 546, 601, 652,
+740, 733, 714, 669, ... 559 us average over calls 21-40, 532 over 41-60, then
+523-526 us), so SETTLE_CALLS untimed calls run before the W warmup calls and
+the K timed ones; the line reports the count as ``settle_calls``.  Without
+them, 5 warmup + 20 timed calls average 613 us on the same box.
 
 Also reported on the same line: the configs[1] sweep (TOPS per shape), the W4
 GEMV (with its CPU baseline per shape), rmsnorm / softmax / silu, fp32 GEMM and
@@ -37,6 +44,7 @@ METRIC = "int8 GEMM TOPS (% MFMA peak); W4 decode tokens/s + HBM GB/s (1 GPU)"
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POPS
 FP32_PEAK_TFS = 157.3    # MI355X dense fp32 MFMA
 HBM_PEAK_GBS = 8000.0
+SETTLE_CALLS = 60        # untimed headline calls before the warmup (clock settling)
 
 
 def gemm_events(fn, a, b, c, steps, warmup, stream):
@@ -505,7 +513,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=40,
-                    help="untimed calls first: the chip takes ~40 calls to settle its clocks")
+                    help="untimed calls right before the timed ones (after SETTLE_CALLS)")
     ap.add_argument("--size", type=int, default=8192)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -556,6 +564,8 @@ def main():
     if args.only in (None, "gemm"):
         a, b, c = make_inputs(n, n, n, dev)
         torch.cuda.synchronize()
+        for _ in range(SETTLE_CALLS):  # clocks settle under the sustained load
+            sa.matmul_u8s8_i32(a, b, c)
         ms = gemm_events(sa.matmul_u8s8_i32, a, b, c, args.steps, args.warmup, stream)
         tops = 2.0 * n * n * n / (ms * 1e-3) / 1e12
         # the dominant kernel alone: HIP events around its launches, on its stream
@@ -609,6 +619,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "settle_calls": SETTLE_CALLS if args.only in (None, "gemm") else 0,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
