@@ -305,7 +305,9 @@ def decode_bench(dev, stream, with_cpu=True):
         w = make_model(cfg, dev, seed=42)
         prompt = np.random.default_rng(42).integers(0, cfg["vocab_size"], 32).astype(np.int32)
         m = sa.Llama(cfg, w)
-        m.generate(prompt, 8, use_graph=True)            # capture + warm
+        # capture + warm: the same positions as the timed run, so every step
+        # graph (one per attention form and chunk count) exists before timing
+        m.generate(prompt, n_new, use_graph=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         toks = m.generate(prompt, n_new, use_graph=True)
