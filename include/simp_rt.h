@@ -175,6 +175,13 @@ int32_t benchmark_int8_matmul_1024(void);
 int32_t benchmark_int8_matmul_2048(void);
 int32_t benchmark_int8_matmul_4096(void);
 
+/* kernel_main() replaces fn kernel_main() -> i32 of
+ * simptensor/benchmarks/bench_int8_matmul.sl:337-339, which returns
+ * benchmark_int8_matmul_256(): the entry point the generic runner looks up
+ * (runtime/include/kernel_runner.hpp:39-56, runtime/src/host.cpp:158-193).
+ * The program returns i32; a host binds it as int32_t (*)(void). */
+int32_t kernel_main(void);
+
 /* int8_chunk_<N>(i8[] A, i8[] B, i32[] C, i64 row_start) replaces
  * fn int8_chunk_<N> of simptensor/benchmarks/bench_int8_matmul_parallel.sl:5-73
  * (typedef ChunkFunc, bench_int8_parallel_runner.cpp:13-16, looked up at :122):
@@ -210,6 +217,22 @@ int32_t simp_rt_matmul_quant(
     const float *in_alloc, const float *in, int64_t in_off, int64_t in_size, int64_t in_stride,
     float *out_alloc, float *out, int64_t out_off, int64_t out_size, int64_t out_stride,
     int64_t rows, int64_t cols, int64_t group_size, int64_t offset);
+
+/* dequant_w4(qweights, scales, zeros, idx, group_size) over a range:
+ * out[i] = q(idx + i) * scales[(idx + i) / group_size] + zeros[(idx + i) / group_size]
+ * for 0 <= i < count, q(e) the unsigned nibble of flat element e (low nibble =
+ * even e), fp32 multiply then add, each rounded.  Replaces DequantW4OpLowering
+ * (src/mlir/lowering/ConvertSimpToMemRef.cpp:2367-2429; builtin operands of
+ * src/mlir/mlir_codegen.cpp:1482-1500, in that order, then the destination and
+ * the element count).  The builtin is a scalar expression the program
+ * evaluates per element inside its own loops; one device call per element
+ * would cost a launch per weight, so the entry point takes a range. */
+int32_t simp_rt_dequant_w4(
+    const int8_t *qw_alloc, const int8_t *qw, int64_t qw_off, int64_t qw_size, int64_t qw_stride,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_size, int64_t s_stride,
+    const float *z_alloc, const float *z, int64_t z_off, int64_t z_size, int64_t z_stride,
+    int64_t idx, int64_t group_size, float *out_alloc, float *out, int64_t out_off,
+    int64_t out_size, int64_t out_stride, int64_t count);
 
 /* Symmetric W4 GEMV / skinny GEMM: out[M,N] = x[M,K] * W^T with W[N,K] packed
  * as signed nibbles in [-8,7] (low nibble = even k, rows of K/2 bytes) and one

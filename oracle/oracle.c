@@ -11,7 +11,9 @@
  *   orc_matmul_i8             -- closed forms (identity/one-hot/constant) +
  *                                reference VNNI kernel compiled in place
  *   orc_matmul_i8_vnni        -- equals orc_matmul_i8 bit for bit (both paths)
- *   orc_int8_recipe_inputs    -- recipe restated; checksum vs reference kernel
+ *   orc_int8_recipe_inputs    -- recipe restated; equals the numpy closed form
+ *                                ((i*N+j)%127)-64 with A = B^T element by element;
+ *                                checksum vs reference kernel
  *   orc_matmul_i4             -- reference packed_matmul_int4<N> checksums (32, 64,
  *                                128) on orc_int4_recipe_inputs; equals the int8
  *                                product of the unpacked nibbles truncated to i16
@@ -22,6 +24,10 @@
  *   orc_rmsnorm/softmax/silu  -- KATs of examples/llama2/kernels/test_*_host.cpp
  *   orc_matmul_quant_f5       -- closed-form KAT of test_quant_roofline.cpp:71-92
  *                                (0x55 bytes, scale .01) + f64 dequant brute force
+ *   orc_dequant_w4            -- 0x55 / scale .01 / zero 0 gives 5 * .01f
+ *                                (test_quant_roofline.cpp:71-92); equals
+ *                                orc_matmul_quant_f5 with one-hot inputs element by
+ *                                element (a swapped nibble or group index fails it)
  *   orc_matmul_w4s            -- F6 == F5 with u = q+8, zero = -8*scale; brute force
  *   orc_rope                  -- pos 0 identity, rotation preserves pair norms,
  *                                closed-form angle for pair 0
@@ -43,6 +49,11 @@
  *   orc_mt_next               -- the C++ standard's check value: the 10000th draw
  *                                of std::mt19937 default-seeded (5489) is
  *                                4123659995 ([rand.predef])
+ *   orc_argmax                -- closed forms of sample_argmax's scan: ties give
+ *                                the first index, NaN at 0 gives 0, NaN elsewhere
+ *                                is skipped, all NaN / all -inf give 0; brute force
+ *                                over every pattern of 5 values from {-inf, -1, 0,
+ *                                -0, 1, NaN}
  *   orc_uniform01f, orc_sample -- equal the library's std::mt19937 /
  *                                uniform_real_distribution<float> sampler
  */
@@ -332,6 +343,20 @@ void orc_silu(const float *in, float *out, int64_t size) {
 }
 
 /* ------------------------------------------------------------------ W4 -- */
+
+/* DequantW4OpLowering (src/mlir/lowering/ConvertSimpToMemRef.cpp:2367-2429)
+ * evaluated at idx .. idx+count-1: q = nibble idx%2 of byte idx/2 (low =
+ * even), g = idx/gs, q*scales[g] rounded, then + zeros[g] rounded. */
+void orc_dequant_w4(const uint8_t *qw, const float *scales, const float *zeros, int64_t idx,
+                    int64_t count, int64_t gs, float *out) {
+  for (int64_t i = 0; i < count; i++) {
+    const int64_t e = idx + i, g = e / gs;
+    const uint8_t byte = qw[e / 2];
+    const uint32_t q = (e % 2 == 0) ? (uint32_t)byte & 15u : ((uint32_t)byte >> 4) & 15u;
+    const float scaled = (float)q * scales[g];
+    out[i] = scaled + zeros[g];
+  }
+}
 
 void orc_matmul_quant_f5(const uint8_t *qw, const float *scales,
                          const float *zeros, const float *in, float *out,
@@ -775,6 +800,8 @@ void orc_llama_quant_forward(const orc_llama_cfg *c, const float *emb, const flo
   free(hb); free(hb2); free(att); free(att_soft);
 }
 
+/* sample_argmax (examples/llama2/generate_stories110M.cpp:73-83): seeded with
+ * logits[0], moves on a strict '>' (NaN compares false). */
 int64_t orc_argmax(const float *logits, int64_t n) {
   int64_t best = 0;
   float mv = logits[0];

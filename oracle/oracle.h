@@ -118,6 +118,11 @@ void orc_silu(const float *in, float *out, int64_t size);
 
 /* ------------------------------------------------------------------ W4 -- */
 
+/* dequant_w4 (ConvertSimpToMemRef.cpp:2367-2429) at idx .. idx+count-1:
+ * unsigned nibble * scale + zero of the element's flat group. */
+void orc_dequant_w4(const uint8_t *qw, const float *scales, const float *zeros, int64_t idx,
+                    int64_t count, int64_t gs, float *out);
+
 /* Reference W4 format (F5): unsigned nibbles, low nibble = even flat index,
  * w = q*scale + zero, groups are flat runs of gs weights.
  * Restates MatMulQuantOpLowering (ConvertSimpToMemRef.cpp:3906-4005): per row,

@@ -51,6 +51,7 @@ _s("orc_rmsnorm", [_P, _P, _P, _I, _F, _I])
 _s("orc_softmax", [_P, _P, _I, _I, _I])
 _s("orc_silu", [_P, _P, _I])
 _s("orc_matmul_quant_f5", [_P, _P, _P, _P, _P, _I, _I, _I, _I])
+_s("orc_dequant_w4", [_P, _P, _P, _I, _I, _I, _P])
 _s("orc_matmul_quant_f5_refidx", [_P, _P, _P, _P, _P, _I, _I, _I, _I])
 _s("orc_quantize_f5", [_P, _I, _I, _P, _P, _P])
 _s("orc_matmul_w4s", [_P, _P, _P, _P, _I, _I, _I, _I])
@@ -338,6 +339,12 @@ def silu(x):
 def matmul_quant_f5(qw, scales, zeros, x, rows, cols, gs, off=0):
     out = np.empty(rows, np.float32)
     _o.orc_matmul_quant_f5(_p(qw), _p(scales), _p(zeros), _p(x), _p(out), rows, cols, gs, off)
+    return out
+
+
+def dequant_w4(qw, scales, zeros, idx, count, gs):
+    out = np.empty(count, np.float32)
+    _o.orc_dequant_w4(_p(qw), _p(scales), _p(zeros), idx, count, gs, _p(out))
     return out
 
 

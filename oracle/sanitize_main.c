@@ -149,6 +149,10 @@ static void w4_paths(void) {
       orc_matmul_quant_f5(q, sc, ze, x, o1, rows, cols, gs, l * rows * cols);
       if (gs == 128) orc_matmul_quant_f5_refidx(q, sc, ze, x, o2, rows, cols, gs, l * rows * cols);
     }
+    /* the whole array, exactly sized, from an odd start to the last element */
+    float *d = xmalloc(sizeof(float) * (size_t)total);
+    orc_dequant_w4(q, sc, ze, 1, total - 1, gs, d);
+    free(d);
     free(w), free(q), free(sc), free(ze), free(x), free(o1), free(o2);
   }
   /* symmetric format: M x vectors, N rows, K = 3 groups of 32 */

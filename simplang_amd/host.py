@@ -60,6 +60,7 @@ for _n in ("simp_rt_tensor_matmul_i8", "simp_rt_tensor_matmul_nt_i8",
     _sig(_n, _D2 * 3)
 _sig("simp_rt_matmul_quant", _D1 * 5 + [_I, _I, _I, _I])
 _sig("simp_rt_matmul_w4s", _D2 * 4 + [_I])
+_sig("simp_rt_dequant_w4", _D1 * 3 + [_I, _I] + _D1 + [_I])
 _sig("simp_rt_matmul_f32", _D1 * 3 + [_I] * 6)
 _sig("simp_rt_tensor_matmul_f32", _D2 * 3)
 _sig("simp_rt_tensor_matmul_nt_f32", _D2 * 3)
@@ -102,7 +103,7 @@ def declared_symbols(header: str = HEADER) -> list[str]:
     # model-level exports keep the reference program's names
     names |= set(re.findall(r"^float\s+(\w+_forward)\s*\(", text, re.M))
     # the int8 benchmark programs keep theirs too
-    names |= set(re.findall(r"^int32_t\s+(benchmark_int8_matmul_\d+)\s*\(", text, re.M))
+    names |= set(re.findall(r"^int32_t\s+(benchmark_int8_matmul_\d+|kernel_main)\s*\(", text, re.M))
     names |= {f"int8_chunk_{n}" for n in re.findall(r"^SIMP_RT_INT8_CHUNK\((\d+)\);", text, re.M)}
     return sorted(names)
 
@@ -321,6 +322,7 @@ BENCH_INT8_SIZES = (32, 64, 128, 256, 384, 512, 768, 1024, 2048, 4096)
 CHUNK_INT8_SIZES = (256, 512, 768, 1024, 2048)
 for _n in BENCH_INT8_SIZES:
     _sig(f"benchmark_int8_matmul_{_n}", [])
+_sig("kernel_main", [])
 for _n in CHUNK_INT8_SIZES:
     _sig(f"int8_chunk_{_n}", [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64] * 3
          + [C.c_int64])
@@ -333,6 +335,16 @@ def benchmark_int8_matmul(n: int) -> int:
     r = getattr(lib, f"benchmark_int8_matmul_{n}")()
     if lib.simp_rt_error_count() != n0:
         raise SimpRTError(f"benchmark_int8_matmul_{n}", -1, last_error())
+    return r
+
+
+def kernel_main() -> int:
+    """``kernel_main()`` of bench_int8_matmul.sl:337-339 (the runner's entry
+    point): ``benchmark_int8_matmul_256()``."""
+    n0 = lib.simp_rt_error_count()
+    r = lib.kernel_main()
+    if lib.simp_rt_error_count() != n0:
+        raise SimpRTError("kernel_main", -1, last_error())
     return r
 
 
@@ -380,6 +392,16 @@ def matmul_quant(qweights, scales, zeros, inp, out, rows, cols, group_size, offs
     _check("simp_rt_matmul_quant",
            lib.simp_rt_matmul_quant(*desc1(qweights), *desc1(scales), *desc1(zeros),
                                     *desc1(inp), *desc1(out), rows, cols, group_size, offset))
+    return out
+
+
+def dequant_w4(qweights, scales, zeros, idx, group_size, out, count=None):
+    """``dequant_w4`` builtin over a range: out[i] = the reference-format weight
+    of flat element idx + i (unsigned nibble * scale + zero), i < count."""
+    count = out.shape[0] if count is None else count
+    _check("simp_rt_dequant_w4",
+           lib.simp_rt_dequant_w4(*desc1(qweights), *desc1(scales), *desc1(zeros), idx,
+                                  group_size, *desc1(out), count))
     return out
 
 

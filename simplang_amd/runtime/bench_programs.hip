@@ -8,6 +8,8 @@
 //       runs tensor_matmul (s8 x s8 -> i32) and returns the i32 wraparound sum
 //       of C.  The programs have no error path; here an error returns 0 and
 //       raises simp_rt_error_count() (message in simp_rt_last_error()).
+//   int32_t kernel_main(void): the program's entry point,
+//       bench_int8_matmul.sl:337-339, = benchmark_int8_matmul_256().
 //   int32_t int8_chunk_<N>(i8[] A, i8[] B, i32[] C, i64 row_start), N in {256,
 //       512, 768, 1024, 2048} with chunks of N/8 rows:
 //       simptensor/benchmarks/bench_int8_matmul_parallel.sl:5-73, typedef and
@@ -125,6 +127,11 @@ SIMP_BENCH(1024)
 SIMP_BENCH(2048)
 SIMP_BENCH(4096)
 #undef SIMP_BENCH
+
+// fn kernel_main() -> i32 { return benchmark_int8_matmul_256(); }
+// (bench_int8_matmul.sl:337-339): the symbol the generic runner dlsyms
+// (runtime/include/kernel_runner.hpp:39-56, runtime/src/host.cpp:158-193).
+int32_t kernel_main(void) { return benchmark_int8_matmul_256(); }
 
 #define SIMP_CHUNK(N)                                                                            \
   int32_t int8_chunk_##N(int8_t *A_alloc, int8_t *A, int64_t A_off, int64_t A_size,              \

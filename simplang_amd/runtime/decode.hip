@@ -729,15 +729,27 @@ __global__ void __launch_bounds__(256)
   tab[i] = make_float2(cosf(a), sinf(a));
 }
 
+// x = emb[token]. A token outside [0, vocab) (no path writes one: the host
+// checks prompts and argmax_advance_k returns an index below vocab) gives a
+// NaN row instead of a read outside emb.
 __global__ void __launch_bounds__(256)
     embed_k(const float *__restrict__ emb, float *__restrict__ x, const StepState *__restrict__ st,
-            int dim) {
+            int dim, int vocab) {
   const int64_t tok = st->token;
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) x[i] = emb[tok * dim + i];
+  const bool ok = tok >= 0 && tok < vocab;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256)
+    x[i] = ok ? emb[tok * dim + i] : __builtin_nanf("");
 }
 
-// Greedy argmax (first maximum wins) and step advance:
+// Greedy argmax and step advance:
 //   out_tokens[pos+1] = next = (pos+1 < n_prompt) ? prompt[pos+1] : argmax(logits)
+// argmax is sample_argmax of generate_stories110M.cpp:73-83: a scan seeded
+// with logits[0] that moves on a strict '>'. NaN compares false, so the scan
+// returns 0 when logits[0] is NaN, and otherwise the first index of the
+// largest non-NaN value (0 when nothing exceeds logits[0], e.g. all -inf).
+// The parallel form: per-thread strict-'>' scans from -inf (NaN never taken),
+// ties to the lower index across threads, then 0 when logits[0] is NaN or no
+// thread found a value above -inf (the maximum is then logits[0] = -inf).
 __global__ void __launch_bounds__(1024)
     argmax_advance_k(const float *__restrict__ logits, int vocab, StepState *st,
                      const int *__restrict__ prompt, int *__restrict__ out_tokens) {
@@ -782,6 +794,8 @@ __global__ void __launch_bounds__(1024)
     int i0 = bi[0];
     for (int w = 1; w < (int)(blockDim.x >> 6); w++)
       if (bv[w] > b0 || (bv[w] == b0 && bi[w] < i0)) { b0 = bv[w]; i0 = bi[w]; }
+    const float l0 = logits[0];
+    if (l0 != l0 || i0 >= vocab) i0 = 0;
     const int p = st->pos + 1;
     const int next = (p < st->n_prompt) ? prompt[p] : i0;
     if (p < st->n_total) out_tokens[p] = next;
@@ -834,8 +848,12 @@ struct Partials {
 // Wo block reads all chunks of every head, so the fold stops paying past four
 // chunks (positions >= 256): measured on the 3B W4 decode at three chunks,
 // Wo 5.0 -> 6.9 us against the 4.0 us combine kernel it replaces.
-bool fold_combine(int fmt, int gs, int attn, int K, const float *x0) {
-  return attn > 1 && attn <= 4 && fmt != SIMP_RT_W_F32 && w4d8_supported(K, gs, x0, nullptr);
+// The fold also needs what the kernel's prologue assumes: one thread per head
+// (at most 256 heads, the smallest block) and whole float4 groups per head;
+// any other step takes the separate attn_combine_k launch.
+bool fold_combine(int fmt, int gs, int attn, int K, int hs, const float *x0) {
+  return attn > 1 && attn <= 4 && fmt != SIMP_RT_W_F32 && hs > 0 && hs % 4 == 0 && K % hs == 0 &&
+         K / hs <= 256 && w4d8_supported(K, gs, x0, nullptr);
 }
 
 // out_mode kPairSwiGLU: segments 0 and 1 are W1 and W3 (same rows), the
@@ -947,7 +965,7 @@ int enqueue_step(LlamaModel &m, int attn) {
   hipStream_t st = m.stream;
   int rc;
   hipLaunchKernelGGL(embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st,
-                     m.w.token_embedding, m.x, m.state, dim);
+                     m.w.token_embedding, m.x, m.state, dim, (int)c.vocab_size);
   SIMP_HIP(hipGetLastError());
   float *q = m.qkv, *k = m.qkv + dim, *v = m.qkv + dim + kv;
   float *g = m.h13;  // silu(h1) * h3
@@ -971,7 +989,7 @@ int enqueue_step(LlamaModel &m, int attn) {
     // head or per chunk of positions; with chunks, the Wo GEMV on the dot8
     // kernel combines them in its prologue
     float *kc = m.kcache + (int64_t)l * c.seq_len * kv, *vc = m.vcache + (int64_t)l * c.seq_len * kv;
-    const bool fold = fold_combine(c.weight_format, gs, attn, dim, m.xb);
+    const bool fold = fold_combine(c.weight_format, gs, attn, dim, hs, m.xb);
     if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb, m.attn_ws, m.state, dim, kv,
                                (int)c.n_heads, (int)c.n_kv_heads, hs, (const float2 *)m.rope,
                                c.seq_len, st, !fold)))
@@ -1657,7 +1675,8 @@ int quant_enqueue_fused(QuantModel &m, int attn, hipStream_t st) {
   const int dim = (int)m.dim, hid = (int)m.hid, kvd = m.kv_dim, gs = (int)m.gs;
   const float eps = 1e-5f;  // llama2_quant.sl:73,146,184
   const GemvCtx cq{kFmtW4U, gs, eps, st};
-  hipLaunchKernelGGL(embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st, m.emb, m.x, m.state, dim);
+  hipLaunchKernelGGL(embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st, m.emb, m.x, m.state, dim,
+                     (int)m.V);
   SIMP_HIP(hipGetLastError());
   // matrix i of layer l: element offset off[i] + l * per (a multiple of gs)
   auto seg = [&](int i, int64_t l, int64_t per, float *out, int rows) {
@@ -1677,7 +1696,7 @@ int quant_enqueue_fused(QuantModel &m, int attn, hipStream_t st) {
     s.n = 3;
     if ((rc = gemv(cq, s, dim, kRmsNorm, kStore, m.x, m.rms_att + l * dim))) return rc;
     float *kc = m.kc + l * m.seq * kvd, *vc = m.vc + l * m.seq * kvd;
-    const bool fold = fold_combine(kFmtW4U, gs, attn, dim, m.xb2);
+    const bool fold = fold_combine(kFmtW4U, gs, attn, dim, (int)m.hs, m.xb2);
     if ((rc = launch_attention(attn, m.qkv, kc, vc, m.xb2, m.attn_ws, m.state, dim, kvd, (int)m.nh,
                                (int)m.nkv, m.hs, nullptr, m.seq, st, !fold)))  // llama2_quant.sl: no RoPE
       return rc;

@@ -563,6 +563,27 @@ __global__ void __launch_bounds__(256)
   O[i] = acc;
 }
 
+// out[i] = dequant_w4(Q, S, Z, idx0 + i, gs) for i < count: the unsigned
+// nibble of flat element idx0 + i (low nibble = even element) times its
+// group's scale, plus its group's zero, rounded after the multiply and after
+// the add as the lowering's separate mulf and addf (ConvertSimpToMemRef.cpp:
+// 2423-2424) do. Q, S and Z start at byte b0 and group g0 of the arrays.
+__global__ void __launch_bounds__(256)
+    dequant_w4_k(const uint8_t *__restrict__ Q, const float *__restrict__ S,
+                 const float *__restrict__ Z, float *__restrict__ O, int64_t idx0, int64_t count,
+                 int64_t gs, int64_t b0, int64_t g0) {
+  // hipcc contracts a*b+c into one fma by default, which rounds once
+#pragma clang fp contract(off)
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t e = idx0 + i, g = e / gs - g0;
+    const uint8_t b = Q[(e >> 1) - b0];
+    const int q = (e & 1) ? (b >> 4) : (b & 15);
+    const float scaled = (float)q * S[g];
+    O[i] = scaled + Z[g];
+  }
+}
+
 }  // namespace
 
 // Launches the symmetric W4 GEMV on device pointers (shared with the decode step).
@@ -760,6 +781,45 @@ int32_t simp_rt_matmul_quant(
     return rc;
   Operand *ops[] = {&oq, &os, &oz, &oi, &oo};
   return finish(ops, 5);
+}
+
+int32_t simp_rt_dequant_w4(
+    const int8_t *qw_alloc, const int8_t *qw, int64_t qw_off, int64_t qw_size, int64_t qw_stride,
+    const float *s_alloc, const float *s, int64_t s_off, int64_t s_size, int64_t s_stride,
+    const float *z_alloc, const float *z, int64_t z_off, int64_t z_size, int64_t z_stride,
+    int64_t idx, int64_t group_size, float *out_alloc, float *out, int64_t out_off,
+    int64_t out_size, int64_t out_stride, int64_t count) {
+  (void)qw_alloc; (void)s_alloc; (void)z_alloc; (void)out_alloc;
+  int rc;
+  if ((rc = check_desc1("qweights", qw, qw_off, qw_size, qw_stride))) return rc;
+  if ((rc = check_desc1("scales", s, s_off, s_size, s_stride))) return rc;
+  if ((rc = check_desc1("zeros", z, z_off, z_size, z_stride))) return rc;
+  if ((rc = check_desc1("output", out, out_off, out_size, out_stride))) return rc;
+  if (idx < 0 || count < 0 || group_size <= 0)
+    return set_error(SIMP_RT_EINVAL, "dequant_w4: bad idx/count/group_size");
+  if (count == 0) return SIMP_RT_OK;
+  const int64_t last = idx + count - 1;  // the last element dequantized
+  const int64_t b0 = idx / 2, b1 = last / 2, g0 = idx / group_size, g1 = last / group_size;
+  if (b1 >= qw_size || g1 >= s_size || g1 >= z_size || count > out_size)
+    return set_error(SIMP_RT_EINVAL,
+                     "dequant_w4: arrays too small for idx=%lld count=%lld gs=%lld",
+                     (long long)idx, (long long)count, (long long)group_size);
+  // only the bytes and groups the range touches are bound (a host array is
+  // staged for that slice alone)
+  Operand oq, os, oz, oo;
+  if ((rc = oq.bind(qw + qw_off + b0, (size_t)(b1 - b0 + 1), Operand::kIn, "qweights"))) return rc;
+  if ((rc = os.bind(s + s_off + g0, sizeof(float) * (size_t)(g1 - g0 + 1), Operand::kIn, "scales")))
+    return rc;
+  if ((rc = oz.bind(z + z_off + g0, sizeof(float) * (size_t)(g1 - g0 + 1), Operand::kIn, "zeros")))
+    return rc;
+  if ((rc = oo.bind(out + out_off, sizeof(float) * (size_t)count, Operand::kOut, "output"))) return rc;
+  const unsigned grid = (unsigned)std::min<int64_t>(cdiv(count, 256), (int64_t)num_cus() * 16);
+  hipLaunchKernelGGL(dequant_w4_k, dim3(grid), dim3(256), 0, cur_stream(),
+                     (const uint8_t *)oq.dev(), (const float *)os.dev(), (const float *)oz.dev(),
+                     (float *)oo.dev(), idx, count, group_size, b0, g0);
+  SIMP_HIP(hipGetLastError());
+  Operand *ops[] = {&oq, &os, &oz, &oo};
+  return finish(ops, 4);
 }
 
 int32_t simp_rt_matmul_w4s(

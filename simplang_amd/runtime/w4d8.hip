@@ -170,7 +170,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
   float *xs = xf + MX * nchunk;                 // [MX][nchunk] sum of the chunk's x (UZ)
   float *ssq = xs + (UZ ? MX * nchunk : 0);     // [NW]
   float *red = ssq + NW;                        // [NW][MX][RM] row totals per wave
-  float *cef = red + NW * MX * RM;              // CMB: [heads][cmax] e_s, then [heads] 1/L
+  float *cef = red + NW * MX * RM;              // CMB: [heads][cn] e_s, then [heads] 1/L
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int team = wave / KT, kw = wave - team * KT;
@@ -310,14 +310,14 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
         if (s < a.cn) {
           const float e = expf(cml[s].x - M);
           L += e * cml[s].y;
-          cef[h * a.cmax + s] = e;
+          cef[h * a.cn + s] = e;
         }
       for (int s = kCmbRegs; s < a.cn; s++) {
         const float e = expf(w[s * st] - M);
         L += e * w[s * st + 1];
-        cef[h * a.cmax + s] = e;
+        cef[h * a.cn + s] = e;
       }
-      cef[heads * a.cmax + h] = 1.f / L;
+      cef[heads * a.cn + h] = 1.f / L;
     }
     lds_barrier();
 #pragma unroll
@@ -326,7 +326,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
       for (int hf = 0; hf < 2; hf++) {
         const int e0 = 8 * min((int)threadIdx.x + NT * ps, ngrp8 - 1) + 4 * hf;
         const int h = e0 / a.chs;
-        const float *ef = cef + h * a.cmax;
+        const float *ef = cef + h * a.cn;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
         auto acc4 = [&](float e, float4 v) {
           o.x = fmaf(e, v.x, o.x);
@@ -339,7 +339,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
           if (s < a.cn) acc4(ef[s], cov[ps][hf][s]);
         const float *w = a.cws + (int64_t)h * a.cmax * st + (e0 - h * a.chs);
         for (int s = kCmbRegs; s < a.cn; s++) acc4(ef[s], *(const float4 *)(w + s * st));
-        const float il = cef[heads * a.cmax + h];
+        const float il = cef[heads * a.cn + h];
         const float4 x = make_float4(o.x * il, o.y * il, o.z * il, o.w * il);
         if (hf == 0) xa[0][ps] = x;
         else xb[0][ps] = x;
@@ -369,12 +369,17 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
 #pragma unroll
       for (int k = 0; k < 8; k++) v[k] *= nv[k];
     }
-    float m = 0.f;
+    // chunk maximum of |v| as an integer maximum of the magnitude bits: NaN
+    // sorts above Inf above every finite value, so a NaN anywhere in the chunk
+    // survives into m (fmaxf would drop it) and turns the chunk's factor into
+    // NaN below, as the fp32 product of the reference propagates it
+    uint32_t mbits = 0;
 #pragma unroll
-    for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(v[k]));
+    for (int k = 0; k < 8; k++) mbits = max(mbits, __float_as_uint(v[k]) & 0x7fffffffu);
     // the 4 k-groups of a chunk are lanes 4c..4c+3 of one wave
-    m = fmaxf(m, dpp_mov<kDppXor1>(m));
-    m = fmaxf(m, dpp_mov<kDppXor2>(m));
+    mbits = max(mbits, (uint32_t)__builtin_amdgcn_mov_dpp((int)mbits, kDppXor1, 0xF, 0xF, false));
+    mbits = max(mbits, (uint32_t)__builtin_amdgcn_mov_dpp((int)mbits, kDppXor2, 0xF, 0xF, false));
+    const float m = __uint_as_float(mbits);
     int e;
     frexpf(m, &e);       // m < 2^e (e = 0 for m = 0)
     e = max(e, -100);    // chunks below 2^-101 keep fewer bits; 2^(e-22) stays normal
@@ -398,6 +403,7 @@ __global__ void __launch_bounds__(64 * NW) w4d8_gemv(W4D8Args a) {
 #pragma unroll
       for (int j = 0; j < 6; j++) xl[(mv * nchunk + ch) * 24 + 4 * j + dd] = L[j];
       if (dd == 0) {
+        // Inf or NaN in the chunk: NaN (the limbs of such a chunk are meaningless)
         const float fe = (m <= 3.4e38f) ? ldexpf(1.f, e - 22) : __int_as_float(0x7fc00000);
         xf[mv * nchunk + ch] = fe;
         if constexpr (UZ) xs[mv * nchunk + ch] = (float)si * fe;
@@ -571,7 +577,7 @@ template <int C, int KT, int NW, int D, int RM, int MX = 1>
 int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
   const int nchunk = a.K / 32;
   const bool uz = a.s[0].Z != nullptr;
-  const size_t cmb = a.cws ? (size_t)(a.K / a.chs) * (a.cmax + 1) : 0;  // e_s and 1/L per head
+  const size_t cmb = a.cws ? (size_t)(a.K / a.chs) * (a.cn + 1) : 0;  // e_s and 1/L per head
   const size_t shm = sizeof(float) * ((size_t)(uz ? 26 : 25) * MX * nchunk + NW + (size_t)NW * MX * RM + cmb);
   if (shm > 160 * 1024) return set_error(SIMP_RT_EUNSUPPORTED, "w4d8: K=%d too large", a.K);
   KernelTimer kt(st, "w4s_gemv_d8");

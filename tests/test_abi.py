@@ -14,6 +14,7 @@ from simplang_amd import host
 def test_every_declared_symbol_is_exported():
     names = host.declared_symbols()
     assert "simp_rt_tensor_matmul_i8" in names
+    assert "kernel_main" in names and "benchmark_int8_matmul_256" in names
     missing = [n for n in names if not hasattr(sa.lib, n)]
     assert not missing, missing
 
@@ -59,3 +60,13 @@ def test_host_mirror_raises_on_error():
     c = np.zeros((4, 8), np.int32)
     with pytest.raises(sa.SimpRTError):
         sa.tensor_matmul_i8(a, b, c)
+
+
+def test_dequant_w4_rejects_out_of_range():
+    qw = np.zeros(16, np.int8)
+    sc = np.zeros(1, np.float32)
+    out = np.zeros(8, np.float32)
+    with pytest.raises(sa.SimpRTError, match="too small"):
+        sa.dequant_w4(qw, sc, sc, 30, 32, out, 8)       # element 37 is past 32 weights
+    with pytest.raises(sa.SimpRTError, match="bad"):
+        sa.dequant_w4(qw, sc, sc, -1, 32, out, 1)

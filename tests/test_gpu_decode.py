@@ -131,6 +131,40 @@ def test_3b_w4_logits_and_greedy(dev, orc):
     torch.cuda.empty_cache()
 
 
+def test_3b_dims_two_layers_every_chunk_count(dev, orc):
+    """The kernels the configs[4] bench times, at its dims (dim 3200, 32 heads
+    of 100, hidden 8640, W4 g32) with 2 layers and a smaller vocabulary: logits
+    at every position 0..319 (attention over 1, 2, 3, 4 chunks of 64 with the
+    combine folded into the Wo GEMV, then 5 chunks with the separate combine),
+    with a 256-token prompt and greedy tokens from there, and the same 64
+    greedy tokens from the captured step graphs."""
+    import torch
+    cfg = dict(CFG_3B_W4, n_layers=2, vocab_size=4096)
+    w = make_model(cfg, dev, seed=33)
+    P, n_new = 256, 64
+    prompt = np.random.default_rng(33).integers(0, cfg["vocab_size"], P).astype(np.int32)
+    m = sa.Llama(cfg, w)
+    o = orc.LlamaOracle(cfg, to_numpy(w))
+    lg = torch.empty(cfg["vocab_size"], device=dev)
+    toks = list(prompt)
+    for pos in range(P + n_new - 1):
+        if pos % 64 == 0:
+            print(f"[decode] 3B dims 2 layers pos {pos}", flush=True)
+        m.forward(int(toks[pos]), pos, lg)
+        want = o.forward(int(toks[pos]), pos).astype(np.float64)
+        got = lg.cpu().numpy().astype(np.float64)
+        err = np.abs(got - want).max()
+        assert err <= TOL * np.abs(want).max(), (pos, err, np.abs(want).max())
+        if pos + 1 >= P:
+            toks.append(orc.argmax(want.astype(np.float32)))
+    print("[decode] 3B dims 2 layers greedy through the graphs", flush=True)
+    got = m.generate(prompt, n_new, use_graph=True)
+    m.close()
+    assert np.array_equal(got, np.array(toks, np.int32))
+    del w
+    torch.cuda.empty_cache()
+
+
 def test_create_rejects_host_weights_and_bad_config(dev):
     import torch
     cfg = dict(SMALL)
@@ -145,3 +179,69 @@ def test_create_rejects_host_weights_and_bad_config(dev):
         m.generate(np.zeros(60, np.int32), 10)   # exceeds seq_len
     m.close()
     torch.cuda.synchronize()
+
+
+def _tie_classifier(cfg, w, dev, j=3, plus=(5, 9, 300), minus=(7, 11, 301)):
+    """A classifier whose logits tie exactly: rows `plus` are +e_j, rows `minus`
+    -e_j, every other row zero. Each logit is one product, so every sum order
+    gives the same bits; the larger group ties among itself and the reference's
+    argmax (generate_stories110M.cpp:73-83) must return its first row."""
+    import torch
+    V, d = cfg["vocab_size"], cfg["dim"]
+    if cfg["weight_format"] == 0:
+        wc = torch.zeros((V, d), device=dev)
+        wc[list(plus), j] = 1.0
+        wc[list(minus), j] = -1.0
+        return dict(w, wcls=wc)
+    q = torch.zeros((V, d), dtype=torch.int64)
+    q[list(plus), j] = 7
+    q[list(minus), j] = -7
+    nib = (q & 15).to(torch.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).to(dev)
+    return dict(w, q_wcls=packed, s_wcls=torch.full((V, d // cfg["group_size"]), 0.1, device=dev))
+
+
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_greedy_exact_ties_pick_first(dev, orc, fmt):
+    cfg = dict(SMALL, weight_format=fmt)
+    w = _tie_classifier(cfg, make_model(cfg, dev, seed=70 + fmt), dev)
+    prompt = np.random.default_rng(70).integers(0, cfg["vocab_size"], 4).astype(np.int32)
+    m = sa.Llama(cfg, w)
+    got = m.generate(prompt, 24, use_graph=True)
+    got_eager = m.generate(prompt, 24, use_graph=False)
+    m.close()
+    want, _ = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 24)
+    gen = got[len(prompt):]
+    assert set(gen.tolist()) <= {5, 7}, gen
+    assert np.array_equal(got, got_eager)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("nan_rows,expect", [("all", 0), ("first", 0), ("mid", None)])
+def test_greedy_nan_logits(dev, orc, nan_rows, expect):
+    """NaN logits follow the reference's scan: NaN compares false, so a NaN at
+    index 0 (or everywhere) gives token 0, and a NaN elsewhere is skipped. The
+    next step embeds that token (no read outside the embedding)."""
+    import torch
+    cfg = dict(SMALL)
+    w = make_model(cfg, dev, seed=80)
+    wc = w["wcls"].clone()
+    if nan_rows == "all":
+        wc[:] = float("nan")
+    elif nan_rows == "first":
+        wc[0] = float("nan")
+    else:
+        wc[[3, 100, 511]] = float("nan")
+    w = dict(w, wcls=wc)
+    prompt = np.random.default_rng(80).integers(1, cfg["vocab_size"], 4).astype(np.int32)
+    m = sa.Llama(cfg, w)
+    got = m.generate(prompt, 12, use_graph=True)
+    m.close()
+    torch.cuda.synchronize()
+    gen = got[len(prompt):]
+    if expect is not None:
+        assert (gen == expect).all(), gen
+    else:
+        assert not np.isin(gen, [3, 100, 511]).any(), gen
+    want, _ = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 12)
+    assert np.array_equal(got, want)

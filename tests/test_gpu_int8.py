@@ -324,6 +324,16 @@ def test_benchmark_int8_programs(dev):
         assert sa.benchmark_int8_matmul(n) == gold[str(n)], n
 
 
+def test_kernel_main(dev):
+    """kernel_main() of bench_int8_matmul.sl:337-339, the runner's entry point
+    (kernel_runner.hpp:39-56), bound as the compiled program defines it:
+    int32_t (*)(void), returning benchmark_int8_matmul_256()'s checksum."""
+    import ctypes as C
+    f = C.CFUNCTYPE(C.c_int32)(C.cast(sa.lib.kernel_main, C.c_void_p).value)
+    assert f() == _gold_checksums()["256"]
+    assert sa.kernel_main() == _gold_checksums()["256"]
+
+
 @pytest.mark.parametrize("n", [256, 512, 768, 1024, 2048])
 def test_int8_chunk_programs(dev, orc, n):
     """int8_chunk_<N> called the way bench_int8_parallel_runner.cpp:38-89 calls

@@ -95,6 +95,28 @@ def test_llama32_bound_program_matches(dev, orc):
     sa.forward_cache_clear()
 
 
+@pytest.mark.parametrize("wide", [True, False])
+def test_llama32_1b_dims(dev, orc, wide):
+    """The kernel instances the bench times at the LLaMA-3.2-1B shape
+    (bench_llama32_1b_int8.cpp:17-25: dim 2048, hidden 8192, 32 heads of 64,
+    8 KV heads, vocab 128256, 4096 cache rows) with 2 layers. The caller owns
+    the int8 caches, so rows below pos are filled with random int8 on both
+    sides and single positions up to the last row are checked."""
+    import torch
+    cfg = dict(dim=2048, hidden_dim=8192, n_layers=2, n_heads=32, n_kv_heads=8,
+               vocab_size=128256, max_seq_len=4096, head_dim=64)
+    arrays = make_arrays(cfg, seed=21 + wide, wide=wide)
+    rng = np.random.default_rng(22)
+    arrays["k_cache"][:] = rng.integers(-128, 128, arrays["k_cache"].size, dtype=np.int8)
+    arrays["v_cache"][:] = rng.integers(-128, 128, arrays["v_cache"].size, dtype=np.int8)
+    ref = {k: v.copy() for k, v in arrays.items()}
+    darr = {k: torch.from_numpy(v).to(dev) for k, v in arrays.items()}
+    _run(orc, cfg, darr, ref, (0, 1, 127, 511, 2047, 4095), seed=23)
+    sa.forward_cache_clear()
+    del darr
+    torch.cuda.empty_cache()
+
+
 def test_llama32_rejects(dev):
     cfg = CFG_SMALL
     arrays = make_arrays(cfg, seed=1)

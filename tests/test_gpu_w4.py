@@ -136,3 +136,54 @@ def test_matmul_quant_unaligned_offset_fallback(dev, orc):
                     rows, cols, gs, off)
     ref = orc.matmul_quant_f5(qw, sc, ze, x, rows, cols, gs, off).astype(np.float64)
     _close(out.cpu().numpy()[None], ref[None])
+
+
+@pytest.mark.parametrize("M,nan_row", [(1, 0), (3, 1), (4, 3), (16, 5)])
+@pytest.mark.parametrize("K,N", [(3200, 640), (640, 96)])
+def test_w4s_nan_in_x_propagates(dev, orc, M, nan_row, K, N):
+    """One NaN element of x makes every output of its row NaN, as the reference's
+    fp32 multiply-adds do (ConvertSimpToMemRef.cpp:3906-4005); the other rows
+    still equal the oracle."""
+    import torch
+    w, s, x = _w4s_inputs(M, N, K, 32, seed=M + K)
+    x[nan_row, K // 3] = np.nan
+    out = torch.zeros((M, N), device=dev)
+    sa.matmul_w4s(*(torch.from_numpy(a).to(dev) for a in (w, s, x)), out, 32)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.isnan(o[nan_row]).all()
+    keep = [m for m in range(M) if m != nan_row]
+    if keep:
+        _close(o[keep], orc.matmul_w4s(w, s, x[keep], 32).astype(np.float64))
+
+
+def test_matmul_quant_nan_in_x_propagates(dev, orc):
+    import torch
+    rows, cols, gs = 1536, 1536, 128
+    qw, sc, ze = orc.quantize_f5(_f5_model(1, rows, cols, gs, seed=5), gs)
+    x = np.random.default_rng(4).standard_normal(cols).astype(np.float32)
+    x[777] = np.nan
+    out = torch.zeros(rows, device=dev)
+    sa.matmul_quant(*(torch.from_numpy(a).to(dev) for a in (qw.view(np.int8), sc, ze, x)), out,
+                    rows, cols, gs, 0)
+    torch.cuda.synchronize()
+    assert np.isnan(out.cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("idx,count,gs", [(0, 1536 * 64, 128), (37, 1000, 32), (1, 1, 128),
+                                          (2 * 1536 * 64 - 5, 5, 128)])
+def test_dequant_w4_bit_exact(dev, orc, idx, count, gs):
+    """dequant_w4 over a range (ConvertSimpToMemRef.cpp:2367-2429) equals the
+    oracle bit for bit, from device arrays and from host arrays (where only the
+    range's bytes and groups are staged)."""
+    import torch
+    w = _f5_model(2, 1536, 64, gs, seed=gs + idx)
+    qw, sc, ze = orc.quantize_f5(w, gs)
+    want = orc.dequant_w4(qw, sc, ze, idx, count, gs)
+    out = torch.full((count,), float("nan"), device=dev)
+    sa.dequant_w4(*(torch.from_numpy(a).to(dev) for a in (qw.view(np.int8), sc, ze)), idx, gs, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+    host = np.full(count, np.nan, np.float32)
+    sa.dequant_w4(qw.view(np.int8), sc, ze, idx, gs, host)
+    assert np.array_equal(host, want)

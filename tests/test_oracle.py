@@ -289,6 +289,34 @@ def _dequant_f5(qw, sc, ze, total, gs):
     return q * sc[g] + ze[g]
 
 
+def test_dequant_w4_pins(orc):
+    """dequant_w4 (ConvertSimpToMemRef.cpp:2367-2429): the test_quant_roofline
+    constants (0x55, scale 0.01, zero 0 -> 5 * 0.01f), agreement with
+    matmul_quant on one-hot inputs element by element (a single product, so
+    exact whatever the sum order; a swapped nibble or group index fails it),
+    and the float64 value within one rounding of each step."""
+    qw = np.full(64, 0x55, np.uint8)
+    sc = np.full(4, 0.01, np.float32)
+    ze = np.zeros(4, np.float32)
+    assert (orc.dequant_w4(qw, sc, ze, 0, 128, 32) == np.float32(5) * np.float32(0.01)).all()
+    rows, cols, gs, layers = 6, 256, 32, 3
+    total = layers * rows * cols
+    qw = RNG.integers(0, 256, total // 2).astype(np.uint8)
+    sc = RNG.uniform(0.001, 0.02, total // gs).astype(np.float32)
+    ze = RNG.uniform(-0.1, 0.1, total // gs).astype(np.float32)
+    off = 2 * rows * cols
+    deq = orc.dequant_w4(qw, sc, ze, off, rows * cols, gs).reshape(rows, cols)
+    for k in (0, 1, 31, 32, 77, 255):
+        x = np.zeros(cols, np.float32)
+        x[k] = 1.0
+        assert np.array_equal(orc.matmul_quant_f5(qw, sc, ze, x, rows, cols, gs, off), deq[:, k]), k
+    want = _dequant_f5(qw, sc, ze, total, gs)
+    got = orc.dequant_w4(qw, sc, ze, 0, total, gs)
+    assert np.abs(got - want).max() <= 2 * np.finfo(np.float32).eps * np.abs(want).max()
+    # an odd start and a range that crosses groups
+    assert np.array_equal(orc.dequant_w4(qw, sc, ze, 37, 100, gs), got[37:137])
+
+
 def test_quant_f5_vs_dequant_and_quantizer(orc):
     rows, cols, gs = 16, 512, 128
     w = RNG.uniform(-0.01, 0.01, rows * cols).astype(np.float32)  # bench_llama_quant.cpp:43-49
@@ -579,3 +607,53 @@ def test_llama32_layer_offsets(orc):
     for c in ("k_cache", "v_cache"):
         assert np.array_equal(a[c].reshape(2, S, kv)[1], b[c].reshape(1, S, kv)[0])
         assert not a[c].reshape(2, S, kv)[0].any()
+
+
+# ---------------------------------------------------------------- argmax --
+# sample_argmax (generate_stories110M.cpp:73-83) scans from logits[0] with a
+# strict '>'. What that scan must return, stated without the scan: 0 when
+# logits[0] is NaN, else the first index holding the largest non-NaN value.
+
+def _argmax_closed_form(v):
+    v = np.asarray(v, np.float32)
+    if np.isnan(v[0]):
+        return 0
+    ok = ~np.isnan(v)
+    return int(np.flatnonzero(ok & (v == v[ok].max()))[0])
+
+
+def test_argmax_closed_forms(orc):
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    assert orc.argmax([1.0, 3.0, 3.0, 2.0]) == 1            # ties: the first wins
+    assert orc.argmax([5.0, 5.0, 5.0]) == 0
+    assert orc.argmax([nan, 1.0, 2.0]) == 0                 # NaN at 0: nothing exceeds it
+    assert orc.argmax([0.0, nan, 2.0, nan]) == 2            # NaN elsewhere is skipped
+    assert orc.argmax([nan] * 7) == 0
+    assert orc.argmax([-inf] * 7) == 0
+    assert orc.argmax([-inf, nan, -inf]) == 0
+    assert orc.argmax([-0.0, 0.0]) == 0                     # -0 == +0: not greater
+    assert orc.argmax([-1.0, inf, inf]) == 1
+    big = np.zeros(32000, np.float32)
+    big[[7, 31999, 20000]] = 4.0
+    assert orc.argmax(big) == 7
+
+
+def test_argmax_brute_force(orc):
+    """Every pattern of 5 values from {-inf, -1, 0, -0, 1, NaN} against the
+    closed form; a '>=' scan or a seed of -inf with index 0 fails it."""
+    import itertools
+    vals = np.array([-np.inf, -1.0, 0.0, -0.0, 1.0, np.nan], np.float32)
+    for pat in itertools.product(range(len(vals)), repeat=5):
+        v = vals[list(pat)]
+        assert orc.argmax(v) == _argmax_closed_form(v), v
+
+
+def test_int8_recipe_inputs_closed_form(orc):
+    """bench_int8_matmul_runner.cpp:33-64: val = ((i*N+j) % 127) - 64,
+    A[i,j] = B[j,i] = val."""
+    for n in (1, 2, 31, 64, 127, 128, 300):
+        a, b = orc.recipe_inputs(n)
+        i, j = np.meshgrid(np.arange(n), np.arange(n), indexing="ij")
+        val = ((i * n + j) % 127 - 64).astype(np.int8)
+        assert np.array_equal(a, val), n
+        assert np.array_equal(b, val.T), n
