@@ -300,8 +300,7 @@ def decode_bench(dev, stream, with_cpu=True):
     import simplang_amd as sa
     from simplang_amd.llama_synth import CFG_110M, CFG_3B_W4, make_model, weight_bytes, kv_bytes
     out = []
-    for name, cfg, n_new, cpu_steps in (("llama-110M f32", CFG_110M, 256, 4),
-                                        ("llama-3B W4 g32", CFG_3B_W4, 128, 2)):
+    for name, cfg, n_new in (("llama-110M f32", CFG_110M, 256), ("llama-3B W4 g32", CFG_3B_W4, 128)):
         w = make_model(cfg, dev, seed=42)
         prompt = np.random.default_rng(42).integers(0, cfg["vocab_size"], 32).astype(np.int32)
         m = sa.Llama(cfg, w)
@@ -321,7 +320,7 @@ def decode_bench(dev, stream, with_cpu=True):
                "frac_hbm": round(byts * steps / el / 1e9 / HBM_PEAK_GBS, 3),
                "tokens_head": [int(t) for t in toks[32:40]]}
         if with_cpu:
-            rec["cpu_baseline"] = decode_cpu(cfg, w, prompt, cpu_steps)
+            rec["cpu_baseline"] = decode_cpu(cfg, w, prompt, steps)
         out.append(rec)
         del w
         torch.cuda.empty_cache()
@@ -382,10 +381,15 @@ def llama32_bench(dev, with_cpu=True):
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
         host = {k: v.cpu().numpy() for k, v in a.items()}
+        n_cpu = 20
         t0 = time.perf_counter()
-        oracle.llama32_int8_forward(host, 0, *dims)
-        rec["cpu_baseline"] = {"tok_s": round(1 / (time.perf_counter() - t0), 3), "cores": 1,
-                               "kind": "port", "sample": "one call of the oracle's restatement at pos 0"}
+        for i in range(n_cpu):
+            oracle.llama32_int8_forward(host, 128 + i, *dims)
+        el = time.perf_counter() - t0
+        rec["cpu_baseline"] = {"tok_s": round(n_cpu / el, 3), "cores": 1, "kind": "port",
+                               "sample": f"{n_cpu} calls at positions 128..{127 + n_cpu} (the "
+                                         "first of the GPU loop's 64) of the oracle's "
+                                         "restatement, one core"}
         del host
     sa.forward_cache_clear()
     del a
@@ -476,29 +480,50 @@ def llama2_quant_bench(dev, with_cpu=True):
                                                               "rms_final_w", "wcls", "scales",
                                                               "zeros")} |
                                     {"qweights": host["qweights"].view(np.uint8)}, GS, offs)
+        # the reference bench's loop (bench_llama_quant.cpp:255-292): 10 calls from pos 0
         t0 = time.perf_counter()
-        o.forward(50, 0)
-        out["cpu_baseline"] = {"tok_s": round(1 / (time.perf_counter() - t0), 3),
-                               "cores": host_info()["cores_used"], "kind": "port",
-                               "sample": "one token (pos 0) of the oracle's llama2_quant_forward"}
+        for pos in range(10):
+            o.forward(50 + pos * 10, pos)
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"tok_s": round(10 / el, 3), "cores": host_info()["cores_used"],
+                               "kind": "port",
+                               "sample": "the reference bench's 10-call loop from pos 0, the "
+                                         "oracle's llama2_quant_forward"}
     del dv, host
     torch.cuda.empty_cache()
     return out
 
 
-def decode_cpu(cfg, w, prompt, steps):
-    """The oracle's restatement of the decode step on the host cores (OpenMP
-    GEMVs, double accumulation), timed over a few steps."""
+def decode_cpu(cfg, w, prompt, n_steps, sample_steps=20):
+    """The decode CPU baseline (oracle/cpu_decode.c: the step restated in fp32,
+    OpenMP GEMVs over output rows in 16 fp32 lanes, the host cores one GPU gets)
+    on a bounded sample of the same generation: `sample_steps` consecutive
+    steps centred on the mean position of the GPU run's `n_steps`, the cache
+    rows below the first one filled with random values (the work of a step does
+    not depend on what the rows hold).  tok/s = steps / wall time of that loop
+    (bench_llama_quant.cpp:255-292)."""
+    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     wn = {k: v.detach().cpu().numpy() for k, v in w.items()}
-    o = oracle.LlamaOracle(cfg, wn)
+    o = oracle.CpuLlama(cfg, wn)
+    p0 = max(0, (n_steps - 1) // 2 - sample_steps // 2)
+    kv = cfg["dim"] * cfg["n_kv_heads"] // cfg["n_heads"]
+    rng = np.random.default_rng(5)
+    for c in (o.kc, o.vc):
+        c.reshape(cfg["n_layers"], cfg["seq_len"], kv)[:, :p0] = \
+            rng.standard_normal((cfg["n_layers"], p0, kv), dtype=np.float32) * 0.1
+    o.forward(int(prompt[0]), p0)     # warm (the step at p0 is timed again below)
     t0 = time.perf_counter()
-    for p in range(steps):
-        o.forward(int(prompt[p]), p)
+    for i in range(sample_steps):
+        o.forward(int(prompt[i % len(prompt)]), p0 + i)
     el = time.perf_counter() - t0
-    return {"tok_s": round(steps / el, 3), "cores": min(os.cpu_count() or 1, 16), "kind": "port",
-            "sample": f"{steps} decode steps of the oracle forward"}
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or os.cpu_count() or 1
+    return {"tok_s": round(sample_steps / el, 3), "ms_per_token": round(el / sample_steps * 1e3, 2),
+            "cores": threads, "kind": "port",
+            "sample": (f"{sample_steps} decode steps at positions {p0}..{p0 + sample_steps - 1} "
+                       f"(centred on the mean position of the GPU run) of the fp32 restatement "
+                       f"(oracle/cpu_decode.c) on {threads} OpenMP threads")}
 
 
 def load_traffic(name):

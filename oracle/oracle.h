@@ -220,6 +220,16 @@ void orc_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
                        float *key_cache, float *value_cache, int64_t token,
                        int64_t pos, float *logits);
 
+/* The CPU baseline of the same step (cpu_decode.c): fp32 throughout, OpenMP
+ * GEMVs over output rows summed in 16 fp32 lanes, W4 dequantized per group
+ * before the multiply-add.  For bench.py's cpu_baseline leg; checked against
+ * orc_llama_forward to 1e-4 (tests/test_oracle_decode.py).  W4 needs gs a
+ * multiple of 32 dividing dim and hidden (cpu_llama_supported). */
+int cpu_llama_supported(const orc_llama_cfg *cfg);
+void cpu_llama_forward(const orc_llama_cfg *cfg, const orc_llama_weights *w,
+                       float *key_cache, float *value_cache, int64_t token,
+                       int64_t pos, float *logits);
+
 /* One token of llama2_quant_forward (examples/llama2/llama2_quant.sl:57-198):
  * the reference's W4 format F5 for the seven layer matrices (one flat nibble
  * array qw with scales/zeros per flat group of gs, per-matrix element offsets

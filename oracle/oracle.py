@@ -115,6 +115,26 @@ class LlamaOracle:
                              self.vc.ctypes.data, token, pos, logits.ctypes.data)
         return logits
 
+_s("cpu_llama_forward", [_P, _P, _P, _P, _I, _I, _P])
+_s("cpu_llama_supported", [_P], C.c_int)
+
+
+class CpuLlama(LlamaOracle):
+    """The decode CPU baseline (cpu_decode.c: fp32, OpenMP GEMVs in 16 fp32
+    lanes) with the same weights and cache layout as LlamaOracle."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        super().__init__(cfg, weights)
+        if not _o.cpu_llama_supported(C.byref(self.c)):
+            raise ValueError("cpu_llama_forward: W4 needs gs a multiple of 32 dividing dim and hidden")
+
+    def forward(self, token: int, pos: int):
+        logits = np.empty(self.cfg["vocab_size"], np.float32)
+        _o.cpu_llama_forward(C.byref(self.c), C.byref(self.w), self.kc.ctypes.data,
+                             self.vc.ctypes.data, token, pos, logits.ctypes.data)
+        return logits
+
+
 _s("orc_llama32_int8_forward", [_P, _I] + [_P] * 22 + [_I], C.c_float)
 
 LLAMA32_ARRAYS = ("x_i8", "rms_att_w", "rms_ffn_w", "rms_final_w", "wq_t", "wk_t", "wv_t",

@@ -230,6 +230,28 @@ def test_forward_w4_equals_fp32_on_dequantized_weights(orc):
     assert _rel(a, _brute_logits(CFG, wf, TOKENS)) <= REL
 
 
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_cpu_baseline_forward_equals_oracle(orc, fmt):
+    """The decode CPU baseline (cpu_decode.c, fp32 accumulation) equals the
+    oracle (double accumulation) to 1e-5 of max|logit| at every position, fp32
+    (rows of 72 and 84: a remainder past the 16 lanes) and W4, with GQA."""
+    cfg = dict(CFG, dim=96 if fmt else 72, hidden_dim=160 if fmt else 84, n_heads=4,
+               n_kv_heads=2, weight_format=fmt, group_size=32, seq_len=12)
+    rng = np.random.default_rng(40 + fmt)
+    w = _weights(cfg, 40 + fmt)
+    if fmt:
+        for k in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls"):
+            shp = w.pop(k).shape
+            rows, K = int(np.prod(shp[:-1])), shp[-1]
+            w["q_" + k] = _pack_w4s(rng.integers(-8, 8, (rows, K)))
+            w["s_" + k] = (np.abs(rng.standard_normal((rows, K // 32))) * np.sqrt(2.0 / K) / 4
+                           ).astype(np.float32)
+    a = _oracle_logits(orc, cfg, w, TOKENS)
+    cpu = orc.CpuLlama(cfg, {k: np.ascontiguousarray(v) for k, v in w.items()})
+    b = np.stack([cpu.forward(t, p).astype(np.float64) for p, t in enumerate(TOKENS)])
+    assert _rel(a, b) <= 1e-5
+
+
 # ------------------------------------------------- orc_llama_quant_forward --
 
 QCFG = dict(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=4, vocab_size=50,
