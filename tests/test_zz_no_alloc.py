@@ -36,6 +36,45 @@ def test_noalloc_matches_allocating_entry_point(dev):
         assert torch.equal(got, want), (M, N, K)
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (2048, 3072, 1040), (256, 320, 192)])
+def test_noalloc_under_graph_capture(dev, M, N, K):
+    """The entry point's callers capture it: one call captured in a HIP graph
+    (B read in place, B transposed into the scratch, and a shape with no
+    scratch), replayed three times on new inputs written into the captured
+    buffers, with eager library work between the replays (which uses the same
+    scratch-free stream workspace); every replay equals the allocating entry
+    point bit for bit."""
+    import torch
+    print(f"[noalloc-graph] M={M} N={N} K={K}", flush=True)
+    a, b = _pair(dev, M, N, K, seed=M + K)
+    c = torch.empty((M, N), dtype=torch.int32, device=dev)
+    main = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(main)
+    with torch.cuda.stream(side):          # first use on this stream, outside the capture
+        sa.set_stream(side)
+        sa.matmul_u8s8_i32_noalloc(a, b, c)
+    main.wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        sa.set_stream(side)
+        sa.matmul_u8s8_i32_noalloc(a, b, c)
+    sa.set_stream(main)
+    want = torch.empty_like(c)
+    for rep in range(3):
+        na, nb = _pair(dev, M, N, K, seed=100 * rep + 7)
+        a.copy_(na)
+        b.copy_(nb)
+        c.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        sa.matmul_u8s8_i32(a, b, want)       # eager work between the replays
+        torch.cuda.synchronize()
+        assert torch.equal(c, want), (rep, M, N, K)
+
+
 def test_noalloc_rejections(dev):
     import torch
     a = np.zeros((64, 64), np.uint8)                       # host memory: would need staging
