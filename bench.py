@@ -222,9 +222,10 @@ def w4_bench(dev, stream, with_cpu=True):
 def norm_bench(dev, stream, with_cpu=True):
     """rmsnorm / softmax / silu (rows a9-a11) as standalone launches at the model
     sizes (768 and 3200 dims, 2048 and 8640 FFN widths, 288 and 512 attention
-    rows): GPU time by HIP-graph replay of back-to-back launches, GB/s over the
-    algorithmic bytes (12n, 16n, 8n), and the oracle's restatement of the
-    reference loop on one host core."""
+    rows), where a launch's latency is the cost, and at 2^24 elements (64 MB
+    vectors, the two-pass multi-block forms), where HBM is: GPU time by HIP-graph
+    replay of back-to-back launches, GB/s over the algorithmic bytes (12n, 16n,
+    8n), and the oracle's restatement of the reference loop on one host core."""
     import numpy as np
     import torch
     import simplang_amd as sa
@@ -233,23 +234,31 @@ def norm_bench(dev, stream, with_cpu=True):
     out = []
     g = torch.Generator(device=dev)
     g.manual_seed(3)
-    cases = [("rmsnorm", n) for n in (768, 3200, 8640)] + \
-            [("softmax", n) for n in (288, 512, 768, 3200, 8640)] + \
-            [("silu", n) for n in (768, 2048, 3200, 8640)]
+    big = 1 << 24
+    cases = [("rmsnorm", n) for n in (768, 3200, 8640, big)] + \
+            [("softmax", n) for n in (288, 512, 768, 3200, 8640, big)] + \
+            [("silu", n) for n in (768, 2048, 3200, 8640, big)]
     for op, n in cases:
-        x = torch.randn(n, device=dev, generator=g)
-        w = torch.randn(n, device=dev, generator=g)
-        o = torch.empty(n, device=dev)
+        # the 2^24 cases rotate through 4 sets of vectors (768 MB for rmsnorm),
+        # more than the 256 MB Infinity Cache, so every launch streams from HBM
+        sets = 4 if n == big else 1
+        xs = [torch.randn(n, device=dev, generator=g) for _ in range(sets)]
+        ws = [torch.randn(n, device=dev, generator=g) for _ in range(sets)]
+        os_ = [torch.empty(n, device=dev) for _ in range(sets)]
+        x, w = xs[0], ws[0]
         if op == "rmsnorm":
-            call, byts = (lambda: sa.rmsnorm(x, w, o, n)), 12 * n
+            calls = [lambda i=i: sa.rmsnorm(xs[i], ws[i], os_[i], n) for i in range(sets)]
+            byts = 12 * n
             cpu = lambda xh=x.cpu().numpy(), wh=w.cpu().numpy(): oracle.rmsnorm(xh, wh)
         elif op == "softmax":
-            call, byts = (lambda: sa.softmax(x, o, n)), 16 * n
+            calls = [lambda i=i: sa.softmax(xs[i], os_[i], n) for i in range(sets)]
+            byts = 16 * n
             cpu = lambda xh=x.cpu().numpy(): oracle.softmax(xh)
         else:
-            call, byts = (lambda: sa.silu(x, o, n)), 8 * n
+            calls = [lambda i=i: sa.silu(xs[i], os_[i], n) for i in range(sets)]
+            byts = 8 * n
             cpu = lambda xh=x.cpu().numpy(): oracle.silu(xh)
-        ms = graph_time_ms([call] * 50, stream)
+        ms = graph_time_ms(calls * (20 if n == big else 50), stream)
         row = {"op": op, "n": n, "us": round(ms * 1e3, 2),
                "GBs": round(byts / (ms * 1e-3) / 1e9, 2)}
         if with_cpu:
@@ -261,6 +270,8 @@ def norm_bench(dev, stream, with_cpu=True):
             row["cpu_baseline"] = {"us": round((time.perf_counter() - t0) / k * 1e6, 2),
                                    "cores": 1, "kind": "port"}
         out.append(row)
+        del xs, ws, os_
+    torch.cuda.empty_cache()
     return out
 
 

@@ -10,6 +10,10 @@
 //   rope     examples/llama2/stories110M.sl:86-112  adjacent pairs, f = theta^-(i%hs/hs)
 // The reference sums sequentially; here sums are wave/block trees (fp32), which
 // changes rounding only (checked to 1e-4 relative against the oracle).
+// rmsnorm and softmax run as one block up to 32767 elements (their cost there
+// is the launch) and as two passes over many blocks from 32768 on.
+#include <algorithm>
+
 #include "rt_device.h"
 #include "rt_internal.h"
 
@@ -76,6 +80,150 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Vectors of kBigNorm elements or more take two passes over many blocks
+// (below it one block is faster: the second launch costs more than the
+// block's extra latency).  Pass 1: every block reduces its contiguous slice
+// (sum of squares; or its maximum and the sum of e^(x - max)) into part[b].
+// Pass 2: every block combines the parts in block order (the same order in
+// every block, so the result is deterministic) and writes its slice.
+constexpr int64_t kBigNorm = 32768;
+
+// Block b's slice [b0, b1) of n elements: multiples of 4 apart, so that with
+// 16-byte aligned arrays every slice but the last is whole float4s.
+__device__ __forceinline__ void slice_of(int64_t n, int64_t *b0, int64_t *b1) {
+  const int64_t per = ((n + gridDim.x - 1) / gridDim.x + 3) & ~(int64_t)3;
+  *b0 = min(n, (int64_t)blockIdx.x * per);
+  *b1 = min(n, *b0 + per);
+}
+
+// f(i, v) over the elements [b0, b1) of the block's threads: float4 loads,
+// four in flight per thread, when `vec` (the arrays 16-byte aligned), then the
+// slice's last n % 4 elements one by one.
+template <typename F>
+__device__ __forceinline__ void for_slice4(const float *__restrict__ x, int64_t b0, int64_t b1,
+                                           bool vec, F f) {
+  int64_t i = b0;
+  if (vec) {
+    const int64_t e4 = b0 + ((b1 - b0) & ~(int64_t)3);
+    const float4 *x4 = (const float4 *)x;
+    int64_t j = b0 / 4 + threadIdx.x;
+    const int64_t j1 = e4 / 4;
+    for (; j + 3 * 256 < j1; j += 4 * 256) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] = x4[j + u * 256];
+#pragma unroll
+      for (int u = 0; u < 4; u++) f(4 * (j + u * 256), v[u]);
+    }
+    for (; j < j1; j += 256) f(4 * j, x4[j]);
+    i = e4;
+  }
+  for (int64_t k = i + threadIdx.x; k < b1; k += 256) f(-k - 1, make_float4(x[k], 0.f, 0.f, 0.f));
+}
+
+__global__ void __launch_bounds__(256)
+    sumsq_parts_k(const float *__restrict__ x, int64_t n, float *__restrict__ part, bool vec) {
+  __shared__ float scratch[16];
+  int64_t b0, b1;
+  slice_of(n, &b0, &b1);
+  float ss = 0.f;
+  for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
+    ss = fmaf(v.x, v.x, ss);
+    if (i >= 0) {
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+  });
+  ss = block_sum(ss, scratch);
+  if (threadIdx.x == 0) part[blockIdx.x] = ss;
+}
+
+__global__ void __launch_bounds__(256)
+    rmsnorm_apply_k(const float *__restrict__ x, const float *__restrict__ w,
+                    float *__restrict__ out, int64_t n, float eps, const float *__restrict__ part,
+                    bool vec) {
+  __shared__ float scratch[16];
+  float t = 0.f;
+  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) t += part[b];
+  t = block_sum(t, scratch);
+  const float rms = sqrtf(t / (float)n + eps);
+  int64_t b0, b1;
+  slice_of(n, &b0, &b1);
+  for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
+    if (i >= 0) {
+      const float4 g = *(const float4 *)(w + i);
+      *(float4 *)(out + i) = make_float4((v.x / rms) * g.x, (v.y / rms) * g.y, (v.z / rms) * g.z,
+                                         (v.w / rms) * g.w);
+    } else {
+      out[-i - 1] = (v.x / rms) * w[-i - 1];
+    }
+  });
+}
+
+__global__ void __launch_bounds__(256)
+    softmax_parts_k(const float *__restrict__ x, int64_t n, float2 *__restrict__ part, bool vec) {
+  __shared__ float scratch[16];
+  int64_t b0, b1;
+  slice_of(n, &b0, &b1);
+  float mx = -INFINITY;
+  for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
+    mx = fmaxf(mx, v.x);
+    if (i >= 0) mx = fmaxf(mx, fmaxf(v.y, fmaxf(v.z, v.w)));
+  });
+  mx = block_max(mx, scratch);
+  float s = 0.f;
+  if (mx > -INFINITY)
+    for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
+      s += expf(v.x - mx);
+      if (i >= 0) s += (expf(v.y - mx) + expf(v.z - mx)) + expf(v.w - mx);
+    });
+  s = block_sum(s, scratch);
+  if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mx, s);
+}
+
+__global__ void __launch_bounds__(256)
+    softmax_apply_k(const float *__restrict__ x, float *__restrict__ out, int64_t n,
+                    const float2 *__restrict__ part, bool vec) {
+  __shared__ float scratch[16];
+  float mx = -INFINITY;
+  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) mx = fmaxf(mx, part[b].x);
+  mx = block_max(mx, scratch);
+  float l = 0.f;
+  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) {
+    const float2 p = part[b];
+    if (p.x > -INFINITY) l += p.y * expf(p.x - mx);
+  }
+  l = block_sum(l, scratch);
+  int64_t b0, b1;
+  slice_of(n, &b0, &b1);
+  for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
+    if (i >= 0)
+      *(float4 *)(out + i) = make_float4(expf(v.x - mx) / l, expf(v.y - mx) / l,
+                                         expf(v.z - mx) / l, expf(v.w - mx) / l);
+    else
+      out[-i - 1] = expf(v.x - mx) / l;
+  });
+}
+
+__global__ void __launch_bounds__(256) silu_big_k(const float *__restrict__ x,
+                                                  float *__restrict__ out, int64_t n) {
+  int64_t b0, b1;
+  slice_of(n, &b0, &b1);
+  for_slice4(x, b0, b1, true, [&](int64_t i, float4 v) {
+    if (i >= 0)
+      *(float4 *)(out + i) = make_float4(v.x / (1.f + expf(-v.x)), v.y / (1.f + expf(-v.y)),
+                                         v.z / (1.f + expf(-v.z)), v.w / (1.f + expf(-v.w)));
+    else
+      out[-i - 1] = v.x / (1.f + expf(-v.x));
+  });
+}
+
+// Blocks of the two-pass forms: about 8 slices of 256 x 8 elements per CU.
+unsigned big_grid(int64_t n) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, 256 * 8), (int64_t)num_cus() * 4));
+}
+
 unsigned grid_for(int64_t n) {
   const int64_t b = cdiv(n, 256);
   const int64_t cap = (int64_t)num_cus() * 8;
@@ -85,7 +233,18 @@ unsigned grid_for(int64_t n) {
 }  // namespace
 
 int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps, hipStream_t st) {
-  hipLaunchKernelGGL(rmsnorm_k, dim3(1), dim3(1024), 0, st, x, w, out, n, eps);
+  if (n >= kBigNorm) {
+    const unsigned g = big_grid(n);
+    float *part = nullptr;
+    int rc = workspace(st, sizeof(float2) * g, (void **)&part, 4);
+    if (rc) return rc;
+    const bool vec = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out) & 15) == 0;
+    hipLaunchKernelGGL(sumsq_parts_k, dim3(g), dim3(256), 0, st, x, (int64_t)n, part, vec);
+    hipLaunchKernelGGL(rmsnorm_apply_k, dim3(g), dim3(256), 0, st, x, w, out, (int64_t)n, eps,
+                       (const float *)part, vec);
+  } else {
+    hipLaunchKernelGGL(rmsnorm_k, dim3(1), dim3(1024), 0, st, x, w, out, n, eps);
+  }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
 }
@@ -139,8 +298,20 @@ int32_t simp_rt_softmax(const float *in_alloc, const float *in, int64_t in_doff,
   Operand oi, oo;
   if ((rc = oi.bind(in + in_doff + input_offset, 4 * (size_t)size, Operand::kIn, "input"))) return rc;
   if ((rc = oo.bind(out + out_doff + output_offset, 4 * (size_t)size, Operand::kOut, "output"))) return rc;
-  hipLaunchKernelGGL(softmax_k, dim3(1), dim3(1024), 0, cur_stream(), (const float *)oi.dev(),
-                     (float *)oo.dev(), (int)size);
+  hipStream_t st = cur_stream();
+  if (size >= kBigNorm) {
+    const unsigned g = big_grid(size);
+    float2 *part = nullptr;
+    if ((rc = workspace(st, sizeof(float2) * g, (void **)&part, 4))) return rc;
+    const bool vec = (((uintptr_t)oi.dev() | (uintptr_t)oo.dev()) & 15) == 0;
+    hipLaunchKernelGGL(softmax_parts_k, dim3(g), dim3(256), 0, st, (const float *)oi.dev(),
+                       (int64_t)size, part, vec);
+    hipLaunchKernelGGL(softmax_apply_k, dim3(g), dim3(256), 0, st, (const float *)oi.dev(),
+                       (float *)oo.dev(), (int64_t)size, (const float2 *)part, vec);
+  } else {
+    hipLaunchKernelGGL(softmax_k, dim3(1), dim3(1024), 0, st, (const float *)oi.dev(),
+                       (float *)oo.dev(), (int)size);
+  }
   SIMP_HIP(hipGetLastError());
   Operand *ops[] = {&oi, &oo};
   return finish(ops, 2);
@@ -159,8 +330,12 @@ int32_t simp_rt_silu(const float *in_alloc, const float *in, int64_t in_off, int
   Operand oi, oo;
   if ((rc = oi.bind(in + in_off, 4 * (size_t)size, Operand::kIn, "input"))) return rc;
   if ((rc = oo.bind(out + out_off, 4 * (size_t)size, Operand::kOut, "output"))) return rc;
-  hipLaunchKernelGGL(silu_k, dim3(grid_for(size)), dim3(256), 0, cur_stream(),
-                     (const float *)oi.dev(), (float *)oo.dev(), size);
+  if (size >= kBigNorm && (((uintptr_t)oi.dev() | (uintptr_t)oo.dev()) & 15) == 0)
+    hipLaunchKernelGGL(silu_big_k, dim3(big_grid(size)), dim3(256), 0, cur_stream(),
+                       (const float *)oi.dev(), (float *)oo.dev(), size);
+  else
+    hipLaunchKernelGGL(silu_k, dim3(grid_for(size)), dim3(256), 0, cur_stream(),
+                       (const float *)oi.dev(), (float *)oo.dev(), size);
   SIMP_HIP(hipGetLastError());
   Operand *ops[] = {&oi, &oo};
   return finish(ops, 2);

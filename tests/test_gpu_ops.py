@@ -49,6 +49,31 @@ def test_rmsnorm_vs_oracle(dev, orc, dim):
     _close(out.cpu().numpy(), orc.rmsnorm(x, w, 1e-5, 2 * dim))
 
 
+@pytest.mark.parametrize("dim", [32767, 32768, 1 << 20, (1 << 22) + 13])
+def test_rmsnorm_two_pass_vs_oracle(dev, orc, dim):
+    """From 32768 elements the two-pass multi-block form (block partials of
+    sum x^2 combined in block order); the single-block form just below it.
+    Against float64: at these sizes the reference's sequential fp32 sum is the
+    less accurate of the two."""
+    import torch
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal(dim).astype(np.float32)
+    w = rng.standard_normal(2 * dim).astype(np.float32)
+    out = torch.full((dim,), float("nan"), device=dev)
+    sa.rmsnorm(_t(dev, x), _t(dev, w), out, dim, 1e-5, dim)
+    torch.cuda.synchronize()
+    # the reference's sequential fp32 sum of squares (the oracle) drifts by
+    # about n * 2^-24 relative at these sizes (2e-4 at 2^20); both are held to
+    # the float64 value, the tree-summed GPU result to 1e-5
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 * x64).mean() + 1e-5) * w[dim:].astype(np.float64)
+    _close(out.cpu().numpy(), exact, tol=1e-5)
+    _close(orc.rmsnorm(x, w, 1e-5, dim), exact, tol=2e-3)
+    out2 = torch.empty(dim, device=dev)                       # deterministic
+    sa.rmsnorm(_t(dev, x), _t(dev, w), out2, dim, 1e-5, dim)
+    assert torch.equal(out, out2)
+
+
 # ----------------------------------------------------------------- softmax --
 
 def test_softmax_kat(dev):
@@ -76,6 +101,31 @@ def test_softmax_offsets_vs_oracle(dev, orc, n):
     assert abs(got[off:off + n].astype(np.float64).sum() - 1.0) < 1e-5
 
 
+@pytest.mark.parametrize("n", [32767, 32768, 1 << 20, (1 << 22) + 5])
+def test_softmax_two_pass_vs_oracle(dev, orc, n):
+    """From 32768 elements the two-pass form (per block its maximum and the sum
+    of e^(x - max), combined in block order); offsets on both arrays, one
+    element far above the rest and a run of -inf (blocks whose slice is all
+    -inf contribute nothing)."""
+    import torch
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n + 64) * 4).astype(np.float32)
+    x[10 + n // 3] = 60.0
+    x[10 + n // 2: 10 + n // 2 + 9000] = -np.inf
+    out = torch.full((n + 64,), -1.0, device=dev)
+    sa.softmax(_t(dev, x), out, n, 10, 20)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = orc.softmax(x, np.full(n + 64, -1.0, np.float32), n, 10, 20)
+    x64 = x[10:10 + n].astype(np.float64)
+    e = np.exp(x64 - x64.max())
+    exact = e / e.sum()
+    _close(got[20:20 + n], exact, tol=1e-5)      # as for rmsnorm: float64 is the bar
+    _close(want[20:20 + n], exact, tol=2e-3)
+    assert (got[:20] == -1).all() and (got[20 + n:] == -1).all()
+    assert abs(got[20:20 + n].astype(np.float64).sum() - 1.0) < 1e-4
+
+
 def test_softmax_constant(dev):
     import torch
     out = torch.empty(17, device=dev)
@@ -97,6 +147,16 @@ def test_silu_kat_and_vs_oracle(dev, orc):
     got = out.cpu().numpy()
     want = orc.silu(x)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n", [32768, (1 << 22) + 3])
+def test_silu_large_vs_oracle(dev, orc, n):
+    """The float4 multi-block form from 32768 elements, with a ragged tail."""
+    import torch
+    x = (np.random.default_rng(n).standard_normal(n) * 6).astype(np.float32)
+    out = torch.empty(n, device=dev)
+    sa.silu(_t(dev, x), out, n)
+    assert np.allclose(out.cpu().numpy(), orc.silu(x), rtol=1e-5, atol=1e-6)
 
 
 def test_swiglu_vs_oracle(dev, orc):
