@@ -504,6 +504,16 @@ float llama32_forward(
 /* Frees the engines and device mirrors the model-level exports created (no
  * reference counterpart). */
 int32_t simp_rt_forward_cache_clear(void);
+/* How the model-level exports notice edits of weight arrays held in host
+ * memory (no reference counterpart: the compiled programs read every weight on
+ * every call).  0 (default): a call that starts a sequence re-hashes every
+ * 64 KiB chunk, any other call one chunk per array in rotation, and a changed
+ * chunk re-checks its whole array, so an edit confined to chunks not sampled
+ * can go unseen until the rotation reaches them or the next sequence start.
+ * 1: every call re-hashes every chunk (the reference's semantics, at the cost
+ * of hashing all host weights per call: about 14 ms for 706 MB).  Device-
+ * resident and simp_rt_register'd weights are used in place either way. */
+int32_t simp_rt_export_verify_all(int32_t on);
 
 /* ------------------------------------------------------- model files -- */
 /* llama2.c checkpoint header, as read by

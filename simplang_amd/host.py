@@ -323,6 +323,7 @@ CHUNK_INT8_SIZES = (256, 512, 768, 1024, 2048)
 for _n in BENCH_INT8_SIZES:
     _sig(f"benchmark_int8_matmul_{_n}", [])
 _sig("kernel_main", [])
+_sig("simp_rt_export_verify_all", [C.c_int32])
 for _n in CHUNK_INT8_SIZES:
     _sig(f"int8_chunk_{_n}", [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64] * 3
          + [C.c_int64])
@@ -357,6 +358,12 @@ def int8_chunk(n: int, a, b, c, row_start: int) -> None:
 
 def forward_cache_clear() -> None:
     _check("simp_rt_forward_cache_clear", lib.simp_rt_forward_cache_clear())
+
+
+def export_verify_all(on: bool) -> None:
+    """Model-level exports: re-check every chunk of host weights on every call
+    (True) or sample one chunk per array mid-sequence (False, the default)."""
+    _check("simp_rt_export_verify_all", lib.simp_rt_export_verify_all(1 if on else 0))
 
 
 def tensor_matvecmul_i8(a, b, c):

@@ -11,12 +11,14 @@
 //     any pos that does not follow the previous call's) re-hashes every chunk
 //     and re-uploads the chunks that changed; any other call re-hashes one
 //     chunk of each array, in rotation, and a mismatch there re-checks the
-//     whole array.  Device-resident weights and ranges the caller registered
+//     whole array (simp_rt_export_verify_all(1): every chunk on every call).
+//     Device-resident weights and ranges the caller registered
 //     with simp_rt_register are used in place (the caller owns their contents).
 //   * the engine's device KV cache is refilled from the caller's cache rows
 //     [0, pos) of every layer whenever a call does not continue the previous
 //     one (first call, a jump or a restart, other cache arrays).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <thread>
 
@@ -154,11 +156,16 @@ int ExportWeights::refresh(Range &r, bool all, size_t first) {
   return SIMP_RT_OK;
 }
 
+// simp_rt_export_verify_all: every call re-checks every chunk (as a sequence
+// start does), so that any edit of a host array is seen by the next call.
+std::atomic<int> g_verify_all{0};
+
 int ExportWeights::verify(bool full) {
   if (fresh_) {  // the copies were made (and hashed) by this very call
     fresh_ = false;
     return SIMP_RT_OK;
   }
+  full = full || g_verify_all.load(std::memory_order_relaxed) != 0;
   for (Range &r : ranges_) {
     if (r.hash.empty()) continue;
     int rc;
@@ -197,3 +204,8 @@ int KvState::prepare(int64_t pos, const void *caller_k, const void *caller_v, vo
 }
 
 }  // namespace simp
+
+extern "C" int32_t simp_rt_export_verify_all(int32_t on) {
+  simp::g_verify_all.store(on ? 1 : 0, std::memory_order_relaxed);
+  return SIMP_RT_OK;
+}

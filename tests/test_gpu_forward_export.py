@@ -226,6 +226,36 @@ def test_stories110M_forward_weights_rewritten_in_place(dev, orc):
     sa.forward_cache_clear()
 
 
+def test_stories110M_forward_verify_all_sees_every_edit(dev, orc):
+    """With simp_rt_export_verify_all(1) a mid-sequence edit of a few rows deep
+    inside a host array (chunks the rotation has not reached) is used by the
+    very next call, as the compiled program, which reads every weight on every
+    call, would use it."""
+    sa.forward_cache_clear()
+    sa.export_verify_all(True)
+    try:
+        wa, arrays = _host_model(41)
+        o = _stories_oracle(orc, wa)
+        for pos, t in enumerate([4, 9]):
+            sa.stories110M_forward(arrays, t, pos, *_cfg_args())
+            _same(arrays["logits"], o.forward(t, pos))
+        d = CFG["dim"]
+        rows = slice(CFG["vocab_size"] - 3, CFG["vocab_size"])    # the last chunk of wcls
+        arrays["wcls"][rows.start * d:rows.stop * d] *= -2.0
+        layer = CFG["n_layers"] - 1                               # the last layer's w2
+        w2 = arrays["w2"].reshape(CFG["n_layers"], d, CFG["hidden_dim"])
+        w2[layer, d // 2] += 0.5
+        wn = {**wa, "wcls": arrays["wcls"].reshape(wa["wcls"].shape),
+              "w2": w2.reshape(wa["w2"].shape)}
+        o2 = _stories_oracle(orc, wn, arrays, upto=2)
+        print("[forward-export] verify_all, edited rows at pos=2", flush=True)
+        sa.stories110M_forward(arrays, 16, 2, *_cfg_args())
+        _same(arrays["logits"], o2.forward(16, 2))
+    finally:
+        sa.export_verify_all(False)
+        sa.forward_cache_clear()
+
+
 def test_stories110M_forward_jumps_and_host_filled_caches(dev, orc):
     """A first call at pos 6 on caches the host filled, a jump back to pos 2,
     and a jump forward: each reads the caller's cache rows [0, pos)."""
