@@ -293,6 +293,184 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
     }
 }
 
+// fp32 GEMM fed by an LDS-DMA ring, for one product with K % 32 == 0: BM x BN
+// C tiles, WGM x WGN waves, v_mfma_f32_16x16x4f32, the whole of K in one
+// workgroup (no split-K partials to sum afterwards).
+//   * K-stages of 32 floats: an A (or B_T) row gives one whole 128-byte line
+//     per stage.  Operand tiles go global -> LDS directly
+//     (global_load_lds_dwordx4, each instruction 1 KB in lane order) into a
+//     ring of SLOTS stages, SLOTS-1 stages ahead of the MFMAs, one barrier per
+//     stage; the loads are counted with the kernel's own s_waitcnt vmcnt.
+//   * A / B_T: an instruction is 8 rows x 128 B, lane l row l/8; slot l%8 of
+//     row r holds 16-byte chunk (l%8) ^ ((r >> 1) & 7), so the 16 lanes of an
+//     operand read (rows R..R+15, one chunk) fall on 16 distinct 16-byte bank
+//     groups.
+//   * B given as [K,N]: a stage is 32 k-rows of BN floats; slot s of k-row k
+//     holds chunk s ^ (4 ((k >> 2) & 3)), so the four k-rows read together
+//     (one per 16-lane group) fall on four distinct 64-byte bank ranges.
+//   * Within each 16 of K, lane group g = lane/16 takes k = 4g..4g+3 over the
+//     four MFMAs: one 16-byte LDS read per A (B_T) fragment, four 4-byte reads
+//     per B fragment.  Fragments are double-buffered in registers.
+//   * The MFMA computes C^T tiles (B fragment first), so a lane ends with 4
+//     consecutive columns of one row of C: 16-byte stores.
+//   * Persistent: gridDim.x workgroups walk the tiles in tile_of_block order.
+//     Rows past M and columns past N load from clamped in-bounds addresses and
+//     are never stored.
+// Requirements (checked by the dispatch): K % 32 == 0, N % 4 == 0, lda, ldb and
+// ldc multiples of 4, 16-byte aligned A, B and C.
+template <int BM, int BN, int WGM, int WGN, int SLOTS, bool BT>
+__global__ void __launch_bounds__(64 * WGM * WGN)
+    gemm_f32_ring(const float *__restrict__ A, int64_t lda, const float *__restrict__ B,
+                  int64_t ldb, float *__restrict__ C, int64_t ldc, int M, int N, int K,
+                  int tiles_m, int tiles_n, float beta) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
+  constexpr int BK = 32;                                   // floats per stage
+  constexpr int SA = BM * BK * 4, SB = BN * BK * 4, STAGE = SA + SB;  // bytes
+  constexpr int DA = SA / 1024 / NW, DB = SB / 1024 / NW;  // DMA instructions per wave
+  constexpr int DPW = DA + DB;
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "wave tile");
+  static_assert(DA >= 1 && DB >= 1 && DA * NW * 1024 == SA && DB * NW * 1024 == SB, "DMA split");
+  static_assert(DPW * (SLOTS - 1) <= 63, "vmcnt range");
+  // [K,N] B: the swizzle XORs chunk indices with up to 12, so a k-row needs 16 chunks
+  static_assert(BT || BN % 64 == 0, "B[K,N] tile width");
+  constexpr int LPR = BN / 4, RPI = 64 / LPR;  // [K,N] B: lanes per k-row, k-rows per DMA
+  __shared__ float4 lds[SLOTS * STAGE / 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+  const int r16 = lane & 15, g = lane >> 4;
+  const int ns = K / BK;
+  const int ntiles = tiles_m * tiles_n;
+  const uint32_t lds_base = lds_offset(lds);
+  const float *lds_f = (const float *)lds;
+
+  for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
+    int tm, tn;
+    tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const float *srcA[DA], *srcB[DB];
+#pragma unroll
+    for (int i = 0; i < DA; i++) {
+      const int r = 8 * (wave * DA + i) + (lane >> 3);
+      srcA[i] = A + (int64_t)min(m0 + r, M - 1) * lda + 4 * ((lane & 7) ^ ((r >> 1) & 7));
+    }
+#pragma unroll
+    for (int i = 0; i < DB; i++) {
+      if constexpr (BT) {
+        const int r = 8 * (wave * DB + i) + (lane >> 3);
+        srcB[i] = B + (int64_t)min(n0 + r, N - 1) * ldb + 4 * ((lane & 7) ^ ((r >> 1) & 7));
+      } else {
+        const int kr = RPI * (wave * DB + i) + lane / LPR;  // k-row within the stage
+        const int cb = (lane % LPR) ^ (((kr >> 2) & 3) << 2);
+        srcB[i] = B + (int64_t)kr * ldb + min(n0 + 4 * cb, N - 4);
+      }
+    }
+    auto issue = [&](int st) {
+      const uint32_t dst = lds_base + (uint32_t)(st % SLOTS) * STAGE;
+      const int64_t ka = (int64_t)st * BK;
+#pragma unroll
+      for (int i = 0; i < DA; i++) dma16(srcA[i] + ka, dst + 1024 * (wave * DA + i));
+      const int64_t kb = BT ? ka : ka * ldb;
+#pragma unroll
+      for (int i = 0; i < DB; i++) dma16(srcB[i] + kb, dst + SA + 1024 * (wave * DB + i));
+    };
+    // fragment reads of stage st, K half h (k = 16 h .. 16 h + 15 of the stage)
+    auto afrag = [&](int st, int r0, int h) {
+      const int r = r0 + r16;
+      const uint32_t off = (uint32_t)(st % SLOTS) * STAGE + r * 128 + (((4 * h + g) ^ ((r >> 1) & 7)) << 4);
+      return lds[off >> 4];
+    };
+    auto bfrag = [&](int st, int c0, int h) {
+      if constexpr (BT) {
+        const int r = c0 + r16;
+        const uint32_t off = (uint32_t)(st % SLOTS) * STAGE + SA + r * 128 +
+                             (((4 * h + g) ^ ((r >> 1) & 7)) << 4);
+        return lds[off >> 4];
+      } else {
+        // k-row 16 h + 4 g + t, column c0 + r16: chunk (c0 + r16) / 4 sits in
+        // slot chunk ^ 4g (rows 16h+4g..16h+4g+3 share the swizzle)
+        const int n = c0 + r16;
+        const uint32_t base = (uint32_t)(st % SLOTS) * STAGE + SA + (16 * h + 4 * g) * (4 * BN) +
+                              ((((n >> 2) ^ (4 * g))) << 4) + 4 * (n & 3);
+        float4 v;
+        v.x = lds_f[(base + 0 * 4 * BN) >> 2];
+        v.y = lds_f[(base + 1 * 4 * BN) >> 2];
+        v.z = lds_f[(base + 2 * 4 * BN) >> 2];
+        v.w = lds_f[(base + 3 * 4 * BN) >> 2];
+        return v;
+      }
+    };
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    float4 fra[2][FM], frb[2][FN];
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the previous tile's stores
+    const int first = min(SLOTS, ns);
+    for (int st = 0; st < first; st++) issue(st);
+    auto wait_after = [&](int n_after) { wait_vm_le<DPW, SLOTS - 1>(n_after); };
+    wait_after(first - 1);  // stage 0 done on this wave ...
+    block_barrier();        // ... and on every wave
+#pragma unroll
+    for (int j = 0; j < FN; j++) frb[0][j] = bfrag(0, wn0 + 16 * j, 0);
+#pragma unroll
+    for (int i = 0; i < FM; i++) fra[0][i] = afrag(0, wm0 + 16 * i, 0);
+    auto mfmas = [&](int cb) {
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+          const float av = t == 0 ? fra[cb][i].x : t == 1 ? fra[cb][i].y : t == 2 ? fra[cb][i].z : fra[cb][i].w;
+#pragma unroll
+          for (int j = 0; j < FN; j++) {
+            const float bv = t == 0 ? frb[cb][j].x : t == 1 ? frb[cb][j].y : t == 2 ? frb[cb][j].z : frb[cb][j].w;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv, av, acc[i][j], 0, 0, 0);
+          }
+        }
+    };
+    for (int s = 0; s < ns; s++) {
+      // half (s,0): read (s,1)'s fragments, run (s,0)
+#pragma unroll
+      for (int j = 0; j < FN; j++) frb[1][j] = bfrag(s, wn0 + 16 * j, 1);
+#pragma unroll
+      for (int i = 0; i < FM; i++) fra[1][i] = afrag(s, wm0 + 16 * i, 1);
+      mfmas(0);
+      const bool more = s + 1 < ns;
+      // stages issued so far: 0 .. min(s + SLOTS - 1, ns - 1); stage s+1 must be done
+      if (more) wait_after(min(SLOTS - 2, ns - 2 - s));
+      __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0);  // this wave's reads of stage s landed
+      block_barrier();
+      if (s + SLOTS < ns) issue(s + SLOTS);
+      // half (s,1): read (s+1,0)'s fragments, run (s,1)
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) frb[0][j] = bfrag(s + 1, wn0 + 16 * j, 0);
+#pragma unroll
+        for (int i = 0; i < FM; i++) fra[0][i] = afrag(s + 1, wm0 + 16 * i, 0);
+      }
+      mfmas(1);
+    }
+    // acc[i][j][r] = C[m0 + wm0 + 16 i + r16][n0 + wn0 + 16 j + 4 g + r]
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+      const int col = n0 + wn0 + 16 * j + 4 * g;
+#pragma unroll
+      for (int i = 0; i < FM; i++) {
+        const int row = m0 + wm0 + 16 * i + r16;
+        if (row >= M || col >= N) continue;  // N % 4 == 0: col < N covers col..col+3
+        float4 *dst = (float4 *)(C + (int64_t)row * ldc + col);
+        float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        if (beta != 0.f) {
+          const float4 o = *dst;
+          v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+        }
+        *dst = v;
+      }
+    }
+  }
+}
+
 // C[z] = beta*C[z] + sum_s P[z][s] (s increasing: deterministic).
 __global__ void __launch_bounds__(256)
     gemm_f32_sum_parts(const float *__restrict__ P, float *__restrict__ C, int64_t ldc, int64_t sc,
@@ -349,6 +527,24 @@ int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int
   return SIMP_RT_OK;
 }
 
+// gemm_f32_ring over the tiles of one product: persistent, up to per_cu
+// workgroups per CU.
+template <int BM, int BN, int WGM, int WGN, int SLOTS, bool BT>
+int launch_ring_f32(const float *A, int64_t lda, const float *B, int64_t ldb, float *C,
+                    int64_t ldc, int M, int N, int K, float beta, int per_cu, hipStream_t st) {
+  const int64_t tm = cdiv(M, BM), tn = cdiv(N, BN);
+  if (tm * tn > INT32_MAX)
+    return set_error(SIMP_RT_EUNSUPPORTED, "gemm: %lld output tiles exceed one launch",
+                     (long long)(tm * tn));
+  const int grid = (int)std::min<int64_t>(tm * tn, (int64_t)per_cu * num_cus());
+  KernelTimer kt(st, "gemm_f32_ring");
+  hipLaunchKernelGGL((gemm_f32_ring<BM, BN, WGM, WGN, SLOTS, BT>), dim3(grid),
+                     dim3(64 * WGM * WGN), 0, st, A, lda, B, ldb, C, ldc, M, N, K, (int)tm,
+                     (int)tn, beta);
+  SIMP_HIP(hipGetLastError());
+  return SIMP_RT_OK;
+}
+
 // fp32 GEMM dispatch on the MFMA path (returns 1 when the operands do not meet
 // its requirements, for the caller's SIMT fallback).
 template <bool BT>
@@ -365,6 +561,19 @@ int dispatch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, i
     return launch_mfma_f32<16, 256, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   if (M <= 32)
     return launch_mfma_f32<32, 128, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
+  // One product whose tiles cover the chip, K % 32 == 0, 16-byte C rows: the
+  // LDS-DMA ring kernel, the whole of K per workgroup.  Two ring slots (plain
+  // double buffering) measured fastest: 4, 6, 8 and 10 slots ran 7-27% slower
+  // at the prefill shapes, the deeper prefetch spreading the CUs of an XCD
+  // over more operand lines than its L2 keeps.  128x128 tiles on 16 waves
+  // from one tile per CU (2048^3: 139.8 us against 157.6 for gemm_f32_mfma;
+  // 4096^3: 1074 against 1104), else 64x64 tiles on 8 waves (128x2048x8192 and
+  // 512x2048x2048: 42.9 us against 49.9 with split-K and its ordered sum).
+  const bool ring_ok = batch == 1 && K % 32 == 0 && N % 4 == 0 && ldc % 4 == 0 && al(C);
+  if (ring_ok && tiles(128, 128) >= cus)
+    return launch_ring_f32<128, 128, 4, 4, 2, BT>(A, lda, B, ldb, C, ldc, M, N, K, beta, 1, st);
+  if (ring_ok && tiles(64, 64) >= cus)
+    return launch_ring_f32<64, 64, 2, 4, 2, BT>(A, lda, B, ldb, C, ldc, M, N, K, beta, 2, st);
   if (tiles(128, 128) >= cus)
     return launch_mfma_f32<128, 128, 2, 2, BT, 32>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   return launch_mfma_f32<64, 64, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);

@@ -41,6 +41,7 @@
 #include <mutex>
 #include <vector>
 
+#include "rt_device.h"
 #include "rt_internal.h"
 
 namespace simp {
@@ -70,20 +71,6 @@ __device__ __forceinline__ void transpose4x4(uint32_t d0, uint32_t d1, uint32_t 
   o1 = __builtin_amdgcn_perm(y0, x0, 0x07060302u);           // a1 b1 c1 e1
   o2 = __builtin_amdgcn_perm(y1, x1, 0x05040100u);
   o3 = __builtin_amdgcn_perm(y1, x1, 0x07060302u);
-}
-
-// Maps the hardware workgroup id to a C tile: XCD-contiguous, then grouped.
-__device__ __forceinline__ void tile_of_block(int bid, int nb, int tiles_m, int tiles_n,
-                                              int &tm, int &tn) {
-  const int q = nb >> 3, r = nb & 7, xcd = bid & 7, local = bid >> 3;
-  const int t = xcd * q + min(xcd, r) + local;
-  constexpr int G = 8;
-  const int gsz = G * tiles_n;
-  const int g = t / gsz, first = g * G;
-  const int gm = min(tiles_m - first, G);
-  const int w = t - g * gsz;
-  tm = first + w % gm;
-  tn = w / gm;
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool BNK, bool AU8, bool ATOMIC>
@@ -409,47 +396,11 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
   }
 }
 
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-// s_waitcnt immediate that waits for lgkmcnt == 0 only.
-constexpr int waitcnt_lgkm0 = 15 | (3 << 14) | (7 << 4);
-
-// One global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at
-// lds_off + 16*lane.  Issued as asm because the compiler, seeing the builtin's
-// LDS write, waits for every outstanding load before any later LDS read; the
-// kernel below counts these loads with its own s_waitcnt instead.
-__device__ __forceinline__ void dma16(const int8_t *src, uint32_t lds_off) {
-  uint32_t saved;
-  // M0 is saved and restored around the load (the compiler owns it); one wait
-  // state separates the M0 write from the LDS-DMA load that reads it.
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(src)
-      : "memory");
-}
-
-// LDS byte offset of a shared-memory pointer.
-__device__ __forceinline__ uint32_t lds_offset(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
-}
-
 // ds_read_b64_tr_b8 at byte offset `off` of the shared array `lds`.
 __device__ __forceinline__ v2i lds_read_tr8(const void *lds, uint32_t off) {
   auto *p = (__attribute__((address_space(3))) v2i *)((__attribute__((address_space(3))) char *)(
                 (const __attribute__((address_space(3))) char *)lds) + off);
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32(p);
-}
-
-__device__ __forceinline__ void block_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Large-problem kernel for K % 64 == 0, B given as B_T[N,K]: 256x256 C tiles,
@@ -657,15 +608,6 @@ __global__ void __launch_bounds__(512)
 //     its slot.  With K / 128 <= SLOTS the whole of K is in flight at once.
 //   * u8 x s8: the waves of the first wave row also sum their B fragments
 //     (v_dot4 against 0x01010101) into the column sums, which meet in LDS.
-// s_waitcnt vmcnt(D * n) for a run-time n in 0..Q (the immediate must be a constant)
-template <int D, int Q>
-__device__ __forceinline__ void wait_vm_le(int n) {
-  if constexpr (Q >= 0) {
-    if (n == Q) __builtin_amdgcn_s_waitcnt(waitcnt_vm(D * Q));
-    else wait_vm_le<D, Q - 1>(n);
-  }
-}
-
 template <int BN>
 __device__ __forceinline__ int ring_fb(int lrow, int lkc) {
   if constexpr (BN == 256) return (lrow >> 1) ^ ((lkc & 1) << 3);

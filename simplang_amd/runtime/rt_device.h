@@ -83,6 +83,71 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// ---- LDS-DMA rings (the int8 and fp32 GEMM kernels)
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate that waits for lgkmcnt == 0 only.
+constexpr int waitcnt_lgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// s_waitcnt vmcnt(D * n) for a run-time n in 0..Q (the immediate must be a constant)
+template <int D, int Q>
+__device__ __forceinline__ void wait_vm_le(int n) {
+  if constexpr (Q >= 0) {
+    if (n == Q) __builtin_amdgcn_s_waitcnt(waitcnt_vm(D * Q));
+    else wait_vm_le<D, Q - 1>(n);
+  }
+}
+
+// One global_load_lds_dwordx4: each lane's 16 bytes at `src` land in LDS at
+// lds_off + 16*lane.  Issued as asm because the compiler, seeing the builtin's
+// LDS write, waits for every outstanding load before any later LDS read; the
+// kernels count these loads with their own s_waitcnt instead.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_off) {
+  uint32_t saved;
+  // M0 is saved and restored around the load (the compiler owns it); one wait
+  // state separates the M0 write from the LDS-DMA load that reads it.
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_off)), "v"(src)
+      : "memory");
+}
+
+// LDS byte offset of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// s_barrier alone: no wait for this wave's outstanding loads or LDS operations
+// (the caller's s_waitcnt says which must have landed).
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Maps the hardware workgroup id to a C tile: XCD-contiguous (workgroups are
+// dispatched round-robin over the 8 XCDs), then in groups of 8 tile rows so
+// that co-resident tiles share operand lines in their XCD's L2.
+__device__ __forceinline__ void tile_of_block(int bid, int nb, int tiles_m, int tiles_n,
+                                              int &tm, int &tn) {
+  const int q = nb >> 3, r = nb & 7, xcd = bid & 7, local = bid >> 3;
+  const int t = xcd * q + min(xcd, r) + local;
+  constexpr int G = 8;
+  const int gsz = G * tiles_n;
+  const int g = t / gsz, first = g * G;
+  const int gm = min(tiles_m - first, G);
+  const int w = t - g * gsz;
+  tm = first + w % gm;
+  tn = w / gm;
+}
+
 // block_sum through LDS with lds_barrier(): global loads stay in flight.
 __device__ __forceinline__ float block_sum_lds(float v, float *scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
