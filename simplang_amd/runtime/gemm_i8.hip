@@ -605,9 +605,10 @@ __global__ void __launch_bounds__(512)
 //     and the stage's one barrier sits between its two K-steps (as in the
 //     whole-line variant of gemm_i8_dma): this wave's DMAs of stage s+1 are
 //     waited for, every wave has read stage s, and stage s+SLOTS is issued into
-//     its slot.  With K / 128 <= SLOTS the whole of K is in flight at once.
-//   * u8 x s8: the waves of the first wave row also sum their B fragments
-//     (v_dot4 against 0x01010101) into the column sums, which meet in LDS.
+//     its slot.
+//   * u8 x s8: the waves also sum their B fragments (v_dot4 against
+//     0x01010101) into column sums, wave row h % WGM taking half-stage h; the
+//     rows' partial sums meet in LDS.
 template <int BN>
 __device__ __forceinline__ int ring_fb(int lrow, int lkc) {
   if constexpr (BN == 256) return (lrow >> 1) ^ ((lkc & 1) << 3);
@@ -712,9 +713,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-    int csum[FN];
+    v4i csacc[AU8 ? FN : 1];  // u8 x s8 column sums (first wave row)
 #pragma unroll
-    for (int j = 0; j < FN; j++) csum[j] = 0;
+    for (int j = 0; j < (AU8 ? FN : 1); j++) csacc[j] = v4i{0, 0, 0, 0};
+    const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
     v4i fra[2][FM], frb[2][FN];
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7");  // VALU writes of the accumulators -> MFMA reads
@@ -731,15 +733,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
 #pragma unroll
     for (int i = 0; i < FM; i++) fra[0][i] = afrag(0, wm0 + 16 * i, 0);
     auto mfmas = [&](int cb) {
-      if constexpr (AU8) {
-        if (wy == 0) {
-#pragma unroll
-          for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-              csum[j] = __builtin_amdgcn_sdot4(frb[cb][j][q], 0x01010101, csum[j], false);
-        }
-      }
       v4i a[FM];
 #pragma unroll
       for (int i = 0; i < FM; i++) a[i] = AU8 ? (fra[cb][i] ^ (int)0x80808080) : fra[cb][i];
@@ -752,6 +745,20 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       for (int i = 0; i < FM; i++)
 #pragma unroll
         for (int j = 0; j < FN; j++) mfma_v(acc[i][j], frb[cb][j], a[i]);
+      // u8 x s8: the first wave row also multiplies each B fragment by ones,
+      // which leaves every lane the column sums of its four output columns
+      // (MFMA work, asynchronous to the wave: the same sums by v_dot4 on the
+      // VALU held the other waves at every barrier, 1024^3 6.2 us against 5.4
+      // for s8 x s8).  The builtin, not asm: the compiler keeps `ones` in
+      // SGPRs and copies it into VGPRs right before each use, a VALU write
+      // that only its own hazard tracking separates from the MFMA read.
+      if constexpr (AU8) {
+        if (wy == 0) {
+#pragma unroll
+          for (int j = 0; j < FN; j++)
+            csacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(frb[cb][j], ones, csacc[j], 0, 0, 0);
+        }
+      }
     };
     for (int s = 0; s < ns; s++) {
       // K-step (s,0): read (s,1)'s fragments, run (s,0)
@@ -779,16 +786,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 15\n\ts_nop 15" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    // u8 x s8: column sums of this tile's columns, from the first wave row
+    // u8 x s8: column sums of this tile's columns, from the first wave row:
+    // csacc[j][r] = sum of column wn0 + 16 j + 4 (l/16) + r in every lane
     if constexpr (AU8) {
-      if (wy == 0) {
+      if (wy == 0 && lrow == 0) {
 #pragma unroll
-        for (int j = 0; j < FN; j++) {
-          int t = csum[j];
-          t += __shfl_xor(t, 16);
-          t += __shfl_xor(t, 32);
-          if (lkc == 0) cs_lds[wn0 + 16 * j + lrow] = t;
-        }
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) cs_lds[wn0 + 16 * j + 4 * lkc + r] = csacc[j][r];
       }
       __syncthreads();
     }
@@ -1233,27 +1238,38 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
   }
   {
     // mid sizes (K % 128 == 0): the ring kernel, 128x128 tiles from about half
-    // a tile per CU on, else 64x64 tiles; 8 waves (2 per SIMD) either way
+    // a tile per CU on, else 64x64 tiles; 8 waves (2 per SIMD) either way.
+    // Ring depth: 2 slots while every workgroup has one tile and K <= 2048, 4
+    // otherwise.  Measured (s8 x s8, graph replay): 768^3 4.55 / 4.79 / 5.05 us
+    // with 2 / 4 / 8 slots, 1024^3 5.36 / 5.66 / 6.23, 2048^3 15.0 / 15.3 (2 /
+    // 4); with K = 3200 or several tiles per workgroup 4 slots win
+    // (64x3200x8640 13.7 / 10.7 / 11.5, 3072^3 54.9 / 49.5).  A deeper
+    // prefetch spreads an XCD's CUs over more operand lines than its L2 keeps;
+    // a shallower one exposes more of the load latency once K is long.
     const bool ok = g.batch == 1 && g.K % 128 == 0 && g.N % 16 == 0 && g.ldb % 16 == 0 &&
                     ((uintptr_t)g.B & 15) == 0;
     const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
-    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) {
-      const int tm = (int)cdiv(g.M, 128), tn = (int)cdiv(g.N, 128);
+    auto ring = [&](auto bm, auto slots) {
+      constexpr int BM = decltype(bm)::value, SL = decltype(slots)::value;
+      const int tm = (int)cdiv(g.M, BM), tn = (int)cdiv(g.N, BM);
       const int grid = (int)std::min<int64_t>((int64_t)tm * tn, cus);
       KernelTimer kt(st, "gemm_i8_ring");
-      hipLaunchKernelGGL((gemm_i8_ring<128, 128, 4, 2, 4, AU8, BNK>), dim3(grid), dim3(512), 0,
-                         st, g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, vec);
-      SIMP_HIP(hipGetLastError());
-      return SIMP_RT_OK;
-    }
-    if (ok && tiles(64, 64) >= cus / 2 && g.M > 32) {
-      const int tm = (int)cdiv(g.M, 64), tn = (int)cdiv(g.N, 64);
-      const int grid = (int)std::min<int64_t>((int64_t)tm * tn, cus);
-      KernelTimer kt(st, "gemm_i8_ring");
-      hipLaunchKernelGGL((gemm_i8_ring<64, 64, 4, 2, 8, AU8, BNK>), dim3(grid), dim3(512), 0, st,
+      hipLaunchKernelGGL((gemm_i8_ring<BM, BM, 4, 2, SL, AU8, BNK>), dim3(grid), dim3(512), 0, st,
                          g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, vec);
       SIMP_HIP(hipGetLastError());
       return SIMP_RT_OK;
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    using I64 = std::integral_constant<int, 64>;
+    using I128 = std::integral_constant<int, 128>;
+    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) {
+      if (g.K <= 2048 && tiles(128, 128) <= cus) return ring(I128(), I2());
+      return ring(I128(), I4());
+    }
+    if (ok && tiles(64, 64) >= cus / 2 && g.M > 32) {
+      if (g.K <= 2048 && tiles(64, 64) <= cus) return ring(I64(), I2());
+      return ring(I64(), I4());
     }
   }
   if constexpr (!BNK) {
