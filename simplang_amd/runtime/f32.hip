@@ -293,9 +293,10 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
     }
 }
 
-// fp32 GEMM fed by an LDS-DMA ring, for one product with K % 32 == 0: BM x BN
-// C tiles, WGM x WGN waves, v_mfma_f32_16x16x4f32, the whole of K in one
-// workgroup (no split-K partials to sum afterwards).
+// fp32 GEMM fed by an LDS-DMA ring, K % 32 == 0: BM x BN C tiles of `batch`
+// products (operand bases sa / sb / sc elements apart), WGM x WGN waves,
+// v_mfma_f32_16x16x4f32, the whole of K in one workgroup (no split-K partials
+// to sum afterwards).
 //   * K-stages of 32 floats: an A (or B_T) row gives one whole 128-byte line
 //     per stage.  Operand tiles go global -> LDS directly
 //     (global_load_lds_dwordx4, each instruction 1 KB in lane order) into a
@@ -313,16 +314,17 @@ __global__ void __launch_bounds__(WGM *WGN * 64)
 //     per B fragment.  Fragments are double-buffered in registers.
 //   * The MFMA computes C^T tiles (B fragment first), so a lane ends with 4
 //     consecutive columns of one row of C: 16-byte stores.
-//   * Persistent: gridDim.x workgroups walk the tiles in tile_of_block order.
+//   * Persistent: gridDim.x workgroups walk the products' tiles, each product's
+//     in tile_of_block order.
 //     Rows past M and columns past N load from clamped in-bounds addresses and
 //     are never stored.
-// Requirements (checked by the dispatch): K % 32 == 0, N % 4 == 0, lda, ldb and
-// ldc multiples of 4, 16-byte aligned A, B and C.
+// Requirements (checked by the dispatch): K % 32 == 0, N % 4 == 0, lda, ldb,
+// ldc and the batch strides multiples of 4, 16-byte aligned A, B and C.
 template <int BM, int BN, int WGM, int WGN, int SLOTS, bool BT>
 __global__ void __launch_bounds__(64 * WGM * WGN)
-    gemm_f32_ring(const float *__restrict__ A, int64_t lda, const float *__restrict__ B,
-                  int64_t ldb, float *__restrict__ C, int64_t ldc, int M, int N, int K,
-                  int tiles_m, int tiles_n, float beta) {
+    gemm_f32_ring(const float *__restrict__ A, int64_t lda, int64_t sa, const float *__restrict__ B,
+                  int64_t ldb, int64_t sb, float *__restrict__ C, int64_t ldc, int64_t sc, int M,
+                  int N, int K, int tiles_m, int tiles_n, int batch, float beta) {
   constexpr int NW = WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 16, FN = WN / 16;
   constexpr int BK = 32;                                   // floats per stage
@@ -344,25 +346,29 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   const uint32_t lds_base = lds_offset(lds);
   const float *lds_f = (const float *)lds;
 
-  for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
+  for (int vb = blockIdx.x; vb < ntiles * batch; vb += gridDim.x) {
+    // product z = vb / ntiles, its tile in tile_of_block order
+    const int z = vb / ntiles;
     int tm, tn;
-    tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    tile_of_block(vb - z * ntiles, ntiles, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
+    const float *Az = A + z * sa, *Bz = B + z * sb;
+    float *Cz = C + z * sc;
     const float *srcA[DA], *srcB[DB];
 #pragma unroll
     for (int i = 0; i < DA; i++) {
       const int r = 8 * (wave * DA + i) + (lane >> 3);
-      srcA[i] = A + (int64_t)min(m0 + r, M - 1) * lda + 4 * ((lane & 7) ^ ((r >> 1) & 7));
+      srcA[i] = Az + (int64_t)min(m0 + r, M - 1) * lda + 4 * ((lane & 7) ^ ((r >> 1) & 7));
     }
 #pragma unroll
     for (int i = 0; i < DB; i++) {
       if constexpr (BT) {
         const int r = 8 * (wave * DB + i) + (lane >> 3);
-        srcB[i] = B + (int64_t)min(n0 + r, N - 1) * ldb + 4 * ((lane & 7) ^ ((r >> 1) & 7));
+        srcB[i] = Bz + (int64_t)min(n0 + r, N - 1) * ldb + 4 * ((lane & 7) ^ ((r >> 1) & 7));
       } else {
         const int kr = RPI * (wave * DB + i) + lane / LPR;  // k-row within the stage
         const int cb = (lane % LPR) ^ (((kr >> 2) & 3) << 2);
-        srcB[i] = B + (int64_t)kr * ldb + min(n0 + 4 * cb, N - 4);
+        srcB[i] = Bz + (int64_t)kr * ldb + min(n0 + 4 * cb, N - 4);
       }
     }
     auto issue = [&](int st) {
@@ -459,7 +465,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
       for (int i = 0; i < FM; i++) {
         const int row = m0 + wm0 + 16 * i + r16;
         if (row >= M || col >= N) continue;  // N % 4 == 0: col < N covers col..col+3
-        float4 *dst = (float4 *)(C + (int64_t)row * ldc + col);
+        float4 *dst = (float4 *)(Cz + (int64_t)row * ldc + col);
         float4 v = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         if (beta != 0.f) {
           const float4 o = *dst;
@@ -527,20 +533,21 @@ int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int
   return SIMP_RT_OK;
 }
 
-// gemm_f32_ring over the tiles of one product: persistent, up to per_cu
+// gemm_f32_ring over the tiles of `batch` products: persistent, up to per_cu
 // workgroups per CU.
 template <int BM, int BN, int WGM, int WGN, int SLOTS, bool BT>
-int launch_ring_f32(const float *A, int64_t lda, const float *B, int64_t ldb, float *C,
-                    int64_t ldc, int M, int N, int K, float beta, int per_cu, hipStream_t st) {
-  const int64_t tm = cdiv(M, BM), tn = cdiv(N, BN);
-  if (tm * tn > INT32_MAX)
+int launch_ring_f32(const float *A, int64_t lda, int64_t sa, const float *B, int64_t ldb,
+                    int64_t sb, float *C, int64_t ldc, int64_t sc, int M, int N, int K, int batch,
+                    float beta, int per_cu, hipStream_t st) {
+  const int64_t tm = cdiv(M, BM), tn = cdiv(N, BN), tiles = tm * tn * batch;
+  if (tiles > INT32_MAX)
     return set_error(SIMP_RT_EUNSUPPORTED, "gemm: %lld output tiles exceed one launch",
-                     (long long)(tm * tn));
-  const int grid = (int)std::min<int64_t>(tm * tn, (int64_t)per_cu * num_cus());
+                     (long long)tiles);
+  const int grid = (int)std::min<int64_t>(tiles, (int64_t)per_cu * num_cus());
   KernelTimer kt(st, "gemm_f32_ring");
   hipLaunchKernelGGL((gemm_f32_ring<BM, BN, WGM, WGN, SLOTS, BT>), dim3(grid),
-                     dim3(64 * WGM * WGN), 0, st, A, lda, B, ldb, C, ldc, M, N, K, (int)tm,
-                     (int)tn, beta);
+                     dim3(64 * WGM * WGN), 0, st, A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
+                     (int)tm, (int)tn, batch, beta);
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
 }
@@ -561,19 +568,28 @@ int dispatch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, i
     return launch_mfma_f32<16, 256, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   if (M <= 32)
     return launch_mfma_f32<32, 128, 1, 4, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
-  // One product whose tiles cover the chip, K % 32 == 0, 16-byte C rows: the
-  // LDS-DMA ring kernel, the whole of K per workgroup.  Two ring slots (plain
+  // Tiles (of all the batch's products) covering the chip, K % 32 == 0, 16-byte
+  // C rows: the LDS-DMA ring kernel, the whole of K per workgroup.  Two ring slots (plain
   // double buffering) measured fastest: 4, 6, 8 and 10 slots ran 7-27% slower
   // at the prefill shapes, the deeper prefetch spreading the CUs of an XCD
   // over more operand lines than its L2 keeps.  128x128 tiles on 16 waves
   // from one tile per CU (2048^3: 139.8 us against 157.6 for gemm_f32_mfma;
   // 4096^3: 1074 against 1104), else 64x64 tiles on 8 waves (128x2048x8192 and
   // 512x2048x2048: 42.9 us against 49.9 with split-K and its ordered sum).
-  const bool ring_ok = batch == 1 && K % 32 == 0 && N % 4 == 0 && ldc % 4 == 0 && al(C);
+  // With K <= 256 (eight K-stages or fewer) four 64x64 workgroups per CU
+  // overlap each other's short K loops: 32 x (512x128x512) 25.1 us against
+  // 28.9 on 128x128 tiles (28.1 for gemm_f32_mfma), 8 x (1024x256x1024) 42.5
+  // against 44.2; from K = 512 on the 128x128 tiles stay ahead.
+  const bool ring_ok = K % 32 == 0 && N % 4 == 0 && ldc % 4 == 0 && sc % 4 == 0 && al(C);
+  if (ring_ok && K <= 256 && tiles(64, 64) >= cus)
+    return launch_ring_f32<64, 64, 2, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
+                                                batch, beta, 4, st);
   if (ring_ok && tiles(128, 128) >= cus)
-    return launch_ring_f32<128, 128, 4, 4, 2, BT>(A, lda, B, ldb, C, ldc, M, N, K, beta, 1, st);
+    return launch_ring_f32<128, 128, 4, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
+                                                  batch, beta, 1, st);
   if (ring_ok && tiles(64, 64) >= cus)
-    return launch_ring_f32<64, 64, 2, 4, 2, BT>(A, lda, B, ldb, C, ldc, M, N, K, beta, 2, st);
+    return launch_ring_f32<64, 64, 2, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
+                                                batch, beta, 2, st);
   if (tiles(128, 128) >= cus)
     return launch_mfma_f32<128, 128, 2, 2, BT, 32>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);
   return launch_mfma_f32<64, 64, 2, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K, batch, beta, st);

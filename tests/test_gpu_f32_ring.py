@@ -2,11 +2,12 @@
 through every entry point that reaches it: tensor_matmul_f32 (B[K,N]),
 tensor_matmul_nt_f32 and tensor_matmul_nhwc (B_T rows), and the accumulating
 matmul builtin (C += A B at element offsets, ConvertSimpToMemRef.cpp:1794-1920).
-The dispatch takes it for one product with K % 32 == 0 and 16-byte aligned rows
-once the tiles cover the chip: 128x128 tiles from 256 of them, else 64x64 tiles
-from 256 of them.  Cases cover both tile sizes with ragged M and N (rows and
-columns past the edge load clamped addresses and must not be stored), one and
-two K-stages, and several tiles per workgroup (the persistent loop).
+The dispatch takes it for products with K % 32 == 0 and 16-byte aligned rows
+once the tiles cover the chip: with K <= 256 64x64 tiles four workgroups per
+CU, else 128x128 tiles from 256 of them, else 64x64 tiles from 256 of them.
+Cases cover every form with ragged M and N (rows and columns past the edge load
+clamped addresses and must not be stored), one and two K-stages, and several
+tiles per workgroup (the persistent loop).
 
 Reference: float64 products (numpy's BLAS).  Tolerance 1e-4 of max|ref|, the
 bar of the other fp32 tests; C starts as NaN so an unwritten element fails.
@@ -32,11 +33,11 @@ def _rand(rng, *shape):
 
 
 # (M, K, N): 64x64 tiles (16x17 = 272 tiles, ragged both ways); one and two
-# K-stages; 64x64 tiles two per workgroup (2x510 tiles on 512 workgroups, M
-# ragged); 128x128 tiles ragged (16x17 tiles on 256 workgroups); 128x128 tiles
-# two per workgroup
-SHAPES = [(1000, 2048, 1028), (1024, 32, 1024), (1088, 64, 1024), (120, 64, 32640),
-          (2000, 320, 2052), (2048, 256, 4096)]
+# K-stages (short K: 64x64 tiles, up to four workgroups per CU); 64x64 tiles
+# two per workgroup (2x510 tiles on 512 workgroups, M ragged); 128x128 tiles
+# ragged (16x17 tiles on 256 workgroups); 128x128 tiles two per workgroup
+SHAPES = [(1000, 2048, 1028), (1024, 32, 1024), (1088, 64, 1024), (120, 320, 32640),
+          (2000, 320, 2052), (2048, 512, 4096)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -95,3 +96,19 @@ def test_ring_nhwc(dev):
     torch.cuda.synchronize()
     want = x.reshape(-1, 64).astype(np.float64) @ w.astype(np.float64).T
     _close(y.cpu().numpy().reshape(-1, 256), want)
+
+
+@pytest.mark.parametrize("bt,M,K,N", [(16, 200, 64, 260), (24, 300, 320, 400), (32, 512, 128, 512)])
+def test_ring_batch(dev, bt, M, K, N):
+    """tensor_batch_matmul: the batch's products share one persistent launch
+    (16 x 4 x 5 and 32 x 8 x 8 tiles of 64x64 at K <= 256; 24 x 3 x 4 tiles of
+    128x128 at K = 320, two per workgroup for some), ragged M and N in the
+    first two."""
+    import torch
+    print(f"[f32-ring] batch {bt} x ({M}x{K}x{N})", flush=True)
+    rng = np.random.default_rng(bt * M + K + N)
+    a, b = _rand(rng, bt, M, K), _rand(rng, bt, K, N)
+    c = torch.full((bt, M, N), float("nan"), device=dev)
+    sa.tensor_batch_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), c)
+    torch.cuda.synchronize()
+    _close(c.cpu().numpy(), np.matmul(a.astype(np.float64), b.astype(np.float64)))
