@@ -487,8 +487,10 @@ float llama2_quant_forward(
  * hidden_dim and head_dim must be multiples of 16 and the int8 weights
  * 16-byte aligned.
  * The KV cache is kept on the device and the rows at pos are copied back into
- * k_cache / v_cache; logits, x_fp32 and xb_fp32 are written; xb_i8,
- * att_scores, att_probs, attn_out and ffn_hb are left untouched.  Weights and
+ * k_cache / v_cache; logits, x_fp32, xb_fp32 and attn_out (the last layer's,
+ * as the program leaves it; its int32 truncation of an fp32 sum may differ by 1
+ * where the summation order moves the sum across an integer) are written;
+ * xb_i8, att_scores, att_probs and ffn_hb are left untouched.  Weights and
  * errors as for stories110M_forward. */
 #define SIMP_RT_DESC_I32(n) int32_t *n##_alloc, int32_t *n, int64_t n##_off, int64_t n##_size, int64_t n##_stride
 float llama32_forward(

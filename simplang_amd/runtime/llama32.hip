@@ -23,8 +23,9 @@
 //
 // State: the KV cache lives on the device (authoritative across calls); each
 // call writes the new row of every layer back to the caller's k_cache/v_cache,
-// and writes logits, x_fp32 and xb_fp32.  att_scores, att_probs, attn_out,
-// xb_i8 and ffn_hb are the program's per-layer scratch and are not written.
+// and writes logits, x_fp32, xb_fp32 and attn_out (the last layer's, as the
+// program leaves it).  att_scores, att_probs, xb_i8 and ffn_hb are the
+// program's per-layer scratch and are not written.
 #include <algorithm>
 #include <cmath>
 #include <limits>
@@ -224,118 +225,144 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// Attention of one layer, one block per head (:161-216).  Scores: one thread
-// per position, the program's order and operations within a position (fp32
-// product then sum, no fused multiply-add), / 8; the 16-byte chunks of four
-// positions are loaded four chunks at a time before any is summed.  Softmax
-// over pos + 1 scores.  V sum: a thread takes 16 consecutive d of every P-th
-// position (four rows in flight), partitions added in order; the first four
-// rows of every thread are loaded at entry, so they arrive alongside the K
-// rows.  attn_out = (i32) sum; xq = its i8 quantization (float)attn_out / 256,
-// clamped.  Head size and kv_dim multiples of 16.
-// LDS: head_size + pos + 1 floats (dynamic, at most 47 KB) + 16 KB.
-__global__ void __launch_bounds__(256)
+// Attention of one layer, one block of 8 waves per head (:161-216).
+//   * Scores: LPP lanes per position (head_size / 16 chunks of 16 bytes,
+//     rounded up to a power of two), 16 dims per lane with the program's fp32
+//     product then sum (no fused multiply-add) over them, the LPP partial sums
+//     added across lanes (DPP), / 8.  q is converted once into registers; the
+//     K rows of four passes are loaded before any is summed.
+//   * Softmax over pos + 1 scores: wave then block maximum and sum (the
+//     waves' values combined in wave order through LDS), p = e / sum.
+//   * V sum: head_size / 4 lanes per row (4 dims each, one dword load), row
+//     group g of wave w taking positions t = 8 RPW s + RPW w + g; the 8 RPW
+//     partial sums of a dim are added in (wave, group) order.
+//   * Long contexts: block (h, s) takes positions [CH s, CH s + CH) of head
+//     h (grid y = nsplit chunks); with nsplit > 1 it writes its chunk's
+//     maximum score, sum of exponentials and normalised V sum to ws[h][s] and
+//     l32_attn_combine_k forms the head's output.  One CU per head moved
+//     512 KB of K and V at pos 4095 (34 us per launch).
+// Only the summation order differs from the program's sequential loops (one
+// thread per position and a 16-dim chain per thread, measured 12.9 us per
+// launch at the 1B shape's positions 128-191 and 38 us at 4095).
+// attn_out = (i32) sum; xq = its i8 quantization (float)attn_out / 256,
+// clamped.  Head size and kv_dim multiples of 16, head size <= 256.
+// LDS: min(pos + 1, CH) floats (dynamic, at most 47 KB) + 8 KB.
+constexpr int kL32AttnWaves = 8;
+__global__ void __launch_bounds__(64 * kL32AttnWaves)
     l32_attn_k(const int32_t *__restrict__ Q, const int8_t *__restrict__ kc,
                const int8_t *__restrict__ vc, int32_t *__restrict__ attn_out,
-               int8_t *__restrict__ xq, int pos, int kv, int hs, int n_rep) {
-  extern __shared__ float sm[];
-  __shared__ float red[4096];
-  __shared__ float scratch[16];
-  constexpr int U = 4, CG = 4;
-  const int h = blockIdx.x, kho = (h / n_rep) * hs, n = pos + 1;
+               int8_t *__restrict__ xq, float *__restrict__ ws, int pos, int kv, int hs,
+               int n_rep, int chunk) {
+  constexpr int NW = kL32AttnWaves, U = 4;
+  extern __shared__ float att[];      // the chunk's scores, then probabilities
+  __shared__ float red[NW * 256];     // V partial sums: NW * RPW rows of hs (RPW * hs <= 256)
+  __shared__ float wv[2][NW];         // per-wave maximum and sum
+  const int h = blockIdx.x, kho = (h / n_rep) * hs;
+  // this block's positions [t_lo, t_lo + n); att[] is indexed from t_lo
+  const int t_lo = blockIdx.y * chunk, n = min(pos + 1 - t_lo, chunk);
+  kc += (int64_t)t_lo * kv;
+  vc += (int64_t)t_lo * kv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hc = hs >> 4;  // 16-byte chunks per row
-  const int P = 256 / hc;  // V position partitions (hs <= 256: P >= 16)
-  const int vcol = threadIdx.x % hc, vp = threadIdx.x / hc;
-  // this thread's first V rows (positions vp + P u), issued ahead of everything
-  uint4 v0[U];
+  int lpp = 1;
+  while (lpp < hc) lpp <<= 1;  // lanes per position: 1, 2, 4, 8 or 16
+  const int ppw = 64 / lpp, ppb = NW * ppw;  // positions per wave and per block pass
+  const int c = lane & (lpp - 1);
+  const bool cl = c < hc;
+  float qv[16];
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    const int t = vp + P * u;
-    v0[u] = (vp < P && t < n) ? *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * vcol)
-                              : make_uint4(0, 0, 0, 0);
-  }
-  float *qf = sm, *att = sm + hs;
-  for (int d = threadIdx.x; d < hs; d += 256) qf[d] = (float)Q[h * hs + d];
-  __syncthreads();
-  for (int t0 = threadIdx.x; t0 < n; t0 += 256 * U) {
-    float score[U];
+  for (int e = 0; e < 16; e++) qv[e] = cl ? (float)Q[h * hs + 16 * c + e] : 0.f;
+  // 1. scores, U passes of loads at a time
+  for (int t0 = wave * ppw + lane / lpp; t0 < n; t0 += U * ppb) {
+    uint4 kr[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) score[u] = 0.f;
-    for (int c0 = 0; c0 < hc; c0 += CG) {
-      uint4 kv4[U][CG];
-#pragma unroll
-      for (int u = 0; u < U; u++)
-#pragma unroll
-        for (int cc = 0; cc < CG; cc++) {
-          const int t = t0 + 256 * u, c = c0 + cc;
-          kv4[u][cc] = (t < n && c < hc) ? *(const uint4 *)(kc + (int64_t)t * kv + kho + 16 * c)
-                                         : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-      for (int u = 0; u < U; u++)
-#pragma unroll
-        for (int cc = 0; cc < CG; cc++) {
-          if (c0 + cc >= hc) break;
-          const uint32_t wd[4] = {kv4[u][cc].x, kv4[u][cc].y, kv4[u][cc].z, kv4[u][cc].w};
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            const float kf = (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)));
-            score[u] = __fadd_rn(score[u], __fmul_rn(qf[16 * (c0 + cc) + e], kf));
-          }
-        }
+    for (int u = 0; u < U; u++) {
+      const int t = t0 + u * ppb;
+      kr[u] = (cl && t < n) ? *(const uint4 *)(kc + (int64_t)t * kv + kho + 16 * c)
+                            : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int u = 0; u < U; u++)
-      if (t0 + 256 * u < n) att[t0 + 256 * u] = score[u] / 8.0f;
+    for (int u = 0; u < U; u++) {
+      const uint32_t wd[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
+      float sc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e++)
+        sc = __fadd_rn(sc, __fmul_rn(qv[e], (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)))));
+      // partial sums of the position's lpp lanes (lanes of one 16-lane row)
+      if (lpp > 1) sc += dpp_mov<kDppXor1>(sc);
+      if (lpp > 2) sc += dpp_mov<kDppXor2>(sc);
+      if (lpp > 4) sc += dpp_mov<kDppHalfMirror>(sc);
+      if (lpp > 8) sc += dpp_mov<kDppMirror>(sc);
+      const int t = t0 + u * ppb;
+      if (c == 0 && t < n) att[t] = sc / 8.0f;
+    }
   }
   __syncthreads();
+  // 2. softmax
   float m = -INFINITY;
-  for (int t = threadIdx.x; t < n; t += 256) m = fmaxf(m, att[t]);
-  m = block_max(m, scratch);
+  for (int t = tid; t < n; t += 64 * NW) m = fmaxf(m, att[t]);
+  m = wave_max_dpp(m);
+  if (lane == 0) wv[0][wave] = m;
+  __syncthreads();
+  m = wv[0][0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) m = fmaxf(m, wv[0][w]);
   float l = 0.f;
-  for (int t = threadIdx.x; t < n; t += 256) {
+  for (int t = tid; t < n; t += 64 * NW) {
     const float e = expf(att[t] - m);
     att[t] = e;
     l += e;
   }
-  l = block_sum(l, scratch);
-  for (int t = threadIdx.x; t < n; t += 256) att[t] = att[t] / l;
+  l = wave_sum_dpp(l);
+  if (lane == 0) wv[1][wave] = l;
   __syncthreads();
-  if (vp < P) {
-    float acc[16];
+  l = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; e++) acc[e] = 0.f;
-    for (int t0 = vp; t0 < n; t0 += P * U) {
-      uint4 v[U];
-      if (t0 == vp) {
+  for (int w = 0; w < NW; w++) l += wv[1][w];
+  for (int t = tid; t < n; t += 64 * NW) att[t] = att[t] / l;
+  __syncthreads();
+  // 3. V sum
+  const int lpr = hs >> 2, rpw = 64 / lpr;  // lanes per V row (4 dims each), rows per wave
+  const int dq = lane % lpr, rg = lane / lpr;
+  if (rg < rpw) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const int step = NW * rpw;
+    for (int t0 = wave * rpw + rg; t0 < n; t0 += U * step) {
+      uint32_t vr[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = v0[u];
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          const int t = min(t0 + P * u, n - 1);
-          v[u] = *(const uint4 *)(vc + (int64_t)t * kv + kho + 16 * vcol);
-        }
+      for (int u = 0; u < U; u++) {
+        const int t = t0 + u * step;
+        vr[u] = t < n ? *(const uint32_t *)(vc + (int64_t)t * kv + kho + 4 * dq) : 0u;
       }
 #pragma unroll
       for (int u = 0; u < U; u++) {
-        if (t0 + P * u >= n) break;
-        const float a = att[t0 + P * u];
-        const uint32_t wd[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        const int t = t0 + u * step;
+        if (t < n) {
+          const float p = att[t];
 #pragma unroll
-        for (int e = 0; e < 16; e++)
-          acc[e] = __fadd_rn(acc[e], __fmul_rn(a, (float)(int8_t)(uint8_t)(wd[e >> 2] >> (8 * (e & 3)))));
+          for (int e = 0; e < 4; e++)
+            acc[e] = __fadd_rn(acc[e], __fmul_rn(p, (float)(int8_t)(uint8_t)(vr[u] >> (8 * e))));
+        }
       }
     }
 #pragma unroll
-    for (int e = 0; e < 16; e++) red[vp * hs + 16 * vcol + e] = acc[e];
+    for (int e = 0; e < 4; e++) red[(wave * rpw + rg) * hs + 4 * dq + e] = acc[e];
   }
   __syncthreads();
-  for (int dd = threadIdx.x; dd < hs; dd += 256) {
+  for (int dd = tid; dd < hs; dd += 64 * NW) {
     float v = red[dd];
-    // in partition order; unrolled so that the LDS reads run ahead of the adds
+    const int parts = NW * rpw;
 #pragma unroll 8
-    for (int pp = 1; pp < P; pp++) v = __fadd_rn(v, red[pp * hs + dd]);
+    for (int pp = 1; pp < parts; pp++) v = __fadd_rn(v, red[pp * hs + dd]);
+    if (gridDim.y > 1) {  // the chunk's (max, sum, normalised V sum) for the combine
+      float *w = ws + ((int64_t)h * gridDim.y + blockIdx.y) * (hs + 2);
+      w[dd] = v;
+      if (dd == 0) {
+        w[hs] = m;
+        w[hs + 1] = l;
+      }
+      continue;
+    }
     const int32_t a = (int32_t)v;
     attn_out[h * hs + dd] = a;
     float s = (float)a * 1.0f / 256.0f;
@@ -345,6 +372,36 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Combines the nsplit chunks of l32_attn_k for head blockIdx.x, thread d:
+// out = sum_s w_s o_s / sum_s w_s with w_s = e^(m_s - M) l_s, M = max_s m_s
+// (o_s the chunk's normalised V sum), then attn_out and xq as l32_attn_k.
+__global__ void __launch_bounds__(256)
+    l32_attn_combine_k(const float *__restrict__ ws, int32_t *__restrict__ attn_out,
+                       int8_t *__restrict__ xq, int hs, int nsplit) {
+  const int h = blockIdx.x;
+  const float *w = ws + (int64_t)h * nsplit * (hs + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; s++) M = fmaxf(M, w[s * (hs + 2) + hs]);
+  for (int dd = threadIdx.x; dd < hs; dd += 256) {
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+      const float *ws_s = w + s * (hs + 2);
+      const float f = expf(ws_s[hs] - M) * ws_s[hs + 1];
+      num = fmaf(f, ws_s[dd], num);
+      den += f;
+    }
+    const int32_t a = (int32_t)(num / den);
+    attn_out[h * hs + dd] = a;
+    float v = (float)a * 1.0f / 256.0f;
+    v = v > 127.0f ? 127.0f : v;
+    v = v < -128.0f ? -128.0f : v;
+    xq[h * hs + dd] = (int8_t)(int32_t)v;
+  }
+}
+
+// Positions per attention block: longer contexts split over blocks.
+constexpr int kL32AttnChunk = 512;
+
 struct L32Model {
   int64_t dim, hid, L, nh, nkv, V, S, hs, kv;
   const float *rms_att, *rms_ffn, *rms_final, *wcls;
@@ -352,6 +409,7 @@ struct L32Model {
   float *x = nullptr, *xb = nullptr, *logits = nullptr;
   int8_t *xi = nullptr, *xq = nullptr, *hq = nullptr, *kc = nullptr, *vc = nullptr;
   int32_t *q = nullptr, *attn = nullptr;
+  float *attn_ws = nullptr;  // l32_attn_k chunk results: nh * cdiv(S, chunk) * (hs + 2)
   ExportWeights weights;
   KvState kvs;
   uint64_t last_use = 0;
@@ -359,11 +417,13 @@ struct L32Model {
 
 void l32_free(L32Model &m) {
   for (void *p : {(void *)m.x, (void *)m.xb, (void *)m.logits, (void *)m.xi, (void *)m.xq,
-                  (void *)m.hq, (void *)m.kc, (void *)m.vc, (void *)m.q, (void *)m.attn})
+                  (void *)m.hq, (void *)m.kc, (void *)m.vc, (void *)m.q, (void *)m.attn,
+                  (void *)m.attn_ws})
     if (p) (void)hipFree(p);
   m.x = m.xb = m.logits = nullptr;
   m.xi = m.xq = m.hq = m.kc = m.vc = nullptr;
   m.q = m.attn = nullptr;
+  m.attn_ws = nullptr;
   m.weights.release();
 }
 
@@ -374,7 +434,9 @@ int l32_alloc(L32Model &m) {
                     {(void **)&m.logits, 4 * (size_t)m.V}, {(void **)&m.xi, (size_t)m.dim},
                     {(void **)&m.xq, (size_t)m.dim},       {(void **)&m.hq, (size_t)m.hid},
                     {(void **)&m.kc, cache},               {(void **)&m.vc, cache},
-                    {(void **)&m.q, 4 * (size_t)m.dim},    {(void **)&m.attn, 4 * (size_t)m.dim}};
+                    {(void **)&m.q, 4 * (size_t)m.dim},    {(void **)&m.attn, 4 * (size_t)m.dim},
+                    {(void **)&m.attn_ws,
+                     4 * (size_t)(m.nh * cdiv(m.S, kL32AttnChunk) * (m.hs + 2))}};
   for (const B &b : bufs) {
     if (hipMalloc(b.p, std::max<size_t>(b.bytes, 16)) != hipSuccess)
       return set_error(SIMP_RT_ENOMEM, "llama32_forward: device buffers");
@@ -431,7 +493,8 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
   hipLaunchKernelGGL(l32_embed_k, dim3((unsigned)cdiv(dim, 256)), dim3(256), 0, st,
                      (const int8_t *)m.xi, m.x, dim);
   int rc;
-  const size_t attn_lds = sizeof(float) * (size_t)(m.hs + pos + 1);
+  const int nsplit = (int)cdiv(pos + 1, kL32AttnChunk);
+  const size_t attn_lds = sizeof(float) * (size_t)std::min<int64_t>(pos + 1, kL32AttnChunk);
   for (int64_t l = 0; l < m.L; l++) {
     int8_t *kc = m.kc + l * m.S * kv, *vc = m.vc + l * m.S * kv;
     L32Segs s{};
@@ -445,9 +508,13 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
                                 vc + pos * kv, nullptr, nullptr, st, m.x, m.rms_att + l * dim,
                                 eps)))
       return rc;
-    hipLaunchKernelGGL(l32_attn_k, dim3((unsigned)m.nh), dim3(256), attn_lds, st,
-                       (const int32_t *)m.q, (const int8_t *)kc, (const int8_t *)vc, m.attn, m.xq,
-                       (int)pos, kv, (int)m.hs, (int)(m.nh / m.nkv));
+    hipLaunchKernelGGL(l32_attn_k, dim3((unsigned)m.nh, (unsigned)nsplit),
+                       dim3(64 * kL32AttnWaves), attn_lds, st, (const int32_t *)m.q,
+                       (const int8_t *)kc, (const int8_t *)vc, m.attn, m.xq, m.attn_ws,
+                       (int)pos, kv, (int)m.hs, (int)(m.nh / m.nkv), kL32AttnChunk);
+    if (nsplit > 1)
+      hipLaunchKernelGGL(l32_attn_combine_k, dim3((unsigned)m.nh), dim3(256), 0, st,
+                         (const float *)m.attn_ws, m.attn, m.xq, (int)m.hs, nsplit);
     s = L32Segs{};
     s.w[0] = m.wo + l * m.dim * m.dim;
     s.rows[0] = dim;
@@ -507,7 +574,7 @@ float llama32_forward(
     int64_t vocab_size, int64_t max_seq_len, int64_t head_dim) {
   const float nan = std::numeric_limits<float>::quiet_NaN();
   clear_error();
-  (void)xb_i8; (void)att_scores; (void)att_probs; (void)attn_out; (void)ffn_hb;
+  (void)xb_i8; (void)att_scores; (void)att_probs; (void)ffn_hb;
   (void)xb_i8_alloc; (void)att_scores_alloc; (void)att_probs_alloc; (void)attn_out_alloc;
   (void)ffn_hb_alloc;
   auto fail = [&](const char *msg) {
@@ -543,7 +610,8 @@ float llama32_forward(
       {xb_fp32, xb_fp32_off, xb_fp32_size, xb_fp32_stride, D, 4, "xb_fp32"},
       {logits, logits_off, logits_size, logits_stride, vocab_size, 4, "logits"},
       {k_cache, k_cache_off, k_cache_size, k_cache_stride, L * max_seq_len * kv, 1, "k_cache"},
-      {v_cache, v_cache_off, v_cache_size, v_cache_stride, L * max_seq_len * kv, 1, "v_cache"}};
+      {v_cache, v_cache_off, v_cache_size, v_cache_stride, L * max_seq_len * kv, 1, "v_cache"},
+      {attn_out, attn_out_off, attn_out_size, attn_out_stride, D, 4, "attn_out"}};
   for (const In &a : ins) {
     if (check_desc1(a.name, a.p, a.off, a.size, a.stride)) return nan;
     if (a.size < a.need) {
@@ -620,6 +688,9 @@ float llama32_forward(
     e = hipMemcpyAsync(x_fp32 + x_fp32_off, m->x, 4 * (size_t)D, hipMemcpyDefault, st);
   if (e == hipSuccess)
     e = hipMemcpyAsync(xb_fp32 + xb_fp32_off, m->xb, 4 * (size_t)D, hipMemcpyDefault, st);
+  // attn_out as the program leaves it: the last layer's attention
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(attn_out + attn_out_off, m->attn, 4 * (size_t)D, hipMemcpyDefault, st);
   if (e == hipSuccess)
     e = hipMemcpy2DAsync(k_cache + k_cache_off + at, pitch, m->kc + at, pitch, row, (size_t)L,
                          hipMemcpyDefault, st);
