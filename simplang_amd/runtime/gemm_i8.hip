@@ -16,9 +16,10 @@
 //   * gemm_i8_dma -- problems of at least one 256x256 tile per CU, K % 64 == 0:
 //     persistent, global -> LDS DMA ring, v_mfma_i32_16x16x64_i8, 16-byte
 //     nontemporal C stores.  B given as [K,N] with 16-byte aligned rows is
-//     read in place and transposed by the LDS reads (ds_read_b64_tr_b8); the
-//     u8 column sums come from colsum_kn_i8.  B_T[N,K] inputs are read as
-//     rows (column sums by colsum_nk_i8), and a [K,N] B the in-place read
+//     read in place and transposed by the LDS reads (ds_read_b64_tr_b8).  The
+//     u8 column sums come from the kernel's own B fragments on the MFMA pipe
+//     up to M = 4096, else from colsum_kn_i8 (colsum_nk_i8 for B_T[N,K]
+//     inputs, which are read as rows), and a [K,N] B the in-place read
 //     cannot serve is first transposed into a workspace B_T (transpose_i8, which
 //     forms the column sums on the way), as the reference materialises B_T
 //     (ConvertSimpToMemRef.cpp:3168-3216).
@@ -433,7 +434,7 @@ __device__ __forceinline__ v2i lds_read_tr8(const void *lds, uint32_t off) {
 //     Column block cb of k-row k sits at block cb ^ (k & 7) ^ 8 ((k >> 4) & 1),
 //     so the 32 lanes of a half-wave read 32 distinct 8-byte bank pairs.
 //     Columns past N read a clamped in-bounds block; they are never stored.
-template <int STAGES, bool AU8, bool BNK>
+template <int STAGES, bool AU8, bool BNK, bool CSK = false>
 __global__ void __launch_bounds__(512)
     gemm_i8_dma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
@@ -450,6 +451,13 @@ __global__ void __launch_bounds__(512)
   const int drow = lane >> 2, dkc = (lane & 3) ^ ((drow >> 1) & 3);  // DMA lane -> row, chunk
   const int rslot = lrow * 4 + (lkc ^ ((lrow >> 1) & 3));          // operand lane -> slot
   const uint32_t lds_wave = lds_offset(lds) + 2048 * wave;  // wave w fills blocks 2w, 2w+1
+  // CS: u8 column sums on the MFMA pipe.  Wave row wy takes its B fragments in
+  // the order j ^ jx (jx = 2 wy), so that its fragments 0 and 1, whose column
+  // sums it forms, are columns 2 wy and 2 wy + 1 of the wave's four.
+  constexpr bool CS = AU8 && CSK;
+  __shared__ v4i cs_lds[CS ? BN / 4 : 1];
+  const int jx = CS ? 2 * (wave / WGN) : 0;
+  const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
   // [K,N] B: lane l reads k-row 16 (l/16) + (l%16)/2 (+8), swizzle of that row
   const uint32_t boff = (16 * lkc + (lrow >> 1)) * 256 + 8 * (lrow & 1);
   const int bsw = (lrow >> 1) ^ ((lkc & 1) << 3);
@@ -489,6 +497,7 @@ __global__ void __launch_bounds__(512)
     // Fragments: A single-buffered and refilled in place right after its last
     // MFMA of the step; B double-buffered (read at the start of the step).
     v4i fa[FM], fb[2][FN];
+    v4i csacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
     auto frag = [&](int kt, int blk) {
       const uint4 v = lds[(kt % STAGES) * (STAGE / 16) + blk * 64 + rslot];
       return v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
@@ -498,9 +507,9 @@ __global__ void __launch_bounds__(512)
     // [k][n] tile, k = 16 (l/16) + 8 t + (l%16)/2, bytes 8 (l & 1) of its block
     auto bfrag = [&](int kt, int j) {
       if constexpr (BNK) {
-        return frag(kt, BOFF + wn0 / 16 + j);
+        return frag(kt, BOFF + wn0 / 16 + (j ^ jx));
       } else {
-        const int cb = ((wn0 >> 4) + j) ^ bsw;
+        const int cb = ((wn0 >> 4) + (j ^ jx)) ^ bsw;
         const uint32_t base = (kt % STAGES) * STAGE + BM * BK + (cb << 4) + boff;
         const v2i lo = lds_read_tr8(lds, base);
         const v2i hi = lds_read_tr8(lds, base + 8 * 256);
@@ -551,6 +560,15 @@ __global__ void __launch_bounds__(512)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][j], a, acc[i][j], 0, 0, 0);
         if (more) fa[i] = frag(kt + 1, wm0 / 16 + i);
         if (i == 3 && kt + STAGES < nk) issue(kt + STAGES);
+        // CS: B fragments 0 and 1 also meet an all-ones operand, which leaves
+        // every lane the sums of its four output columns of those fragments
+        // (two more MFMAs per 32 on every wave)
+        if constexpr (CS) {
+          if (i == 1 || i == 5) {
+            const int t = i == 1 ? 0 : 1;
+            csacc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][t], ones, csacc[t], 0, 0, 0);
+          }
+        }
       }
     };
     int kt = 0;
@@ -559,14 +577,25 @@ __global__ void __launch_bounds__(512)
       step(kt + 1, 1);
     }
     if (kt < nk) step(kt, 0);
-    // acc[i][j][r] = C[m0 + wm0 + 16 i + l%16][n0 + wn0 + 16 j + 4 (l/16) + r]
+    if constexpr (CS) {
+      // csacc[t][r] = sum of column wn0 + 16 (t ^ jx) + 4 (l/16) + r; the
+      // other wave row of the same columns holds the other two fragments
+      if (lrow == 0) {
+        cs_lds[(wn0 + 16 * jx) / 4 + lkc] = csacc[0];
+        cs_lds[(wn0 + 16 * (1 ^ jx)) / 4 + lkc] = csacc[1];
+      }
+      __syncthreads();
+    }
+    // acc[i][j][r] = C[m0 + wm0 + 16 i + l%16][n0 + wn0 + 16 (j ^ jx) + 4 (l/16) + r]
 #pragma unroll
     for (int j = 0; j < FN; j++) {
-      const int col = n0 + wn0 + 16 * j + 4 * lkc;
+      const int col = n0 + wn0 + 16 * (j ^ jx) + 4 * lkc;
       // u8 x s8: C = (A^0x80) B + 128 colsum(B)
       // (N % 16 == 0 and col % 4 == 0, so col < N covers col..col+3)
       v4i bias = v4i{0, 0, 0, 0};
-      if constexpr (AU8) {
+      if constexpr (CS) {
+        bias = cs_lds[(wn0 + 16 * (j ^ jx)) / 4 + lkc] * 128;
+      } else if constexpr (AU8) {
         if (col < N) bias = *(const v4i *)(colsum + col) * 128;
       }
 #pragma unroll
@@ -1173,10 +1202,16 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     const int grid = (int)std::max<int64_t>(8, std::min<int64_t>(cus, (int64_t)tm * tn) / 8 * 8);
     // B[K,N] with 16-byte aligned rows is read in place by gemm_i8_dma
     const bool direct = !BNK && g.K % 64 == 0 && g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0;
-    // Workspace: [colsum: N int32, 256-byte aligned][B_T: N x K bytes when B is [K,N]
-    // and not read in place]
+    // u8 x s8 column sums inside gemm_i8_dma (CSK) up to 16 tile rows: every
+    // tile row forms its columns' sums again, two more MFMAs per 32 (+4% per
+    // K-step), against a pass over B and its zero fill ahead of the GEMM.
+    // Measured whole calls: 4096^3 73.7 against 81.3 us, 4096x8192x4096 131
+    // against 141; 8192^3 502 against 500, so larger M keeps the pass.
+    const bool csk = AU8 && tm <= 16 && (direct || (BNK && g.K % 64 == 0));
+    // Workspace: [colsum: N int32, 256-byte aligned, unless CSK][B_T: N x K bytes
+    // when B is [K,N] and not read in place]
     GemmArgs h = g;
-    const size_t cs_bytes = AU8 ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
+    const size_t cs_bytes = AU8 && !csk ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
     void *ws = nullptr;
     const size_t need = cs_bytes + (BNK || direct ? 0 : (size_t)g.K * g.N);
     if (g.scratch) {
@@ -1186,11 +1221,24 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
                          "allocation-free maximum of %zu bytes", need, g.M, g.N, g.K,
                          g.scratch_bytes);
       ws = g.scratch;
-    } else {
+    } else if (need) {
       int rc = workspace(st, need, &ws);
       if (rc) return rc;
     }
-    int32_t *colsum = AU8 ? (int32_t *)ws : nullptr;
+    int32_t *colsum = AU8 && !csk ? (int32_t *)ws : nullptr;
+    if (csk) {
+      KernelTimer kt(st, "gemm_i8_dma");
+      if (direct)
+        hipLaunchKernelGGL((gemm_i8_dma<4, true, false, true>), dim3(grid), dim3(512), 0, st,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn,
+                           (const int32_t *)nullptr, vec);
+      else
+        hipLaunchKernelGGL((gemm_i8_dma<4, true, true, true>), dim3(grid), dim3(512), 0, st,
+                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn,
+                           (const int32_t *)nullptr, vec);
+      SIMP_HIP(hipGetLastError());
+      return SIMP_RT_OK;
+    }
     if (direct) {
       if (AU8) {
         constexpr int KT = 64;

@@ -170,6 +170,7 @@ def test_int8_recipe_checksums(dev, orc):
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (8192, 8192, 8192),
                                    (4100, 4112, 4096),    # ragged M, N on the LDS-DMA kernel
+                                   (4000, 4112, 4096),    # the same with in-kernel u8 sums
                                    (4100, 4112, 4000)])   # K % 64 != 0: register-staged kernel
 @pytest.mark.parametrize("variant", ["u8s8", "s8s8", "nt_u8s8", "nt_s8s8"])
 def test_int8_full_size_identities(dev, orc, M, N, K, variant):
@@ -229,18 +230,27 @@ def test_int8_strided_views(dev, orc):
 @pytest.mark.parametrize("M,N,K", [(8192, 8192, 128),     # K-steps < ring stages
                                    (8192, 8192, 512),     # 4 tiles per workgroup
                                    (8192, 4096, 1088),    # odd K-step count
-                                   (4100, 4112, 1024)])   # ragged last tiles
-@pytest.mark.parametrize("variant", ["u8s8", "s8s8"])
+                                   (4100, 4112, 1024),    # ragged last tiles
+                                   (4000, 4112, 1024)])   # u8: column sums in the kernel
+@pytest.mark.parametrize("variant", ["u8s8", "s8s8", "nt_u8s8"])
 def test_int8_persistent_kernel_exact(dev, orc, M, N, K, variant):
     """Every element of the persistent LDS-DMA kernel's output, at sizes where
     workgroups walk several tiles (tile transitions overlap one tile's stores
-    with the next tile's loads), against the oracle."""
+    with the next tile's loads), against the oracle.  Up to 16 tile rows
+    (M <= 4096) the u8 column sums come from the kernel's own MFMAs, which
+    the last shape reaches with ragged tiles and 272 tiles on 256 workgroups
+    (the sums' LDS exchange reused by a second tile); beyond, from a pass
+    over B."""
     import torch
     print(f"[int8-persistent] {variant} M={M} N={N} K={K}", flush=True)
     a, b = _inputs(M, N, K, seed=9)
     if variant == "s8s8":
         a = a.view(np.int8)
-    want, _ = orc.matmul_i8_vnni(a, b, a_unsigned=variant == "u8s8", nthreads=8)
+    want, _ = orc.matmul_i8_vnni(a, b, a_unsigned=variant != "s8s8", nthreads=8)
+    if variant == "nt_u8s8":
+        got = _run(dev, sa.matmul_nt_u8s8_i32, a, np.ascontiguousarray(b.T), M, N)
+        assert np.array_equal(got, want)
+        return
     fn = sa.matmul_u8s8_i32 if variant == "u8s8" else sa.tensor_matmul_i8
     got = _run(dev, fn, a, b, M, N)
     assert np.array_equal(got, want)

@@ -1,11 +1,13 @@
 """simp_rt_matmul_u8s8_i32_noalloc (the allocation-free variant of
 simp_rt_matmul_u8s8_i32, whose large-shape scratch lives in a static device
 array) against simp_rt_matmul_u8s8_i32 itself, bit for bit, through the C ABI:
-two calls in a row that take the large-tile path with B read in place (column
-sums in the static scratch), two that transpose B there (K % 64 != 0: column
-sums and B_T in the scratch), each second call smaller, so it must clear and
-refill what the first left; a small shape (no scratch); and the documented
-rejections (host operands, a scratch need above the maximum)."""
+two calls in a row that take the large-tile path with B read in place and M
+above 4096 (column sums in the static scratch), two that transpose B there
+(K % 64 != 0: column sums and B_T in the scratch), each second call smaller,
+so it must clear and refill what the first left; the large-tile path at
+M = 4096 (column sums inside the GEMM kernel, no scratch) and a small shape (no
+scratch); and the documented rejections (host operands, a scratch need above
+the maximum)."""
 import numpy as np
 import pytest
 
@@ -24,8 +26,9 @@ def _pair(dev, M, N, K, seed):
 
 def test_noalloc_matches_allocating_entry_point(dev):
     import torch
-    for (M, N, K, seed) in ((4096, 4096, 4096, 1), (4096, 4096, 1024, 2),
-                            (4096, 4096, 2064, 4), (4096, 4096, 1040, 5), (256, 320, 192, 3)):
+    for (M, N, K, seed) in ((8192, 4096, 2048, 1), (8192, 2048, 1024, 2),
+                            (4096, 4096, 2064, 4), (4096, 4096, 1040, 5),
+                            (4096, 4096, 1024, 6), (256, 320, 192, 3)):
         print(f"[noalloc] M={M} N={N} K={K}", flush=True)
         a, b = _pair(dev, M, N, K, seed)
         want = torch.empty((M, N), dtype=torch.int32, device=dev)
@@ -36,11 +39,13 @@ def test_noalloc_matches_allocating_entry_point(dev):
         assert torch.equal(got, want), (M, N, K)
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (2048, 3072, 1040), (256, 320, 192)])
+@pytest.mark.parametrize("M,N,K", [(8192, 2048, 1024), (2048, 3072, 1040), (4096, 4096, 1024),
+                                   (256, 320, 192)])
 def test_noalloc_under_graph_capture(dev, M, N, K):
     """The entry point's callers capture it: one call captured in a HIP graph
-    (B read in place, B transposed into the scratch, and a shape with no
-    scratch), replayed three times on new inputs written into the captured
+    (B read in place with the column sums in the scratch, B transposed into the
+    scratch, and two shapes with no scratch: column sums inside the large-tile
+    kernel, and a small shape), replayed three times on new inputs written into the captured
     buffers, with eager library work between the replays (which uses the same
     scratch-free stream workspace); every replay equals the allocating entry
     point bit for bit."""
