@@ -579,11 +579,18 @@ int dispatch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, i
   // With K <= 256 (eight K-stages or fewer) four 64x64 workgroups per CU
   // overlap each other's short K loops: 32 x (512x128x512) 25.1 us against
   // 28.9 on 128x128 tiles (28.1 for gemm_f32_mfma), 8 x (1024x256x1024) 42.5
-  // against 44.2; from K = 512 on the 128x128 tiles stay ahead.
+  // against 44.2; from K = 512 on the 128x128 tiles stay ahead.  From two
+  // 256x128 tiles per CU, 8 waves of 128x32 (half the operand bytes per flop
+  // of the 128x128 tiles): 4096^3 1028 us against 1077, 4096x1024x4096 270
+  // against 281, 8192x2048x8192 2078 against 2168 (128x256 tiles: 1038, 270,
+  // 2096; 64x64 waves: 1039 at 4096^3; three ring slots: 1056).
   const bool ring_ok = K % 32 == 0 && N % 4 == 0 && ldc % 4 == 0 && sc % 4 == 0 && al(C);
   if (ring_ok && K <= 256 && tiles(64, 64) >= cus)
     return launch_ring_f32<64, 64, 2, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
                                                 batch, beta, 4, st);
+  if (ring_ok && tiles(256, 128) >= 2 * cus)
+    return launch_ring_f32<256, 128, 2, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
+                                                  batch, beta, 1, st);
   if (ring_ok && tiles(128, 128) >= cus)
     return launch_ring_f32<128, 128, 4, 4, 2, BT>(A, lda, sa, B, ldb, sb, C, ldc, sc, M, N, K,
                                                   batch, beta, 1, st);

@@ -1,6 +1,6 @@
 """GPU parity of the fp32 tensor_matmul at every shape bench.py's f32_gemm
 section times, so each reported rate is backed by a check of the kernels that
-produce it: the 128x128-tile kernel at 4096^3, the prefill tiles (M = 8, 128,
+produce it: the 256x128-tile ring kernel at 4096^3, the prefill tiles (M = 8, 128,
 512 against 2048-wide operands, M = 8 with K split 16 ways and summed by
 gemm_f32_sum_parts), and the rank-3 batch on grid z.
 

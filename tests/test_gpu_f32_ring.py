@@ -4,7 +4,8 @@ tensor_matmul_nt_f32 and tensor_matmul_nhwc (B_T rows), and the accumulating
 matmul builtin (C += A B at element offsets, ConvertSimpToMemRef.cpp:1794-1920).
 The dispatch takes it for products with K % 32 == 0 and 16-byte aligned rows
 once the tiles cover the chip: with K <= 256 64x64 tiles four workgroups per
-CU, else 128x128 tiles from 256 of them, else 64x64 tiles from 256 of them.
+CU, else 256x128 tiles from 512 of them (8 waves of 128x32), else 128x128
+tiles from 256 of them, else 64x64 tiles from 256 of them.
 Cases cover every form with ragged M and N (rows and columns past the edge load
 clamped addresses and must not be stored), one and two K-stages, and several
 tiles per workgroup (the persistent loop).
@@ -35,9 +36,10 @@ def _rand(rng, *shape):
 # (M, K, N): 64x64 tiles (16x17 = 272 tiles, ragged both ways); one and two
 # K-stages (short K: 64x64 tiles, up to four workgroups per CU); 64x64 tiles
 # two per workgroup (2x510 tiles on 512 workgroups, M ragged); 128x128 tiles
-# ragged (16x17 tiles on 256 workgroups); 128x128 tiles two per workgroup
+# ragged (16x17 tiles on 256 workgroups); 128x128 tiles two per workgroup;
+# 256x128 tiles ragged both ways (16x33 tiles on 256 workgroups, some with three)
 SHAPES = [(1000, 2048, 1028), (1024, 32, 1024), (1088, 64, 1024), (120, 320, 32640),
-          (2000, 320, 2052), (2048, 512, 4096)]
+          (2000, 320, 2052), (2048, 512, 4096), (4000, 320, 4100)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
