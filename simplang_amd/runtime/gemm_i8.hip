@@ -16,13 +16,12 @@
 //   * gemm_i8_dma -- problems of at least one 256x256 tile per CU, K % 64 == 0:
 //     persistent, global -> LDS DMA ring, v_mfma_i32_16x16x64_i8, 16-byte
 //     nontemporal C stores.  B given as [K,N] with 16-byte aligned rows is
-//     read in place and transposed by the LDS reads (ds_read_b64_tr_b8).  The
-//     u8 column sums come from the kernel's own B fragments on the MFMA pipe
-//     up to M = 4096, else from colsum_kn_i8 (colsum_nk_i8 for B_T[N,K]
-//     inputs, which are read as rows), and a [K,N] B the in-place read
-//     cannot serve is first transposed into a workspace B_T (transpose_i8, which
-//     forms the column sums on the way), as the reference materialises B_T
-//     (ConvertSimpToMemRef.cpp:3168-3216).
+//     read in place and transposed by the LDS reads (ds_read_b64_tr_b8);
+//     B_T[N,K] inputs are read as rows.  The u8 column sums come from the
+//     kernel's own B fragments on the MFMA pipe.  A [K,N] B the in-place read
+//     cannot serve is first transposed into a workspace B_T (transpose_i8,
+//     which forms the column sums on the way), as the reference materialises
+//     B_T (ConvertSimpToMemRef.cpp:3168-3216).
 //   * gemm_i8_nt16 -- the same tile sizes for K % 64 != 0 (K % 16 == 0), LDS
 //     double-buffered through registers, on B_T.
 //   * gemm_i8_mfma -- smaller problems and batches (grid z): BMxBN tiles on
@@ -434,7 +433,13 @@ __device__ __forceinline__ v2i lds_read_tr8(const void *lds, uint32_t off) {
 //     Column block cb of k-row k sits at block cb ^ (k & 7) ^ 8 ((k >> 4) & 1),
 //     so the 32 lanes of a half-wave read 32 distinct 8-byte bank pairs.
 //     Columns past N read a clamped in-bounds block; they are never stored.
-template <int STAGES, bool AU8, bool BNK, bool CSK = false>
+// Where gemm_i8_dma's u8 x s8 column sums come from (CSM):
+constexpr int kColsumPass = 0;  // colsum[], from a pass over B before the kernel
+constexpr int kColsumRows = 1;  // the kernel's MFMAs; tiles grouped by tile rows, so a
+                                // workgroup forms the sums for every tile
+constexpr int kColsumOnce = 2;  // the kernel's MFMAs; tiles grouped by tile columns, so a
+                                // workgroup forms them once per column tile it visits
+template <int STAGES, bool AU8, bool BNK, int CSM = kColsumPass>
 __global__ void __launch_bounds__(512)
     gemm_i8_dma(const int8_t *__restrict__ A, int64_t lda, const int8_t *__restrict__ B,
                 int64_t ldb, int32_t *__restrict__ C, int64_t ldc, int M, int N, int K,
@@ -453,18 +458,24 @@ __global__ void __launch_bounds__(512)
   const uint32_t lds_wave = lds_offset(lds) + 2048 * wave;  // wave w fills blocks 2w, 2w+1
   // CS: u8 column sums on the MFMA pipe.  Wave row wy takes its B fragments in
   // the order j ^ jx (jx = 2 wy), so that its fragments 0 and 1, whose column
-  // sums it forms, are columns 2 wy and 2 wy + 1 of the wave's four.
-  constexpr bool CS = AU8 && CSK;
+  // sums it forms, are columns 2 wy and 2 wy + 1 of the wave's four.  The
+  // sums stay in cs_lds for the workgroup's next tile of the same columns.
+  constexpr bool CS = AU8 && CSM != kColsumPass;
   __shared__ v4i cs_lds[CS ? BN / 4 : 1];
   const int jx = CS ? 2 * (wave / WGN) : 0;
   const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  int cs_tn = -1;  // column tile whose sums cs_lds holds
   // [K,N] B: lane l reads k-row 16 (l/16) + (l%16)/2 (+8), swizzle of that row
   const uint32_t boff = (16 * lkc + (lrow >> 1)) * 256 + 8 * (lrow & 1);
   const int bsw = (lrow >> 1) ^ ((lkc & 1) << 3);
 
   for (int vb = blockIdx.x; vb < ntiles; vb += gridDim.x) {
     int tm, tn;
-    tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    // kColsumOnce walks the tiles in groups of 8 tile columns instead of rows,
+    // so that a workgroup's successive tiles share their columns
+    if constexpr (CSM == kColsumOnce) tile_of_block(vb, ntiles, tiles_n, tiles_m, tn, tm);
+    else tile_of_block(vb, ntiles, tiles_m, tiles_n, tm, tn);
+    const bool form_cs = CS && tn != cs_tn;  // uniform over the workgroup
     const int m0 = tm * BM, n0 = tn * BN;
     const int8_t *srcA0 = A + (int64_t)min(m0 + 32 * wave + drow, M - 1) * lda + 16 * dkc;
     const int8_t *srcA1 = A + (int64_t)min(m0 + 32 * wave + 16 + drow, M - 1) * lda + 16 * dkc;
@@ -551,6 +562,14 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
         for (int j = 0; j < FN; j++) fb[cb ^ 1][j] = bfrag(kt + 1, j);
       }
+      // kColsumOnce: the same two MFMAs, on the tiles that form the sums, ahead
+      // of the step's main MFMAs (a branch between those split their schedule)
+      if constexpr (CS && CSM == kColsumOnce) {
+        if (form_cs) {
+          csacc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][0], ones, csacc[0], 0, 0, 0);
+          csacc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][1], ones, csacc[1], 0, 0, 0);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < FM; i++) {
         v4i a = fa[i];
@@ -563,7 +582,7 @@ __global__ void __launch_bounds__(512)
         // CS: B fragments 0 and 1 also meet an all-ones operand, which leaves
         // every lane the sums of its four output columns of those fragments
         // (two more MFMAs per 32 on every wave)
-        if constexpr (CS) {
+        if constexpr (CS && CSM == kColsumRows) {
           if (i == 1 || i == 5) {
             const int t = i == 1 ? 0 : 1;
             csacc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][t], ones, csacc[t], 0, 0, 0);
@@ -577,14 +596,17 @@ __global__ void __launch_bounds__(512)
       step(kt + 1, 1);
     }
     if (kt < nk) step(kt, 0);
-    if constexpr (CS) {
+    if (form_cs) {
       // csacc[t][r] = sum of column wn0 + 16 (t ^ jx) + 4 (l/16) + r; the
-      // other wave row of the same columns holds the other two fragments
+      // other wave row of the same columns holds the other two fragments.
+      // Every wave read the previous sums in cs_lds before this tile's first
+      // barrier.
       if (lrow == 0) {
         cs_lds[(wn0 + 16 * jx) / 4 + lkc] = csacc[0];
         cs_lds[(wn0 + 16 * (1 ^ jx)) / 4 + lkc] = csacc[1];
       }
       __syncthreads();
+      cs_tn = tn;
     }
     // acc[i][j][r] = C[m0 + wm0 + 16 i + l%16][n0 + wn0 + 16 (j ^ jx) + 4 (l/16) + r]
 #pragma unroll
@@ -940,55 +962,6 @@ __global__ void __launch_bounds__(256)
   if (lane == 0) colsum[n] = acc;
 }
 
-// colsum[n] += sum of B[k][n] over the rows k of blockIdx.y's KT-row band, as
-// signed bytes; B as [K,N] with 16-byte aligned rows, N % 16 == 0.  A lane
-// takes 16 columns (one 16-byte load per row, eight rows in flight), a wave
-// 1024 columns, the 8 waves of a workgroup every 8th row of the band; the
-// waves' sums meet in LDS and one atomic per column and workgroup adds them
-// (exact: integer sums).
-template <int KT>
-__global__ void __launch_bounds__(512)
-    colsum_kn_i8(const int8_t *__restrict__ B, int64_t ldb, int32_t *__restrict__ colsum, int K,
-                 int N) {
-  constexpr int NW = 8, U = 8;
-  __shared__ int part[NW][1024];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c0 = blockIdx.x * 1024 + 16 * lane;
-  const int kb = blockIdx.y * KT, ke = min(K, kb + KT);
-  int sum[16];
-#pragma unroll
-  for (int c = 0; c < 16; c++) sum[c] = 0;
-  auto add = [&](const uint4 &v) {
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int c = 0; c < 16; c++)
-      sum[c] = __builtin_amdgcn_sdot4((int)d[c >> 2], 1 << (8 * (c & 3)), sum[c], false);
-  };
-  if (c0 < N) {
-    const int8_t *p = B + c0;
-    int k = kb + wave;
-    for (; k + NW * (U - 1) < ke; k += NW * U) {
-      uint4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) v[u] = *(const uint4 *)(p + (int64_t)(k + NW * u) * ldb);
-#pragma unroll
-      for (int u = 0; u < U; u++) add(v[u]);
-    }
-    for (; k < ke; k += NW) add(*(const uint4 *)(p + (int64_t)k * ldb));
-  }
-#pragma unroll
-  for (int c = 0; c < 16; c++) part[wave][16 * lane + c] = sum[c];
-  __syncthreads();
-#pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int col = 2 * threadIdx.x + q, n = blockIdx.x * 1024 + col;
-    int t = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) t += part[w][col];
-    if (n < N) atomicAdd(colsum + n, t);
-  }
-}
-
 // Skinny product, M <= MR <= 2 rows of A, B as [K,N] (K % 16 == 0, N % 8 == 0,
 // 8-byte aligned rows): a v_dot4_i32_i8 GEMV instead of MFMA tiles.
 //   * Workgroup (g, s) takes columns 512 g .. 512 g + 511 and the K band
@@ -1202,14 +1175,21 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     const int grid = (int)std::max<int64_t>(8, std::min<int64_t>(cus, (int64_t)tm * tn) / 8 * 8);
     // B[K,N] with 16-byte aligned rows is read in place by gemm_i8_dma
     const bool direct = !BNK && g.K % 64 == 0 && g.ldb % 16 == 0 && ((uintptr_t)g.B & 15) == 0;
-    // u8 x s8 column sums inside gemm_i8_dma (CSK) up to 16 tile rows: every
-    // tile row forms its columns' sums again, two more MFMAs per 32 (+4% per
-    // K-step), against a pass over B and its zero fill ahead of the GEMM.
-    // Measured whole calls: 4096^3 73.7 against 81.3 us, 4096x8192x4096 131
-    // against 141; 8192^3 502 against 500, so larger M keeps the pass.
-    const bool csk = AU8 && tm <= 16 && (direct || (BNK && g.K % 64 == 0));
-    // Workspace: [colsum: N int32, 256-byte aligned, unless CSK][B_T: N x K bytes
-    // when B is [K,N] and not read in place]
+    // u8 x s8 column sums inside gemm_i8_dma, on the MFMA pipe (two more MFMAs
+    // per 32 while a workgroup forms them), wherever it reads B directly:
+    //   * up to 16 tile rows, tiles grouped by rows and the sums formed for
+    //     every tile (kColsumRows): whole call 4096^3 71.0-73.7 us against
+    //     74.5-81.3 with a pass over B and its zero fill ahead of the GEMM,
+    //     4096x8192x4096 131 against 141;
+    //   * beyond, tiles grouped by columns, so a workgroup's tiles share their
+    //     columns and it forms the sums once per column tile (kColsumOnce):
+    //     8192^3 476 against 485 us with the pass (every tile: 488),
+    //     8192x4096x8192 263 against 272-276.  (Grouped by columns, s8 x s8
+    //     ran 443 against 449 us at 8192^3; at 4096^3 the row groups stay
+    //     ahead, 71.0 against 72.1 us.)
+    const bool csk = AU8 && (direct || (BNK && g.K % 64 == 0));
+    // Workspace: [colsum: N int32, 256-byte aligned, unless in the kernel][B_T:
+    // N x K bytes when B is [K,N] and not read in place]
     GemmArgs h = g;
     const size_t cs_bytes = AU8 && !csk ? ((size_t)g.N * 4 + 255) / 256 * 256 : 0;
     void *ws = nullptr;
@@ -1226,32 +1206,27 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       if (rc) return rc;
     }
     int32_t *colsum = AU8 && !csk ? (int32_t *)ws : nullptr;
-    if (csk) {
+    if (csk || direct) {
       KernelTimer kt(st, "gemm_i8_dma");
-      if (direct)
-        hipLaunchKernelGGL((gemm_i8_dma<4, true, false, true>), dim3(grid), dim3(512), 0, st,
-                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn,
-                           (const int32_t *)nullptr, vec);
-      else
-        hipLaunchKernelGGL((gemm_i8_dma<4, true, true, true>), dim3(grid), dim3(512), 0, st,
-                           g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn,
-                           (const int32_t *)nullptr, vec);
-      SIMP_HIP(hipGetLastError());
-      return SIMP_RT_OK;
-    }
-    if (direct) {
-      if (AU8) {
-        constexpr int KT = 64;
-        hipLaunchKernelGGL(fill_i32_2d, dim3((unsigned)cdiv(g.N, 256)), dim3(256), 0, st, colsum,
-                           (int64_t)g.N, 1, g.N, (int64_t)0);
-        KernelTimer kt(st, "colsum_kn_i8");
-        hipLaunchKernelGGL(colsum_kn_i8<KT>, dim3((unsigned)cdiv(g.N, 1024), (unsigned)cdiv(g.K, KT)),
-                           dim3(512), 0, st, g.B, g.ldb, colsum, g.K, g.N);
+      auto launch = [&](auto bnk, auto csm) {
+        hipLaunchKernelGGL((gemm_i8_dma<4, AU8, decltype(bnk)::value, decltype(csm)::value>),
+                           dim3(grid), dim3(512), 0, st, g.A, g.lda, g.B, g.ldb, g.C, g.ldc, g.M,
+                           g.N, g.K, tm, tn, (const int32_t *)nullptr, vec);
+      };
+      using Rows = std::integral_constant<int, kColsumRows>;
+      using Once = std::integral_constant<int, kColsumOnce>;
+      using Pass = std::integral_constant<int, kColsumPass>;
+      if (!AU8) {
+        // s8 x s8 (no sums): tiles grouped by columns beyond 16 tile rows
+        if (tm <= 16) launch(std::false_type{}, Pass{});
+        else launch(std::false_type{}, Once{});
+      } else if (direct) {
+        if (tm <= 16) launch(std::false_type{}, Rows{});
+        else launch(std::false_type{}, Once{});
+      } else {
+        if (tm <= 16) launch(std::true_type{}, Rows{});
+        else launch(std::true_type{}, Once{});
       }
-      KernelTimer kt(st, "gemm_i8_dma");
-      hipLaunchKernelGGL((gemm_i8_dma<4, AU8, false>), dim3(grid), dim3(512), 0, st, g.A, g.lda,
-                         g.B, g.ldb, g.C, g.ldc, g.M, g.N, g.K, tm, tn, (const int32_t *)colsum,
-                         vec);
       SIMP_HIP(hipGetLastError());
       return SIMP_RT_OK;
     }

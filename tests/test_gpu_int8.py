@@ -236,11 +236,14 @@ def test_int8_strided_views(dev, orc):
 def test_int8_persistent_kernel_exact(dev, orc, M, N, K, variant):
     """Every element of the persistent LDS-DMA kernel's output, at sizes where
     workgroups walk several tiles (tile transitions overlap one tile's stores
-    with the next tile's loads), against the oracle.  Up to 16 tile rows
-    (M <= 4096) the u8 column sums come from the kernel's own MFMAs, which
-    the last shape reaches with ragged tiles and 272 tiles on 256 workgroups
-    (the sums' LDS exchange reused by a second tile); beyond, from a pass
-    over B."""
+    with the next tile's loads), against the oracle.  The u8 column sums come
+    from the kernel's own MFMAs.  Up to 16 tile rows (M <= 4096) the tiles are
+    grouped by rows and each tile forms them; the last shape reaches that with
+    ragged tiles and 272 tiles on 256 workgroups (the sums' LDS exchange
+    reused by a second tile).  Beyond, the tiles are grouped by columns and a
+    workgroup forms the sums once per column tile it visits: at 8192 x 8192
+    it keeps them for its four tiles, and at 4100 x 4112 some workgroups
+    move to another column tile and form them again."""
     import torch
     print(f"[int8-persistent] {variant} M={M} N={N} K={K}", flush=True)
     a, b = _inputs(M, N, K, seed=9)

@@ -1,13 +1,12 @@
 """simp_rt_matmul_u8s8_i32_noalloc (the allocation-free variant of
 simp_rt_matmul_u8s8_i32, whose large-shape scratch lives in a static device
 array) against simp_rt_matmul_u8s8_i32 itself, bit for bit, through the C ABI:
-two calls in a row that take the large-tile path with B read in place and M
-above 4096 (column sums in the static scratch), two that transpose B there
-(K % 64 != 0: column sums and B_T in the scratch), each second call smaller,
-so it must clear and refill what the first left; the large-tile path at
-M = 4096 (column sums inside the GEMM kernel, no scratch) and a small shape (no
-scratch); and the documented rejections (host operands, a scratch need above
-the maximum)."""
+two calls in a row that transpose B into the scratch (K % 64 != 0: column sums
+and B_T in the scratch), the second smaller, so it must clear and refill what
+the first left; large-tile calls with B read in place, whose column sums the
+GEMM kernel forms itself (no scratch: M = 8192 with tiles grouped by columns,
+M = 4096 by rows); a small shape (no scratch); and the documented rejections
+(host operands, a scratch need above the maximum)."""
 import numpy as np
 import pytest
 
@@ -43,9 +42,10 @@ def test_noalloc_matches_allocating_entry_point(dev):
                                    (256, 320, 192)])
 def test_noalloc_under_graph_capture(dev, M, N, K):
     """The entry point's callers capture it: one call captured in a HIP graph
-    (B read in place with the column sums in the scratch, B transposed into the
-    scratch, and two shapes with no scratch: column sums inside the large-tile
-    kernel, and a small shape), replayed three times on new inputs written into the captured
+    (B transposed into the scratch, and three shapes with no scratch: B read in
+    place with the column sums formed in the large-tile kernel, by column and
+    by row groups of tiles, and a small shape), replayed three times on new
+    inputs written into the captured
     buffers, with eager library work between the replays (which uses the same
     scratch-free stream workspace); every replay equals the allocating entry
     point bit for bit."""
