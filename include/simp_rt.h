@@ -119,11 +119,11 @@ int32_t simp_rt_matmul_nt_u8s8_i32(
  * A, B and C must already be device memory (or inside simp_rt_register'd
  * ranges); host pointers are rejected (SIMP_RT_EINVAL).  Its kernels use a
  * static device array of 64 MiB + 64 KiB per GPU (held until the process ends)
- * for the column sums of B and, where B is not read in place (K % 64 != 0, or
- * rows of B not 16-byte aligned), B transposed: shapes that take the large-tile
- * path need 4*N (rounded up to 256) bytes there, plus K*N when B is transposed;
- * larger requests (e.g. K*N above 64 MiB with K % 64 != 0) are rejected with
- * SIMP_RT_EINVAL.
+ * where the large-tile path cannot read B in place (K % 64 != 0, or rows of B
+ * not 16-byte aligned): B transposed (K*N bytes) and its column sums (4*N,
+ * rounded up to 256).  Where it reads B in place the kernel forms the column
+ * sums itself and the array is not used.  Larger requests (e.g. K*N above
+ * 64 MiB with K % 64 != 0) are rejected with SIMP_RT_EINVAL.
  * All calls on one GPU share that array: calls that overlap on one GPU (other
  * streams or threads) race and must be ordered by the caller.  The device
  * address of each GPU's copy is looked up by simp_rt_init() or by the first
