@@ -549,11 +549,18 @@ __global__ void __launch_bounds__(512)
     // writes land while every wave reads stage kt+1's B fragments, and the whole
     // kernel at 8192^3 measured 3-4% slower (issuing after any row from 1 to 7
     // is within 1% of row 3).
-    auto step = [&](int kt, int cb) {
-      const bool more = kt + 1 < nk;  // stage kt+1 exists
+    // steady (a compile-time flag): stages kt+1 .. kt+STAGES exist, so the
+    // step has no branches on nk.  Those branches split the step's schedule,
+    // and u8's A flips of a row then wait behind the previous row's MFMAs:
+    // u8 8192^3 474-478 us against 480 with them, 8192x4096x8192 262-263
+    // against 266.5.  s8 x s8 (no flips) ran 1-2% slower without them, so it
+    // keeps them.
+    auto step = [&](int kt, int cb, auto steady) {
+      constexpr bool S = decltype(steady)::value;
+      const bool more = S || kt + 1 < nk;  // stage kt+1 exists
       if (more) {
         // issued: stages up to min(kt+STAGES-1, nk-1); stage kt+1 must be done
-        if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * (STAGES - 2)));
+        if (S || kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * (STAGES - 2)));
         else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       }
       __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0);  // this wave's reads of stage kt landed
@@ -578,7 +585,7 @@ __global__ void __launch_bounds__(512)
         for (int j = 0; j < FN; j++)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[cb][j], a, acc[i][j], 0, 0, 0);
         if (more) fa[i] = frag(kt + 1, wm0 / 16 + i);
-        if (i == 3 && kt + STAGES < nk) issue(kt + STAGES);
+        if (i == 3 && (S || kt + STAGES < nk)) issue(kt + STAGES);
         // CS: B fragments 0 and 1 also meet an all-ones operand, which leaves
         // every lane the sums of its four output columns of those fragments
         // (two more MFMAs per 32 on every wave)
@@ -591,11 +598,16 @@ __global__ void __launch_bounds__(512)
       }
     };
     int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-      step(kt, 0);
-      step(kt + 1, 1);
+    using Steady = std::integral_constant<bool, AU8>;
+    for (; kt + 1 + STAGES < nk; kt += 2) {
+      step(kt, 0, Steady{});
+      step(kt + 1, 1, Steady{});
     }
-    if (kt < nk) step(kt, 0);
+    for (; kt + 1 < nk; kt += 2) {
+      step(kt, 0, std::false_type{});
+      step(kt + 1, 1, std::false_type{});
+    }
+    if (kt < nk) step(kt, 0, std::false_type{});
     if (form_cs) {
       // csacc[t][r] = sum of column wn0 + 16 (t ^ jx) + 4 (l/16) + r; the
       // other wave row of the same columns holds the other two fragments.
@@ -1216,7 +1228,7 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
       using Rows = std::integral_constant<int, kColsumRows>;
       using Once = std::integral_constant<int, kColsumOnce>;
       using Pass = std::integral_constant<int, kColsumPass>;
-      if (!AU8) {
+      if constexpr (!AU8) {
         // s8 x s8 (no sums): tiles grouped by columns beyond 16 tile rows
         if (tm <= 16) launch(std::false_type{}, Pass{});
         else launch(std::false_type{}, Once{});

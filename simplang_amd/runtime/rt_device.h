@@ -134,7 +134,9 @@ __device__ __forceinline__ void block_barrier() {
 
 // Maps the hardware workgroup id to a C tile: XCD-contiguous (workgroups are
 // dispatched round-robin over the 8 XCDs), then in groups of 8 tile rows so
-// that co-resident tiles share operand lines in their XCD's L2.
+// that co-resident tiles share operand lines in their XCD's L2.  (int8 GEMM,
+// 256x256 tiles, 8192^3: groups of 4 ran level with 8, groups of 2, 16 and 32
+// 2-5% slower.)
 __device__ __forceinline__ void tile_of_block(int bid, int nb, int tiles_m, int tiles_n,
                                               int &tm, int &tn) {
   const int q = nb >> 3, r = nb & 7, xcd = bid & 7, local = bid >> 3;
