@@ -1274,13 +1274,18 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
   {
     // mid sizes (K % 128 == 0): the ring kernel, 128x128 tiles from about half
     // a tile per CU on, else 64x64 tiles; 8 waves (2 per SIMD) either way.
-    // Ring depth: 2 slots while every workgroup has one tile and K <= 2048, 4
-    // otherwise.  Measured (s8 x s8, graph replay): 768^3 4.55 / 4.79 / 5.05 us
-    // with 2 / 4 / 8 slots, 1024^3 5.36 / 5.66 / 6.23, 2048^3 15.0 / 15.3 (2 /
-    // 4); with K = 3200 or several tiles per workgroup 4 slots win
-    // (64x3200x8640 13.7 / 10.7 / 11.5, 3072^3 54.9 / 49.5).  A deeper
-    // prefetch spreads an XCD's CUs over more operand lines than its L2 keeps;
-    // a shallower one exposes more of the load latency once K is long.
+    // Ring depth (u8 x s8 whole calls, graph replay, 2 against 4 slots):
+    //   * 128x128 tiles: 2 slots at every shape measured: 2048^3 x K = 3200,
+    //     4096, 8192: 22.2 / 24.0, 26.5 / 28.8, 46.8 / 50.4 us; 3072^3 (several
+    //     tiles per workgroup) 56.9 / 60.2; 512x3200x8640 41.1 / 42.4.
+    //   * 64x64 tiles: 2 slots while every workgroup has one tile and K <= 2048
+    //     (768^3 4.55 / 4.79 / 5.05 us with 2 / 4 / 8, 1024^3 5.36 / 5.66 /
+    //     6.23), or K <= 4096 with the chip about full (1024x3200x1024 11.5 /
+    //     12.3, 1024x4096x1024 13.7 / 15.1); else 4 (1024x8192x1024 33.2 /
+    //     26.5, 64x3200x8640 on 135 tiles 14.2 / 12.3).
+    // A deeper prefetch spreads an XCD's CUs over more operand lines than its
+    // L2 keeps; a shallower one exposes the load latency when a CU has the
+    // memory system to itself for longer (long K, part of the chip idle).
     const bool ok = g.batch == 1 && g.K % 128 == 0 && g.N % 16 == 0 && g.ldb % 16 == 0 &&
                     ((uintptr_t)g.B & 15) == 0;
     const int vec = g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
@@ -1298,12 +1303,10 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     using I4 = std::integral_constant<int, 4>;
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;
-    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) {
-      if (g.K <= 2048 && tiles(128, 128) <= cus) return ring(I128(), I2());
-      return ring(I128(), I4());
-    }
+    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) return ring(I128(), I2());
     if (ok && tiles(64, 64) >= cus / 2 && g.M > 32) {
-      if (g.K <= 2048 && tiles(64, 64) <= cus) return ring(I64(), I2());
+      const int64_t t = tiles(64, 64);
+      if (t <= cus && (g.K <= 2048 || (g.K <= 4096 && 4 * t >= 3 * cus))) return ring(I64(), I2());
       return ring(I64(), I4());
     }
   }
