@@ -1303,10 +1303,18 @@ int dispatch(const GemmArgs &g, hipStream_t st) {
     using I4 = std::integral_constant<int, 4>;
     using I64 = std::integral_constant<int, 64>;
     using I128 = std::integral_constant<int, 128>;
-    if (ok && tiles(128, 128) >= cus / 2 && g.M > 64) return ring(I128(), I2());
-    if (ok && tiles(64, 64) >= cus / 2 && g.M > 32) {
-      const int64_t t = tiles(64, 64);
-      if (t <= cus && (g.K <= 2048 || (g.K <= 4096 && 4 * t >= 3 * cus))) return ring(I64(), I2());
+    // 128x128 tiles also where 64x64 ones would need a second round on some
+    // CUs and K is long (96 and 128 x 3200 x 8640: 20.2 and 21.4 us on 68
+    // tiles against 22.4 and 22.7 on 270); 4 slots where the operands stream
+    // from HBM rather than L2 (128x3200x32000: 24.5 against 25.0 us).
+    const int64_t t128 = tiles(128, 128), t64 = tiles(64, 64);
+    if (ok && g.M > 64 && (2 * t128 >= cus || (t64 > cus && 4 * t128 >= cus && g.K >= 3072))) {
+      if ((int64_t)g.K * (g.M + g.N) >= (int64_t(64) << 20)) return ring(I128(), I4());
+      return ring(I128(), I2());
+    }
+    if (ok && 2 * t64 >= cus && g.M > 32) {
+      if (t64 <= cus && (g.K <= 2048 || (g.K <= 4096 && 4 * t64 >= 3 * cus)))
+        return ring(I64(), I2());
       return ring(I64(), I4());
     }
   }

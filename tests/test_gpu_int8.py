@@ -69,13 +69,16 @@ def test_int8_nt_variants_bit_exact(dev, orc, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(1024, 1024, 128), (1024, 1024, 256), (1000, 1040, 1024),
                                    (768, 768, 768), (2048, 2048, 384), (2000, 2064, 1152),
-                                   (1536, 1024, 2048), (2048, 2048, 2560), (1000, 1024, 3200)])
+                                   (1536, 1024, 2048), (2048, 2048, 2560), (1000, 1024, 3200),
+                                   (96, 8640, 3200), (128, 32000, 3200)])
 def test_int8_ring_kernel_bit_exact(dev, orc, M, N, K):
     """Mid sizes with K % 128 == 0 run the ring kernel (64x64 or 128x128 tiles,
     K-stages of 128 through a ring of 2 slots, or of 4 for 64x64 tiles with
-    several tiles per workgroup, part of the chip idle or K > 4096): one stage,
-    fewer stages than slots, both slot counts, several tiles per workgroup,
-    ragged M and N, B as [K,N] and as B_T, u8 and s8 A."""
+    several tiles per workgroup, part of the chip idle or K > 4096, and for
+    128x128 tiles whose operands stream from HBM): one stage, fewer stages
+    than slots, both slot counts on both tile sizes, several tiles per
+    workgroup, 128x128 tiles on part of the chip (M = 96, 68 tiles), ragged M
+    and N, B as [K,N] and as B_T, u8 and s8 A."""
     print(f"[int8-ring] M={M} N={N} K={K}", flush=True)
     a, b = _inputs(M, N, K, seed=13)
     bt = np.ascontiguousarray(b.T)
