@@ -490,17 +490,25 @@ __global__ void __launch_bounds__(kAttnThreads)
 // (4 waves and 64 positions: 8 waves and 128 positions measured 8.4 against
 // 6.4 us per launch at pos 150, one CU moving twice the rows); the grid has
 // exactly the chunks of the step's position range.  Latency is what costs
-// here, so:
-//   * every load is issued first, before pos is known: wave w's 16 positions
-//     t (4 lanes per position, float4 j = sub + 4 i of the head dimension),
-//     q and this token's k, v, and for the V sum V[t][d4] of the wave's 16
-//     positions (lane d4 < head_size / 4); then pos and the RoPE row of pos;
+// here, and the loads' return path of a CU (every lane's bytes, duplicates
+// included), so:
+//   * lane (half, j) owns float4 j of the head dimension and the wave's
+//     positions tw + 2e + half (e < 8): it loads q, this token's k and v and
+//     the RoPE row once, and 16 cache rows (K, V) of 16 bytes.  An earlier
+//     layout with 4 lanes per position loaded q, k and the RoPE row in every
+//     position's lanes, 49 KB per wave against 20 KB here, and its launch
+//     took 1.3 us longer (6.4 against 5.1 us in a 3B-shaped layer graph);
+//   * every load that does not depend on pos is issued first, the RoPE row
+//     after pos;
 //   * rows at or past pos are loaded (clamped to the cache) and never used:
 //     position pos takes this token's k, v, which the first head of each kv
 //     head stores into the cache at pos;
-//   * each wave takes the scores of its positions (4-lane DPP sums), a softmax
-//     over them (m_w, l_w) and the V sum o_w with the probabilities broadcast
-//     from their lanes (v_readlane), all in the VALU;
+//   * the 8 partial dot products of a lane are summed over the 32 lanes of its
+//     half by a transposed butterfly (rows of 16 swapped, DPP row rotations
+//     and mirrors), which leaves position (half, e)'s score in lanes
+//     32 half + 4 e .. + 3; a softmax over the wave's 16 positions (m_w, l_w)
+//     and the V sum o_w (probabilities broadcast by v_readlane, the halves
+//     added by v_permlane32_swap) stay in the VALU;
 //   * one barrier, then the NWV (m_w, l_w, o_w) are combined into the
 //     chunk's (m, l, o).
 // A single chunk (pos < TP) writes out = o / l directly; otherwise (o, m, l)
@@ -518,97 +526,118 @@ __global__ void __launch_bounds__(64 * NWV)
                  const StepState *__restrict__ st, int dim, int kv_dim, int n_heads,
                  int n_kv_heads, int hs, const float2 *__restrict__ rope, int max_splits,
                  int nsplit, int seq_len) {
-  constexpr int KF = 8;   // float4 per lane and position: head_size <= 128
-  constexpr int WP = 16;  // positions per wave
+  constexpr int WP = 16;          // positions per wave
+  constexpr int E = WP / 2;       // positions per lane
   constexpr int TP = WP * NWV;
   __shared__ __align__(16) float4 wo[NWV][32];
   __shared__ float wml[NWV][2];
   const int h = blockIdx.x, s = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, j = lane & 31;
   const int t0 = s * TP, tw = t0 + WP * wave;  // first position of the wave
   const int kvh = h * n_kv_heads / n_heads;
-  const int hs4 = hs >> 2;
-  const int lp = lane >> 2, sub = lane & 3;  // position (of the wave) and quarter of this lane
+  const int hs4 = hs >> 2, kv4 = kv_dim >> 2;
+  const int jj = min(j, hs4 - 1);
   const float4 *kbase = (const float4 *)(kc + kvh * hs), *vbase = (const float4 *)(vc + kvh * hs);
-  const int kv4 = kv_dim >> 2;
   // 1. loads, all before pos
-  float4 kr[KF], qv[KF], kn[KF];
-  {
-    const int t = min(tw + lp, seq_len - 1);
-    const float4 *q4 = (const float4 *)(qkv + h * hs), *k4 = (const float4 *)(qkv + dim + kvh * hs);
+  float4 kr[E], vv[E];
 #pragma unroll
-    for (int i = 0; i < KF; i++) {
-      const int j = min(sub + 4 * i, hs4 - 1);
-      kr[i] = kbase[(int64_t)t * kv4 + j];
-      qv[i] = q4[j];
-      kn[i] = k4[j];
-    }
-  }
-  const int d4 = min(lane, hs4 - 1);
-  float4 vv[WP];
+  for (int e = 0; e < E; e++)
+    kr[e] = kbase[(int64_t)min(tw + 2 * e + half, seq_len - 1) * kv4 + jj];
+  float4 qv = ((const float4 *)(qkv + h * hs))[jj];
+  float4 kn = ((const float4 *)(qkv + dim + kvh * hs))[jj];
+  const float4 vn = ((const float4 *)(qkv + dim + kv_dim + kvh * hs))[jj];
 #pragma unroll
-  for (int e = 0; e < WP; e++) vv[e] = vbase[(int64_t)min(tw + e, seq_len - 1) * kv4 + d4];
-  const float4 vn = ((const float4 *)(qkv + dim + kv_dim + kvh * hs))[d4];
+  for (int e = 0; e < E; e++)
+    vv[e] = vbase[(int64_t)min(tw + 2 * e + half, seq_len - 1) * kv4 + jj];
   const int pos = st->pos;
-  float4 rf[KF];  // (cos, sin) of the two pairs of float4 j at pos
-#pragma unroll
-  for (int i = 0; i < KF; i++) {
-    const int j = min(sub + 4 * i, hs4 - 1);
-    rf[i] = rope ? ((const float4 *)(rope + (int64_t)pos * (hs >> 1)))[j] : make_float4(1.f, 0.f, 1.f, 0.f);
-  }
+  // (cos, sin) of the two pairs of float4 j at pos
+  const float4 rf = rope ? ((const float4 *)(rope + (int64_t)pos * (hs >> 1)))[jj]
+                         : make_float4(1.f, 0.f, 1.f, 0.f);
   // 2. RoPE of q and of this token's k (pairs (x, y) and (z, w) of a float4)
   auto rot = [](float4 a, float4 f) {
     return make_float4(a.x * f.x - a.y * f.y, a.x * f.y + a.y * f.x, a.z * f.z - a.w * f.w,
                        a.z * f.w + a.w * f.z);
   };
-#pragma unroll
-  for (int i = 0; i < KF; i++) {
-    qv[i] = rot(qv[i], rf[i]);
-    kn[i] = rot(kn[i], rf[i]);
-  }
+  qv = rot(qv, rf);
+  kn = rot(kn, rf);
   // the first head of each kv head stores k, v at pos (chunk holding pos)
   const bool writer = (h == 0 || ((h - 1) * n_kv_heads / n_heads) != kvh) && pos >= t0 &&
                       pos < t0 + TP && wave == 0;
-  if (writer) {
-    float4 *krow = (float4 *)(kc + (int64_t)pos * kv_dim + kvh * hs);
-    if (lane < 4)
-#pragma unroll
-      for (int i = 0; i < KF; i++)
-        if (sub + 4 * i < hs4) krow[sub + 4 * i] = kn[i];
-    if (lane < hs4) ((float4 *)(vc + (int64_t)pos * kv_dim + kvh * hs))[lane] = vn;
+  if (writer && half == 0 && j < hs4) {
+    ((float4 *)(kc + (int64_t)pos * kv_dim + kvh * hs))[j] = kn;
+    ((float4 *)(vc + (int64_t)pos * kv_dim + kvh * hs))[j] = vn;
   }
-  // 3. scores of the wave's positions
-  const int t = tw + lp;
-  float sc = 0.f;
+  // 3. scores: this lane's part of the dot product for each of its positions,
+  // then a reduce-scatter over the 32 lanes of the half
+  float v[E];
 #pragma unroll
-  for (int i = 0; i < KF; i++) {
-    if (sub + 4 * i < hs4) {
-      const float4 a = t == pos ? kn[i] : kr[i], b = qv[i];
-      sc = fmaf(a.x, b.x, sc);
-      sc = fmaf(a.y, b.y, sc);
-      sc = fmaf(a.z, b.z, sc);
-      sc = fmaf(a.w, b.w, sc);
-    }
+  for (int e = 0; e < E; e++) {
+    const float4 a = tw + 2 * e + half == pos ? kn : kr[e];
+    float d = a.x * qv.x;
+    d = fmaf(a.y, qv.y, d);
+    d = fmaf(a.z, qv.z, d);
+    d = fmaf(a.w, qv.w, d);
+    v[e] = j < hs4 ? d : 0.f;
   }
-  sc += dpp_mov<kDppXor1>(sc);
+  const bool b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
+  float w4[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {  // lanes 16 apart: bit 4 clear keeps index i, set i + 4
+    float a = v[i], b = v[i + 4];
+    permlane16_swap(a, b);
+    w4[i] = a + b;
+  }
+  float w2[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {  // lanes 8 apart: bit 3 clear keeps i, set i + 2
+    const float a = b3 ? w4[i + 2] : w4[i], b = b3 ? w4[i] : w4[i + 2];
+    w2[i] = a + dpp_mov<kDppRor8>(b);
+  }
+  float sc;
+  {  // lanes l and l ^ 7 (bit 2 differs): bit 2 clear keeps 0, set 1
+    const float a = b2 ? w2[1] : w2[0], b = b2 ? w2[0] : w2[1];
+    sc = a + dpp_mov<kDppHalfMirror>(b);
+  }
+  sc += dpp_mov<kDppXor1>(sc);  // the 4 lanes l ^ {0, 1, 2, 3}: all 32 lanes added
   sc += dpp_mov<kDppXor2>(sc);
-  sc = t <= pos ? sc * (1.f / sqrtf((float)hs)) : -INFINITY;
+  // lanes 32 half + 4 e .. + 3 hold position tw + 2 e + half, e = 4 b4 + 2 b3 + b2
+  const int pl = tw + 2 * ((b4 ? 4 : 0) + (b3 ? 2 : 0) + (b2 ? 1 : 0)) + half;
+  sc = pl <= pos ? sc * (1.f / sqrtf((float)hs)) : -INFINITY;
   // 4. softmax over the wave's positions (each replicated in 4 lanes)
   const float m = wave_max_dpp(sc);
-  const float pe = t <= pos ? expf(sc - m) : 0.f;  // t <= pos: m is finite
-  const float l = wave_sum_dpp(sub == 0 ? pe : 0.f);
-  // 5. V sum: lane d4 over the wave's positions, probabilities from lanes 4e
+  const float pe = pl <= pos ? expf(sc - m) : 0.f;  // pl <= pos: m is finite
+  const float l = wave_sum_dpp((lane & 3) == 0 ? pe : 0.f);
+  // 5. V sum: lane (half, j) over its positions, probabilities from lanes
+  // 32 half + 4 e; the two halves added
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int e = 0; e < WP; e++) {
-    const float pt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 4 * e));
+  for (int e = 0; e < E; e++) {
+    const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 4 * e));
+    const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 32 + 4 * e));
+    const float pt = half ? p1 : p0;
+    const int p = tw + 2 * e + half;
     // rows past pos are selected out, not weighted by 0: the cache beyond
     // the written positions holds whatever the memory held (0 * NaN = NaN)
-    const float4 x = tw + e == pos ? vn : tw + e < pos ? vv[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 x = p == pos ? vn : p < pos ? vv[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     o.x = fmaf(pt, x.x, o.x);
     o.y = fmaf(pt, x.y, o.y);
     o.z = fmaf(pt, x.z, o.z);
     o.w = fmaf(pt, x.w, o.w);
+  }
+  {
+    float a = o.x, b = o.x;
+    permlane32_swap(a, b);
+    o.x = a + b;
+    a = b = o.y;
+    permlane32_swap(a, b);
+    o.y = a + b;
+    a = b = o.z;
+    permlane32_swap(a, b);
+    o.z = a + b;
+    a = b = o.w;
+    permlane32_swap(a, b);
+    o.w = a + b;
   }
   if (lane < hs4) wo[wave][lane] = o;
   if (lane == 0) {
