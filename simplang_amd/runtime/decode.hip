@@ -707,16 +707,15 @@ int64_t attn_ws_floats(int64_t n_heads, int64_t seq_len, int hs) {
 }
 
 // The key for a step at pos: the split kernel alone while one chunk covers the
-// context, then the one-block kernel up to `split_from`, then split + combine
-// (the split kernel needs head_size % 4 == 0 and <= 128).  split_from is where
-// split + combine measured faster on MI355X (26/12 layers, cold caches): for
-// 32 heads of 100 from pos 64 on, for 12 heads of 64 from about 480.  Fewer
-// heads leave the one-block kernel more CUs per head, so it keeps up longer.
+// context, then split + combine (the split kernel needs head_size % 4 == 0 and
+// <= 128; otherwise the one-block kernel).  With the split kernel's
+// lane-per-float4 layout this holds for 12 heads of 64 as well: the 110M
+// decode (positions 0..287) ran 3021-3031 tok/s against 2974 with the
+// one-block kernel up to pos 480, where the earlier split kernel crossed over.
 int attn_key(int64_t pos, bool have_ws, int64_t n_heads) {
+  (void)n_heads;
   if (!have_ws) return 0;
-  if (pos < kAttnTP) return 1;
-  const int64_t split_from = n_heads >= 32 ? kAttnTP : 480;
-  return pos >= split_from ? (int)(pos / kAttnTP + 1) : 0;
+  return (int)(pos / kAttnTP + 1);
 }
 
 // One decode step's attention for one layer (cache rows [seq_len, kv_dim]).

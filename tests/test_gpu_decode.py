@@ -71,9 +71,10 @@ LONG = dict(dim=400, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2, vocab_
 
 @pytest.mark.parametrize("fmt", [0, 1])
 def test_long_context_split_attention(dev, orc, fmt):
-    """Context up to 511 (head size 100 or 96, GQA): from position 192 the step takes
-    the attention split over 64-position chunks; logits at every position of a
-    300-token prompt, then 480 greedy tokens with and without the graph."""
+    """Context up to 511 (head size 100 or 96, GQA): the attention is split over
+    64-position chunks (one chunk alone below position 64, then the chunks and
+    their combine); logits at every position of a 300-token prompt, then 480
+    greedy tokens with and without the graph."""
     cfg = dict(LONG, weight_format=fmt, dim=400 if fmt == 0 else 384)  # head size 100 / 96
     w = make_model(cfg, dev, seed=11 + fmt)
     rng = np.random.default_rng(20 + fmt)
@@ -87,6 +88,27 @@ def test_long_context_split_attention(dev, orc, fmt):
     m.close()
     want, margins = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 480)
     assert np.array_equal(got, got_eager)
+    if not np.array_equal(got, want):
+        i = int(np.argmax(got != want))
+        print("first divergence at", i, "oracle top-2 margin", margins[i - len(prompt)])
+    assert np.array_equal(got, want)
+
+
+def test_one_block_attention_head_size_over_128(dev, orc):
+    """Head size 136 (above the split kernel's 128): every step takes the
+    one-block attention kernel; logits at every position of a 150-token prompt
+    and 100 greedy tokens against the oracle."""
+    cfg = dict(LONG, dim=272, n_heads=2, n_kv_heads=1, seq_len=256)
+    w = make_model(cfg, dev, seed=29)
+    rng = np.random.default_rng(30)
+    print("[decode] head size 136 logits", flush=True)
+    _check_logits(dev, orc, cfg, w, rng.integers(0, cfg["vocab_size"], 150).astype(np.int32))
+    prompt = rng.integers(0, cfg["vocab_size"], 8).astype(np.int32)
+    m = sa.Llama(cfg, w)
+    print("[decode] head size 136 greedy", flush=True)
+    got = m.generate(prompt, 100, use_graph=True)
+    m.close()
+    want, margins = _oracle_greedy(orc, cfg, to_numpy(w), prompt, 100)
     if not np.array_equal(got, want):
         i = int(np.argmax(got != want))
         print("first divergence at", i, "oracle top-2 margin", margins[i - len(prompt)])
