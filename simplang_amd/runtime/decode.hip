@@ -37,7 +37,9 @@ namespace {
 
 constexpr int kMaxSeg = 3;
 
-enum Prologue { kPlain = 0, kRmsNorm = 1 };
+// GEMV input prologues: x as given, RMSNorm of x, or x combined from split-
+// attention partials (fp32 GEMV; the dot8 W4 kernel has its own CMB form).
+enum Prologue { kPlain = 0, kRmsNorm = 1, kCombine = 2 };
 // GEMV output modes: store, accumulate into the output (residual add), or
 // paired rows: row i of segment 0 (W1) and of segment 1 (W3) are computed
 // together and segment 0's output receives silu(h1[i]) * h3[i].
@@ -59,6 +61,14 @@ struct Segs {
 // Step state on the device: [0] token, [1] pos, [2] n_prompt, [3] n_total.
 struct StepState {
   int token, pos, n_prompt, n_total;
+};
+
+// Split-attention partials that a GEMV combines into its x (launch_attention
+// with combine false): n chunks of max_splits per head of hs, each hs floats
+// of o, then m and l (a stride of hs + 4 floats).
+struct Partials {
+  const float *ws;
+  int hs, max_splits, n;
 };
 
 __device__ __forceinline__ float silu_mul(float h1, float h3) {
@@ -103,6 +113,53 @@ struct XStage {
   }
 };
 
+// The kCombine prologue: x[i] from the split-attention partials of i's head,
+// in attn_combine_k's arithmetic (M = max_s m_s, L = sum_s e^(m_s - M) l_s,
+// x = (sum_s e^(m_s - M) o_s) / L), for at most CR chunks.  load() requests
+// every chunk's o of the thread's elements and their heads' (m, l) at once;
+// finish() combines in registers.
+template <int KP>
+struct XStageCmb {
+  static constexpr int CR = 8;
+  float o[KP][CR];
+  float2 ml[KP][CR];
+  __device__ __forceinline__ void load(const Partials &cp, int K) {
+    const int st = cp.hs + 4;
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+      const int i = min((int)threadIdx.x + 256 * k, K - 1);
+      const int h = i / cp.hs;
+      const float *w = cp.ws + (int64_t)h * cp.max_splits * st;
+#pragma unroll
+      for (int s = 0; s < CR; s++) {
+        o[k][s] = s < cp.n ? w[s * st + (i - h * cp.hs)] : 0.f;
+        ml[k][s] = s < cp.n ? *(const float2 *)(w + s * st + cp.hs) : make_float2(-INFINITY, 0.f);
+      }
+    }
+  }
+  template <class Put>
+  __device__ __forceinline__ void finish(const Partials &cp, int K, Put put) {
+#pragma unroll
+    for (int k = 0; k < KP; k++) {
+      const int i = (int)threadIdx.x + 256 * k;
+      if (i >= K) continue;
+      float M = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < CR; s++)
+        if (s < cp.n) M = fmaxf(M, ml[k][s].x);
+      float L = 0.f, v = 0.f;
+#pragma unroll
+      for (int s = 0; s < CR; s++)
+        if (s < cp.n) {
+          const float e = expf(ml[k][s].x - M);
+          L += e * ml[k][s].y;
+          v = fmaf(e, o[k][s], v);
+        }
+      put(i, v * (1.f / L));
+    }
+  }
+};
+
 __device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
   int i = 0;
   while (i + 1 < sg.n && row >= sg.s[i].rows) {
@@ -121,7 +178,7 @@ __device__ __forceinline__ const Seg &seg_of_row(const Segs &sg, int &row) {
 template <int PRO, int OUT, int J, int KP>
 __global__ void __launch_bounds__(256)
     dgemv_f32(Segs sg, int total_rows, int K, const float *__restrict__ x0,
-              const float *__restrict__ nw, float eps) {
+              const float *__restrict__ nw, float eps, Partials cp) {
   constexpr int NR = OUT == kPairSwiGLU ? 2 : 1;  // weight rows per output row
   extern __shared__ float xs[];
   __shared__ float scratch[16];
@@ -149,10 +206,17 @@ __global__ void __launch_bounds__(256)
       }
     }
   };
-  XStage<PRO, KP> xst;
-  xst.load(x0, nw, K);                         // input loads first ...
-  if (J > 0 && r < total_rows) load(r, a);     // ... then the first row's weights
-  xst.finish(K, eps, scratch, [&](int i, float v) { xs[i] = v; });
+  if constexpr (PRO == kCombine) {
+    XStageCmb<KP> xst;
+    xst.load(cp, K);                           // partials first ...
+    if (J > 0 && r < total_rows) load(r, a);   // ... then the first row's weights
+    xst.finish(cp, K, [&](int i, float v) { xs[i] = v; });
+  } else {
+    XStage<PRO, KP> xst;
+    xst.load(x0, nw, K);                       // input loads first ...
+    if (J > 0 && r < total_rows) load(r, a);   // ... then the first row's weights
+    xst.finish(K, eps, scratch, [&](int i, float v) { xs[i] = v; });
+  }
   lds_barrier();
   for (; r < total_rows; r += nw_total) {
     float s[NR];
@@ -864,24 +928,24 @@ struct GemvCtx {
   hipStream_t st;
 };
 
-// Split-attention partials that a GEMV combines into its x (launch_attention
-// with combine false): n chunks of max_splits per head of hs.
-struct Partials {
-  const float *ws;
-  int hs, max_splits, n;
-};
 
 // Whether the Wo GEMV of a step with attention key `attn` takes the partials
-// (the dot8 kernel; the other GEMVs read the combine kernel's output).  Every
-// Wo block reads all chunks of every head, so the fold stops paying past four
-// chunks (positions >= 256): measured on the 3B W4 decode at three chunks,
-// Wo 5.0 -> 6.9 us against the 4.0 us combine kernel it replaces.
-// The fold also needs what the kernel's prologue assumes: one thread per head
-// (at most 256 heads, the smallest block) and whole float4 groups per head;
-// any other step takes the separate attn_combine_k launch.
+// (the other GEMVs read the combine kernel's output).  Every Wo block reads
+// all chunks of every head:
+//   * W4 (the dot8 kernel): the fold stops paying past four chunks (positions
+//     >= 256); measured on the 3B W4 decode at three chunks, Wo 5.0 -> 6.9 us
+//     against the 4.0 us combine kernel it replaces.  It also needs what the
+//     kernel's prologue assumes: one thread per head (at most 256 heads, the
+//     smallest block) and whole float4 groups per head.
+//   * fp32 (dgemv_f32's kCombine prologue): dim <= 1024 (four elements per
+//     thread) and up to eight chunks (positions < 512).  110M decode: 3110
+//     tok/s against 3010-3031 with the combine kernel (and 2934 with a
+//     prologue that read the heads' (m, l) chunk by chunk after the weights).
+// Any other step takes the separate attn_combine_k launch.
 bool fold_combine(int fmt, int gs, int attn, int K, int hs, const float *x0) {
-  return attn > 1 && attn <= 4 && fmt != SIMP_RT_W_F32 && hs > 0 && hs % 4 == 0 && K % hs == 0 &&
-         K / hs <= 256 && w4d8_supported(K, gs, x0, nullptr);
+  if (attn <= 1 || hs <= 0 || hs % 4 != 0 || K % hs != 0) return false;
+  if (fmt == SIMP_RT_W_F32) return attn <= 8 && K <= 1024;
+  return attn <= 4 && K / hs <= 256 && w4d8_supported(K, gs, x0, nullptr);
 }
 
 // out_mode kPairSwiGLU: segments 0 and 1 are W1 and W3 (same rows), the
@@ -889,8 +953,10 @@ bool fold_combine(int fmt, int gs, int attn, int K, int hs, const float *x0) {
 // fold_combine holds).
 int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x0, const float *nw,
          const Partials *cp = nullptr) {
-  if (cp && (c.fmt == SIMP_RT_W_F32 || !w4d8_supported(K, c.gs, x0, nullptr)))
-    return set_error(SIMP_RT_EINVAL, "step GEMV: attention partials need the dot8 kernel");
+  if (cp && (c.fmt == SIMP_RT_W_F32 ? K > 1024 : !w4d8_supported(K, c.gs, x0, nullptr)))
+    return set_error(SIMP_RT_EINVAL,
+                     "step GEMV: attention partials need the dot8 kernel or fp32 with K <= 1024");
+  const Partials pc = cp ? *cp : Partials{nullptr, 1, 1, 0};
   const float eps = c.eps;
   hipStream_t st = c.st;
   const bool pair = out_mode == kPairSwiGLU;
@@ -901,7 +967,7 @@ int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x
     const unsigned grid = (unsigned)std::min<int64_t>(cdiv(total, 4), (int64_t)num_cus() * 8);
     const size_t shm = sizeof(float) * (size_t)K;
     const int J = (int)cdiv(K / 4, 64);
-#define DGJ(P, O, JV, KPV) hipLaunchKernelGGL((dgemv_f32<P, O, JV, KPV>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, nw, eps)
+#define DGJ(P, O, JV, KPV) hipLaunchKernelGGL((dgemv_f32<P, O, JV, KPV>), dim3(grid), dim3(256), shm, st, sg, total, K, x0, nw, eps, pc)
 // (paired rows hold two rows of weights per wave: the 16-slot variant is left
 // to the loop form there)
 #define DG(P, O)                                              \
@@ -911,7 +977,8 @@ int gemv(const GemvCtx &c, Segs sg, int K, int pro, int out_mode, const float *x
     else if (J <= 16 && O != kPairSwiGLU) DGJ(P, O, 16, 16);  \
     else DGJ(P, O, 0, 36);                                    \
   } while (0)
-    if (pro == kRmsNorm) { if (pair) DG(kRmsNorm, kPairSwiGLU); else DG(kRmsNorm, kStore); }
+    if (cp) DGJ(kCombine, kAccum, 4, 4);  // K <= 1024: J <= 4
+    else if (pro == kRmsNorm) { if (pair) DG(kRmsNorm, kPairSwiGLU); else DG(kRmsNorm, kStore); }
     else { if (out_mode == kAccum) DG(kPlain, kAccum); else DG(kPlain, kStore); }
 #undef DG
 #undef DGJ
