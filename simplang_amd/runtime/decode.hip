@@ -258,7 +258,7 @@ __global__ void __launch_bounds__(256)
       }
     }
 #pragma unroll
-    for (int e = 0; e < NR; e++) s[e] = wave_sum(s[e]);
+    for (int e = 0; e < NR; e++) s[e] = wave_sum_dpp(s[e]);
     if (lane == 0) {
       int row = r;
       const Seg &sgm = OUT == kPairSwiGLU ? sg.s[0] : seg_of_row(sg, row);
