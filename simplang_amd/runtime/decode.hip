@@ -98,7 +98,7 @@ struct XStage {
       float ss = 0.f;
 #pragma unroll
       for (int k = 0; k < KP; k++) ss = fmaf(a[k], a[k], ss);
-      ss = block_sum_lds(ss, scratch);  // weight loads issued before stay in flight
+      ss = block_sum_lds<true>(ss, scratch);  // weight loads issued before stay in flight
       rms = sqrtf(ss / (float)K + eps);
     }
 #pragma unroll

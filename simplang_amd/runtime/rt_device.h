@@ -151,9 +151,13 @@ __device__ __forceinline__ void tile_of_block(int bid, int nb, int tiles_m, int 
 }
 
 // block_sum through LDS with lds_barrier(): global loads stay in flight.
+// DPP: the wave sums by DPP and permlane swaps (VALU only) instead of
+// __shfl_xor; a different summation order, so each caller keeps the one its
+// tests pin.
+template <bool DPP = false>
 __device__ __forceinline__ float block_sum_lds(float v, float *scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  v = wave_sum(v);
+  v = DPP ? wave_sum_dpp(v) : wave_sum(v);
   lds_barrier();  // scratch may still be read by a previous call
   if (lane == 0) scratch[wave] = v;
   lds_barrier();
