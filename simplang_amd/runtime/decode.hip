@@ -842,11 +842,30 @@ __global__ void __launch_bounds__(256)
 // The parallel form: per-thread strict-'>' scans from -inf (NaN never taken),
 // ties to the lower index across threads, then 0 when logits[0] is NaN or no
 // thread found a value above -inf (the maximum is then logits[0] = -inf).
+// The step state, logits[0] and the prompt token of pos + 1 are requested
+// before the scan (they are what the last thread's decision waits on), and the
+// cross-lane steps are DPP and permlane moves.
+__device__ __forceinline__ void argmax_pair(float &best, int &idx, float ov, int oi) {
+  if (ov > best || (ov == best && oi < idx)) {
+    best = ov;
+    idx = oi;
+  }
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float &best, int &idx) {
+  const float ov = dpp_mov<CTRL>(best);
+  const int oi = __builtin_amdgcn_mov_dpp(idx, CTRL, 0xF, 0xF, false);
+  argmax_pair(best, idx, ov, oi);
+}
 __global__ void __launch_bounds__(1024)
     argmax_advance_k(const float *__restrict__ logits, int vocab, StepState *st,
                      const int *__restrict__ prompt, int *__restrict__ out_tokens) {
   __shared__ float bv[16];
   __shared__ int bi[16];
+  const int pos0 = st->pos, n_prompt = st->n_prompt, n_total = st->n_total;
+  const float l0 = logits[0];
+  const int p = pos0 + 1;
+  const int ptok = p < n_prompt ? prompt[p] : 0;
   float best = -INFINITY;
   int idx = 0x7fffffff;
   // each thread scans its elements in increasing index order (strict '>' keeps
@@ -873,24 +892,35 @@ __global__ void __launch_bounds__(1024)
     const float v = logits[i];
     if (v > best) { best = v; idx = i; }  // strictly greater: first max per thread
   }
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float ov = __shfl_xor(best, d);
-    const int oi = __shfl_xor(idx, d);
-    if (ov > best || (ov == best && oi < idx)) { best = ov; idx = oi; }
-  }
+  // across the wave (each step pairs every lane with one partner, and the
+  // pair rule is symmetric, so both end with the same (best, idx))
+  argmax_dpp<kDppXor1>(best, idx);
+  argmax_dpp<kDppXor2>(best, idx);
+  argmax_dpp<kDppHalfMirror>(best, idx);
+  argmax_dpp<kDppMirror>(best, idx);
+  // rows of 16, then halves of 32: each swap leaves this lane's pair and its
+  // partner's in (a, b) in some order
+  auto swap_step = [&](auto swapfn) {
+    float a = best, b = best, ai = __int_as_float(idx), bi2 = ai;
+    swapfn(a, b);
+    swapfn(ai, bi2);
+    int ni = __float_as_int(ai);
+    argmax_pair(a, ni, b, __float_as_int(bi2));
+    best = a;
+    idx = ni;
+  };
+  swap_step([](float &a, float &b) { permlane16_swap(a, b); });
+  swap_step([](float &a, float &b) { permlane32_swap(a, b); });
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
   __syncthreads();
   if (threadIdx.x == 0) {
     float b0 = bv[0];
     int i0 = bi[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
-      if (bv[w] > b0 || (bv[w] == b0 && bi[w] < i0)) { b0 = bv[w]; i0 = bi[w]; }
-    const float l0 = logits[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_pair(b0, i0, bv[w], bi[w]);
     if (l0 != l0 || i0 >= vocab) i0 = 0;
-    const int p = st->pos + 1;
-    const int next = (p < st->n_prompt) ? prompt[p] : i0;
-    if (p < st->n_total) out_tokens[p] = next;
+    const int next = (p < n_prompt) ? ptok : i0;
+    if (p < n_total) out_tokens[p] = next;
     st->token = next;
     st->pos = p;
   }
