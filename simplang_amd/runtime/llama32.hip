@@ -64,10 +64,24 @@ __device__ __forceinline__ int32_t dot16(uint4 a, uint4 b, int32_t acc) {
   return acc;
 }
 
+// Sum over the wave, every lane gets it: DPP quad and row moves, then the
+// rows and halves swapped by v_permlane{16,32}_swap (VALU only; integer sums,
+// so the order does not matter).
+template <int CTRL>
+__device__ __forceinline__ int32_t idpp(int32_t v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
 __device__ __forceinline__ int32_t wave_isum(int32_t v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
-  return v;
+  v += idpp<kDppXor1>(v);
+  v += idpp<kDppXor2>(v);
+  v += idpp<kDppHalfMirror>(v);
+  v += idpp<kDppMirror>(v);
+  float a = __int_as_float(v), b = a;
+  permlane16_swap(a, b);
+  v = __float_as_int(a) + __float_as_int(b);
+  a = b = __int_as_float(v);
+  permlane32_swap(a, b);
+  return __float_as_int(a) + __float_as_int(b);
 }
 
 // x = (float)x_i8 (:79-83)
