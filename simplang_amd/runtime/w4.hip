@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(256)
     for (int i = 0; i < XE; i++) {
       const int m = wave + 4 * i;
       const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-      const float mx = wave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      const float mx = wave_max_dpp(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
       int ex = 0;
       if (mx > 16384.f) frexpf(mx * (1.f / 16384.f), &ex);  // mx / 2^ex < 16384
       const float down = ldexpf(1.f, -ex);
@@ -399,10 +399,12 @@ __global__ void __launch_bounds__(256)
       }
       __builtin_memcpy(&xh[m][4 * lane], h, 8);
       __builtin_memcpy(&xl[m][4 * lane], l, 8);
+      // sum over the 8 lanes of a group: quads, then quad with quad (the half
+      // mirror pairs lane i with 7 - i, the same two quad sums as lane ^ 4)
       float t = (v[0] + v[1]) + (v[2] + v[3]);
-      t += __shfl_xor(t, 1);
-      t += __shfl_xor(t, 2);
-      t += __shfl_xor(t, 4);
+      t += dpp_mov<kDppXor1>(t);
+      t += dpp_mov<kDppXor2>(t);
+      t += dpp_mov<kDppHalfMirror>(t);
       if ((lane & 7) == 0) xs[m][lane >> 3] = t;
       if (lane == 0) fm[m] = ldexpf(1.f, 24 + ex);
     }
