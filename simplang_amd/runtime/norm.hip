@@ -20,32 +20,86 @@
 namespace simp {
 namespace {
 
-__global__ void __launch_bounds__(1024)
-    rmsnorm_k(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ out,
-              int n, float eps) {
+// Single-block forms: thread t keeps elements t + k T (k < R) in registers, so
+// x (and w) are read once, all before the block reductions (DPP within a wave,
+// LDS across waves; loads of w stay in flight across them), and out is
+// written once.  Every read precedes the first barrier, so out may alias x.
+template <int T, int R>
+__global__ void __launch_bounds__(T)
+    rmsnorm_k(const float *__restrict__ x, const float *__restrict__ w, float *out, int n,
+              float eps) {
   __shared__ float scratch[16];
+  float xv[R], wv[R];
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int i = threadIdx.x + k * T;
+    xv[k] = i < n ? x[i] : 0.f;
+    wv[k] = i < n ? w[i] : 0.f;
+  }
   float ss = 0.f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) ss = fmaf(x[i], x[i], ss);
-  ss = block_sum(ss, scratch);
+#pragma unroll
+  for (int k = 0; k < R; k++) ss = fmaf(xv[k], xv[k], ss);
+  ss = block_sum_lds<true>(ss, scratch);
   const float rms = sqrtf(ss / (float)n + eps);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] / rms) * w[i];
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int i = threadIdx.x + k * T;
+    if (i < n) out[i] = (xv[k] / rms) * wv[k];
+  }
 }
 
-__global__ void __launch_bounds__(1024)
-    softmax_k(const float *__restrict__ x, float *__restrict__ out, int n) {
+template <int T, int R>
+__global__ void __launch_bounds__(T) softmax_k(const float *__restrict__ x, float *out, int n) {
   __shared__ float scratch[16];
+  float v[R];
   float mx = -INFINITY;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) mx = fmaxf(mx, x[i]);
-  mx = block_max(mx, scratch);
-  float s = 0.f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const float e = expf(x[i] - mx);
-    out[i] = e;
-    s += e;
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int i = threadIdx.x + k * T;
+    v[k] = i < n ? x[i] : -INFINITY;
+    mx = fmaxf(mx, v[k]);
   }
-  s = block_sum(s, scratch);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = out[i] / s;
+  mx = block_max_lds<true>(mx, scratch);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    if (threadIdx.x + k * T < n) {
+      v[k] = expf(v[k] - mx);
+      s += v[k];
+    }
+  }
+  s = block_sum_lds<true>(s, scratch);
+#pragma unroll
+  for (int k = 0; k < R; k++) {
+    const int i = threadIdx.x + k * T;
+    if (i < n) out[i] = v[k] / s;
+  }
 }
+
+// Launches the single-block form whose T x R covers n (n < 32768).
+template <template <int, int> class K, typename... Args>
+void launch_one_block(int n, hipStream_t st, Args... args) {
+  auto go = [&](auto t, auto r) {
+    constexpr int T = decltype(t)::value, R = decltype(r)::value;
+    hipLaunchKernelGGL((K<T, R>::fn), dim3(1), dim3(T), 0, st, args...);
+  };
+  using I256 = std::integral_constant<int, 256>;
+  using I1024 = std::integral_constant<int, 1024>;
+  if (n <= 256) go(I256{}, std::integral_constant<int, 1>{});
+  else if (n <= 1024) go(I256{}, std::integral_constant<int, 4>{});
+  else if (n <= 4096) go(I256{}, std::integral_constant<int, 16>{});
+  else if (n <= 8192) go(I1024{}, std::integral_constant<int, 8>{});
+  else if (n <= 16384) go(I1024{}, std::integral_constant<int, 16>{});
+  else go(I1024{}, std::integral_constant<int, 32>{});
+}
+template <int T, int R>
+struct RmsnormOne {
+  static constexpr auto fn = rmsnorm_k<T, R>;
+};
+template <int T, int R>
+struct SoftmaxOne {
+  static constexpr auto fn = softmax_k<T, R>;
+};
 
 __global__ void __launch_bounds__(256) silu_k(const float *__restrict__ x, float *__restrict__ out,
                                               int64_t n) {
@@ -161,25 +215,28 @@ __global__ void __launch_bounds__(256)
   });
 }
 
+// One read of the slice: every thread keeps a running maximum m and the sum l
+// of e^(x - m), rescaling l when m grows (once per float4 at most).
 __global__ void __launch_bounds__(256)
     softmax_parts_k(const float *__restrict__ x, int64_t n, float2 *__restrict__ part, bool vec) {
   __shared__ float scratch[16];
   int64_t b0, b1;
   slice_of(n, &b0, &b1);
-  float mx = -INFINITY;
+  float m = -INFINITY, l = 0.f;
   for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
-    mx = fmaxf(mx, v.x);
-    if (i >= 0) mx = fmaxf(mx, fmaxf(v.y, fmaxf(v.z, v.w)));
+    const float m4 = i >= 0 ? fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)) : v.x;
+    if (m4 > m) {
+      l *= expf(m - m4);  // e^-inf = 0 on the first finite value
+      m = m4;
+    }
+    if (m > -INFINITY) {
+      l += expf(v.x - m);
+      if (i >= 0) l += (expf(v.y - m) + expf(v.z - m)) + expf(v.w - m);
+    }
   });
-  mx = block_max(mx, scratch);
-  float s = 0.f;
-  if (mx > -INFINITY)
-    for_slice4(x, b0, b1, vec, [&](int64_t i, float4 v) {
-      s += expf(v.x - mx);
-      if (i >= 0) s += (expf(v.y - mx) + expf(v.z - mx)) + expf(v.w - mx);
-    });
-  s = block_sum(s, scratch);
-  if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mx, s);
+  const float mx = block_max_lds<true>(m, scratch);
+  const float t = block_sum_lds<true>(m > -INFINITY ? l * expf(m - mx) : 0.f, scratch);
+  if (threadIdx.x == 0) part[blockIdx.x] = make_float2(mx, t);
 }
 
 __global__ void __launch_bounds__(256)
@@ -243,7 +300,7 @@ int launch_rmsnorm(const float *x, const float *w, float *out, int n, float eps,
     hipLaunchKernelGGL(rmsnorm_apply_k, dim3(g), dim3(256), 0, st, x, w, out, (int64_t)n, eps,
                        (const float *)part, vec);
   } else {
-    hipLaunchKernelGGL(rmsnorm_k, dim3(1), dim3(1024), 0, st, x, w, out, n, eps);
+    launch_one_block<RmsnormOne>(n, st, x, w, out, n, eps);
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;
@@ -309,8 +366,8 @@ int32_t simp_rt_softmax(const float *in_alloc, const float *in, int64_t in_doff,
     hipLaunchKernelGGL(softmax_apply_k, dim3(g), dim3(256), 0, st, (const float *)oi.dev(),
                        (float *)oo.dev(), (int64_t)size, (const float2 *)part, vec);
   } else {
-    hipLaunchKernelGGL(softmax_k, dim3(1), dim3(1024), 0, st, (const float *)oi.dev(),
-                       (float *)oo.dev(), (int)size);
+    launch_one_block<SoftmaxOne>((int)size, st, (const float *)oi.dev(), (float *)oo.dev(),
+                                 (int)size);
   }
   SIMP_HIP(hipGetLastError());
   Operand *ops[] = {&oi, &oo};

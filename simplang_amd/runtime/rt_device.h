@@ -165,6 +165,17 @@ __device__ __forceinline__ float block_sum_lds(float v, float *scratch) {
   for (int i = 0; i < nw; i++) t += scratch[i];
   return t;
 }
+template <bool DPP = false>
+__device__ __forceinline__ float block_max_lds(float v, float *scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = DPP ? wave_max_dpp(v) : wave_max(v);
+  lds_barrier();
+  if (lane == 0) scratch[wave] = v;
+  lds_barrier();
+  float t = scratch[0];
+  for (int i = 1; i < nw; i++) t = fmaxf(t, scratch[i]);
+  return t;
+}
 
 // Block-wide sum for blockDim.x <= 1024 (multiple of 64); every thread gets the
 // result.  `scratch` holds at least 16 floats of LDS; it is reused on return.

@@ -37,8 +37,10 @@ def test_rmsnorm_kat(dev):
     assert abs(out[0].item() - want) < 1e-4       # test_rmsnorm_host.cpp:34-48
 
 
-@pytest.mark.parametrize("dim", [768, 3200, 8640, 5])
+@pytest.mark.parametrize("dim", [768, 3200, 8640, 5, 257, 6000, 20000])
 def test_rmsnorm_vs_oracle(dev, orc, dim):
+    """Each register-tile shape of the single-block form (up to 256, 1024,
+    4096, 8192, 16384 and 32767 elements)."""
     import torch
     rng = np.random.default_rng(dim)
     x = rng.standard_normal(dim).astype(np.float32)
@@ -76,6 +78,24 @@ def test_rmsnorm_two_pass_vs_oracle(dev, orc, dim):
 
 # ----------------------------------------------------------------- softmax --
 
+@pytest.mark.parametrize("dim", [700, 3200, 20000])
+def test_rmsnorm_softmax_in_place(dev, orc, dim):
+    """out == x: the single-block forms read every element before their first
+    barrier."""
+    import torch
+    rng = np.random.default_rng(dim + 1)
+    x = rng.standard_normal(dim).astype(np.float32)
+    w = rng.standard_normal(dim).astype(np.float32)
+    xt = _t(dev, x)
+    sa.rmsnorm(xt, _t(dev, w), xt, dim, 1e-5, 0)
+    torch.cuda.synchronize()
+    _close(xt.cpu().numpy(), orc.rmsnorm(x, w, 1e-5, 0))
+    xt = _t(dev, x * 4)
+    sa.softmax(xt, xt, dim)
+    torch.cuda.synchronize()
+    _close(xt.cpu().numpy(), orc.softmax(x * 4, np.zeros(dim, np.float32), dim, 0, 0))
+
+
 def test_softmax_kat(dev):
     import torch
     out = torch.zeros(4, device=dev)
@@ -84,11 +104,11 @@ def test_softmax_kat(dev):
     assert abs(out[0].item() - e[0] / e.sum()) < 1e-4     # test_softmax_host.cpp:34-45
 
 
-@pytest.mark.parametrize("n", [1, 7, 33, 288, 512, 4096])
+@pytest.mark.parametrize("n", [1, 7, 33, 288, 512, 4096, 6000, 12000, 30000])
 def test_softmax_offsets_vs_oracle(dev, orc, n):
     import torch
     rng = np.random.default_rng(n)
-    seq, h = 600 if n <= 512 else 4200, 3
+    seq, h = 600 if n <= 512 else n + 104, 3
     att = rng.standard_normal(4 * seq).astype(np.float32) * 4   # [n_heads, seq_len]
     out = torch.full((4 * seq,), -1.0, device=dev)
     off = h * seq
