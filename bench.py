@@ -233,10 +233,11 @@ def norm_bench(dev, stream, with_cpu=True):
     sizes (768 and 3200 dims, 2048 and 8640 FFN widths, 288 and 512 attention
     rows), where a launch's latency is the cost, and at 2^24 elements (64 MB
     vectors, the two-pass multi-block forms), where HBM is: GPU time by HIP-graph
-    replay of back-to-back launches, GB/s over the algorithmic bytes (12n, 8n,
-    8n: each input read once, the output written once; the two-pass forms read
-    x twice), and the oracle's restatement of the reference loop on one host
-    core."""
+    replay of back-to-back launches, GB/s over the algorithmic bytes of the
+    reference loops (12n; 16n for softmax's read, write, re-read and write;
+    8n), and the oracle's restatement of the reference loop on one host core.
+    The kernels move 12n, 8n and 8n up to 32767 elements and 16n, 12n and 8n
+    in the two-pass forms beyond (x read twice)."""
     import numpy as np
     import torch
     import simplang_amd as sa
@@ -263,7 +264,7 @@ def norm_bench(dev, stream, with_cpu=True):
             cpu = lambda xh=x.cpu().numpy(), wh=w.cpu().numpy(): oracle.rmsnorm(xh, wh)
         elif op == "softmax":
             calls = [lambda i=i: sa.softmax(xs[i], os_[i], n) for i in range(sets)]
-            byts = 8 * n
+            byts = 16 * n
             cpu = lambda xh=x.cpu().numpy(): oracle.softmax(xh)
         else:
             calls = [lambda i=i: sa.silu(xs[i], os_[i], n) for i in range(sets)]
