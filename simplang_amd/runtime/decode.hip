@@ -63,6 +63,16 @@ struct StepState {
   int token, pos, n_prompt, n_total;
 };
 
+// Synchronises s on scope exit unless cleared: a call that returns early
+// (an error) after queueing copies from its own stack or the caller's arrays
+// still lets them finish before those go away.
+struct StreamDrain {
+  hipStream_t s;
+  ~StreamDrain() {
+    if (s) (void)hipStreamSynchronize(s);
+  }
+};
+
 // Split-attention partials that a GEMV combines into its x (launch_attention
 // with combine false): n chunks of max_splits per head of hs, each hs floats
 // of o, then m and l (a stride of hs + 4 floats).
@@ -1350,6 +1360,7 @@ int32_t simp_rt_llama_forward(simp_rt_llama *h, int64_t token, int64_t pos, floa
   m->stream = cur_stream();
   StepState s{(int)token, (int)pos, 0, 0};
   SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->stream));
+  StreamDrain drain{m->stream};  // s is read by the copy until the stream drains
   int rc = enqueue_step(*m, attn_key(pos, m->attn_ws != nullptr, m->cfg.n_heads));
   if (rc) return rc;
   if (logits) {
@@ -1360,6 +1371,7 @@ int32_t simp_rt_llama_forward(simp_rt_llama *h, int64_t token, int64_t pos, floa
     Operand *ops[] = {&ol};
     if ((rc = finish(ops, 1))) return rc;
   }
+  drain.s = nullptr;
   SIMP_HIP(hipStreamSynchronize(m->stream));
   return SIMP_RT_OK;
 }
@@ -1381,6 +1393,7 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
   SIMP_HIP(hipMemcpyAsync(m->tokens, prompt, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, st));
   StepState s{prompt[0], 0, (int)n_prompt, (int)total};
   SIMP_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, st));
+  StreamDrain drain{st};  // s and the caller's arrays are read until the stream drains
   int rc;
   const int64_t steps = total - 1;  // the last sampled token needs no forward pass
   // step i runs at pos i
@@ -1395,6 +1408,7 @@ int32_t simp_rt_llama_generate(simp_rt_llama *h, const int32_t *prompt, int64_t 
       if ((rc = enqueue_step(*m, mode_of(i)))) return rc;
   }
   SIMP_HIP(hipMemcpyAsync(out_tokens, m->tokens, 4 * (size_t)total, hipMemcpyDeviceToHost, st));
+  drain.s = nullptr;
   SIMP_HIP(hipStreamSynchronize(st));
   return SIMP_RT_OK;
 }
@@ -1749,11 +1763,11 @@ int quant_alloc(QuantModel &m) {
 int quant_step(QuantModel &m, int64_t token, int64_t pos, hipStream_t st) {
   const int dim = (int)m.dim, hid = (int)m.hid, kvd = m.kv_dim, gs = (int)m.gs;
   const float eps = 1e-5f;  // llama2_quant.sl:73,146,184
-  StepState s{(int)token, (int)pos, 0, 0};
-  SIMP_HIP(hipMemcpyAsync(m.state, &s, sizeof s, hipMemcpyHostToDevice, st));
+  int rc;
+  // from the pinned staging buffer: the copy may still be pending on return
+  if ((rc = m.io.upload_state(token, pos, m.state, st))) return rc;
   SIMP_HIP(hipMemcpyAsync(m.x, m.emb + token * m.dim, 4 * (size_t)dim, hipMemcpyDeviceToDevice, st));
   const unsigned gd = (unsigned)cdiv(dim, 256), gh = (unsigned)cdiv(hid, 256);
-  int rc;
   for (int64_t l = 0; l < m.L; l++) {
     if ((rc = launch_rmsnorm(m.x, m.rms_att + l * dim, m.xb, dim, eps, st))) return rc;
     if ((rc = launch_w4u(m.qw, m.scales, m.zeros, m.xb, m.qkv, dim, dim, gs, m.off[0] + l * m.dim * m.dim, st))) return rc;
