@@ -478,14 +478,24 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// out[m][n] = sum over parts p (in order) of P[p][m][n].
+// out[m][n] = sum over parts p (in order) of P[p][m][n]; the loads of B
+// parts are issued together (B about nparts: one round of loads instead of
+// one per part took 8640->3200 M=16 from 21.8 to 19.0 us).
+template <int B>
 __global__ void __launch_bounds__(256)
     w4s_sum_parts(const float *__restrict__ P, int nparts, float *__restrict__ O, int64_t ldo, int M,
                   int N) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)M * N) return;
   float t = 0.f;
-  for (int p = 0; p < nparts; p++) t += P[(int64_t)p * M * N + i];
+  for (int p = 0; p < nparts; p += B) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) v[u] = p + u < nparts ? P[(int64_t)(p + u) * M * N + i] : 0.f;
+#pragma unroll
+    for (int u = 0; u < B; u++)
+      if (p + u < nparts) t += v[u];
+  }
   const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
   O[(int64_t)m * ldo + n] = t;
 }
@@ -639,9 +649,12 @@ int launch_w4s(const uint8_t *W, int64_t ldw, const float *S, int64_t lds, const
     else
       hipLaunchKernelGGL((w4s_h16<2, RT>), dim3((unsigned)nb, (unsigned)parts), dim3(256), 0, st, W,
                          ldw, S, lds, X, ldx, O, ldo, P, M, N, K, chunks);
-    if (parts > 1)
-      hipLaunchKernelGGL(w4s_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256)), dim3(256), 0, st, P,
-                         parts, O, ldo, M, N);
+    if (parts > 1) {
+      const dim3 g((unsigned)cdiv((int64_t)M * N, 256));
+      if (parts <= 4) hipLaunchKernelGGL(w4s_sum_parts<4>, g, dim3(256), 0, st, P, parts, O, ldo, M, N);
+      else if (parts <= 8) hipLaunchKernelGGL(w4s_sum_parts<8>, g, dim3(256), 0, st, P, parts, O, ldo, M, N);
+      else hipLaunchKernelGGL(w4s_sum_parts<16>, g, dim3(256), 0, st, P, parts, O, ldo, M, N);
+    }
   } else if (M == 1 && w4d8_supported(K, gs, X, nullptr)) {
     // one x vector: exact integer chunk products on v_dot8_i32_i4 (w4d8.hip)
     W4D8Args a{};
