@@ -477,7 +477,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN)
   }
 }
 
-// C[z] = beta*C[z] + sum_s P[z][s] (s increasing: deterministic).
+// C[z] = beta*C[z] + sum_s P[z][s] (s increasing: deterministic); the loads
+// of B parts are issued together.
+template <int B>
 __global__ void __launch_bounds__(256)
     gemm_f32_sum_parts(const float *__restrict__ P, float *__restrict__ C, int64_t ldc, int64_t sc,
                        int M, int N, int parts, float beta) {
@@ -486,7 +488,14 @@ __global__ void __launch_bounds__(256)
   if (i >= mn) return;
   const float *p = P + (int64_t)blockIdx.z * parts * mn + i;
   float v = 0.f;
-  for (int s = 0; s < parts; s++) v += p[s * mn];
+  for (int s = 0; s < parts; s += B) {
+    float t[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) t[u] = s + u < parts ? p[(int64_t)(s + u) * mn] : 0.f;
+#pragma unroll
+    for (int u = 0; u < B; u++)
+      if (s + u < parts) v += t[u];
+  }
   const int64_t r = i / N, c = i - r * N;
   float *o = C + blockIdx.z * sc + r * ldc + c;
   *o = beta != 0.f ? *o + v : v;
@@ -526,8 +535,16 @@ int launch_mfma_f32(const float *A, int64_t lda, int64_t sa, const float *B, int
                      beta);
   SIMP_HIP(hipGetLastError());
   if (splits > 1) {
-    hipLaunchKernelGGL(gemm_f32_sum_parts, dim3((unsigned)cdiv((int64_t)M * N, 256), 1, (unsigned)batch),
-                       dim3(256), 0, st, (const float *)P, C, ldc, sc, M, N, (int)splits, beta);
+    const dim3 g((unsigned)cdiv((int64_t)M * N, 256), 1, (unsigned)batch);
+    if (splits <= 4)
+      hipLaunchKernelGGL(gemm_f32_sum_parts<4>, g, dim3(256), 0, st, (const float *)P, C, ldc, sc,
+                         M, N, (int)splits, beta);
+    else if (splits <= 8)
+      hipLaunchKernelGGL(gemm_f32_sum_parts<8>, g, dim3(256), 0, st, (const float *)P, C, ldc, sc,
+                         M, N, (int)splits, beta);
+    else
+      hipLaunchKernelGGL(gemm_f32_sum_parts<16>, g, dim3(256), 0, st, (const float *)P, C, ldc, sc,
+                         M, N, (int)splits, beta);
     SIMP_HIP(hipGetLastError());
   }
   return SIMP_RT_OK;
