@@ -750,20 +750,32 @@ __global__ void __launch_bounds__(64 * NWV)
   }
 }
 
-// Combines the nsplit (> 1) chunks of attn_split_k.
+// Combines the nsplit (> 1) chunks of attn_split_k: the chunks' (m, l) go
+// through LDS (one load each), and each output element requests its chunks'
+// o values eight at a time; sums in chunk order.  LDS: nsplit float2.
 __global__ void __launch_bounds__(128)
     attn_combine_k(const float *__restrict__ ws, float *__restrict__ out, int hs, int max_splits,
                    int nsplit) {
-  const int h = blockIdx.x;
-  const float *w = ws + (int64_t)h * max_splits * (hs + 4);
+  extern __shared__ float2 mls[];
+  const int h = blockIdx.x, st = hs + 4;
+  const float *w = ws + (int64_t)h * max_splits * st;
+  for (int s = threadIdx.x; s < nsplit; s += blockDim.x) mls[s] = *(const float2 *)(w + s * st + hs);
+  __syncthreads();
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; s++) M = fmaxf(M, w[s * (hs + 4) + hs]);
+  for (int s = 0; s < nsplit; s++) M = fmaxf(M, mls[s].x);
   float L = 0.f;
-  for (int s = 0; s < nsplit; s++) L += expf(w[s * (hs + 4) + hs] - M) * w[s * (hs + 4) + hs + 1];
+  for (int s = 0; s < nsplit; s++) L += expf(mls[s].x - M) * mls[s].y;
   const float il = 1.f / L;
-  for (int d = threadIdx.x; d < hs; d += 128) {
+  for (int d = threadIdx.x; d < hs; d += blockDim.x) {
     float o = 0.f;
-    for (int s = 0; s < nsplit; s++) o = fmaf(expf(w[s * (hs + 4) + hs] - M), w[s * (hs + 4) + d], o);
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = s0 + u < nsplit ? w[(s0 + u) * st + d] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (s0 + u < nsplit) o = fmaf(expf(mls[s0 + u].x - M), v[u], o);
+    }
     out[h * hs + d] = o * il;
   }
 }
@@ -810,8 +822,8 @@ int launch_attention(int key, const float *qkv, float *kc, float *vc, float *out
                        dim3(64 * kAttnNWV), 0, st, qkv, kc, vc, out, ws, state, dim, kv_dim,
                        n_heads, n_kv_heads, hs, rope, splits, key, (int)seq_len);
     if (key > 1 && combine)
-      hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128), 0, st,
-                         (const float *)ws, out, hs, splits, key);
+      hipLaunchKernelGGL(attn_combine_k, dim3((unsigned)n_heads), dim3(128),
+                         sizeof(float2) * (size_t)key, st, (const float *)ws, out, hs, splits, key);
   }
   SIMP_HIP(hipGetLastError());
   return SIMP_RT_OK;

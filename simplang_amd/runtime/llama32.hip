@@ -389,20 +389,33 @@ __global__ void __launch_bounds__(64 * kL32AttnWaves)
 // Combines the nsplit chunks of l32_attn_k for head blockIdx.x, thread d:
 // out = sum_s w_s o_s / sum_s w_s with w_s = e^(m_s - M) l_s, M = max_s m_s
 // (o_s the chunk's normalised V sum), then attn_out and xq as l32_attn_k.
+// The chunks' (m, l) go through LDS (one load each) and each element requests
+// its chunks' o values eight at a time; sums in chunk order.  LDS: nsplit
+// float2.
 __global__ void __launch_bounds__(256)
     l32_attn_combine_k(const float *__restrict__ ws, int32_t *__restrict__ attn_out,
                        int8_t *__restrict__ xq, int hs, int nsplit) {
-  const int h = blockIdx.x;
-  const float *w = ws + (int64_t)h * nsplit * (hs + 2);
+  extern __shared__ float2 mls[];
+  const int h = blockIdx.x, st = hs + 2;
+  const float *w = ws + (int64_t)h * nsplit * st;
+  for (int s = threadIdx.x; s < nsplit; s += blockDim.x) mls[s] = make_float2(w[s * st + hs], w[s * st + hs + 1]);
+  __syncthreads();
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; s++) M = fmaxf(M, w[s * (hs + 2) + hs]);
+  for (int s = 0; s < nsplit; s++) M = fmaxf(M, mls[s].x);
   for (int dd = threadIdx.x; dd < hs; dd += 256) {
     float num = 0.f, den = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-      const float *ws_s = w + s * (hs + 2);
-      const float f = expf(ws_s[hs] - M) * ws_s[hs + 1];
-      num = fmaf(f, ws_s[dd], num);
-      den += f;
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = s0 + u < nsplit ? w[(s0 + u) * st + dd] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        if (s0 + u < nsplit) {
+          const float f = expf(mls[s0 + u].x - M) * mls[s0 + u].y;
+          num = fmaf(f, v[u], num);
+          den += f;
+        }
+      }
     }
     const int32_t a = (int32_t)(num / den);
     attn_out[h * hs + dd] = a;
@@ -527,8 +540,9 @@ int l32_step(L32Model &m, int64_t pos, hipStream_t st) {
                        (const int8_t *)kc, (const int8_t *)vc, m.attn, m.xq, m.attn_ws,
                        (int)pos, kv, (int)m.hs, (int)(m.nh / m.nkv), kL32AttnChunk);
     if (nsplit > 1)
-      hipLaunchKernelGGL(l32_attn_combine_k, dim3((unsigned)m.nh), dim3(256), 0, st,
-                         (const float *)m.attn_ws, m.attn, m.xq, (int)m.hs, nsplit);
+      hipLaunchKernelGGL(l32_attn_combine_k, dim3((unsigned)m.nh), dim3(256),
+                         sizeof(float2) * (size_t)nsplit, st, (const float *)m.attn_ws, m.attn,
+                         m.xq, (int)m.hs, nsplit);
     s = L32Segs{};
     s.w[0] = m.wo + l * m.dim * m.dim;
     s.rows[0] = dim;
