@@ -193,13 +193,28 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x == 0) part[blockIdx.x] = ss;
 }
 
+// The blocks' partials, four per thread requested together (each thread's in
+// increasing block order, as a strided loop would add them).
+template <typename T, typename F>
+__device__ __forceinline__ void for_parts(const T *__restrict__ part, F f) {
+  const int G = (int)gridDim.x;
+  for (int b0 = threadIdx.x; b0 < G; b0 += 4 * 256) {
+    T v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = b0 + 256 * u < G ? part[b0 + 256 * u] : T{};
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (b0 + 256 * u < G) f(v[u]);
+  }
+}
+
 __global__ void __launch_bounds__(256)
     rmsnorm_apply_k(const float *__restrict__ x, const float *__restrict__ w,
                     float *__restrict__ out, int64_t n, float eps, const float *__restrict__ part,
                     bool vec) {
   __shared__ float scratch[16];
   float t = 0.f;
-  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) t += part[b];
+  for_parts(part, [&](float p) { t += p; });
   t = block_sum(t, scratch);
   const float rms = sqrtf(t / (float)n + eps);
   int64_t b0, b1;
@@ -244,13 +259,12 @@ __global__ void __launch_bounds__(256)
                     const float2 *__restrict__ part, bool vec) {
   __shared__ float scratch[16];
   float mx = -INFINITY;
-  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) mx = fmaxf(mx, part[b].x);
+  for_parts(part, [&](float2 p) { mx = fmaxf(mx, p.x); });
   mx = block_max(mx, scratch);
   float l = 0.f;
-  for (int b = threadIdx.x; b < (int)gridDim.x; b += 256) {
-    const float2 p = part[b];
+  for_parts(part, [&](float2 p) {
     if (p.x > -INFINITY) l += p.y * expf(p.x - mx);
-  }
+  });
   l = block_sum(l, scratch);
   int64_t b0, b1;
   slice_of(n, &b0, &b1);
