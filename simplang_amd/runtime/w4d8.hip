@@ -595,7 +595,8 @@ int launch_rm(const W4D8Args &a, int G, hipStream_t st) {
 
 // Blocks: at least one per CU, and enough that a team has at most 16 rows
 // (about 16 rows per team streams best; caps of 24 and 32 with fewer blocks
-// measured 2-3% slower on the 3B W4 decode).
+// measured 2-3% slower on the 3B W4 decode, and a cap of 8 with more blocks
+// slower too: 3200->8640 6.7 against 6.1 us).
 template <int C, int KT, int NW, int D, int MX = 1>
 int launch_cfg(W4D8Args a, hipStream_t st) {
   constexpr int teams = NW / KT;
