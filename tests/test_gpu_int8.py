@@ -178,8 +178,6 @@ def test_int8_recipe_checksums(dev, orc):
 @pytest.mark.parametrize("variant", ["u8s8", "s8s8", "nt_u8s8", "nt_s8s8"])
 def test_int8_full_size_identities(dev, orc, M, N, K, variant):
     import torch
-    if M == 8192 and variant.startswith("nt"):
-        pytest.skip("NT at 8192 covered by the KN path's identical kernel")
     print(f"[int8-full] {variant} M={M} N={N} K={K}", flush=True)
     a, b = _inputs(M, N, K)
     if "s8s8" in variant:
