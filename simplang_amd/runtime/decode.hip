@@ -1462,10 +1462,12 @@ class StepIO {
     return SIMP_RT_OK;
   }
   // Copies lg_bytes of logits and L rows of `row` bytes (`pitch` apart) of K
-  // and V to the caller's arrays, then synchronises st.
+  // and V to the caller's arrays, then synchronises st; *first gets logits[0]
+  // (from the same device logits, through the pinned buffer, so the call's
+  // return value needs no copy of its own).
   int copy_back(void *lg_dst, const void *lg_src, size_t lg_bytes, char *k_dst, char *v_dst,
                 const char *k_src, const char *v_src, size_t row, size_t pitch, int64_t L,
-                hipStream_t st) {
+                hipStream_t st, float *first) {
     const void *dv;
     const size_t span = (size_t)(L - 1) * pitch + row;
     const bool lg_host = !try_device_view(lg_dst, lg_bytes, &dv);
@@ -1484,7 +1486,9 @@ class StepIO {
       SIMP_HIP(hipMemcpy2DAsync(k_dst, pitch, k_src, pitch, row, (size_t)L, hipMemcpyDefault, st));
       SIMP_HIP(hipMemcpy2DAsync(v_dst, pitch, v_src, pitch, row, (size_t)L, hipMemcpyDefault, st));
     }
+    if (!lg_host) SIMP_HIP(hipMemcpyAsync(buf_ + kFirst, lg_src, sizeof(float), hipMemcpyDeviceToHost, st));
     SIMP_HIP(hipStreamSynchronize(st));
+    std::memcpy(first, lg_host ? buf_ + o_lg : buf_ + kFirst, sizeof(float));
     if (lg_host) std::memcpy(lg_dst, buf_ + o_lg, lg_bytes);
     if (kv_host)
       for (int64_t l = 0; l < L; l++) {
@@ -1495,7 +1499,8 @@ class StepIO {
   }
 
  private:
-  static constexpr size_t kHead = 256;  // the state slot
+  static constexpr size_t kHead = 256;   // the state slot and logits[0]
+  static constexpr size_t kFirst = 64;   // logits[0] within the head
   static size_t align(size_t n) { return (n + 255) & ~(size_t)255; }
   int reserve(size_t n) {
     n = std::max(n, kHead);
@@ -1675,13 +1680,12 @@ float stories110M_forward(
     hip_fail(hipGetLastError(), "stories110M_forward: hipGraphLaunch");
     return nan;
   }
+  float l0 = nan;
   if (ent.io.copy_back(lg, m->logits, 4 * (size_t)vocab_size, (char *)(key_cache + key_cache_off + at),
                        (char *)(value_cache + value_cache_off + at), (const char *)(m->kcache + at),
-                       (const char *)(m->vcache + at), row, pitch, L, m->stream))
+                       (const char *)(m->vcache + at), row, pitch, L, m->stream, &l0))
     return nan;
   ent.kv.done(pos);
-  float l0 = nan;
-  if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
   return l0;
 }
 
@@ -2020,13 +2024,12 @@ float llama2_quant_forward(
     return nan;
   if (quant_forward_device(*m, token, pos, st)) return nan;
   float *lg = logits + logits_off;
+  float l0 = nan;
   if (m->io.copy_back(lg, m->logits, 4 * (size_t)vocab_size, (char *)(key_cache + key_cache_off + at),
                       (char *)(value_cache + value_cache_off + at), (const char *)(m->kc + at),
-                      (const char *)(m->vc + at), row, pitch, L, st))
+                      (const char *)(m->vc + at), row, pitch, L, st, &l0))
     return nan;
   m->kv.done(pos);
-  float l0 = nan;
-  if (hipMemcpy(&l0, lg, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
   return l0;
 }
 
