@@ -437,6 +437,7 @@ struct L32Model {
   int8_t *xi = nullptr, *xq = nullptr, *hq = nullptr, *kc = nullptr, *vc = nullptr;
   int32_t *q = nullptr, *attn = nullptr;
   float *attn_ws = nullptr;  // l32_attn_k chunk results: nh * cdiv(S, chunk) * (hs + 2)
+  float *first = nullptr;    // pinned: logits[0], the call's return value
   ExportWeights weights;
   KvState kvs;
   uint64_t last_use = 0;
@@ -451,6 +452,8 @@ void l32_free(L32Model &m) {
   m.xi = m.xq = m.hq = m.kc = m.vc = nullptr;
   m.q = m.attn = nullptr;
   m.attn_ws = nullptr;
+  if (m.first) (void)hipHostFree(m.first);
+  m.first = nullptr;
   m.weights.release();
 }
 
@@ -468,6 +471,10 @@ int l32_alloc(L32Model &m) {
     if (hipMalloc(b.p, std::max<size_t>(b.bytes, 16)) != hipSuccess)
       return set_error(SIMP_RT_ENOMEM, "llama32_forward: device buffers");
     SIMP_HIP(hipMemset(*b.p, 0, b.bytes));
+  }
+  if (hipHostMalloc((void **)&m.first, 64, hipHostMallocDefault) != hipSuccess) {
+    m.first = nullptr;
+    return set_error(SIMP_RT_ENOMEM, "llama32_forward: pinned return slot");
   }
   return SIMP_RT_OK;
 }
@@ -725,15 +732,15 @@ float llama32_forward(
   if (e == hipSuccess)
     e = hipMemcpy2DAsync(v_cache + v_cache_off + at, pitch, m->vc + at, pitch, row, (size_t)L,
                          hipMemcpyDefault, st);
+  // logits[0] for the return value, in the same synchronisation
+  if (e == hipSuccess) e = hipMemcpyAsync(m->first, m->logits, sizeof(float), hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   if (e != hipSuccess) {
     hip_fail(e, "llama32_forward: result copies");
     return nan;
   }
   m->kvs.done(pos);
-  float l0 = nan;
-  if (hipMemcpy(&l0, logits + logits_off, sizeof l0, hipMemcpyDefault) != hipSuccess) return nan;
-  return l0;
+  return *m->first;
 }
 
 #undef SIMP_DESC_F32
